@@ -1,0 +1,8 @@
+"""exl3mi: MI355X-native (gfx950) EXL3 trellis-quantized linear and grouped-MoE hot path.
+
+Import with importlib (the directory name is not a Python identifier):
+    exl3 = importlib.import_module("b70-inference_amd")
+"""
+from ._lib import ACT_GELU_TANH, ACT_SILU, Exl3Error, lib  # noqa: F401
+from .linear import (BC_LinearEXL3, exl3_gemm, exl3_reconstruct, had_r_128, reconstruct,  # noqa: F401
+                     reconstruct_slice)

@@ -1,0 +1,120 @@
+// Device-side building blocks of the EXL3 trellis kernels for gfx950 (CDNA4, wave64).
+//
+// Tile format (ext-op-inventory.md:717-733; glm/xpu/csrc/exl3_esimd.h:4-14): a 16x16 tile of K-bit codes is 8K
+// little-endian uint32 words = one MSB-first ring of 256K bits. Position t (0..255) decodes the 16-bit window of ring
+// bits [(t+1)K - 16, (t+1)K) (circular) and lands at row 8((t>>1)&1) + 2((t>>3)&3) + (t&1) (input / k index),
+// column (t>>5) + 8((t>>2)&1) (output / n index).
+//
+// Lane chunking used by every kernel here: a wave covers a strip of 8 consecutive tiles of one tile-row (128 output
+// columns). Lane l owns chunk q = l & 7 of tile l >> 3: the K words [Kq, Kq + K) of that tile, i.e. exactly the 32
+// positions t = 32q .. 32q + 31, which are columns q and q + 8 over all 16 rows. The strip is 64K contiguous words,
+// lane l reading words [Kl, Kl + K): one fully coalesced K-dword load per lane per tile-row, for every K. The only
+// other bits a lane needs are the up-to-15 bits before its chunk: the last word of lane l - 1, or (q == 0) of
+// lane l + 7 (the ring wraps inside the tile), fetched with one cross-lane permute.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kMul1 = 0x83DCD12Du;
+constexpr float kRsqrt128 = 0.08838834764831845f;
+
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// ------------------------------------------------------------------------------------------------ windows
+
+// State (in the low 16 bits; upper bits are garbage) of position u (0..31) of the lane's chunk.
+// R[0] is the word before the chunk, R[1..K] the chunk's words. In R's bit string the chunk starts at bit 32, so
+// position u's window is bits [16 + (u+1)K, 32 + (u+1)K). All offsets are compile-time after unrolling.
+template <int K>
+__device__ __forceinline__ uint32_t window_raw(const uint32_t* R, int u) {
+    const int E = 32 + (u + 1) * K;        // exclusive end bit
+    const int IW = (E - 1) >> 5;           // word holding the last bit
+    const int SH = 32 * (IW + 1) - E;      // right shift that aligns the window end with bit 0
+    if (SH == 0) return R[IW];
+    if (E - 16 >= 32 * IW) return R[IW] >> SH;
+    return __builtin_amdgcn_alignbit(R[IW - 1], R[IW], SH);
+}
+
+// mul1 codebook for two states (low 16 bits used), packed fp16 pair (lo = s0, hi = s1).
+// x = s * 0x83DCD12D mod 2^32; 0x6400 + bytesum(x) is the fp16 bit pattern of 1024 + bytesum(x) (sad_u8 adds the
+// four unsigned bytes, sad_hi_u8 adds them into the high half); w = fma(h, 0x1EEE, 0xC931) in fp16, one rounding:
+// bit-exact with the reference decode (glm/xpu/csrc/exl3_esimd.h:46-68).
+__device__ __forceinline__ h2_t mul1_pair(uint32_t s0, uint32_t s1) {
+    uint32_t x0 = (s0 & 0xFFFFu) * kMul1;
+    uint32_t x1 = (s1 & 0xFFFFu) * kMul1;
+    uint32_t h = __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u));
+    const h2_t c1 = {(_Float16)0.00676727294921875f, (_Float16)0.00676727294921875f};
+    const h2_t c2 = {(_Float16)-10.3828125f, (_Float16)-10.3828125f};
+    return __builtin_elementwise_fma(__builtin_bit_cast(h2_t, h), c1, c2);
+}
+
+// The same without the affine: packed fp16 pair of h = 1024 + bytesum(x) (exact integers). A dot product over
+// decoded weights is then sum_k a_k w_k = c1 * sum_k a_k h_k + c2 * sum_k a_k (the reference's fold,
+// glm/xpu/csrc/exl3_esimd.h:82-91); kernels apply c1 and c2 once per output instead of once per weight.
+constexpr float kMul1C1 = 0.00676727294921875f, kMul1C2 = -10.3828125f;
+__device__ __forceinline__ h2_t mul1_pair_raw(uint32_t s0, uint32_t s1) {
+    uint32_t x0 = (s0 & 0xFFFFu) * kMul1;
+    uint32_t x1 = (s1 & 0xFFFFu) * kMul1;
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_sad_hi_u8(x1, 0u, __builtin_amdgcn_sad_u8(x0, 0u, 0x64006400u)));
+}
+
+// row (k index inside the tile) and column half (0: column q, 1: column q + 8) of chunk position u
+__host__ __device__ constexpr int pos_row(int u) { return 8 * ((u >> 1) & 1) + 2 * ((u >> 3) & 3) + (u & 1); }
+__host__ __device__ constexpr int pos_half(int u) { return (u >> 2) & 1; }
+
+// Load the lane's K chunk words of one tile-row strip and the word before the chunk. `p` points at the strip's
+// first word; returns R[0..K].
+template <int K>
+__device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ p, int lane, uint32_t* R) {
+    const uint32_t* q = p + lane * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) R[1 + i] = __builtin_nontemporal_load(q + i);
+}
+
+template <int K>
+__device__ __forceinline__ void chunk_prev(int lane, uint32_t* R) {
+    int src = (lane & 7) ? lane - 1 : lane + 7;
+    R[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)R[K]);
+}
+
+// Decode the lane's 32 positions into 16 packed fp16 pairs: pair j holds positions (2j, 2j+1), i.e. rows
+// (pos_row(2j), pos_row(2j)+1) of column half pos_half(2j).
+template <int K>
+__device__ __forceinline__ void decode_chunk(const uint32_t* R, h2_t* w) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = mul1_pair(window_raw<K>(R, 2 * j), window_raw<K>(R, 2 * j + 1));
+}
+
+// Same positions, codebook affine left out (h = 1024 + bytesum).
+template <int K>
+__device__ __forceinline__ void decode_chunk_raw(const uint32_t* R, h2_t* w) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) w[j] = mul1_pair_raw(window_raw<K>(R, 2 * j), window_raw<K>(R, 2 * j + 1));
+}
+
+// ------------------------------------------------------------------------------------------------ Hadamard
+
+// Unnormalised natural-order Sylvester FWHT-128 across a wave: lane l holds elements l (a) and l + 64 (b).
+__device__ __forceinline__ void fwht128_wave(float& a, float& b, int lane) {
+    float s = a + b, d = a - b;
+    a = s;
+    b = d;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        float pa = __shfl_xor(a, m), pb = __shfl_xor(b, m);
+        bool hi = lane & m;
+        a = hi ? pa - a : a + pa;
+        b = hi ? pb - b : b + pb;
+    }
+}
+
+__device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
+
+}  // namespace exl3

@@ -1,0 +1,151 @@
+// Decode-in-GEMV core shared by the dense linear and the grouped MoE kernels.
+//
+// A workgroup of 4 waves works on one 128-column strip of one projection over a k range made of whole Hadamard
+// blocks (128 k = 8 tile-rows). The transformed activations of that range sit in LDS; each wave streams every 4th
+// tile-row of the strip, decodes its 32 positions per lane in registers and accumulates sum_k a_k * h_k with
+// v_dot2_f32_f16 (h = 1024 + bytesum, the codebook affine is applied once per output: c1 * acc + c2 * sum_k a_k).
+#pragma once
+
+#include "exl3_device.h"
+
+namespace exl3 {
+
+constexpr int kGemvKBMax = 8;        // Hadamard blocks (128 k) per workgroup split
+constexpr int kGemvTargetWG = 1024;  // workgroups a dense GEMV launch aims for (256 CUs x 4)
+constexpr int kGemvMaxRows = 8;      // rows per GEMV pass
+
+// acc[m][h] += sum over tile-rows lt = lt0, lt0 + step, ... < nt of sum_r xs[m * xs_ld + 16 lt + r] * h(16 lt + r, col)
+// where `sp` points at tile-row 0 of the strip, tile-rows are `rs` words apart, and lane l owns columns
+// 16(l >> 3) + (l & 7) + 8h. Three register buffers in a ring: loads run two tile-rows ahead of the decode and every
+// buffer is consumed in place, so a decode only waits for its own load.
+template <int K, int M>
+__device__ __forceinline__ void strip_tile_row(const uint32_t (&D)[K], int lane, const _Float16* xr, int xs_ld,
+                                               float (&acc)[M][2]) {
+    uint32_t R[K + 1];
+#pragma unroll
+    for (int i = 0; i < K; ++i) R[1 + i] = D[i];
+    chunk_prev<K>(lane, R);
+    h2_t w[16];
+    decode_chunk_raw<K>(R, w);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int r = pos_row(2 * j), h = pos_half(2 * j);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            h2_t xv = *reinterpret_cast<const h2_t*>(xr + m * xs_ld + r);
+            acc[m][h] = __builtin_amdgcn_fdot2(w[j], xv, acc[m][h], false);
+        }
+    }
+}
+
+// Unconditional (the index is clamped to the last tile-row, nt > 0), so the waitcnt pass sees straight-line loads.
+template <int K>
+__device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __restrict__ base, size_t rs, int lt,
+                                           int nt) {
+    const size_t off = (size_t)(lt < nt ? lt : nt - 1) * rs;
+#pragma unroll
+    for (int i = 0; i < K; ++i) D[i] = __builtin_nontemporal_load(base + off + i);
+    __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
+}
+
+template <int K, int M>
+__device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
+                                           int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2]) {
+    if (lt0 >= nt) return;
+    const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
+    const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
+    const size_t rstep = rs * step;
+    uint32_t A[K], B[K], C[K];
+    strip_load<K>(A, base, rstep, 0, n);
+    strip_load<K>(B, base, rstep, 1, n);
+    int i = 0;
+    for (; i + 3 <= n; i += 3) {                         // branch-free body: loads stay two tile-rows ahead
+        strip_load<K>(C, base, rstep, i + 2, n);
+        strip_tile_row<K, M>(A, lane, xs + (lt0 + i * step) * 16, xs_ld, acc);
+        strip_load<K>(A, base, rstep, i + 3, n);
+        strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
+        strip_load<K>(B, base, rstep, i + 4, n);
+        strip_tile_row<K, M>(C, lane, xs + (lt0 + (i + 2) * step) * 16, xs_ld, acc);
+    }
+    if (i < n) strip_tile_row<K, M>(A, lane, xs + (lt0 + i * step) * 16, xs_ld, acc);
+    if (i + 1 < n) strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
+}
+
+// ------------------------------------------------------------------------------------------------ split-K handoff
+// Workgroups of one output strip publish fp32 partials; the last to arrive (per-strip counter) reduces them.
+// Partials are written with agent-scope relaxed atomic stores (write-through past the XCD-local L2) and read with
+// agent-scope atomic loads, and every wave drains its stores (s_waitcnt) before the arrival atomic. This avoids the
+// device-scope fence, which on gfx950 writes back the whole L2 of the XCD once per workgroup.
+#ifndef EXL3_SPLITK_FENCE
+#define EXL3_SPLITK_FENCE 0
+#endif
+
+__device__ __forceinline__ void splitk_store(float* p, float v) {
+#if EXL3_SPLITK_FENCE
+    *p = v;
+#else
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#endif
+}
+
+__device__ __forceinline__ float splitk_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in every thread of the last-arriving workgroup (of `nparts`); that workgroup resets the counter
+// when it is done (splitk_reset), so counters are zero between launches.
+__device__ __forceinline__ bool splitk_arrive(int* cnt, int nparts, int* s_flag) {
+#if EXL3_SPLITK_FENCE
+    __threadfence();
+#else
+    __builtin_amdgcn_s_waitcnt(0);     // this wave's partial stores have completed
+#endif
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = (old == nparts - 1);
+    }
+    __syncthreads();
+    bool last = *s_flag;
+#if EXL3_SPLITK_FENCE
+    if (last) __threadfence();
+#endif
+    return last;
+}
+
+// Input transform of one 128-block for one row by one wave: returns fp16(H128(fp16(x * suh)) / sqrt(128)) at
+// elements lane and lane + 64 (as floats holding fp16 values) and writes them to dst[lane], dst[lane + 64].
+// x == nullptr gives zeros. Returns the block's element sum (every lane gets it).
+__device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ suh,
+                                              _Float16* dst, int lane) {
+    float va = 0.f, vb = 0.f;
+    if (x) {
+        va = (float)(_Float16)(h2f(x[lane]) * h2f(suh[lane]));
+        vb = (float)(_Float16)(h2f(x[lane + 64]) * h2f(suh[lane + 64]));
+    }
+    fwht128_wave(va, vb, lane);
+    _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
+    dst[lane] = ha;
+    dst[lane + 64] = hb;
+    float s = (float)ha + (float)hb;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    return s;
+}
+
+// Same for an activation block that is already in the Hadamard domain (fp16): copy to LDS and sum.
+__device__ __forceinline__ float copy_block(const uint16_t* __restrict__ x, _Float16* dst, int lane) {
+    _Float16 ha = (_Float16)0.f, hb = (_Float16)0.f;
+    if (x) {
+        ha = __builtin_bit_cast(_Float16, x[lane]);
+        hb = __builtin_bit_cast(_Float16, x[lane + 64]);
+    }
+    dst[lane] = ha;
+    dst[lane + 64] = hb;
+    float s = (float)ha + (float)hb;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    return s;
+}
+
+}  // namespace exl3

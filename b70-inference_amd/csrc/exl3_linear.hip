@@ -1,0 +1,339 @@
+// EXL3 dense linear on gfx950: reconstruct, blockwise Hadamard, and the small-M decode GEMV.
+//
+// Reference semantics: exllamav3 reconstruct_slice / had_r_128 / exl3_gemm (ext-op-inventory.md:498-612) and the
+// XPU library's exl3_reconstruct / exl3_gemm_small (glm/xpu/csrc/exl3_ops.sycl:258-321, 539-555).
+#include "exl3_device.h"
+#include "exl3_gemv.h"
+#include "exl3_runtime.h"
+
+namespace exl3 {
+
+// ================================================================================================ reconstruct
+// One wave per (128-column strip, tile-row): lanes decode their chunks, stage the 16 x 128 fp16 block in LDS, then
+// write it out with 16-byte row stores.
+template <int K>
+__global__ __launch_bounds__(64) void reconstruct_kernel(const uint32_t* __restrict__ tr, int tn, int n0_tiles,
+                                                         uint16_t* __restrict__ out, int64_t out_ld) {
+    __shared__ __attribute__((aligned(16))) uint16_t blk[16][136];
+    const int lane = threadIdx.x;
+    const int strip = blockIdx.x, trow = blockIdx.y;
+    const uint32_t* p = tr + ((size_t)trow * tn + n0_tiles + (size_t)strip * 8) * (8 * K);
+    uint32_t R[K + 1];
+    load_chunk<K>(p, lane, R);
+    chunk_prev<K>(lane, R);
+    h2_t w[16];
+    decode_chunk<K>(R, w);
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int r = pos_row(2 * j), c = cbase + 8 * pos_half(2 * j);
+        const uint32_t v = __builtin_bit_cast(uint32_t, w[j]);   // element 0 in the low half
+        blk[r][c] = (uint16_t)(v & 0xFFFFu);
+        blk[r + 1][c] = (uint16_t)(v >> 16);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = i * 64 + lane, r = idx >> 4, c8 = idx & 15;
+        uint4 v = *reinterpret_cast<const uint4*>(&blk[r][c8 * 8]);
+        *reinterpret_cast<uint4*>(out + (size_t)(16 * trow + r) * out_ld + (size_t)strip * 128 + c8 * 8) = v;
+    }
+}
+
+// ================================================================================================ had_r_128
+template <bool F16>
+__global__ __launch_bounds__(64) void had_kernel(const void* __restrict__ in, int64_t in_ld, void* __restrict__ out,
+                                                 int64_t out_ld, const uint16_t* __restrict__ pre,
+                                                 const uint16_t* __restrict__ post, float r) {
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const int c0 = blockIdx.y * 128 + lane, c1 = c0 + 64;
+    float a, b;
+    if (F16) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(in) + row * in_ld;
+        a = h2f(src[c0]);
+        b = h2f(src[c1]);
+        if (pre) {
+            a = (float)(_Float16)(a * h2f(pre[c0]));
+            b = (float)(_Float16)(b * h2f(pre[c1]));
+        }
+    } else {
+        const float* src = reinterpret_cast<const float*>(in) + row * in_ld;
+        a = src[c0];
+        b = src[c1];
+        if (pre) {
+            a *= h2f(pre[c0]);
+            b *= h2f(pre[c1]);
+        }
+    }
+    fwht128_wave(a, b, lane);
+    a *= r;
+    b *= r;
+    if (F16) {
+        a = (float)(_Float16)a;
+        b = (float)(_Float16)b;
+        if (!pre && post) {
+            a = (float)(_Float16)(a * h2f(post[c0]));
+            b = (float)(_Float16)(b * h2f(post[c1]));
+        }
+        uint16_t* dst = reinterpret_cast<uint16_t*>(out) + row * out_ld;
+        dst[c0] = f2h(a);
+        dst[c1] = f2h(b);
+    } else {
+        if (!pre && post) {
+            a *= h2f(post[c0]);
+            b *= h2f(post[c1]);
+        }
+        float* dst = reinterpret_cast<float*>(out) + row * out_ld;
+        dst[c0] = a;
+        dst[c1] = b;
+    }
+}
+
+// ================================================================================================ dense GEMV
+// Workgroup = 4 waves on one 128-column strip and one k-split (a run of Hadamard blocks). Phase 1 computes the
+// split's transformed activations into LDS; phase 2 streams the strip's tile-rows (wave w takes tile-rows w, w+4,..);
+// phase 3 reduces the waves in LDS and, across splits, through per-strip partials and an arrival counter: the last
+// workgroup of a strip sums the partials in split order (deterministic), applies the output Hadamard and svh.
+struct GemvArgs {
+    const uint16_t* x;
+    int64_t x_ld;
+    int m;
+    const uint32_t* tr;
+    int tn;
+    const uint16_t* suh;
+    const uint16_t* svh;
+    void* out;
+    int64_t out_ld;
+    float* part;
+    int* cnt;
+    int P;
+    int nblk;
+};
+
+template <int K, int M, bool F32>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[M][kGemvKBMax * 128];
+    __shared__ float red[4][M][2][64];
+    __shared__ float bsum[M][kGemvKBMax];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = blockIdx.x, p = blockIdx.y;
+    const int b0 = (int)((int64_t)p * a.nblk / a.P), b1 = (int)((int64_t)(p + 1) * a.nblk / a.P);
+    const int kb = b1 - b0;
+
+    // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums
+    for (int i = wave; i < M * kb; i += 4) {
+        const int m = i / kb, b = i - m * kb;
+        const int k0 = (b0 + b) * 128;
+        float s = had_in_block(m < a.m ? a.x + (int64_t)m * a.x_ld + k0 : nullptr, a.suh + k0, &xs[m][b * 128], lane);
+        if (lane == 0) bsum[m][b] = s;
+    }
+    __syncthreads();
+
+    // phase 2: decode-in-GEMV over the split's tile-rows
+    float acc[M][2];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.f;
+    const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
+    const uint32_t* sp = a.tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
+    strip_gemv<K, M>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc);
+
+    // phase 3: reduce waves, then splits
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        red[wave][m][0][lane] = acc[m][0];
+        red[wave][m][1][lane] = acc[m][1];
+    }
+    __syncthreads();
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    float* mypart = a.part + ((size_t)strip * a.P + p) * M * 128;
+    if (wave == 0) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float sx = 0.f;
+            for (int b = 0; b < kb; ++b) sx += bsum[m][b];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float v = red[0][m][h][lane] + red[1][m][h][lane] + red[2][m][h][lane] + red[3][m][h][lane];
+                splitk_store(mypart + m * 128 + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+            }
+        }
+    }
+    if (!splitk_arrive(&a.cnt[strip], a.P, &s_last)) return;
+    for (int m = wave; m < M && m < a.m; m += 4) {
+        float va = 0.f, vb = 0.f;
+        for (int pp = 0; pp < a.P; ++pp) {
+            const float* q = a.part + (((size_t)strip * a.P + pp) * M + m) * 128;
+            va += splitk_load(q + lane);
+            vb += splitk_load(q + lane + 64);
+        }
+        fwht128_wave(va, vb, lane);
+        const int c0 = strip * 128 + lane, c1 = c0 + 64;
+        va *= kRsqrt128 * h2f(a.svh[c0]);
+        vb *= kRsqrt128 * h2f(a.svh[c1]);
+        if (F32) {
+            float* o = reinterpret_cast<float*>(a.out) + (int64_t)m * a.out_ld;
+            o[c0] = va;
+            o[c1] = vb;
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)m * a.out_ld;
+            o[c0] = f2h(va);
+            o[c1] = f2h(vb);
+        }
+    }
+    if (threadIdx.x == 0) a.cnt[strip] = 0;
+}
+
+// ------------------------------------------------------------------------------------------------ dispatch
+typedef void (*gemv_fn)(GemvArgs);
+
+template <int K, int M>
+static gemv_fn gemv_pick(bool f32) {
+    return f32 ? (gemv_fn)gemv_kernel<K, M, true> : (gemv_fn)gemv_kernel<K, M, false>;
+}
+
+template <int K>
+static gemv_fn gemv_pick_m(int M, bool f32) {
+    switch (M) {
+        case 1: return gemv_pick<K, 1>(f32);
+        case 2: return gemv_pick<K, 2>(f32);
+        case 3: return gemv_pick<K, 3>(f32);
+        case 4: return gemv_pick<K, 4>(f32);
+        case 5: return gemv_pick<K, 5>(f32);
+        case 6: return gemv_pick<K, 6>(f32);
+        case 7: return gemv_pick<K, 7>(f32);
+        default: return gemv_pick<K, 8>(f32);
+    }
+}
+
+static gemv_fn gemv_select(int K, int M, bool f32) {
+    switch (K) {
+        case 1: return gemv_pick_m<1>(M, f32);
+        case 2: return gemv_pick_m<2>(M, f32);
+        case 3: return gemv_pick_m<3>(M, f32);
+        case 4: return gemv_pick_m<4>(M, f32);
+        case 5: return gemv_pick_m<5>(M, f32);
+        case 6: return gemv_pick_m<6>(M, f32);
+        case 7: return gemv_pick_m<7>(M, f32);
+        default: return gemv_pick_m<8>(M, f32);
+    }
+}
+
+// Number of k-splits: enough workgroups to cover the chip, at most kGemvKBMax Hadamard blocks per split.
+static int gemv_splits(int strips, int nblk) {
+    int P = (kGemvTargetWG + strips - 1) / strips;
+    int pmin = (nblk + kGemvKBMax - 1) / kGemvKBMax;
+    if (P < pmin) P = pmin;
+    if (P > nblk) P = nblk;
+    return P < 1 ? 1 : P;
+}
+
+int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
+                int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st) {
+    const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
+    const int P = gemv_splits(strips, nblk);
+    const int Mmax = kGemvMaxRows;
+    Workspace ws;
+    int rc = workspace((size_t)strips * P * Mmax * 128 * sizeof(float), (size_t)strips, &ws);
+    if (rc) return rc;
+    for (int64_t m0 = 0; m0 < m; m0 += Mmax) {
+        const int mm = (int)((m - m0) < Mmax ? (m - m0) : Mmax);
+        GemvArgs ga;
+        ga.x = A + m0 * a_ld;
+        ga.x_ld = a_ld;
+        ga.m = mm;
+        ga.tr = tr;
+        ga.tn = tn;
+        ga.suh = suh;
+        ga.svh = svh;
+        ga.out = f32 ? (void*)(reinterpret_cast<float*>(C) + m0 * c_ld) : (void*)(reinterpret_cast<uint16_t*>(C) + m0 * c_ld);
+        ga.out_ld = c_ld;
+        ga.part = reinterpret_cast<float*>(ws.scratch);
+        ga.cnt = ws.counters;
+        ga.P = P;
+        ga.nblk = nblk;
+        gemv_fn fn = gemv_select(K, mm, f32);
+        hipLaunchKernelGGL(fn, dim3(strips, P), dim3(256), 0, st, ga);
+        EXL3_CHECK_HIP(hipGetLastError());
+    }
+    return EXL3_OK;
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" {
+
+int exl3_reconstruct(const int16_t* trellis, int64_t k, int64_t n_total, int K, int cb, int64_t n_offset,
+                     int64_t n_slice, uint16_t* out, int64_t out_ld, void* stream) {
+    if (cb != 2) return fail(EXL3_ERR_UNSUPPORTED, "exl3_reconstruct: codebook %d not supported (mul1 = 2 only)", cb);
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_reconstruct: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(trellis && out, "exl3_reconstruct: null pointer");
+    EXL3_CHECK_ARG(k > 0 && k % 16 == 0 && n_total % 16 == 0, "exl3_reconstruct: k=%lld n=%lld must be multiples of 16",
+                   (long long)k, (long long)n_total);
+    EXL3_CHECK_ARG(n_offset % 128 == 0 && n_slice % 128 == 0 && n_offset >= 0 && n_slice >= 0 &&
+                       n_offset + n_slice <= n_total,
+                   "exl3_reconstruct: slice [%lld, +%lld) of %lld must be 128-aligned and in range",
+                   (long long)n_offset, (long long)n_slice, (long long)n_total);
+    EXL3_CHECK_ARG(out_ld >= n_slice && out_ld % 8 == 0 && aligned(out, 16),
+                   "exl3_reconstruct: output must be 16-byte aligned with a row stride that is a multiple of 8");
+    EXL3_CHECK_ARG(aligned(trellis, 4), "exl3_reconstruct: trellis must be 4-byte aligned");
+    if (n_slice == 0) return EXL3_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(trellis);
+    dim3 grid((unsigned)(n_slice / 128), (unsigned)(k / 16));
+    const int tn = (int)(n_total / 16), n0t = (int)(n_offset / 16);
+    switch (K) {
+        case 1: hipLaunchKernelGGL(reconstruct_kernel<1>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 2: hipLaunchKernelGGL(reconstruct_kernel<2>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 3: hipLaunchKernelGGL(reconstruct_kernel<3>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 4: hipLaunchKernelGGL(reconstruct_kernel<4>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 5: hipLaunchKernelGGL(reconstruct_kernel<5>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 6: hipLaunchKernelGGL(reconstruct_kernel<6>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        case 7: hipLaunchKernelGGL(reconstruct_kernel<7>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+        default: hipLaunchKernelGGL(reconstruct_kernel<8>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
+    }
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+int exl3_had_r_128(const void* in, int64_t in_ld, void* out, int64_t out_ld, int64_t rows, int64_t cols, int dtype,
+                   const uint16_t* pre, const uint16_t* post, float scale, void* stream) {
+    EXL3_CHECK_ARG(in && out, "exl3_had_r_128: null pointer");
+    EXL3_CHECK_ARG(dtype == EXL3_F16 || dtype == EXL3_F32, "exl3_had_r_128: dtype must be fp16 or fp32");
+    EXL3_CHECK_ARG(rows >= 0 && cols % 128 == 0 && in_ld >= cols && out_ld >= cols,
+                   "exl3_had_r_128: cols=%lld must be a multiple of 128 and row strides >= cols", (long long)cols);
+    if (rows == 0 || cols == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(rows <= 0x7FFFFFFF && cols / 128 <= 65535, "exl3_had_r_128: shape too large");
+    dim3 grid((unsigned)rows, (unsigned)(cols / 128));
+    float r = scale * kRsqrt128;
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == EXL3_F16)
+        hipLaunchKernelGGL(had_kernel<true>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
+    else
+        hipLaunchKernelGGL(had_kernel<false>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K, void* C,
+              int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
+              void* stream) {
+    (void)A_had;
+    if (cb != 2) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm: codebook %d not supported (mul1 = 2 only)", cb);
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(c_dtype == EXL3_F16 || c_dtype == EXL3_F32, "exl3_gemm: C must be fp16 or fp32");
+    EXL3_CHECK_ARG(m >= 0 && k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0,
+                   "exl3_gemm: k=%lld and n=%lld must be positive multiples of 128", (long long)k, (long long)n);
+    EXL3_CHECK_ARG(a_ld >= k && c_ld >= n, "exl3_gemm: row strides must cover k / n");
+    if (m == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(A && B && C && suh && svh, "exl3_gemm: null pointer");
+    EXL3_CHECK_ARG(aligned(B, 4), "exl3_gemm: trellis must be 4-byte aligned");
+    EXL3_CHECK_ARG(n / 128 <= 65535, "exl3_gemm: n too large");
+    return launch_gemv(A, a_ld, m, k, reinterpret_cast<const uint32_t*>(B), n, K, C, c_ld, c_dtype == EXL3_F32, suh,
+                       svh, (hipStream_t)stream);
+}
+
+}  // extern "C"

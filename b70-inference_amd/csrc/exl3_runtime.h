@@ -1,0 +1,54 @@
+// Host-side runtime shared by the EXL3 C-ABI entry points: status codes, the thread-local error message, and the
+// per-device workspace (split-K partials, arrival counters, routing tables, intermediate activations).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/exl3mi.h"
+
+namespace exl3 {
+
+// Records a message for exl3_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define EXL3_CHECK_ARG(cond, ...) \
+    do { if (!(cond)) return ::exl3::fail(EXL3_ERR_INVALID, __VA_ARGS__); } while (0)
+#define EXL3_CHECK_HIP(expr)                                                                          \
+    do {                                                                                              \
+        hipError_t e_ = (expr);                                                                       \
+        if (e_ != hipSuccess) return ::exl3::fail(EXL3_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// Device workspace of the current device. `bytes` of plain scratch (256-byte aligned) and `ncounters` int32 arrival
+// counters that are zero between calls (kernels that use a counter reset it before they exit). Grows on demand;
+// growing synchronises the device. Calls that share a device must be ordered on one stream (as the reference's
+// library-owned scratch, glm/xpu/csrc/exl3_ops.sycl:202-207).
+struct Workspace {
+    char* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    int* counters = nullptr;
+    size_t ncounters = 0;
+};
+int workspace(size_t bytes, size_t ncounters, Workspace* out);
+
+// Bump allocator over one workspace request.
+struct Carve {
+    char* p;
+    size_t left;
+    template <typename T>
+    T* take(size_t n) {
+        size_t b = (n * sizeof(T) + 255) & ~(size_t)255;
+        if (b > left) return nullptr;
+        T* r = reinterpret_cast<T*>(p);
+        p += b;
+        left -= b;
+        return r;
+    }
+};
+inline size_t carve_size(size_t n, size_t elem) { return (n * elem + 255) & ~(size_t)255; }
+
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+}  // namespace exl3

@@ -1,0 +1,145 @@
+"""EXL3 linear layer on the HIP kernels: the exllamav3 ext ops of the linear path and the BC_LinearEXL3 shim.
+
+Interfaces mirror the reference boundary:
+  * BC_LinearEXL3(trellis, suh, svh, K, bias, mcg, mul1, xh) with run(x, y) / run_alloc(x, out_features, output_fp32)
+    (glm/xpu/glm_xpu/ops.py:34-88; ext-op-inventory.md:471-496)
+  * exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1, force_num_sms) (ext-op-inventory.md:498-557)
+  * reconstruct / reconstruct_slice (ext-op-inventory.md:597-612), exl3_reconstruct (glm/xpu/csrc/exl3_ops.sycl:539-555)
+  * had_r_128(input, output, pre_scale, post_scale, scale) (ext-op-inventory.md:576-595)
+Tensors live on the GPU; every op is asynchronous on the current stream and writes its output in place.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import EXL3_F16, EXL3_F32, Exl3Error, check, lib, ptr, require_device, stream_of
+
+CB_MUL1 = 2
+
+
+def _cb(mcg: bool, mul1: bool) -> int:
+    if mcg:
+        raise NotImplementedError("exl3mi: only the mul1 codebook is implemented (mcg requested)")
+    if not mul1:
+        raise NotImplementedError("exl3mi: only the mul1 codebook is implemented (3inst requested)")
+    return CB_MUL1
+
+
+def _K_of(trellis: torch.Tensor, K=None) -> int:
+    if trellis.dim() != 3 or trellis.dtype != torch.int16:
+        raise Exl3Error(f"trellis must be int16 [k/16, n/16, 16K], got {tuple(trellis.shape)} {trellis.dtype}")
+    Kt = trellis.shape[-1] / 16
+    if K is not None and float(K) != Kt:
+        raise Exl3Error(f"K={K} does not match trellis.shape[-1]={trellis.shape[-1]}")
+    if Kt != int(Kt):
+        raise NotImplementedError("exl3mi: half-integer bitrates are not supported")
+    return int(Kt)
+
+
+def exl3_reconstruct(trellis: torch.Tensor, w: torch.Tensor, n0: int, K: int, cb: int = CB_MUL1) -> None:
+    """w[:, :] = W_hat[:, n0 : n0 + w.shape[1]] (fp16, Hadamard domain); exl3xpu_C::exl3_reconstruct."""
+    require_device(trellis, w)
+    if w.dtype != torch.float16 or w.dim() != 2 or w.stride(1) != 1:
+        raise Exl3Error("reconstruct output must be a 2D fp16 tensor with unit column stride")
+    if not trellis.is_contiguous():
+        raise Exl3Error("trellis must be contiguous")
+    k = trellis.shape[0] * 16
+    if w.shape[0] != k:
+        raise Exl3Error(f"reconstruct output has {w.shape[0]} rows, trellis has {k}")
+    check(lib().exl3_reconstruct(ptr(trellis), k, trellis.shape[1] * 16, int(K), int(cb), int(n0), w.shape[1], ptr(w),
+                                 w.stride(0), stream_of(w)), "exl3_reconstruct")
+
+
+def reconstruct(unpacked: torch.Tensor, packed: torch.Tensor, K, mcg: bool, mul1: bool) -> None:
+    """exllamav3 ext reconstruct(unpacked, packed, K, mcg, mul1)."""
+    exl3_reconstruct(packed, unpacked, 0, _K_of(packed, K), _cb(mcg, mul1))
+
+
+def reconstruct_slice(unpacked: torch.Tensor, packed: torch.Tensor, K, mcg: bool, mul1: bool, n_offset: int) -> None:
+    """exllamav3 ext reconstruct_slice(unpacked, packed, K, mcg, mul1, n_offset)."""
+    exl3_reconstruct(packed, unpacked, n_offset, _K_of(packed, K), _cb(mcg, mul1))
+
+
+def had_r_128(input: torch.Tensor, output: torch.Tensor, pre_scale, post_scale, scale: float) -> None:
+    """Blockwise H128 * scale / sqrt(128) with optional fp16 pre/post scales (pre wins), written into output."""
+    require_device(input, output, pre_scale, post_scale)
+    if input.shape != output.shape or input.dim() != 2:
+        raise Exl3Error("had_r_128: input and output must be 2D with equal shapes")
+    if input.dtype != output.dtype or input.dtype not in (torch.float16, torch.float32):
+        raise Exl3Error("had_r_128: input/output must both be fp16 or both fp32")
+    if input.stride(1) != 1 or output.stride(1) != 1:
+        raise Exl3Error("had_r_128: rows must be contiguous")
+    for v in (pre_scale, post_scale):
+        if v is not None and (v.dtype != torch.float16 or v.numel() != input.shape[1] or not v.is_contiguous()):
+            raise Exl3Error("had_r_128: scales must be contiguous fp16 [cols]")
+    dt = EXL3_F16 if input.dtype == torch.float16 else EXL3_F32
+    check(lib().exl3_had_r_128(ptr(input), input.stride(0), ptr(output), output.stride(0), input.shape[0],
+                               input.shape[1], dt, ptr(pre_scale), ptr(post_scale), float(scale), stream_of(input)),
+          "had_r_128")
+
+
+def exl3_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor, A_had, svh: torch.Tensor,
+              force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True, force_num_sms: int = 0) -> int:
+    """C = Hn(Hk(A * suh) @ W_hat) * svh; A fp16 [..., k] contiguous, C fp16/fp32 [..., n]. Returns 0 (kernel tag)."""
+    require_device(A, B, C, suh, svh)
+    K = _K_of(B)
+    cb = _cb(mcg, mul1)
+    k, n = B.shape[0] * 16, B.shape[1] * 16
+    if A.dtype != torch.float16 or A.shape[-1] != k:
+        raise Exl3Error(f"exl3_gemm: A must be fp16 [..., {k}]")
+    if C.shape[-1] != n or C.dtype not in (torch.float16, torch.float32):
+        raise Exl3Error(f"exl3_gemm: C must be fp16/fp32 [..., {n}]")
+    if not A.is_contiguous() or not B.is_contiguous() or not C.is_contiguous():
+        raise Exl3Error("exl3_gemm: A, B and C must be contiguous")
+    if suh.dtype != torch.float16 or svh.dtype != torch.float16 or suh.numel() != k or svh.numel() != n:
+        raise Exl3Error("exl3_gemm: suh/svh must be fp16 [k] / [n]")
+    m = A.numel() // k
+    if C.numel() // n != m:
+        raise Exl3Error("exl3_gemm: A and C row counts differ")
+    dt = EXL3_F32 if C.dtype == torch.float32 else EXL3_F16
+    check(lib().exl3_gemm(ptr(A), k, m, k, ptr(B), n, K, ptr(C), n, dt, ptr(suh.contiguous()), ptr(A_had),
+                          ptr(svh.contiguous()), cb, stream_of(A)), "exl3_gemm")
+    return 0
+
+
+class BC_LinearEXL3:
+    """EXL3 linear: y = Had(Had(x * suh) @ W_hat) * svh (+ bias), on the HIP kernels (mul1 codebook).
+
+    Holds the fields other modules read to build pointer tables (trellis, suh, svh, K, bias, mcg, mul1, xh), exactly
+    as the reference shim does (glm/xpu/glm_xpu/ops.py:34-88)."""
+
+    def __init__(self, trellis, suh, svh, K, bias, mcg, mul1, xh):
+        self.trellis = trellis
+        self.suh = suh
+        self.svh = svh
+        self.K = K
+        self.bias = bias
+        self.mcg = mcg
+        self.mul1 = mul1
+        self.xh = xh
+        self.cb = _cb(mcg, mul1)
+        self.Ki = _K_of(trellis, K)
+        self.in_features = trellis.shape[0] * 16
+        self.out_features = trellis.shape[1] * 16
+
+    def run(self, x: torch.Tensor, y: torch.Tensor) -> None:
+        """x fp16 [..., k] -> y (fp16 or fp32, preallocated) [..., n]."""
+        x2 = x.reshape(-1, self.in_features)
+        if x2.dtype != torch.float16:
+            x2 = x2.half()
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        y2 = y.view(-1, self.out_features)
+        if x2.shape[0] == 0:
+            return
+        exl3_gemm(x2, self.trellis, y2, self.suh, self.xh, self.svh, -1, self.mcg, self.mul1, 0)
+        if self.bias is not None:
+            y2.add_(self.bias)
+
+    def run_alloc(self, x: torch.Tensor, out_features: int, output_fp32: bool) -> torch.Tensor:
+        y = torch.empty(x.shape[:-1] + (out_features,), dtype=torch.float if output_fp32 else torch.half,
+                        device=x.device)
+        if out_features == 0:
+            return y
+        self.run(x.reshape(-1, x.shape[-1]), y.view(-1, out_features))
+        return y

@@ -1,0 +1,337 @@
+"""NumPy restatement of the EXL3 (exllamav3 trellis, mul1 codebook) linear and MoE-layer semantics.
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the timed CPU baseline. The product never imports it.
+
+Sources restated (paths relative to the reference root):
+  * bitstream + window     glm/docs/ext-op-inventory.md:717-725, 746-757; glm/xpu/csrc/exl3_esimd.h:4-14, 117-149;
+                           dsv41/xpu/dsv_xpu/exl3_tri.py:22-35
+  * mul1 codebook          glm/xpu/csrc/exl3_esimd.h:40-68; ext-op-inventory.md:559-571, 738-743
+  * position -> (row,col)  glm/xpu/csrc/exl3_esimd.h:7-8; ext-op-inventory.md:727-733
+  * reconstruct            glm/xpu/csrc/exl3_ops.sycl:539-555; ext-op-inventory.md:597-612, 758-760
+  * had_r_128              ext-op-inventory.md:576-595; glm/xpu/glm_xpu/ops.py:118-142
+  * linear                 ext-op-inventory.md:512-535, 707-712, 762-773
+  * expert math / MoE      ext-op-inventory.md:923-942; glm/xpu/csrc/exl3_moe.n128.sycl:253-271, 370-379, 405-408;
+                           dsv41/xpu/dsv_xpu/moe.py:967-994
+  * activations            ext-op-inventory.md:944-956 (SiLU, act_limit clamp); GELU-tanh = torch gelu(approximate='tanh')
+  * routing                trellis-serve.patch:395-441 (softmax -> top-k -> renormalise, +1e-20)
+  * align / pair lists     glm/xpu/csrc/exl3_moe.n128.sycl:691-734
+
+Every floating-point reduction here runs in float64 unless a caller asks for float32 (`acc`), so the oracle is at
+least as accurate as the fp32-accumulated reference. Rounding points that the reference fixes (fp16 x*suh, fp16
+transformed activations, fp16 gate/up/act) are reproduced exactly.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+MUL1 = 0x83DCD12D
+K_INV = 0.00676727294921875      # fp16 bit pattern 0x1EEE
+K_BIAS = -10.3828125             # fp16 bit pattern 0xC931
+RSQRT128 = 1.0 / math.sqrt(128.0)
+
+# ------------------------------------------------------------------------------------------------ codebook
+
+
+def mul1_values(states: np.ndarray) -> np.ndarray:
+    """mul1 codebook on 16-bit states -> float16. x = st * 0x83DCD12D mod 2^32, s = byte sum of x,
+    w = fp16((1024 + s) * K_INV + K_BIAS) with one rounding (exl3_esimd.h:46-68, inventory:559-571).
+    (1024 + s) * K_INV is exact in float64 and in float32, so the single rounding is the cast to float16."""
+    st = np.asarray(states, dtype=np.uint64) & 0xFFFF
+    x = (st * MUL1) & 0xFFFFFFFF
+    s = (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + ((x >> 24) & 0xFF)
+    v = (1024.0 + s.astype(np.float64)) * K_INV + K_BIAS
+    return v.astype(np.float16)
+
+
+_LUT = None
+
+
+def mul1_lut() -> np.ndarray:
+    """[65536] float16: the codebook value of every 16-bit state."""
+    global _LUT
+    if _LUT is None:
+        _LUT = mul1_values(np.arange(65536, dtype=np.uint64))
+        _LUT.setflags(write=False)
+    return _LUT
+
+
+# ------------------------------------------------------------------------------------------------ tile layout
+
+
+def pos_row_col():
+    """Position t (0..255) of the tile stream -> (row, col) of the 16x16 tile; row is the input (k) index, col the
+    output (n) index (exl3_esimd.h:7-8, inventory:727-733)."""
+    t = np.arange(256)
+    row = 8 * ((t >> 1) & 1) + 2 * ((t >> 3) & 3) + (t & 1)
+    col = (t >> 5) + 8 * ((t >> 2) & 1)
+    return row, col
+
+
+def tile_states(words: np.ndarray, K: int) -> np.ndarray:
+    """words [..., 8K] uint32 (little-endian int16 pairs) -> [..., 256] 16-bit states. Position t's state is the
+    window of stream bits [(t+1)K - 16, (t+1)K), MSB-first, circular within the tile (inventory:746-757)."""
+    assert 1 <= K <= 8
+    w = np.asarray(words, dtype=np.uint64)
+    assert w.shape[-1] == 8 * K
+    t = np.arange(256)
+    e = (t + 1) * K
+    ih = (e - 1) // 32
+    sh = (32 * (ih + 1) - e).astype(np.uint64)
+    il = (ih - 1) % (8 * K)
+    st = (((w[..., il] << np.uint64(32)) | w[..., ih]) >> sh) & np.uint64(0xFFFF)
+    return st.astype(np.uint16)
+
+
+def trellis_words(trellis: np.ndarray) -> np.ndarray:
+    """int16 [tk, tn, 16K] -> uint32 [tk, tn, 8K] (word i = u16[2i] | u16[2i+1] << 16)."""
+    tr = np.ascontiguousarray(trellis)
+    assert tr.dtype == np.int16 and tr.shape[-1] % 16 == 0
+    return tr.view(np.uint32)
+
+
+def decode_tiles(words: np.ndarray, K: int) -> np.ndarray:
+    """uint32 [..., 8K] -> float16 [..., 16, 16] (tile[row, col])."""
+    vals = mul1_lut()[tile_states(words, K)]
+    row, col = pos_row_col()
+    tiles = np.empty(vals.shape[:-1] + (16, 16), dtype=np.float16)
+    tiles[..., row, col] = vals
+    return tiles
+
+
+def reconstruct(trellis: np.ndarray, K: int, n0: int = 0, n_slice: int | None = None) -> np.ndarray:
+    """W_hat[:, n0 : n0 + n_slice] as float16 [k, n_slice], Hadamard domain, no sign vectors
+    (exl3_ops.sycl:539-555, inventory:597-612, 758-760)."""
+    tk, tn, w = trellis.shape
+    assert w == 16 * K
+    if n_slice is None:
+        n_slice = tn * 16 - n0
+    assert n0 % 16 == 0 and n_slice % 16 == 0 and n0 + n_slice <= tn * 16
+    words = trellis_words(trellis)[:, n0 // 16:(n0 + n_slice) // 16]
+    tiles = decode_tiles(words, K)                                        # [tk, tn', 16, 16]
+    return tiles.transpose(0, 2, 1, 3).reshape(tk * 16, n_slice)
+
+
+def reconstruct_mixed(words: np.ndarray, kmap: np.ndarray, woff: np.ndarray, k: int, n: int) -> np.ndarray:
+    """Per-tile K: tile i (row-major over [k/16, n/16]) is stored at words[woff[i] : woff[i] + 8 kmap[i]]."""
+    tk, tn = k // 16, n // 16
+    kmap = np.asarray(kmap).reshape(-1)
+    woff = np.asarray(woff, dtype=np.int64).reshape(-1)
+    assert kmap.size == tk * tn and woff.size == tk * tn + 1
+    tiles = np.empty((tk * tn, 16, 16), dtype=np.float16)
+    for K in np.unique(kmap):
+        idx = np.nonzero(kmap == K)[0]
+        gather = woff[idx][:, None] + np.arange(8 * int(K))[None, :]
+        tiles[idx] = decode_tiles(words[gather], int(K))
+    return tiles.reshape(tk, tn, 16, 16).transpose(0, 2, 1, 3).reshape(k, n)
+
+
+# ------------------------------------------------------------------------------------------------ Hadamard
+
+_H = None
+
+
+def sylvester128() -> np.ndarray:
+    """Natural-order Sylvester H128, entries +-1, H[i, j] = (-1)^popcount(i & j) (inventory:514-516)."""
+    global _H
+    if _H is None:
+        h = np.ones((1, 1))
+        while h.shape[0] < 128:
+            h = np.block([[h, h], [h, -h]])
+        _H = h
+        _H.setflags(write=False)
+    return _H
+
+
+def had_blocks(v: np.ndarray) -> np.ndarray:
+    """Blockwise unnormalised H128 along the last axis, float64."""
+    s = v.shape
+    return (np.asarray(v, dtype=np.float64).reshape(-1, 128) @ sylvester128()).reshape(s)
+
+
+def had_r_128(x: np.ndarray, pre: np.ndarray | None = None, post: np.ndarray | None = None, scale: float = 1.0,
+              out_dtype=None) -> np.ndarray:
+    """exllamav3 had_r_128 (inventory:576-595). fp16 path: x*pre rounded to fp16, butterfly exact, *scale/sqrt(128),
+    rounded to fp16, then *post rounded to fp16. fp32 path: no intermediate roundings. If both pre and post are given
+    only pre is applied (the reference's if/else chain)."""
+    if out_dtype is None:
+        out_dtype = x.dtype
+    r = scale * RSQRT128
+    if x.dtype == np.float16:
+        v = x if pre is None else (x.astype(np.float32) * pre.astype(np.float32)).astype(np.float16)
+        y = (had_blocks(v) * r).astype(np.float16)
+        if pre is None and post is not None:
+            y = (y.astype(np.float32) * post.astype(np.float32)).astype(np.float16)
+        return y.astype(out_dtype)
+    v = x.astype(np.float64) if pre is None else x.astype(np.float64) * pre.astype(np.float64)
+    y = had_blocks(v) * r
+    if pre is None and post is not None:
+        y = y * post.astype(np.float64)
+    return y.astype(out_dtype)
+
+
+def had_in(x: np.ndarray, suh: np.ndarray) -> np.ndarray:
+    """Input transform: fp16( H128(fp16(x * suh)) / sqrt(128) ) (inventory:523-525, exl3_esimd.h:300)."""
+    return had_r_128(x.astype(np.float16), pre=suh.astype(np.float16))
+
+
+# ------------------------------------------------------------------------------------------------ linear
+
+
+def linear_acc(xh: np.ndarray, W: np.ndarray, acc=np.float64) -> np.ndarray:
+    return xh.astype(acc) @ W.astype(acc)
+
+
+def had_out(acc: np.ndarray, svh: np.ndarray, out_dtype) -> np.ndarray:
+    """Output transform: H128(acc) / sqrt(128) * svh; fp16 outputs round once at the end (XPU form,
+    exl3_esimd.h:317-338; the CUDA fp16 form rounds before *svh, within 1 ulp)."""
+    y = had_blocks(acc) * RSQRT128 * svh.astype(np.float64)
+    return y.astype(out_dtype)
+
+
+def exl3_linear(x: np.ndarray, trellis: np.ndarray, suh: np.ndarray, svh: np.ndarray, K: int,
+                out_dtype=np.float32, acc=np.float64, W: np.ndarray | None = None) -> np.ndarray:
+    """y = Hn( Hk(x * suh) @ W_hat ) * svh with the reference rounding points (inventory:512-535)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    xh = had_in(x2, suh)
+    if W is None:
+        W = reconstruct(trellis, K)
+    y = had_out(linear_acc(xh, W, acc), svh, out_dtype)
+    return y.reshape(x.shape[:-1] + (y.shape[-1],))
+
+
+def dense_weight(trellis: np.ndarray, suh: np.ndarray, svh: np.ndarray, K: int) -> np.ndarray:
+    """Original-basis weight W = diag(suh) Hblk W_hat Hblk diag(svh), float64 (inventory:707-712)."""
+    Wh = reconstruct(trellis, K).astype(np.float64)
+    k, n = Wh.shape
+    Hb = sylvester128() * RSQRT128
+    # Hblk W_hat: transform every 128-block of rows; W_hat Hblk: every 128-block of columns
+    t = (Hb @ Wh.reshape(k // 128, 128, n)).reshape(k, n)
+    t = (t.reshape(k, n // 128, 128) @ Hb).reshape(k, n)
+    return suh.astype(np.float64)[:, None] * t * svh.astype(np.float64)[None, :]
+
+
+# ------------------------------------------------------------------------------------------------ activations
+
+ACT_SILU, ACT_GELU_TANH = 0, 1
+
+
+def act_mul(g: np.ndarray, u: np.ndarray, act: int, limit: float = 0.0) -> np.ndarray:
+    """Gated activation in float64, rounded to fp16 by the caller.
+    SiLU: a = min(silu(g), L) * clamp(u, -L, L), L = 0 disables the clamp (inventory:944-956).
+    GELU-tanh: a = 0.5 g (1 + tanh(sqrt(2/pi)(g + 0.044715 g^3))) * u (inventory:311, 892)."""
+    g = g.astype(np.float64)
+    u = u.astype(np.float64)
+    if act == ACT_SILU:
+        s = g / (1.0 + np.exp(-g))
+        if limit:
+            s = np.minimum(s, limit)
+            u = np.clip(u, -limit, limit)
+        return s * u
+    if act == ACT_GELU_TANH:
+        c = math.sqrt(2.0 / math.pi)
+        return 0.5 * g * (1.0 + np.tanh(c * (g + 0.044715 * g ** 3))) * u
+    raise ValueError(act)
+
+
+# ------------------------------------------------------------------------------------------------ MLP / MoE
+
+
+class Proj:
+    """One EXL3 projection. Uniform K (`trellis` int16 [k/16, n/16, 16K]) or per-tile K (`words`, `kmap`, `woff`)."""
+
+    def __init__(self, suh, svh, trellis=None, K=None, words=None, kmap=None, woff=None):
+        self.suh, self.svh = suh, svh
+        self.trellis, self.K = trellis, K
+        self.words, self.kmap, self.woff = words, kmap, woff
+        self.k, self.n = suh.shape[0], svh.shape[0]
+        self._W = None
+
+    def W(self) -> np.ndarray:
+        if self._W is None:
+            if self.trellis is not None:
+                self._W = reconstruct(self.trellis, self.K)
+            else:
+                self._W = reconstruct_mixed(self.words, self.kmap, self.woff, self.k, self.n)
+        return self._W
+
+    def drop(self):
+        self._W = None
+
+    def __call__(self, x, out_dtype, acc=np.float64):
+        xh = had_in(x.reshape(-1, self.k), self.suh)
+        return had_out(linear_acc(xh, self.W(), acc), self.svh, out_dtype)
+
+
+def gated_mlp(x: np.ndarray, gate: Proj, up: Proj, down: Proj, act: int, limit: float = 0.0,
+              acc=np.float64) -> np.ndarray:
+    """g, u = gate(x), up(x) (fp16); a = fp16(act(g, u)); d = down(a) (fp32) (inventory:923-942, 1172-1187)."""
+    g = gate(x, np.float16, acc)
+    u = up(x, np.float16, acc)
+    a = act_mul(g, u, act, limit).astype(np.float16)
+    return down(a, np.float32, acc)
+
+
+def moe_layer(x: np.ndarray, experts, ids: np.ndarray, w: np.ndarray, act: int = ACT_SILU, limit: float = 0.0,
+              shared=None, acc=np.float64, drop_weights: bool = False) -> np.ndarray:
+    """out[t] = sum_{j in slot order} w[t, j] * expert_{ids[t, j]}(x[t]) (fp32 sum) + shared(x[t]).
+    `experts[e]` is a (gate, up, down) tuple of Proj. Slots with ids < 0 are inactive. Output float32 [M, H]."""
+    M, H = x.shape
+    y = np.zeros((M, ids.shape[1], H), dtype=np.float64)
+    for e in np.unique(ids[ids >= 0]):
+        rows, slots = np.nonzero(ids == e)
+        d = gated_mlp(x[rows], *experts[int(e)], act, limit, acc)
+        y[rows, slots] = d.astype(np.float64) * w[rows, slots].astype(np.float64)[:, None]
+        if drop_weights:
+            for p in experts[int(e)]:
+                p.drop()
+    out = np.zeros((M, H), dtype=np.float32)
+    for j in range(ids.shape[1]):                       # fixed slot order, fp32 sum
+        out += y[:, j].astype(np.float32)
+    if shared is not None:
+        out += gated_mlp(x, *shared, act, limit, acc)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ routing
+
+
+def topk_lowest_index(key: np.ndarray, k: int) -> np.ndarray:
+    """Top-k indices by descending key; exact ties go to the lower expert index."""
+    order = np.argsort(-key, axis=-1, kind="stable")
+    return order[..., :k]
+
+
+def route_softmax_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None):
+    """softmax over (logits + bias) -> top-k -> renormalise with +1e-20 (trellis-serve.patch:395-441).
+    Returns ids int32 [M, k] (descending probability) and w float32 [M, k]."""
+    z = logits.astype(np.float32)
+    if bias is not None:
+        z = z + bias.astype(np.float32)[None, :]
+    z64 = z.astype(np.float64)
+    p = np.exp(z64 - z64.max(-1, keepdims=True))
+    p = p / p.sum(-1, keepdims=True)
+    ids = topk_lowest_index(z, k)
+    pw = np.take_along_axis(p, ids, -1)
+    w = pw / (pw.sum(-1, keepdims=True) + 1e-20)
+    return ids.astype(np.int32), w.astype(np.float32)
+
+
+def align(ids: np.ndarray, w: np.ndarray, E: int, pad: int = 1):
+    """Pairs sorted by expert (stable: flat pair order within an expert), per active expert start / count / padded
+    start, and the inverse map (exl3_moe.n128.sycl:691-734). Returns a dict of numpy arrays."""
+    flat = ids.reshape(-1).astype(np.int64)
+    topk = ids.shape[1]
+    cnt = np.bincount(flat[flat >= 0], minlength=E)[:E]
+    start = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+    order = np.argsort(np.where(flat >= 0, flat, E), kind="stable")[: int(cnt.sum())]
+    act = np.nonzero(cnt)[0]
+    pc = (cnt + pad - 1) // pad * pad
+    pstart = np.concatenate([[0], np.cumsum(pc)[:-1]])
+    pair_of = np.full(flat.size, -1, dtype=np.int64)
+    pair_of[order] = np.arange(order.size)
+    return dict(act_expert=act.astype(np.int32), act_start=start[act].astype(np.int32),
+                act_cnt=cnt[act].astype(np.int32), n_act=np.int32(act.size), act_pstart=pstart[act].astype(np.int32),
+                pair_tok=(order // topk).astype(np.int32), pair_w=w.reshape(-1)[order].astype(np.float32),
+                pair_of=pair_of.astype(np.int32), count=cnt.astype(np.int32))

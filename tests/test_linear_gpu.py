@@ -1,0 +1,124 @@
+"""GPU parity of the dense EXL3 linear path against the CPU oracle (same seeded bytes on both sides).
+
+Bars: decoded weights bit-exact (fp16 bit patterns); had_r_128 within one fp16 ulp (the kernel's fp32 butterfly vs the
+oracle's exact sum) and 1e-6 relative in fp32; linear outputs within max|y - r| / max|r| <= 2e-3 of the oracle's
+float64-accumulated result (the reference's max_rel convention, trellis-serve.patch:3889).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+MAX_REL = 2e-3
+pytestmark = pytest.mark.gpu
+
+
+def max_rel(y, r):
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    return float(np.abs(y - r).max() / np.abs(r).max())
+
+
+def synth():
+    import importlib
+    return importlib.import_module("b70-inference_amd.synth")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("k,n", [(128, 128), (256, 384), (512, 1024)])
+def test_reconstruct_bit_exact(exl3, oracle, K, k, n):
+    tr, _, _ = synth().linear(k, n, K, 1000 + K)
+    w = torch.empty(k, n, dtype=torch.float16, device="cuda")
+    exl3.exl3_reconstruct(tr.cuda(), w, 0, K)
+    ref = oracle.reconstruct(tr.numpy(), K)
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_reconstruct_slice_and_stride(exl3, oracle):
+    tr, _, _ = synth().linear(256, 1024, 3, 5)
+    buf = torch.zeros(256, 512, dtype=torch.float16, device="cuda")
+    exl3.reconstruct_slice(buf[:, 128:384], tr.cuda(), 3, False, True, 256)
+    ref = oracle.reconstruct(tr.numpy(), 3, 256, 256)
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[:, 128:384].view(np.uint16), ref.view(np.uint16))
+    assert (got[:, :128] == 0).all() and (got[:, 384:] == 0).all()
+
+
+def test_reconstruct_full_c1(exl3, oracle):
+    """4096 x 4096, K=4 (the single-linear workload): every weight bit-exact."""
+    tr, _, _ = synth().linear(4096, 4096, 4, 1001)
+    w = torch.empty(4096, 4096, dtype=torch.float16, device="cuda")
+    exl3.exl3_reconstruct(tr.cuda(), w, 0, 4)
+    assert np.array_equal(w.cpu().numpy().view(np.uint16), oracle.reconstruct(tr.numpy(), 4).view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_had_r_128(exl3, oracle, dtype):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(7, 384, generator=g).to(dtype)
+    pre = (torch.randint(0, 2, (384,), generator=g) * 2 - 1).half() * 0.75
+    for p, q in ((None, None), (pre, None), (None, pre), (pre, pre)):
+        out = torch.empty_like(x, device="cuda")
+        exl3.had_r_128(x.cuda(), out, None if p is None else p.cuda(), None if q is None else q.cuda(), 1.5)
+        ref = oracle.had_r_128(x.numpy(), None if p is None else p.numpy(), None if q is None else q.numpy(), 1.5)
+        got = out.cpu().numpy()
+        if dtype == torch.float16:
+            d = np.abs(got.view(np.uint16).astype(np.int32) - ref.view(np.uint16).astype(np.int32))
+            assert d.max() <= 1
+        else:
+            assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    # in place
+    y = x.cuda()
+    ref = oracle.had_r_128(x.numpy(), None, None, 1.0)
+    exl3.had_r_128(y, y, None, None, 1.0)
+    assert np.abs(y.cpu().numpy().astype(np.float64) - ref).max() <= 1e-3 * np.abs(ref).max()
+
+
+def _linear_case(exl3, oracle, k, n, K, M, out_dtype, seed):
+    S = synth()
+    tr, suh, svh = S.linear(k, n, K, seed)
+    x = S.activations(M, k, seed + 1)
+    lin = exl3.BC_LinearEXL3(tr.cuda(), suh.cuda(), svh.cuda(), K, None, False, True, None)
+    y = lin.run_alloc(x.cuda(), n, out_dtype == torch.float32)
+    ref = oracle.exl3_linear(x.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), K,
+                             np.float32 if out_dtype == torch.float32 else np.float16)
+    return y.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8])
+def test_gemm_small_shapes(exl3, oracle, K, M):
+    y, ref = _linear_case(exl3, oracle, 512, 384, K, M, torch.float32, 2000 + 10 * K + M)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("M", [5, 9, 17])
+def test_gemm_fp16_out_and_row_chunks(exl3, oracle, M):
+    y, ref = _linear_case(exl3, oracle, 1024, 256, 3, M, torch.float16, 3000 + M)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemm_c1_full_size(exl3, oracle, M):
+    """Single dense linear 4096 -> 4096, K=4, fp16 output."""
+    y, ref = _linear_case(exl3, oracle, 4096, 4096, 4, M, torch.float16, 1000)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_gemm_deterministic_and_bias(exl3):
+    S = synth()
+    tr, suh, svh = S.linear(2048, 1024, 3, 77)
+    x = S.activations(3, 2048, 78).cuda()
+    bias = torch.randn(1024).half().cuda()
+    lin = exl3.BC_LinearEXL3(tr.cuda(), suh.cuda(), svh.cuda(), 3, None, False, True, None)
+    y1 = lin.run_alloc(x, 1024, True)
+    y2 = lin.run_alloc(x, 1024, True)
+    assert torch.equal(y1, y2)
+    lin_b = exl3.BC_LinearEXL3(tr.cuda(), suh.cuda(), svh.cuda(), 3, bias, False, True, None)
+    y3 = lin_b.run_alloc(x, 1024, True)
+    assert torch.allclose(y3, y1 + bias.float(), atol=1e-3)
+    # run() with a preallocated fp16 output and a 3D input
+    y4 = torch.empty(1, 3, 1024, dtype=torch.float16, device="cuda")
+    lin.run(x.view(1, 3, 2048), y4)
+    assert torch.allclose(y4.view(3, 1024).float(), y1, rtol=2e-3, atol=2e-3)

@@ -1,0 +1,317 @@
+"""Pins the CPU oracle (oracle/exl3_oracle.py) before it is trusted as the checker.
+
+The reference holds no golden vectors for this path (its parity tests need checkpoints and the un-vendored exllamav3
+testlib), so every oracle function is pinned by an independent statement or by mathematics:
+  * codebook: six textual statements of mul1 in the reference must agree over all 65536 states, plus the value
+    invariants the reference states (913 distinct values, range [-3.453, 3.348]);
+  * tile permutation: three statements (bit-field, ring, inverse) agree and form a bijection;
+  * window extraction + whole-tile decode: a brute-force C decoder that materialises the ring bit by bit;
+  * Hadamard: orthogonality, basis vectors, involution, dense +-1 matmul;
+  * linear: the transform path equals x @ W with W = diag(suh) Hblk W_hat Hblk diag(svh) built the other way round;
+  * routing / align: closed-form invariants and hand-built ties;
+  * MoE: linearity in the routing weights, the dense-weight form of every expert, slot bookkeeping.
+"""
+import ctypes
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import exl3_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BF_LIB = os.path.join(ROOT, "oracle", "_build", "libexl3_oracle.so")
+
+
+@pytest.fixture(scope="module")
+def bf():
+    if not os.path.exists(BF_LIB):
+        import subprocess
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True, capture_output=True)
+    L = ctypes.CDLL(BF_LIB)
+    L.exl3_bf_mul1.restype = ctypes.c_uint16
+    L.exl3_bf_mul1.argtypes = [ctypes.c_uint32]
+    L.exl3_bf_f64_to_f16.restype = ctypes.c_uint16
+    L.exl3_bf_f64_to_f16.argtypes = [ctypes.c_double]
+    L.exl3_bf_reconstruct.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    return L
+
+
+def bf_reconstruct(bf, tr):
+    tk, tn, w = tr.shape
+    out = np.empty((tk * 16, tn * 16), dtype=np.uint16)
+    tr = np.ascontiguousarray(tr)
+    assert bf.exl3_bf_reconstruct(tr.ctypes.data, tk, tn, w // 16, out.ctypes.data) == 0
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ codebook
+
+def test_lut_invariants():
+    lut = O.mul1_lut()
+    v = lut.astype(np.float64)
+    assert np.unique(lut.view(np.uint16)).size == 913
+    assert v.min() == -3.453125 and v.max() == 3.34765625
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 1.0) < 0.01
+    # the two fp16 constants are the bit patterns the reference names (0x1EEE, 0xC931)
+    assert np.array([O.K_INV], np.float16).view(np.uint16)[0] == 0x1EEE
+    assert np.array([O.K_BIAS], np.float16).view(np.uint16)[0] == 0xC931
+
+
+def test_lut_statements_agree(bf):
+    st = np.arange(65536, dtype=np.uint64)
+    lut = O.mul1_lut().view(np.uint16)
+    x = (st * 0x83DCD12D) & 0xFFFFFFFF
+    # (1) MUL16 split of the multiply, glm/xpu/csrc/exl3_esimd.h:47-53
+    x16 = (st * 0xD12D + (((st * 0x83DC) & 0xFFFF) << 16)) & 0xFFFFFFFF
+    assert np.array_equal(x, x16)
+    # (2) dp4a form: 0x6400 + byte sum is the fp16 bit pattern of 1024 + byte sum (exl3_esimd.h:57-59)
+    s = sum(((x >> (8 * i)) & 0xFF) for i in range(4))
+    h_bits = (0x6400 + s).astype(np.uint16)
+    assert np.array_equal(h_bits.view(np.float16).astype(np.float64), 1024.0 + s)
+    # (3) fp16 fma with one rounding == fp32 affine (exact) rounded once (triton_kernels.py:38-42, exl3_tri.py:38-43)
+    h = h_bits.view(np.float16).astype(np.float32)
+    v32 = (h * np.float32(O.K_INV) + np.float32(O.K_BIAS))
+    exact = h.astype(np.float64) * O.K_INV + O.K_BIAS
+    assert np.array_equal(v32.astype(np.float64), exact)            # the fp32 affine is exact
+    assert np.array_equal(v32.astype(np.float16).view(np.uint16), lut)
+    # (4) glm/xpu/tests/units.py:45-49 form: ((1024 + s).double() * K_INV - 10.3828125).float().half()
+    v4 = ((1024 + s).astype(np.float64) * 0.00676727294921875 - 10.3828125).astype(np.float32).astype(np.float16)
+    assert np.array_equal(v4.view(np.uint16), lut)
+    # (5) brute-force C: byte loop + hand-written round-to-nearest-even
+    sample = np.random.default_rng(1).integers(0, 65536, 4096)
+    assert all(bf.exl3_bf_mul1(int(t)) == lut[t] for t in sample)
+    assert all(bf.exl3_bf_mul1(int(t)) == lut[t] for t in range(0, 65536, 97))
+
+
+def test_bruteforce_f16_rounding_matches_numpy(bf):
+    # the C converter used by the brute-force decoder is itself checked against numpy on hard cases
+    vals = np.concatenate([np.random.default_rng(2).normal(0, 4, 2000), [0.0, -0.0, 2 ** -24, 2 ** -25, 3 * 2 ** -26,
+                           65504.0, 65519.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -2.5e-5, 6.1e-5]])
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([bf.exl3_bf_f64_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(ref, got)
+
+
+# ------------------------------------------------------------------------------------------------ layout
+
+def test_permutation_statements_agree():
+    row, col = O.pos_row_col()
+    t = np.arange(256)
+    # ring form (dsv41/xpu/dsv_xpu/exl3_tri.py:4-9)
+    tt, j = t // 8, t % 8
+    r2 = (tt % 4) * 2 + (j & 1) + 8 * ((j >> 1) & 1)
+    c2 = tt // 4 + 8 * ((j >> 2) & 1)
+    assert np.array_equal(row, r2) and np.array_equal(col, c2)
+    # inverse form (glm/xpu/exl3xpu/triton_kernels.py:4-7): t = 32(c&7) + 8((r>>1)&3) + 4(c>>3) + 2(r>>3) + (r&1)
+    inv = 32 * (col & 7) + 8 * ((row >> 1) & 3) + 4 * (col >> 3) + 2 * (row >> 3) + (row & 1)
+    assert np.array_equal(inv, t)
+    # bijection onto the 16 x 16 tile
+    assert np.unique(row * 16 + col).size == 256
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_decode_vs_bruteforce(bf, K):
+    rng = np.random.default_rng(100 + K)
+    tr = rng.integers(-32768, 32768, size=(3, 4, 16 * K), dtype=np.int16)
+    assert np.array_equal(O.reconstruct(tr, K).view(np.uint16), bf_reconstruct(bf, tr))
+
+
+def test_window_special_cases(bf):
+    # K = 8: windows are byte aligned; K = 1: 15 of 16 bits of early windows come from the ring's end
+    for K in (1, 8, 16 // 2, 3):
+        tr = np.zeros((1, 1, 16 * K), dtype=np.int16)
+        tr.view(np.uint32)[0, 0, -1] = 0x0000FFFF          # ones at the very end of the ring
+        W = O.reconstruct(tr, K)
+        assert np.array_equal(W.view(np.uint16), bf_reconstruct(bf, tr))
+        st = O.tile_states(tr.view(np.uint32)[0, 0], K)
+        # position 0's window starts in the last word: it sees (16 - K) trailing ones then K zeros
+        assert st[0] == ((0xFFFF << K) & 0xFFFF)
+
+
+def test_reconstruct_slice_consistency():
+    rng = np.random.default_rng(3)
+    tr = rng.integers(-32768, 32768, size=(4, 24, 48), dtype=np.int16)
+    W = O.reconstruct(tr, 3)
+    assert np.array_equal(O.reconstruct(tr, 3, 128, 256), W[:, 128:384])
+
+
+def test_mixed_k_reconstruct_matches_uniform():
+    rng = np.random.default_rng(4)
+    k, n = 64, 96
+    tk, tn = k // 16, n // 16
+    kmap = rng.integers(1, 3, tk * tn).astype(np.uint8)
+    woff = np.concatenate([[0], np.cumsum(kmap.astype(np.int64) * 8)])
+    words = rng.integers(0, 2 ** 32, int(woff[-1]), dtype=np.uint64).astype(np.uint32)
+    W = O.reconstruct_mixed(words, kmap, woff, k, n)
+    for i in range(tk * tn):
+        a, b = divmod(i, tn)
+        K = int(kmap[i])
+        tile = words[woff[i]:woff[i] + 8 * K].view(np.int16).reshape(1, 1, 16 * K)
+        assert np.array_equal(W[16 * a:16 * a + 16, 16 * b:16 * b + 16], O.reconstruct(tile, K))
+
+
+# ------------------------------------------------------------------------------------------------ Hadamard
+
+def test_hadamard_properties():
+    H = O.sylvester128()
+    assert np.array_equal(H @ H.T, 128 * np.eye(128))
+    i = np.arange(128)
+    pc = np.array([bin(v).count("1") for v in range(128)])
+    assert np.array_equal(H, (-1.0) ** pc[np.bitwise_and.outer(i, i)])
+    e = np.eye(128)[37:38]
+    assert np.array_equal(O.had_blocks(e)[0], H[37])
+    x = np.random.default_rng(5).normal(size=(3, 256))
+    y = O.had_r_128(O.had_r_128(x.astype(np.float32)), None)   # involution up to fp32 rounding
+    assert np.allclose(y, x, atol=1e-5)
+
+
+def test_had_r_128_rounding_points():
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(4, 256)).astype(np.float16)
+    pre = (rng.integers(0, 2, 256) * 2 - 1).astype(np.float16) * np.float16(0.37)
+    y = O.had_r_128(x, pre=pre)
+    xp = (x.astype(np.float32) * pre.astype(np.float32)).astype(np.float16)     # x * pre rounded first
+    ref = ((xp.astype(np.float64).reshape(-1, 128) @ O.sylvester128()) / math.sqrt(128)).reshape(x.shape)
+    assert np.array_equal(y, ref.astype(np.float16))
+    post = pre
+    y2 = O.had_r_128(x, post=post)
+    ref2 = (((x.astype(np.float64).reshape(-1, 128) @ O.sylvester128()) / math.sqrt(128)).reshape(x.shape)
+            .astype(np.float16).astype(np.float32) * post.astype(np.float32)).astype(np.float16)
+    assert np.array_equal(y2, ref2)
+    # both given: only pre applies
+    assert np.array_equal(O.had_r_128(x, pre=pre, post=post), y)
+
+
+# ------------------------------------------------------------------------------------------------ linear
+
+def _lin(k, n, K, seed):
+    rng = np.random.default_rng(seed)
+    tr = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16)
+    suh = ((rng.integers(0, 2, k) * 2 - 1) * 0.75).astype(np.float16)
+    svh = ((rng.integers(0, 2, n) * 2 - 1) / math.sqrt(k)).astype(np.float16)
+    return tr, suh, svh
+
+
+@pytest.mark.parametrize("K", [2, 4])
+def test_linear_equals_dense_weight(K):
+    tr, suh, svh = _lin(256, 384, K, 7)
+    x = np.random.default_rng(8).normal(size=(3, 256)).astype(np.float16)
+    Wd = O.dense_weight(tr, suh, svh, K)
+    ref = x.astype(np.float64) @ Wd
+    # transform path without the fp16 rounding points == dense form, to fp64 precision
+    xh = O.had_blocks(x.astype(np.float64) * suh.astype(np.float64)) / math.sqrt(128)
+    y = O.had_blocks(xh @ O.reconstruct(tr, K).astype(np.float64)) / math.sqrt(128) * svh.astype(np.float64)
+    assert np.abs(y - ref).max() < 1e-9 * np.abs(ref).max()
+    # with the reference rounding points: within the fp16 rounding of the activations
+    y32 = O.exl3_linear(x, tr, suh, svh, K, np.float32)
+    assert np.abs(y32 - ref).max() / np.abs(ref).max() < 2e-3
+
+
+def test_linear_tiny_bruteforce(bf):
+    tr, suh, svh = _lin(128, 128, 3, 9)
+    W_bf = bf_reconstruct(bf, tr).view(np.float16).astype(np.float64)
+    Hb = O.sylvester128() / math.sqrt(128)
+    Wd = suh.astype(np.float64)[:, None] * (Hb @ W_bf @ Hb) * svh.astype(np.float64)[None, :]
+    x = np.random.default_rng(10).normal(size=(2, 128)).astype(np.float16)
+    y = O.exl3_linear(x, tr, suh, svh, 3, np.float32)
+    ref = x.astype(np.float64) @ Wd
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-3
+
+
+# ------------------------------------------------------------------------------------------------ routing / align
+
+def test_route_softmax_topk():
+    rng = np.random.default_rng(11)
+    logits = rng.normal(size=(5, 64)).astype(np.float32)
+    logits[0, [3, 9, 20]] = 4.0                         # exact ties: lower index first
+    ids, w = O.route_softmax_topk(logits, 4)
+    assert list(ids[0, :3]) == [3, 9, 20]
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    for r in range(5):
+        top = np.argsort(-logits[r], kind="stable")[:4]
+        assert list(ids[r]) == list(top)
+        assert np.allclose(w[r], p[r, top] / p[r, top].sum(), rtol=1e-6)
+    assert np.allclose(w.sum(1), 1.0, atol=1e-6)
+    bias = np.zeros(64, np.float32)
+    bias[50] = 100.0
+    ids_b, w_b = O.route_softmax_topk(logits, 4, bias)
+    assert (ids_b[:, 0] == 50).all() and (w_b[:, 0] > 0.99).all()
+
+
+def test_align_invariants():
+    rng = np.random.default_rng(12)
+    ids = rng.integers(0, 16, size=(9, 4)).astype(np.int32)
+    w = rng.random((9, 4)).astype(np.float32)
+    a = O.align(ids, w, 16, pad=4)
+    cnt = np.bincount(ids.reshape(-1), minlength=16)
+    assert np.array_equal(a["count"], cnt)
+    assert np.array_equal(a["act_expert"], np.nonzero(cnt)[0])
+    assert np.array_equal(a["act_start"], np.concatenate([[0], np.cumsum(cnt)])[a["act_expert"]])
+    assert (a["act_pstart"] % 4 == 0).all()
+    flat = ids.reshape(-1)
+    for i in range(flat.size):
+        pos = a["pair_of"][i]
+        assert a["pair_tok"][pos] == i // 4 and a["pair_w"][pos] == w.reshape(-1)[i]
+    assert np.unique(a["pair_of"]).size == flat.size
+
+
+# ------------------------------------------------------------------------------------------------ MoE
+
+def _experts(E, H, I, K, seed):
+    out = []
+    for e in range(E):
+        ps = []
+        for j, (k, n) in enumerate(((H, I), (H, I), (I, H))):
+            tr, suh, svh = _lin(k, n, K, seed + 10 * e + j)
+            ps.append(O.Proj(suh, svh, trellis=tr, K=K))
+        out.append(tuple(ps))
+    return out
+
+
+def test_moe_layer_structure():
+    H, I, E = 256, 128, 5
+    ex = _experts(E, H, I, 2, 300)
+    rng = np.random.default_rng(13)
+    x = rng.normal(size=(3, H)).astype(np.float16)
+    ids = np.array([[0, 3], [3, 3], [4, 1]], np.int32)      # duplicate expert within a token
+    w = rng.random((3, 2)).astype(np.float32)
+    out = O.moe_layer(x, ex, ids, w, O.ACT_SILU)
+    out2 = O.moe_layer(x, ex, ids, 2 * w, O.ACT_SILU)
+    assert np.allclose(out2, 2 * out, rtol=1e-6, atol=1e-6)  # linear in the routing weights
+    # each expert against its dense-weight form (fp64, no fp16 rounding points)
+    dense = []
+    for g, u, d in ex:
+        dense.append([O.dense_weight(p.trellis, p.suh, p.svh, p.K) for p in (g, u, d)])
+    ref = np.zeros((3, H))
+    for t in range(3):
+        for j in range(2):
+            Wg, Wu, Wd = dense[ids[t, j]]
+            xg = x[t].astype(np.float64)
+            a = O.act_mul(xg @ Wg, xg @ Wu, O.ACT_SILU)
+            ref[t] += w[t, j] * (a @ Wd)
+    assert np.abs(out - ref).max() / np.abs(ref).max() < 5e-3
+    # inactive slots contribute nothing
+    ids_m = ids.copy()
+    ids_m[2, 1] = -1
+    w_m = w.copy()
+    w_m[2, 1] = 0
+    assert np.allclose(O.moe_layer(x, ex, ids_m, w, O.ACT_SILU), O.moe_layer(x, ex, ids, w_m, O.ACT_SILU), atol=1e-6)
+
+
+def test_gelu_tanh_and_silu_closed_forms():
+    g = np.array([-3.0, -0.5, 0.0, 0.7, 2.0])
+    u = np.array([1.0, 2.0, 3.0, -1.0, 0.5])
+    silu = g / (1 + np.exp(-g)) * u
+    assert np.allclose(O.act_mul(g, u, O.ACT_SILU), silu)
+    clamp = np.minimum(g / (1 + np.exp(-g)), 1.0) * np.clip(u, -1.0, 1.0)
+    assert np.allclose(O.act_mul(g, u, O.ACT_SILU, 1.0), clamp)
+    # GELU-tanh at known points: gelu(0) = 0, gelu(x) -> x for large x, odd-symmetry gelu(x) - gelu(-x) = x
+    ge = O.act_mul(g, np.ones_like(g), O.ACT_GELU_TANH)
+    assert ge[2] == 0.0
+    assert np.allclose(O.act_mul(np.array([10.0]), np.ones(1), O.ACT_GELU_TANH), 10.0)
+    xs = np.linspace(-4, 4, 17)
+    gx = O.act_mul(xs, np.ones_like(xs), O.ACT_GELU_TANH)
+    assert np.allclose(gx - gx[::-1], xs, atol=1e-12)
