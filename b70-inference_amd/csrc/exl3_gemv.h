@@ -71,6 +71,43 @@ __device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size
     if (i + 1 < n) strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
 }
 
+// Per-tile K (mixed bitrate): tile i of the projection (row-major over [k/16, n/16]) holds 8 * kmap[i] words at
+// words + woff[i]. A wave still covers 8 consecutive tiles of a tile-row; lanes branch on their tile's K (all lanes
+// of one tile take the same branch, so the cross-lane `prev` permute stays inside the branch).
+template <int K, int M>
+__device__ __forceinline__ void mixed_tile_row(const uint32_t* __restrict__ tw, int lane, const _Float16* xr,
+                                               int xs_ld, float (&acc)[M][2]) {
+    uint32_t D[K];
+    const uint32_t* q = tw + (lane & 7) * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) D[i] = __builtin_nontemporal_load(q + i);
+    strip_tile_row<K, M>(D, lane, xr, xs_ld, acc);
+}
+
+template <int M>
+__device__ __forceinline__ void strip_gemv_mixed(const uint32_t* __restrict__ words, const uint8_t* __restrict__ kmap,
+                                                 const int32_t* __restrict__ woff, int tn, int tile_n0, int tr0,
+                                                 int lt0, int nt, int step, int lane, const _Float16* xs, int xs_ld,
+                                                 float (&acc)[M][2]) {
+    for (int lt = lt0; lt < nt; lt += step) {
+        const int tile = (tr0 + lt) * tn + tile_n0 + (lane >> 3);
+        const int Kt = kmap[tile];
+        const uint32_t* tw = words + woff[tile];
+        const _Float16* xr = xs + lt * 16;
+        switch (Kt) {
+            case 1: mixed_tile_row<1, M>(tw, lane, xr, xs_ld, acc); break;
+            case 2: mixed_tile_row<2, M>(tw, lane, xr, xs_ld, acc); break;
+            case 3: mixed_tile_row<3, M>(tw, lane, xr, xs_ld, acc); break;
+            case 4: mixed_tile_row<4, M>(tw, lane, xr, xs_ld, acc); break;
+            case 5: mixed_tile_row<5, M>(tw, lane, xr, xs_ld, acc); break;
+            case 6: mixed_tile_row<6, M>(tw, lane, xr, xs_ld, acc); break;
+            case 7: mixed_tile_row<7, M>(tw, lane, xr, xs_ld, acc); break;
+            case 8: mixed_tile_row<8, M>(tw, lane, xr, xs_ld, acc); break;
+            default: break;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ split-K handoff
 // Workgroups of one output strip publish fp32 partials; the last to arrive (per-strip counter) reduces them.
 // Partials are written with agent-scope relaxed atomic stores (write-through past the XCD-local L2) and read with

@@ -1,0 +1,638 @@
+// Grouped EXL3 MoE on gfx950: routing tables, decode GEMV path (gate|up + fused activation epilogue, down, combine),
+// and the softmax/top-k router.
+//
+// Per layer call (all on the caller's stream, no host synchronisation):
+//   align    one workgroup: expert histogram -> pairs grouped by expert, the inverse map pair_of[token, slot], and
+//            "items" = (expert, first pair, <= MR rows) work units; the GEMV grids are sized for the worst case and
+//            surplus workgroups exit (the reference's max_act launch, glm/xpu/csrc/exl3_moe.n128.sycl:691-734, 1380-1439)
+//   gateup   workgroup per (item, 128-column block of I, k-split of H): gate and up strips (2 waves each), split-K
+//            handoff, and in the last workgroup: Hadamard * svh -> fp16 g, u -> fp16 act(g, u) -> * suh_d -> Hadamard
+//            -> fp16 down input (the reference's GateUpKernel epilogue, exl3_moe.n128.sycl:253-271)
+//   down     workgroup per (item, 128-column block of H, k-split of I): Hadamard * svh_d * w -> y[pair] fp32
+//   combine  out[t] = sum over slots in order of y[pair_of[t, slot]] (deterministic, exl3_moe.n128.sycl:385-410)
+// Experts with more than MR rows (prefill) are handled by the MFMA grouped GEMM (exl3_mfma.hip).
+#include "exl3_device.h"
+#include "exl3_gemv.h"
+#include "exl3_moe.h"
+#include "exl3_runtime.h"
+
+namespace exl3 {
+
+// ================================================================================================ align
+// Exclusive scan of n ints in LDS by a 1024-thread workgroup (each thread a contiguous run). Returns the total.
+__device__ int block_scan_exclusive(int* a, int n, int* tmp /* [1024] */) {
+    const int t = threadIdx.x, T = blockDim.x;
+    const int per = (n + T - 1) / T;
+    const int lo = t * per, hi = min(n, lo + per);
+    int s = 0;
+    for (int i = lo; i < hi; ++i) s += a[i];
+    tmp[t] = s;
+    __syncthreads();
+    for (int d = 1; d < T; d <<= 1) {
+        int v = t >= d ? tmp[t - d] : 0;
+        __syncthreads();
+        tmp[t] += v;
+        __syncthreads();
+    }
+    int run = tmp[t] - s;   // exclusive prefix of this thread's run
+    const int total = tmp[T - 1];
+    for (int i = lo; i < hi; ++i) {
+        int v = a[i];
+        a[i] = run;
+        run += v;
+    }
+    __syncthreads();
+    return total;
+}
+
+__global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
+    extern __shared__ int sm[];
+    int* cnt = sm;                 // [E]
+    int* start = sm + r.E;         // [E]
+    int* fill = sm + 2 * r.E;      // [E]
+    int* nch = sm + 3 * r.E;       // [E]
+    int* tmp = sm + 4 * r.E;       // [1024]
+    const int t = threadIdx.x, T = blockDim.x;
+    const int np = r.M * r.slots;
+    for (int e = t; e < r.E; e += T) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int i = t; i < np; i += T) {
+        const int tok = i / r.slots, j = i - tok * r.slots;
+        const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
+        if (e >= 0 && e < r.E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    for (int e = t; e < r.E; e += T) {
+        start[e] = cnt[e];
+        nch[e] = (cnt[e] + r.MR - 1) / r.MR;
+    }
+    __syncthreads();
+    block_scan_exclusive(start, r.E, tmp);
+    const int nitems = block_scan_exclusive(nch, r.E, tmp);
+    for (int e = t; e < r.E; e += T) {
+        const int c = cnt[e];
+        if (r.counts) r.counts[e] = c;
+        for (int q = 0, it = nch[e]; q * r.MR < c; ++q, ++it) {
+            if (r.item_e) {
+                r.item_e[it] = e;
+                r.item_p0[it] = start[e] + q * r.MR;
+                r.item_cnt[it] = min(r.MR, c - q * r.MR);
+            }
+        }
+    }
+    if (t == 0 && r.n_items) r.n_items[0] = nitems;
+    __syncthreads();
+    for (int i = t; i < np; i += T) {
+        const int tok = i / r.slots, j = i - tok * r.slots;
+        const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
+        if (e >= 0 && e < r.E) {
+            const int pos = start[e] + atomicAdd(&fill[e], 1);
+            r.pair_tok[pos] = tok;
+            r.pair_w[pos] = j < r.topk ? r.tw[tok * r.topk + j] : 1.0f;
+            r.pair_of[i] = pos;
+        } else {
+            r.pair_of[i] = -1;
+        }
+    }
+}
+
+// ================================================================================================ activation
+__device__ __forceinline__ float act_mul(float g, float u, int act, float L) {
+    if (act == EXL3_ACT_GELU_TANH) {
+        // 0.5 g (1 + tanh(z)) == g * sigmoid(2z): the sigmoid form has no cancellation for negative g
+        const float z2 = 1.5957691216057308f * (g + 0.044715f * g * g * g);   // 2 sqrt(2 / pi) (g + 0.044715 g^3)
+        return g / (1.f + expf(-z2)) * u;
+    }
+    float s = g / (1.f + expf(-g));
+    if (L > 0.f) {
+        s = fminf(s, L);
+        u = fminf(fmaxf(u, -L), L);
+    }
+    return s * u;
+}
+
+// ================================================================================================ gate | up
+template <int K, int MR>
+__global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][MR][kGemvKBMax * 128];
+    __shared__ float red[4][MR][2][64];
+    __shared__ float bsum[2][MR][kGemvKBMax];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nbI = a.I / 128;
+    const int item = blockIdx.x / nbI, nb = blockIdx.x - item * nbI, p = blockIdx.y;
+    if (item >= a.n_items[0]) return;
+    const int e = a.item_e[item], p0 = a.item_p0[item], cnt = a.item_cnt[item];
+    const int64_t E = a.E;
+    const int b0 = (int)((int64_t)p * a.nblk_h / a.P_gu), b1 = (int)((int64_t)(p + 1) * a.nblk_h / a.P_gu);
+    const int kb = b1 - b0;
+
+    // phase 1: both projections' input transforms for the item's rows
+    for (int i = wave; i < 2 * MR * kb; i += 4) {
+        const int proj = i / (MR * kb), rem = i - proj * MR * kb, m = rem / kb, b = rem - m * kb;
+        const int k0 = (b0 + b) * 128;
+        const uint16_t* suh = reinterpret_cast<const uint16_t*>(a.tables[(3 * proj + 1) * E + e]);
+        const uint16_t* xr = m < cnt ? a.x + (int64_t)a.pair_tok[p0 + m] * a.x_ld + k0 : nullptr;
+        float s = had_in_block(xr, suh + k0, &xs[proj][m][b * 128], lane);
+        if (lane == 0) bsum[proj][m][b] = s;
+    }
+    __syncthreads();
+
+    // phase 2: waves 0, 1 stream the gate strip, waves 2, 3 the up strip (alternating tile-rows)
+    const int proj = wave >> 1, half = wave & 1;
+    float acc[MR][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(a.tables[(3 * proj) * E + e]);
+    const int tn = a.I / 16;
+    if (K > 0) {
+        const size_t rs = (size_t)tn * (8 * K);
+        strip_gemv<(K > 0 ? K : 1), MR>(tr + (size_t)nb * (64 * K) + (size_t)b0 * 8 * rs, rs, half, kb * 8, 2, lane,
+                                        &xs[proj][0][0], kGemvKBMax * 128, acc);
+    } else {
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(a.kmaps[(2 * proj) * E + e]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(a.kmaps[(2 * proj + 1) * E + e]);
+        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &xs[proj][0][0],
+                             kGemvKBMax * 128, acc);
+    }
+
+    // phase 3: per projection, fold the two waves, the codebook affine, publish the split's partial
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        red[wave][m][0][lane] = acc[m][0];
+        red[wave][m][1][lane] = acc[m][1];
+    }
+    __syncthreads();
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    const size_t slot = (size_t)item * nbI + nb;
+    if (half == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float sx = 0.f;
+            for (int b = 0; b < kb; ++b) sx += bsum[proj][m][b];
+            float* dst = a.part_gu + (((slot * a.P_gu + p) * 2 + proj) * MR + m) * 128;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float v = red[wave][m][h][lane] + red[wave + 1][m][h][lane];
+                splitk_store(dst + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+            }
+        }
+    }
+    if (!splitk_arrive(&a.cnt_gu[slot], a.P_gu, &s_last)) return;
+
+    // epilogue (last workgroup of this item / column block)
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(a.tables[2 * E + e]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(a.tables[5 * E + e]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(a.tables[7 * E + e]) + nb * 128;
+    for (int m = wave; m < cnt; m += 4) {
+        float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+        for (int pp = 0; pp < a.P_gu; ++pp) {
+            const float* q = a.part_gu + ((slot * a.P_gu + pp) * 2) * MR * 128 + m * 128;
+            g0 += splitk_load(q + lane);
+            g1 += splitk_load(q + lane + 64);
+            u0 += splitk_load(q + MR * 128 + lane);
+            u1 += splitk_load(q + MR * 128 + lane + 64);
+        }
+        fwht128_wave(g0, g1, lane);
+        fwht128_wave(u0, u1, lane);
+        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(svg[lane]));
+        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(svg[lane + 64]));
+        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(svu[lane]));
+        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(svu[lane + 64]));
+        float a0 = (float)(_Float16)act_mul(g0, u0, a.act, a.limit);
+        float a1 = (float)(_Float16)act_mul(g1, u1, a.act, a.limit);
+        a0 = (float)(_Float16)(a0 * h2f(sud[lane]));
+        a1 = (float)(_Float16)(a1 * h2f(sud[lane + 64]));
+        fwht128_wave(a0, a1, lane);
+        uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
+        dst[lane] = f2h(a0 * kRsqrt128);
+        dst[lane + 64] = f2h(a1 * kRsqrt128);
+    }
+    if (threadIdx.x == 0) a.cnt_gu[slot] = 0;
+}
+
+// ================================================================================================ down
+template <int K, int MR>
+__global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[MR][kGemvKBMax * 128];
+    __shared__ float red[4][MR][2][64];
+    __shared__ float bsum[MR][kGemvKBMax];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nbH = a.H / 128;
+    const int item = blockIdx.x / nbH, nb = blockIdx.x - item * nbH, p = blockIdx.y;
+    if (item >= a.n_items[0]) return;
+    const int e = a.item_e[item], p0 = a.item_p0[item], cnt = a.item_cnt[item];
+    const int64_t E = a.E;
+    const int b0 = (int)((int64_t)p * a.nblk_i / a.P_d), b1 = (int)((int64_t)(p + 1) * a.nblk_i / a.P_d);
+    const int kb = b1 - b0;
+
+    for (int i = wave; i < MR * kb; i += 4) {
+        const int m = i / kb, b = i - m * kb;
+        const uint16_t* src = m < cnt ? a.abuf + (size_t)(p0 + m) * a.I + (b0 + b) * 128 : nullptr;
+        float s = copy_block(src, &xs[m][b * 128], lane);
+        if (lane == 0) bsum[m][b] = s;
+    }
+    __syncthreads();
+
+    float acc[MR][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(a.tables[6 * E + e]);
+    const int tn = a.H / 16;
+    if (K > 0) {
+        const size_t rs = (size_t)tn * (8 * K);
+        strip_gemv<(K > 0 ? K : 1), MR>(tr + (size_t)nb * (64 * K) + (size_t)b0 * 8 * rs, rs, wave, kb * 8, 4, lane,
+                                        &xs[0][0], kGemvKBMax * 128, acc);
+    } else {
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(a.kmaps[4 * E + e]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(a.kmaps[5 * E + e]);
+        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128,
+                             acc);
+    }
+
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        red[wave][m][0][lane] = acc[m][0];
+        red[wave][m][1][lane] = acc[m][1];
+    }
+    __syncthreads();
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    const size_t slot = (size_t)item * nbH + nb;
+    if (wave == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float sx = 0.f;
+            for (int b = 0; b < kb; ++b) sx += bsum[m][b];
+            float* dst = a.part_d + ((slot * a.P_d + p) * MR + m) * 128;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float v = red[0][m][h][lane] + red[1][m][h][lane] + red[2][m][h][lane] + red[3][m][h][lane];
+                splitk_store(dst + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+            }
+        }
+    }
+    if (!splitk_arrive(&a.cnt_d[slot], a.P_d, &s_last)) return;
+
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(a.tables[8 * E + e]) + nb * 128;
+    for (int m = wave; m < cnt; m += 4) {
+        float v0 = 0.f, v1 = 0.f;
+        for (int pp = 0; pp < a.P_d; ++pp) {
+            const float* q = a.part_d + ((slot * a.P_d + pp) * MR + m) * 128;
+            v0 += splitk_load(q + lane);
+            v1 += splitk_load(q + lane + 64);
+        }
+        fwht128_wave(v0, v1, lane);
+        const float w = a.pair_w[p0 + m];
+        float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 128;
+        dst[lane] = v0 * kRsqrt128 * h2f(svd[lane]) * w;
+        dst[lane + 64] = v1 * kRsqrt128 * h2f(svd[lane + 64]) * w;
+    }
+    if (threadIdx.x == 0) a.cnt_d[slot] = 0;
+}
+
+// ================================================================================================ combine
+__global__ __launch_bounds__(64) void combine_kernel(MoeArgs a) {
+    const int lane = threadIdx.x;
+    const int t = blockIdx.x, nb = blockIdx.y;
+    const int c0 = nb * 128 + lane, c1 = c0 + 64;
+    float v0 = 0.f, v1 = 0.f;
+    for (int j = 0; j < a.slots; ++j) {
+        const int pr = a.pair_of[t * a.slots + j];
+        if (pr < 0) continue;
+        const float* y = a.y + (size_t)pr * a.H;
+        v0 += y[c0];
+        v1 += y[c1];
+    }
+    if (a.out_f32) {
+        float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
+        o[c0] = v0;
+        o[c1] = v1;
+    } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
+        o[c0] = f2h(v0);
+        o[c1] = f2h(v1);
+    }
+}
+
+// ================================================================================================ router
+// One wave per row: softmax statistics over E logits (+ bias), then k rounds of a wave argmax over the key z.
+__global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, int64_t ld, int E,
+                                                   const float* __restrict__ bias, int k, int32_t* __restrict__ ids,
+                                                   float* __restrict__ w) {
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const float* z = logits + row * ld;
+    float mx = -INFINITY;
+    for (int i = lane; i < E; i += 64) mx = fmaxf(mx, z[i] + (bias ? bias[i] : 0.f));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    float sum = 0.f;
+    for (int i = lane; i < E; i += 64) sum += expf(z[i] + (bias ? bias[i] : 0.f) - mx);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
+    // k rounds of a wave argmax over the key z (ties to the lower index); picks are kept in LDS
+    __shared__ int s_taken[32];
+    float ptaken = 0.f;
+    int taken = -1;
+    for (int j = 0; j < k; ++j) {
+        float best = -INFINITY;
+        int bi = 0x7FFFFFFF;
+        for (int i = lane; i < E; i += 64) {
+            bool used = false;
+            for (int q = 0; q < j; ++q) used |= (s_taken[q] == i);
+            if (used) continue;
+            const float v = z[i] + (bias ? bias[i] : 0.f);
+            if (v > best || (v == best && i < bi)) {
+                best = v;
+                bi = i;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ob = __shfl_xor(best, m);
+            const int oi = __shfl_xor(bi, m);
+            if (ob > best || (ob == best && oi < bi)) {
+                best = ob;
+                bi = oi;
+            }
+        }
+        if (lane == j) {
+            taken = bi;
+            ptaken = expf(best - mx) / sum;
+        }
+        if (lane == 0) s_taken[j] = bi;
+        __syncthreads();
+    }
+    float s = lane < k ? ptaken : 0.f;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    if (lane < k) {
+        ids[row * k + lane] = taken;
+        w[row * k + lane] = ptaken / (s + 1e-20f);
+    }
+}
+
+// ================================================================================================ act_mul
+template <bool F16>
+__global__ __launch_bounds__(256) void act_mul_kernel(const void* __restrict__ x, const void* __restrict__ y,
+                                                      uint16_t* __restrict__ z, int64_t n, int act, float L) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float g, u;
+    if (F16) {
+        g = h2f(reinterpret_cast<const uint16_t*>(x)[i]);
+        u = h2f(reinterpret_cast<const uint16_t*>(y)[i]);
+    } else {
+        g = reinterpret_cast<const float*>(x)[i];
+        u = reinterpret_cast<const float*>(y)[i];
+    }
+    z[i] = f2h(act_mul(g, u, act, L));
+}
+
+// ================================================================================================ host
+static size_t align_lds_bytes(int E) { return (size_t)(4 * E + 1024) * sizeof(int); }
+
+int launch_align(const RouteArgs& r, hipStream_t st) {
+    const size_t lds = align_lds_bytes(r.E);
+    hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), lds, st, r);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+static int moe_splits(int units, int nblk) {
+    int P = (kGemvTargetWG + units - 1) / (units > 0 ? units : 1);
+    int pmin = (nblk + kGemvKBMax - 1) / kGemvKBMax;
+    if (P < pmin) P = pmin;
+    if (P > nblk) P = nblk;
+    return P < 1 ? 1 : P;
+}
+
+typedef void (*moe_fn)(MoeArgs);
+
+template <int MR>
+static moe_fn pick_gateup(int K) {
+    switch (K) {
+        case 0: return gateup_kernel<0, MR>;
+        case 1: return gateup_kernel<1, MR>;
+        case 2: return gateup_kernel<2, MR>;
+        case 3: return gateup_kernel<3, MR>;
+        case 4: return gateup_kernel<4, MR>;
+        case 5: return gateup_kernel<5, MR>;
+        case 6: return gateup_kernel<6, MR>;
+        case 7: return gateup_kernel<7, MR>;
+        default: return gateup_kernel<8, MR>;
+    }
+}
+
+template <int MR>
+static moe_fn pick_down(int K) {
+    switch (K) {
+        case 0: return down_kernel<0, MR>;
+        case 1: return down_kernel<1, MR>;
+        case 2: return down_kernel<2, MR>;
+        case 3: return down_kernel<3, MR>;
+        case 4: return down_kernel<4, MR>;
+        case 5: return down_kernel<5, MR>;
+        case 6: return down_kernel<6, MR>;
+        case 7: return down_kernel<7, MR>;
+        default: return down_kernel<8, MR>;
+    }
+}
+
+static moe_fn gateup_select(int K, int MR) {
+    switch (MR) {
+        case 1: return pick_gateup<1>(K);
+        case 2: return pick_gateup<2>(K);
+        case 4: return pick_gateup<4>(K);
+        default: return pick_gateup<8>(K);
+    }
+}
+
+static moe_fn down_select(int K, int MR) {
+    switch (MR) {
+        case 1: return pick_down<1>(K);
+        case 2: return pick_down<2>(K);
+        case 4: return pick_down<4>(K);
+        default: return pick_down<8>(K);
+    }
+}
+
+// Decode path: items of <= MR rows through the GEMV kernels. `a` has every field but the route/workspace ones set.
+int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
+    const int max_items = a.max_items;
+    const int nbI = a.I / 128, nbH = a.H / 128;
+    a.nblk_h = a.H / 128;
+    a.nblk_i = a.I / 128;
+    a.P_gu = moe_splits(max_items < 16 ? max_items * nbI : 16 * nbI, a.nblk_h);
+    a.P_d = moe_splits(max_items < 16 ? max_items * nbH : 16 * nbH, a.nblk_i);
+    const int MR = a.MR;
+    Workspace ws;
+    const size_t n_gu = (size_t)max_items * nbI, n_d = (size_t)max_items * nbH;
+    size_t bytes = carve_size((size_t)4 * max_items + 1, 4) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
+                   carve_size(npairs * a.I, 2) + carve_size(npairs * a.H, 4) +
+                   carve_size(n_gu * a.P_gu * 2 * MR * 128, 4) + carve_size(n_d * a.P_d * MR * 128, 4);
+    int rc = workspace(bytes, n_gu + n_d, &ws);
+    if (rc) return rc;
+    Carve c{ws.scratch, ws.scratch_bytes};
+    int* ib = c.take<int>((size_t)4 * max_items + 1);
+    a.n_items = ib;
+    a.item_e = ib + 1;
+    a.item_p0 = ib + 1 + max_items;
+    a.item_cnt = ib + 1 + 2 * max_items;
+    int* pb = c.take<int>(npairs * 2);
+    a.pair_tok = pb;
+    a.pair_of = pb + npairs;
+    a.pair_w = c.take<float>(npairs);
+    a.abuf = c.take<uint16_t>(npairs * a.I);
+    a.y = c.take<float>(npairs * a.H);
+    a.part_gu = c.take<float>(n_gu * a.P_gu * 2 * MR * 128);
+    a.part_d = c.take<float>(n_d * a.P_d * MR * 128);
+    if (!a.part_d) return fail(EXL3_ERR_INVALID, "moe: workspace carve failed");
+    a.cnt_gu = ws.counters;
+    a.cnt_d = ws.counters + n_gu;
+
+    RouteArgs r{};
+    r.ids = a.ids;
+    r.tw = a.tw;
+    r.M = a.M;
+    r.topk = a.topk;
+    r.slots = a.slots;
+    r.E = a.E;
+    r.shared = a.shared;
+    r.MR = MR;
+    r.n_items = a.n_items;
+    r.item_e = a.item_e;
+    r.item_p0 = a.item_p0;
+    r.item_cnt = a.item_cnt;
+    r.pair_tok = a.pair_tok;
+    r.pair_w = a.pair_w;
+    r.pair_of = a.pair_of;
+    rc = launch_align(r, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
+    EXL3_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
+    EXL3_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(combine_kernel, dim3(a.M, nbH), dim3(64), 0, st, a);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+static int check_K(int K, const char* what) {
+    if (K < 0 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward: %s K=%d not in 0..8", what, K);
+    return EXL3_OK;
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" {
+
+int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
+                     const float* topk_w, int64_t topk, int64_t E, const int64_t* tables, const int64_t* kmaps,
+                     int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
+                     int64_t out_ld, int out_dtype, void* stream) {
+    int rc;
+    if ((rc = check_K(K_gate, "gate")) || (rc = check_K(K_up, "up")) || (rc = check_K(K_down, "down"))) return rc;
+    if (K_gate != K_up)
+        return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward: gate and up must share K (got %d, %d)", K_gate, K_up);
+    EXL3_CHECK_ARG(act == EXL3_ACT_SILU || act == EXL3_ACT_GELU_TANH, "exl3_moe_forward: unknown activation %d", act);
+    EXL3_CHECK_ARG(out_dtype == EXL3_F16 || out_dtype == EXL3_F32, "exl3_moe_forward: out must be fp16 or fp32");
+    EXL3_CHECK_ARG(M >= 0 && topk >= 0 && topk <= 64 && E > 0 && E <= kMoeMaxExperts,
+                   "exl3_moe_forward: M=%lld topk=%lld E=%lld out of range", (long long)M, (long long)topk,
+                   (long long)E);
+    EXL3_CHECK_ARG(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0, "exl3_moe_forward: H and I must be multiples of 128");
+    EXL3_CHECK_ARG(x_ld >= H && out_ld >= H, "exl3_moe_forward: row strides must cover H");
+    EXL3_CHECK_ARG(shared < E, "exl3_moe_forward: shared expert index %lld >= E", (long long)shared);
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(x && tables && out && (topk == 0 || (topk_ids && topk_w)), "exl3_moe_forward: null pointer");
+    EXL3_CHECK_ARG(K_gate != 0 && K_down != 0 ? true : kmaps != nullptr,
+                   "exl3_moe_forward: per-tile K (K=0) needs the kmaps table");
+    MoeArgs a{};
+    a.x = x;
+    a.x_ld = x_ld;
+    a.M = (int)M;
+    a.H = (int)H;
+    a.I = (int)I;
+    a.topk = (int)topk;
+    a.slots = (int)topk + (shared >= 0 ? 1 : 0);
+    a.E = (int)E;
+    a.ids = topk_ids;
+    a.tw = topk_w;
+    a.tables = tables;
+    a.kmaps = kmaps;
+    a.Kg = K_gate;
+    a.Kd = K_down;
+    a.act = act;
+    a.limit = act_limit;
+    a.shared = (int)shared;
+    a.out = out;
+    a.out_ld = out_ld;
+    a.out_f32 = out_dtype == EXL3_F32;
+    const int64_t npairs = M * a.slots;
+    a.MR = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    int64_t mi = E + npairs / a.MR;
+    if (mi > npairs) mi = npairs;
+    a.max_items = (int)mi;
+    EXL3_CHECK_ARG((int64_t)a.max_items * (H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
+    return moe_decode_path(a, npairs, (hipStream_t)stream);
+}
+
+int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int64_t M, int64_t topk, int64_t E, int64_t shared,
+                   int32_t* counts, int32_t* pair_tok, float* pair_w, int32_t* pair_of, void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && topk >= 0 && E > 0 && E <= kMoeMaxExperts && shared < E, "exl3_moe_align: bad sizes");
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(topk_ids && topk_w && counts && pair_tok && pair_w && pair_of, "exl3_moe_align: null pointer");
+    RouteArgs r{};
+    r.ids = topk_ids;
+    r.tw = topk_w;
+    r.M = (int)M;
+    r.topk = (int)topk;
+    r.slots = (int)topk + (shared >= 0 ? 1 : 0);
+    r.E = (int)E;
+    r.shared = (int)shared;
+    r.MR = 1;
+    r.counts = counts;
+    r.pair_tok = pair_tok;
+    r.pair_w = pair_w;
+    r.pair_of = pair_of;
+    return launch_align(r, (hipStream_t)stream);
+}
+
+int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype, int act, float act_limit,
+                 void* stream) {
+    EXL3_CHECK_ARG(dtype == EXL3_F16 || dtype == EXL3_F32, "exl3_act_mul: dtype must be fp16 or fp32");
+    EXL3_CHECK_ARG(act == EXL3_ACT_SILU || act == EXL3_ACT_GELU_TANH, "exl3_act_mul: unknown activation %d", act);
+    EXL3_CHECK_ARG(n >= 0, "exl3_act_mul: negative size");
+    if (n == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(x && y && z, "exl3_act_mul: null pointer");
+    const int64_t blocks = (n + 255) / 256;
+    EXL3_CHECK_ARG(blocks <= 0x7FFFFFFF, "exl3_act_mul: too large");
+    if (dtype == EXL3_F16)
+        hipLaunchKernelGGL(act_mul_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y, z, n,
+                           act, act_limit);
+    else
+        hipLaunchKernelGGL(act_mul_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y, z,
+                           n, act, act_limit);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
+                            int32_t* ids, float* w, void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && E > 0 && k > 0 && k <= 32 && k <= E && ld >= E, "exl3_route_softmax_topk: bad sizes");
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(logits && ids && w, "exl3_route_softmax_topk: null pointer");
+    EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_softmax_topk: too many rows");
+    hipLaunchKernelGGL(route_kernel, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
+                       (int)k, ids, w);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,251 @@
+"""Grouped EXL3 MoE on the HIP kernels: expert pointer tables, the routed multi-GEMM, routers, gated MLPs.
+
+Interfaces mirror the reference boundary:
+  * moe_forward(x, topk_ids, topk_w, tables, ...) -> out, the exl3xpu_moe::moe_forward op
+    (glm/xpu/csrc/exl3_moe.n128.sycl:1380-1439, 1681-1682) over the nine per-projection pointer tables that
+    BC_BlockSparseMLP / exl3_moe take (ext-op-inventory.md:1027-1034, 1060-1093)
+  * BlockSparseMLP.forward(x, params, out_dtype) -> fp32 routed sum + shared expert, the patched forward of
+    glm/xpu/glm_xpu/moe_patch.py:68-94 and dsv41/xpu/dsv_xpu/moe.py:1563-1630
+  * BC_GatedMLP(...).run_bszN(x, d) (glm/xpu/glm_xpu/ops.py:157-172), silu_mul / gelu_mul (ext-op-inventory.md:944-956)
+  * route_softmax_topk: the fused softmax/top-k router of trellis-serve (trellis-serve.patch:395-441)
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import ACT_GELU_TANH, ACT_SILU, EXL3_F16, EXL3_F32, Exl3Error, check, lib, ptr, require_device, stream_of
+from .linear import BC_LinearEXL3
+
+ACTS = {"silu": ACT_SILU, "gelu_tanh": ACT_GELU_TANH, ACT_SILU: ACT_SILU, ACT_GELU_TANH: ACT_GELU_TANH}
+
+
+class MixedEXL3:
+    """An EXL3 projection whose 16x16 tiles carry their own K (1..8): tile i (row-major over [k/16, n/16]) holds
+    8 * kmap[i] uint32 words at words[woff[i]:]. A per-projection K is the special case of a constant map."""
+
+    def __init__(self, words: torch.Tensor, kmap: torch.Tensor, woff: torch.Tensor, suh: torch.Tensor,
+                 svh: torch.Tensor):
+        if kmap.dtype != torch.uint8 or woff.dtype != torch.int32 or words.dtype not in (torch.int32, torch.int16):
+            raise Exl3Error("MixedEXL3: words int32, kmap uint8, woff int32 expected")
+        self.words, self.kmap, self.woff, self.suh, self.svh = words, kmap, woff, suh, svh
+        self.in_features, self.out_features = suh.numel(), svh.numel()
+        if kmap.numel() != (self.in_features // 16) * (self.out_features // 16) or woff.numel() != kmap.numel() + 1:
+            raise Exl3Error("MixedEXL3: kmap / woff sizes do not match the shape")
+        self.K = 0
+        self.trellis = words
+
+    def to(self, dev):
+        return MixedEXL3(*(t.to(dev) for t in (self.words, self.kmap, self.woff, self.suh, self.svh)))
+
+
+def _proj_K(p) -> int:
+    return 0 if isinstance(p, MixedEXL3) else p.Ki
+
+
+class ExpertTables:
+    """Device tables of E experts: int64 [9, E] = (trellis, suh, svh) addresses of gate, up, down, plus int64 [6, E]
+    (kmap, woff) addresses for per-tile-K projections. Holds references to every tensor it points at."""
+
+    def __init__(self, gates, ups, downs):
+        if not (len(gates) == len(ups) == len(downs)) or not gates:
+            raise Exl3Error("ExpertTables: gate/up/down lists must be non-empty and equally long")
+        self.E = len(gates)
+        self.projs = (list(gates), list(ups), list(downs))
+        Ks = []
+        for plist in self.projs:
+            ks = {_proj_K(p) for p in plist}
+            if len(ks) != 1:
+                raise NotImplementedError("ExpertTables: every expert of a projection must share K (or all be per-tile)")
+            Ks.append(ks.pop())
+        self.K_gate, self.K_up, self.K_down = Ks
+        g0, d0 = gates[0], downs[0]
+        self.H, self.I = g0.in_features, g0.out_features
+        for p in gates + ups:
+            if (p.in_features, p.out_features) != (self.H, self.I):
+                raise Exl3Error("ExpertTables: gate/up shapes differ")
+        for p in downs:
+            if (p.in_features, p.out_features) != (self.I, self.H):
+                raise Exl3Error("ExpertTables: down shapes differ")
+        dev = g0.suh.device
+        rows = []
+        for plist in self.projs:
+            rows.append([p.trellis.data_ptr() for p in plist])
+            rows.append([p.suh.data_ptr() for p in plist])
+            rows.append([p.svh.data_ptr() for p in plist])
+        self.tables = torch.tensor(rows, dtype=torch.int64).to(dev)
+        self.kmaps = None
+        if 0 in Ks:
+            krows = []
+            for plist in self.projs:
+                krows.append([p.kmap.data_ptr() if isinstance(p, MixedEXL3) else 0 for p in plist])
+                krows.append([p.woff.data_ptr() if isinstance(p, MixedEXL3) else 0 for p in plist])
+            self.kmaps = torch.tensor(krows, dtype=torch.int64).to(dev)
+
+    def weight_bytes(self, experts) -> int:
+        """Trellis + sign-vector bytes of the given expert indices (the algorithmic HBM bytes of reading them)."""
+        tot = 0
+        for e in experts:
+            for p in (self.projs[0][e], self.projs[1][e], self.projs[2][e]):
+                tot += p.trellis.numel() * p.trellis.element_size() + 2 * (p.in_features + p.out_features)
+                if isinstance(p, MixedEXL3):
+                    tot += p.kmap.numel() + 4 * p.woff.numel()
+        return tot
+
+
+def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, tables: ExpertTables, act=ACT_SILU,
+                act_limit: float = 0.0, shared: int = -1, out: torch.Tensor | None = None,
+                out_dtype=torch.float32) -> torch.Tensor:
+    """out[t] = sum_j topk_w[t, j] * expert_{topk_ids[t, j]}(x[t]) (+ expert `shared` with weight 1), fp32 sums.
+    x fp16 [M, H]; topk_ids int32 [M, k] (negative = inactive); topk_w fp32 [M, k]."""
+    require_device(x, topk_ids, topk_w)
+    if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1 or x.shape[1] != tables.H:
+        raise Exl3Error(f"moe_forward: x must be fp16 [M, {tables.H}] with contiguous rows")
+    M = x.shape[0]
+    if topk_ids.dtype != torch.int32 or topk_w.dtype != torch.float32:
+        raise Exl3Error("moe_forward: topk_ids int32 and topk_w fp32 expected")
+    if topk_ids.shape != topk_w.shape or topk_ids.dim() != 2 or topk_ids.shape[0] != M:
+        raise Exl3Error("moe_forward: topk_ids / topk_w must be [M, k]")
+    topk_ids, topk_w = topk_ids.contiguous(), topk_w.contiguous()
+    if out is None:
+        out = torch.empty(M, tables.H, dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.float16, torch.float32) or out.stride(1) != 1 or tuple(out.shape) != (M, tables.H):
+        raise Exl3Error("moe_forward: out must be fp16/fp32 [M, H] with contiguous rows")
+    a = ACTS.get(act)
+    if a is None:
+        raise NotImplementedError(f"moe_forward: activation {act!r}")
+    check(lib().exl3_moe_forward(ptr(x), x.stride(0), M, tables.H, tables.I, ptr(topk_ids), ptr(topk_w),
+                                 topk_ids.shape[1], tables.E, ptr(tables.tables), ptr(tables.kmaps), tables.K_gate,
+                                 tables.K_up, tables.K_down, a, float(act_limit), int(shared), ptr(out),
+                                 out.stride(0), EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, stream_of(x)),
+          "moe_forward")
+    return out
+
+
+def moe_align(topk_ids: torch.Tensor, topk_w: torch.Tensor, E: int, shared: int = -1):
+    """(counts int32 [E], pair_tok int32 [P], pair_w fp32 [P], pair_of int32 [M*slots]) as the kernels build them."""
+    require_device(topk_ids, topk_w)
+    M, k = topk_ids.shape
+    slots = k + (1 if shared >= 0 else 0)
+    dev = topk_ids.device
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    pair_tok = torch.full((M * slots,), -1, dtype=torch.int32, device=dev)
+    pair_w = torch.zeros(M * slots, dtype=torch.float32, device=dev)
+    pair_of = torch.empty(M * slots, dtype=torch.int32, device=dev)
+    check(lib().exl3_moe_align(ptr(topk_ids.contiguous()), ptr(topk_w.contiguous()), M, k, E, shared, ptr(counts),
+                               ptr(pair_tok), ptr(pair_w), ptr(pair_of), stream_of(topk_ids)), "moe_align")
+    return counts, pair_tok, pair_w, pair_of
+
+
+def route_softmax_topk(logits: torch.Tensor, k: int, bias: torch.Tensor | None = None):
+    """softmax(logits + bias) -> top-k (descending, ties to the lower index) -> renormalised weights."""
+    require_device(logits, bias)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise Exl3Error("route_softmax_topk: logits must be fp32 [M, E] with contiguous rows")
+    M, E = logits.shape
+    ids = torch.empty(M, k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=logits.device)
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E):
+        raise Exl3Error("route_softmax_topk: bias must be fp32 [E]")
+    check(lib().exl3_route_softmax_topk(ptr(logits), logits.stride(0), M, E, ptr(bias), k, ptr(ids), ptr(w),
+                                        stream_of(logits)), "route_softmax_topk")
+    return ids, w
+
+
+def _act_mul(x, y, z, act, act_limit):
+    require_device(x, y, z)
+    if x.shape != y.shape or x.numel() != z.numel() or x.dtype != y.dtype or z.dtype != torch.float16:
+        raise Exl3Error("act_mul: x, y same shape and dtype, z fp16 with as many elements")
+    if not (x.is_contiguous() and y.is_contiguous() and z.is_contiguous()):
+        raise Exl3Error("act_mul: tensors must be contiguous")
+    dt = EXL3_F16 if x.dtype == torch.float16 else EXL3_F32
+    check(lib().exl3_act_mul(ptr(x), ptr(y), ptr(z), x.numel(), dt, act, float(act_limit), stream_of(x)), "act_mul")
+
+
+def silu_mul(x, y, z, act_limit):
+    """z = min(silu(x), L) * clamp(y, -L, L) (L = act_limit, 0 disables), written into z (fp16)."""
+    _act_mul(x, y, z, ACT_SILU, act_limit)
+
+
+def gelu_mul(x, y, z, act_limit=0.0):
+    """z = gelu_tanh(x) * y, written into z (fp16)."""
+    _act_mul(x, y, z, ACT_GELU_TANH, 0.0)
+
+
+class BC_GatedMLP:
+    """Dense / shared-expert gated MLP: g, u = gate(x), up(x); a = act(g, u); d = down(a). run_bszN(x, d) writes the
+    fp32 result into d. Runs as a one-expert table through the grouped kernels (fused activation epilogue).
+    Constructor mirrors glm/xpu/glm_xpu/ops.py:157-172 (scratch buffers and fused pointer tables are accepted and
+    ignored; gate and up handles are required)."""
+
+    def __init__(self, guh, gu, a, down_xh, gu_ptrs_trellis, gu_ptrs_suh, gu_ptrs_svh, gu_K, gu_mcg, gu_mul1,
+                 act_silu, act_gelu, act_relu2, gate, up, down, act_limit):
+        if gate is None or up is None:
+            raise NotImplementedError("BC_GatedMLP: fused gate/up pointer tables without gate/up handles")
+        if act_relu2:
+            raise NotImplementedError("BC_GatedMLP: relu2 activation")
+        if not (act_silu or act_gelu):
+            raise NotImplementedError("BC_GatedMLP: activation must be SiLU or GELU")
+        self.gate, self.up, self.down = gate, up, down
+        self.act = ACT_SILU if act_silu else ACT_GELU_TANH
+        self.act_limit = act_limit
+        self.tables = ExpertTables([gate], [up], [down])
+        self._ids = {}
+
+    def run_bszN(self, x: torch.Tensor, d: torch.Tensor) -> None:
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.dtype != torch.float16:
+            x2 = x2.half()
+        x2 = x2.contiguous()
+        M = x2.shape[0]
+        key = (x2.device, M)
+        if key not in self._ids:
+            self._ids[key] = (torch.empty(M, 0, dtype=torch.int32, device=x2.device),
+                              torch.empty(M, 0, dtype=torch.float32, device=x2.device))
+        ids, w = self._ids[key]
+        d2 = d.view(-1, d.shape[-1])
+        moe_forward(x2, ids, w, self.tables, self.act, self.act_limit, shared=0, out=d2)
+
+    def forward(self, x: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+        d = torch.empty(x.shape[:-1] + (self.down.out_features,), dtype=out_dtype, device=x.device)
+        self.run_bszN(x, d)
+        return d
+
+
+class BlockSparseMLP:
+    """Routed MoE layer: route (softmax / top-k over router logits, optional per-expert selection bias), grouped
+    routed experts, plus the shared expert (weight 1, added after the routed slots). forward returns fp32.
+
+    `experts` holds the routed experts first and, when `has_shared`, the shared expert as the last table entry.
+    Router logits come from `router_weight` (fp16 [H, E]: logits = x @ W in fp32) or from params["router_logits"]."""
+
+    def __init__(self, experts: ExpertTables, num_experts_per_tok: int, has_shared: bool = False, act="silu",
+                 act_limit: float = 0.0, router_weight: torch.Tensor | None = None,
+                 selection_bias: torch.Tensor | None = None):
+        self.experts = experts
+        self.num_experts = experts.E - (1 if has_shared else 0)
+        self.num_experts_per_tok = num_experts_per_tok
+        self.shared = experts.E - 1 if has_shared else -1
+        self.act = ACTS[act]
+        self.act_limit = act_limit
+        self.router_weight = router_weight
+        self.selection_bias = selection_bias
+
+    def route(self, x2: torch.Tensor, params=None):
+        logits = None if params is None else params.get("router_logits")
+        if logits is None:
+            if self.router_weight is None:
+                raise Exl3Error("BlockSparseMLP: no router weight and no params['router_logits']")
+            logits = x2.float() @ self.router_weight.float()
+        logits = logits.reshape(-1, self.num_experts).float().contiguous()
+        return route_softmax_topk(logits, self.num_experts_per_tok, self.selection_bias)
+
+    def forward(self, x: torch.Tensor, params=None, out_dtype=None) -> torch.Tensor:
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.dtype != torch.float16:
+            x2 = x2.half()
+        x2 = x2.contiguous()
+        ids, w = self.route(x2, params)
+        out = moe_forward(x2, ids, w, self.experts, self.act, self.act_limit, self.shared,
+                          out_dtype=torch.float32)
+        out = out.view(x.shape[:-1] + (self.experts.H,))
+        return out if out_dtype is None else out.to(out_dtype)

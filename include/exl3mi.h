@@ -66,6 +66,51 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
               int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
               void* stream);
 
+/* Gated activation z = act(x, y) elementwise over n values, fp16 (dtype EXL3_F16) or fp32 (EXL3_F32) inputs, fp16
+ * output (in place on y allowed). SiLU: z = min(silu(x), L) * clamp(y, -L, L) (L = act_limit, 0 disables);
+ * GELU-tanh: z = gelu_tanh(x) * y. Computed in fp32, rounded once.
+ * Replaces: exllamav3 ext silu_mul / gelu_mul (ext-op-inventory.md:944-956; glm/xpu/glm_xpu/ops.py:147-154). */
+int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype, int act, float act_limit,
+                 void* stream);
+
+/* ---------------------------------------------------------------------------------------------- grouped MoE
+ * Expert tables: `tables` is a device int64 array [9][E] of device addresses, row 3p + {0, 1, 2} = (trellis, suh,
+ * svh) of projection p = 0 gate [H -> I], 1 up [H -> I], 2 down [I -> H], the nine per-projection pointer tables of
+ * the reference's BC_BlockSparseMLP / exl3_moe (ext-op-inventory.md:1027-1034, 1060-1093).
+ * K_gate / K_up / K_down: bits per weight of each projection (1..8, gate and up equal), or 0 = per-tile K: then
+ * `kmaps` (device int64 [6][E]) holds for projection p the address of a uint8 [k/16 * n/16] tile-K map (row-major
+ * tiles) at row 2p and of an int32 [k/16 * n/16 + 1] word-offset prefix at row 2p + 1; the trellis address is the
+ * base of the concatenated tile words (tile i: 8 * kmap[i] words at offset woff[i]). kmaps may be NULL otherwise. */
+
+/* Routed MoE layer: out[t] = sum_{j < topk, slot order} w[t, j] * expert_{ids[t, j]}(x[t]) (+ expert `shared`(x[t])
+ * with weight 1 after the routed slots when shared >= 0). expert(x) = down(act(gate(x), up(x))) with the reference
+ * rounding points: gate/up outputs fp16, activation fp16, down input transform fp16, fp32 accumulation.
+ * x fp16 [M, H] (row stride x_ld); topk_ids int32 [M, topk] in [0, E) (negative = inactive slot); topk_w fp32
+ * [M, topk]; out fp32 or fp16 [M, H] (row stride out_ld). H % 128 == 0, I % 128 == 0.
+ * act: EXL3_ACT_SILU (a = min(silu(g), L) * clamp(u, -L, L), L = act_limit, 0 = no clamp) or EXL3_ACT_GELU_TANH.
+ * Experts with up to 8 rows use the decode GEMV kernels; experts with more rows use the fp16 MFMA grouped GEMM.
+ * Replaces: exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) (glm/xpu/csrc/exl3_moe.n128.sycl:
+ *           1380-1439, bound at :1681-1682), BC_BlockSparseMLP.run_bszN and exl3_moe + exl3_moe_gather
+ *           (ext-op-inventory.md:1036-1102), dsv_moe::moe_gemv with per-item K (dsv41/xpu/csrc/dsv_moe.sycl:157-170). */
+int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
+                     const float* topk_w, int64_t topk, int64_t E, const int64_t* tables, const int64_t* kmaps,
+                     int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
+                     int64_t out_ld, int out_dtype, void* stream);
+
+/* Routing tables as the MoE kernels build them (pairs grouped by expert), for tests and debugging.
+ * Writes counts int32 [E], pair_tok int32 [M*slots], pair_w fp32 [M*slots], pair_of int32 [M*slots]
+ * (slots = topk + (shared >= 0)); pair order inside an expert is unspecified.
+ * Replaces: exl3xpu_moe::moe_align (glm/xpu/csrc/exl3_moe.n128.sycl:1441-1448). */
+int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int64_t M, int64_t topk, int64_t E, int64_t shared,
+                   int32_t* counts, int32_t* pair_tok, float* pair_w, int32_t* pair_of, void* stream);
+
+/* Softmax router: p = softmax(logits + bias) over E experts, top-k by p (ties to the lower index, descending),
+ * weights renormalised over the k picks with +1e-20. logits fp32 [M, E] (row stride ld), bias fp32 [E] or NULL;
+ * ids int32 [M, k], w fp32 [M, k]. k <= 32.
+ * Replaces: the fused softmax/top-k router of trellis-serve (trellis-serve.patch:395-441). */
+int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
+                            int32_t* ids, float* w, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,177 @@
+"""GPU parity of the grouped MoE path (routing tables, gate|up + activation epilogue, down, combine, routers, gated
+MLP) against the CPU oracle on identical seeded bytes. Bar: max|y - r| / max|r| <= 2e-3 against the oracle's
+float64-accumulated layer output (the reference's max_rel, trellis-serve.patch:3889); routing ids exact."""
+import numpy as np
+import pytest
+import torch
+
+from moe_util import make_experts, max_rel
+
+pytestmark = pytest.mark.gpu
+MAX_REL = 2e-3
+
+
+def _ids_w(M, k, E, seed, dup=False, inactive=False):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(M)]).to(torch.int32)
+    if dup and M > 1:
+        ids[1, 0] = ids[0, 0]            # same expert in two tokens
+    w = torch.rand(M, k, generator=g)
+    w = (w / w.sum(1, keepdim=True)).float()
+    if inactive:
+        ids[0, -1] = -1
+    return ids, w
+
+
+def _run(exl3, oracle, tables, orc, x, ids, w, act=0, limit=0.0, shared=-1, out_dtype=torch.float32):
+    out = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables, act, limit, shared, out_dtype=out_dtype)
+    ref = oracle.moe_layer(x.numpy(), orc[:tables.E - (1 if shared >= 0 else 0)], ids.numpy(), w.numpy(), act, limit,
+                           orc[shared] if shared >= 0 else None)
+    return out.float().cpu().numpy(), ref
+
+
+@pytest.fixture(scope="module")
+def small(exl3, oracle):
+    return make_experts(exl3, oracle, 12, 256, 256, 3, 3, 500)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 9])
+def test_moe_small_silu(exl3, oracle, small, M):
+    tables, orc = small
+    ids, w = _ids_w(M, 4, 12, 600 + M, dup=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(M)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_moe_inactive_slots_shared_and_fp16_out(exl3, oracle, small):
+    tables, orc = small
+    ids, w = _ids_w(3, 3, 11, 701, inactive=True)          # experts 0..10 routed, 11 = shared
+    x = torch.randn(3, 256, generator=torch.Generator().manual_seed(5)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=11)
+    assert max_rel(y, ref) <= MAX_REL
+    y16, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=11, out_dtype=torch.float16)
+    assert max_rel(y16, ref) <= MAX_REL
+
+
+def test_moe_gelu_and_clamp(exl3, oracle, small):
+    tables, orc = small
+    ids, w = _ids_w(2, 4, 12, 702)
+    x = (4 * torch.randn(2, 256, generator=torch.Generator().manual_seed(6))).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, act=1)
+    assert max_rel(y, ref) <= MAX_REL
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, act=0, limit=0.5)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_moe_deterministic(exl3, small):
+    tables, _ = small
+    ids, w = _ids_w(4, 4, 12, 703, dup=True)
+    x = torch.randn(4, 256, generator=torch.Generator().manual_seed(7)).half().cuda()
+    a = exl3.moe_forward(x, ids.cuda(), w.cuda(), tables)
+    b = exl3.moe_forward(x, ids.cuda(), w.cuda(), tables)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("Kgu,Kd", [(2, 3), (1, 4), (4, 2), (8, 5)])
+def test_moe_per_projection_k(exl3, oracle, Kgu, Kd):
+    tables, orc = make_experts(exl3, oracle, 6, 384, 256, Kgu, Kd, 800 + 10 * Kgu + Kd)
+    ids, w = _ids_w(2, 3, 6, 801)
+    x = torch.randn(2, 384, generator=torch.Generator().manual_seed(8)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("Ks,probs", [((1, 2), (0.38, 0.62)), ((1, 2, 3, 4, 5, 6, 7, 8), (0.125,) * 8)])
+def test_moe_per_tile_k(exl3, oracle, Ks, probs):
+    tables, orc = make_experts(exl3, oracle, 5, 256, 384, 0, 0, 900, per_tile=(Ks, probs))
+    assert tables.K_gate == 0 and tables.kmaps is not None
+    ids, w = _ids_w(3, 2, 5, 901)
+    x = torch.randn(3, 256, generator=torch.Generator().manual_seed(9)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_moe_c3_full_size(exl3, oracle):
+    """Fine-grained MoE decode layer: H=2048, 512 experts of I=512, K=3, top-10 softmax routing, M = 1, 2, 4."""
+    tables, orc = make_experts(exl3, oracle, 512, 2048, 512, 3, 3, 3000)
+    for M in (1, 2, 4):
+        g = torch.Generator().manual_seed(3100 + M)
+        logits = torch.randn(M, 512, generator=g)
+        x = torch.randn(M, 2048, generator=g).half()
+        ids, w = exl3.route_softmax_topk(logits.cuda(), 10)
+        rid, rw = oracle.route_softmax_topk(logits.numpy(), 10)
+        assert np.array_equal(ids.cpu().numpy(), rid)
+        assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+        y, ref = _run(exl3, oracle, tables, orc, x, ids.cpu(), w.cpu())
+        assert max_rel(y, ref) <= MAX_REL, (M, max_rel(y, ref))
+
+
+def test_align_tables(exl3, oracle):
+    ids, w = _ids_w(9, 4, 16, 1000, dup=True, inactive=True)
+    counts, ptok, pw, pof = exl3.moe_align(ids.cuda(), w.cuda(), 16, shared=-1)
+    counts, ptok, pw, pof = (t.cpu().numpy() for t in (counts, ptok, pw, pof))
+    ref = oracle.align(ids.numpy(), w.numpy(), 16)
+    assert np.array_equal(counts, ref["count"])
+    flat = ids.numpy().reshape(-1)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    for i, e in enumerate(flat):
+        if e < 0:
+            assert pof[i] == -1
+            continue
+        assert starts[e] <= pof[i] < starts[e] + counts[e]      # grouped by expert
+        assert ptok[pof[i]] == i // 4 and pw[pof[i]] == w.numpy().reshape(-1)[i]
+    valid = pof[pof >= 0]
+    assert np.unique(valid).size == valid.size == counts.sum()
+
+
+def test_router_ties_bias_and_sizes(exl3, oracle):
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(7, 160, generator=g)
+    logits[0, [5, 40, 99]] = 3.0                 # exact ties: lower index first
+    bias = -1.1 * torch.log(torch.arange(1, 161).float())[torch.randperm(160, generator=g)]
+    for b in (None, bias):
+        ids, w = exl3.route_softmax_topk(logits.cuda(), 8, None if b is None else b.cuda())
+        rid, rw = oracle.route_softmax_topk(logits.numpy(), 8, None if b is None else b.numpy())
+        assert np.array_equal(ids.cpu().numpy(), rid)
+        assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+
+
+def test_act_mul_ops(exl3, oracle):
+    g = torch.Generator().manual_seed(12)
+    x = (3 * torch.randn(4, 512, generator=g)).half()
+    y = torch.randn(4, 512, generator=g).half()
+    for fn, act, lim in ((exl3.silu_mul, 0, 0.0), (exl3.silu_mul, 0, 1.0), (exl3.gelu_mul, 1, 0.0)):
+        z = torch.empty_like(x, device="cuda")
+        fn(x.cuda(), y.cuda(), z, lim)
+        exact = oracle.act_mul(x.numpy(), y.numpy(), act, lim)
+        ref = exact.astype(np.float16)
+        # within one fp16 ulp of the correctly rounded value (fp32 exp vs the oracle's float64)
+        ulp = np.spacing(np.abs(ref)).astype(np.float64)
+        assert (np.abs(z.cpu().numpy().astype(np.float64) - ref.astype(np.float64)) <= ulp).all()
+
+
+def test_gated_mlp_dense(exl3, oracle):
+    """Dense gated MLP (GELU-tanh) as the shared-expert path, M = 1, 2, 4."""
+    tables, orc = make_experts(exl3, oracle, 1, 512, 1024, 4, 4, 1200)
+    g, u, d = tables.projs[0][0], tables.projs[1][0], tables.projs[2][0]
+    mlp = exl3.BC_GatedMLP(None, None, None, None, None, None, None, 4, False, True, False, True, False, g, u, d, 0.0)
+    for M in (1, 2, 4):
+        x = torch.randn(M, 512, generator=torch.Generator().manual_seed(1300 + M)).half()
+        out = torch.empty(1, M, 512, dtype=torch.float32, device="cuda")
+        mlp.run_bszN(x.cuda().view(1, M, 512), out)
+        ref = oracle.gated_mlp(x.numpy(), *orc[0], oracle.ACT_GELU_TANH)
+        assert max_rel(out.view(M, 512).cpu().numpy(), ref) <= MAX_REL
+
+
+def test_block_sparse_mlp_forward(exl3, oracle, small):
+    tables, orc = small
+    mod = exl3.BlockSparseMLP(tables, 3, has_shared=True)
+    g = torch.Generator().manual_seed(14)
+    logits = torch.randn(1, 2, 11, generator=g)
+    x = torch.randn(1, 2, 256, generator=g).half()
+    out = mod.forward(x.cuda(), {"router_logits": logits.cuda()})
+    assert out.dtype == torch.float32 and tuple(out.shape) == (1, 2, 256)
+    rid, rw = oracle.route_softmax_topk(logits.view(2, 11).numpy(), 3)
+    ref = oracle.moe_layer(x.view(2, 256).numpy(), orc[:11], rid, rw, 0, 0.0, orc[11])
+    assert max_rel(out.view(2, 256).cpu().numpy(), ref) <= MAX_REL
