@@ -24,6 +24,8 @@ SIGNATURES = {
     "exl3_last_error": [],
     "exl3_abi_version": [],
     "exl3_reserve_workspace": [_i64, _i64],
+    "exl3_profile_enable": [_i32],
+    "exl3_profile_read": [ctypes.c_char_p, _i64],
     "exl3_reconstruct": [_vp, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64, _vp],
     "exl3_had_r_128": [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _f32, _vp],
     "exl3_gemm": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp],
@@ -74,6 +76,21 @@ def ptr(t: torch.Tensor | None):
 def stream_of(t: torch.Tensor):
     """The caller's current stream on t's device (launches are asynchronous on it, as in the reference)."""
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def profile_enable(on: bool = True):
+    check(lib().exl3_profile_enable(1 if on else 0), "exl3_profile_enable")
+
+
+def profile_read() -> dict:
+    """{kernel name: (launches, average microseconds)} since the last profile_enable (synchronises)."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    check(lib().exl3_profile_read(buf, len(buf)), "exl3_profile_read")
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, avg = line.rsplit(" ", 2)
+        out[name] = (int(cnt), float(avg))
+    return out
 
 
 def require_device(*ts):

@@ -254,8 +254,7 @@ int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uin
         ga.P = P;
         ga.nblk = nblk;
         gemv_fn fn = gemv_select(K, mm, f32);
-        hipLaunchKernelGGL(fn, dim3(strips, P), dim3(256), 0, st, ga);
-        EXL3_CHECK_HIP(hipGetLastError());
+        EXL3_LAUNCH("gemv", fn, dim3(strips, P), dim3(256), 0, st, ga);
     }
     return EXL3_OK;
 }
@@ -285,17 +284,11 @@ int exl3_reconstruct(const int16_t* trellis, int64_t k, int64_t n_total, int K, 
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(trellis);
     dim3 grid((unsigned)(n_slice / 128), (unsigned)(k / 16));
     const int tn = (int)(n_total / 16), n0t = (int)(n_offset / 16);
-    switch (K) {
-        case 1: hipLaunchKernelGGL(reconstruct_kernel<1>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 2: hipLaunchKernelGGL(reconstruct_kernel<2>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 3: hipLaunchKernelGGL(reconstruct_kernel<3>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 4: hipLaunchKernelGGL(reconstruct_kernel<4>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 5: hipLaunchKernelGGL(reconstruct_kernel<5>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 6: hipLaunchKernelGGL(reconstruct_kernel<6>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        case 7: hipLaunchKernelGGL(reconstruct_kernel<7>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-        default: hipLaunchKernelGGL(reconstruct_kernel<8>, grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld); break;
-    }
-    EXL3_CHECK_HIP(hipGetLastError());
+    typedef void (*rfn)(const uint32_t*, int, int, uint16_t*, int64_t);
+    static const rfn fns[8] = {reconstruct_kernel<1>, reconstruct_kernel<2>, reconstruct_kernel<3>,
+                               reconstruct_kernel<4>, reconstruct_kernel<5>, reconstruct_kernel<6>,
+                               reconstruct_kernel<7>, reconstruct_kernel<8>};
+    EXL3_LAUNCH("reconstruct", fns[K - 1], grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld);
     return EXL3_OK;
 }
 
@@ -311,10 +304,9 @@ int exl3_had_r_128(const void* in, int64_t in_ld, void* out, int64_t out_ld, int
     float r = scale * kRsqrt128;
     hipStream_t st = (hipStream_t)stream;
     if (dtype == EXL3_F16)
-        hipLaunchKernelGGL(had_kernel<true>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
+        EXL3_LAUNCH("had_r_128", had_kernel<true>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
     else
-        hipLaunchKernelGGL(had_kernel<false>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
-    EXL3_CHECK_HIP(hipGetLastError());
+        EXL3_LAUNCH("had_r_128", had_kernel<false>, grid, dim3(64), 0, st, in, in_ld, out, out_ld, pre, post, r);
     return EXL3_OK;
 }
 

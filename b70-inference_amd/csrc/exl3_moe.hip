@@ -398,8 +398,7 @@ static size_t align_lds_bytes(int E) { return (size_t)(4 * E + 1024) * sizeof(in
 
 int launch_align(const RouteArgs& r, hipStream_t st) {
     const size_t lds = align_lds_bytes(r.E);
-    hipLaunchKernelGGL(align_kernel, dim3(1), dim3(1024), lds, st, r);
-    EXL3_CHECK_HIP(hipGetLastError());
+    EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), lds, st, r);
     return EXL3_OK;
 }
 
@@ -513,12 +512,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.pair_of = a.pair_of;
     rc = launch_align(r, st);
     if (rc) return rc;
-    hipLaunchKernelGGL(gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
-    EXL3_CHECK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
-    EXL3_CHECK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(combine_kernel, dim3(a.M, nbH), dim3(64), 0, st, a);
-    EXL3_CHECK_HIP(hipGetLastError());
+    EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
+    EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
+    EXL3_LAUNCH("moe_combine", combine_kernel, dim3(a.M, nbH), dim3(64), 0, st, a);
     return EXL3_OK;
 }
 
@@ -614,12 +610,11 @@ int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype
     const int64_t blocks = (n + 255) / 256;
     EXL3_CHECK_ARG(blocks <= 0x7FFFFFFF, "exl3_act_mul: too large");
     if (dtype == EXL3_F16)
-        hipLaunchKernelGGL(act_mul_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y, z, n,
-                           act, act_limit);
+        EXL3_LAUNCH("act_mul", act_mul_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y,
+                    z, n, act, act_limit);
     else
-        hipLaunchKernelGGL(act_mul_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y, z,
-                           n, act, act_limit);
-    EXL3_CHECK_HIP(hipGetLastError());
+        EXL3_LAUNCH("act_mul", act_mul_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, y,
+                    z, n, act, act_limit);
     return EXL3_OK;
 }
 
@@ -629,9 +624,8 @@ int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t 
     if (M == 0) return EXL3_OK;
     EXL3_CHECK_ARG(logits && ids && w, "exl3_route_softmax_topk: null pointer");
     EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_softmax_topk: too many rows");
-    hipLaunchKernelGGL(route_kernel, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
-                       (int)k, ids, w);
-    EXL3_CHECK_HIP(hipGetLastError());
+    EXL3_LAUNCH("route_softmax_topk", route_kernel, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld,
+                (int)E, bias, (int)k, ids, w);
     return EXL3_OK;
 }
 

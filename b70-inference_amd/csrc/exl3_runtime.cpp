@@ -5,6 +5,9 @@
 #include <stdio.h>
 
 #include <mutex>
+#include <string>
+#include <string.h>
+#include <vector>
 
 namespace exl3 {
 
@@ -59,9 +62,84 @@ int workspace(size_t bytes, size_t ncounters, Workspace* out) {
     return EXL3_OK;
 }
 
+namespace {
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+bool g_prof_on = false;
+std::vector<hipEvent_t> g_pool;
+size_t g_pool_used = 0;
+std::vector<ProfRec> g_recs;
+bool g_prof_overflow = false;
+
+hipEvent_t take_event() {
+    if (g_pool_used == g_pool.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        g_pool.push_back(e);
+    }
+    return g_pool[g_pool_used++];
+}
+}  // namespace
+
+void prof_start(const char* name, hipStream_t s) {
+    if (!g_prof_on) return;
+    if (g_recs.size() >= 100000) {
+        g_prof_overflow = true;
+        return;
+    }
+    ProfRec r{name, take_event(), take_event()};
+    if (!r.a || !r.b) return;
+    hipEventRecord(r.a, s);
+    g_recs.push_back(r);
+}
+
+void prof_stop(hipStream_t s) {
+    if (!g_prof_on || g_recs.empty() || g_prof_overflow) return;
+    hipEventRecord(g_recs.back().b, s);
+}
+
 }  // namespace exl3
 
 extern "C" {
+
+int exl3_profile_enable(int on) {
+    exl3::g_prof_on = on != 0;
+    exl3::g_recs.clear();
+    exl3::g_pool_used = 0;
+    exl3::g_prof_overflow = false;
+    return EXL3_OK;
+}
+
+int exl3_profile_read(char* out, int64_t cap) {
+    using namespace exl3;
+    std::vector<std::pair<std::string, std::pair<double, long>>> agg;
+    for (const ProfRec& r : g_recs) {
+        EXL3_CHECK_HIP(hipEventSynchronize(r.b));
+        float ms = 0.f;
+        EXL3_CHECK_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+        size_t i = 0;
+        while (i < agg.size() && agg[i].first != r.name) ++i;
+        if (i == agg.size()) agg.push_back({r.name, {0.0, 0}});
+        agg[i].second.first += ms * 1000.0;
+        agg[i].second.second += 1;
+    }
+    std::string txt;
+    char line[256];
+    for (auto& a : agg) {
+        snprintf(line, sizeof(line), "%s %ld %.4f\n", a.first.c_str(), a.second.second,
+                 a.second.first / (double)a.second.second);
+        txt += line;
+    }
+    if (cap > 0 && out) {
+        size_t n = txt.size() < (size_t)cap - 1 ? txt.size() : (size_t)cap - 1;
+        memcpy(out, txt.data(), n);
+        out[n] = 0;
+    }
+    return (int64_t)txt.size() < cap ? EXL3_OK : fail(EXL3_ERR_INVALID, "exl3_profile_read: buffer too small");
+}
+
 
 const char* exl3_last_error(void) { return exl3::g_err; }
 

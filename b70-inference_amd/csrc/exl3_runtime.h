@@ -51,4 +51,17 @@ inline size_t carve_size(size_t n, size_t elem) { return (n * elem + 255) & ~(si
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Opt-in kernel timing (exl3_profile_enable): a HIP event pair on the launch stream around every library launch,
+// aggregated per kernel name by exl3_profile_read. Off by default; never used under graph capture.
+void prof_start(const char* name, hipStream_t s);
+void prof_stop(hipStream_t s);
+
+#define EXL3_LAUNCH(name, kernel, grid, block, lds, stream, ...)                   \
+    do {                                                                         \
+        ::exl3::prof_start(name, stream);                                        \
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);       \
+        ::exl3::prof_stop(stream);                                               \
+        EXL3_CHECK_HIP(hipGetLastError());                                       \
+    } while (0)
+
 }  // namespace exl3

@@ -40,6 +40,12 @@ int exl3_abi_version(void);
  * e.g. before HIP graph capture. No reference counterpart (the reference grows its scratch inside the op). */
 int exl3_reserve_workspace(int64_t bytes, int64_t ncounters);
 
+/* Kernel timing: while enabled, every kernel the library launches is bracketed by a HIP event pair on its stream.
+ * exl3_profile_read writes "name count avg_us" lines (one per kernel) for the launches since the last enable.
+ * Not for use under graph capture. No reference counterpart (the reference times with torch.profiler). */
+int exl3_profile_enable(int on);
+int exl3_profile_read(char* out, int64_t cap);
+
 /* Decoded Hadamard-domain weight slice: out[r, c] = W_hat[r, n_offset + c] (fp16 bits, row stride out_ld elements),
  * no sign vectors applied. Bit-exact with the reference decode.
  * Replaces: exllamav3 ext reconstruct / reconstruct_slice (ext-op-inventory.md:597-612) and
