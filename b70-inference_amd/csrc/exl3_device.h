@@ -114,6 +114,41 @@ __device__ __forceinline__ void fwht128_wave(float& a, float& b, int lane) {
     }
 }
 
+// ------------------------------------------------------------------------------------------------ wave reductions
+// DPP reductions over the 64 lanes of a wave (gfx9 row_bcast form): xor 1 and xor 2 inside quads, mirrors inside
+// half-rows and rows, then row_bcast15 / row_bcast31 across rows; lane 63 ends with the result, read back uniformly.
+#define EXL3_DPP(v, ctrl, rmask) \
+    (uint32_t) __builtin_amdgcn_update_dpp((int)ident, (int)(v), ctrl, rmask, 0xF, false)
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    const uint32_t ident = 0u;
+    v = max(v, EXL3_DPP(v, 0xB1, 0xF));    // quad_perm [1,0,3,2]
+    v = max(v, EXL3_DPP(v, 0x4E, 0xF));    // quad_perm [2,3,0,1]
+    v = max(v, EXL3_DPP(v, 0x141, 0xF));   // row_half_mirror
+    v = max(v, EXL3_DPP(v, 0x140, 0xF));   // row_mirror
+    v = max(v, EXL3_DPP(v, 0x142, 0xA));   // row_bcast:15 into rows 1, 3
+    v = max(v, EXL3_DPP(v, 0x143, 0xC));   // row_bcast:31 into rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    const uint32_t ident = 0xFFFFFFFFu;
+    v = min(v, EXL3_DPP(v, 0xB1, 0xF));
+    v = min(v, EXL3_DPP(v, 0x4E, 0xF));
+    v = min(v, EXL3_DPP(v, 0x141, 0xF));
+    v = min(v, EXL3_DPP(v, 0x140, 0xF));
+    v = min(v, EXL3_DPP(v, 0x142, 0xA));
+    v = min(v, EXL3_DPP(v, 0x143, 0xC));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+#undef EXL3_DPP
+
+// Order-preserving map of a float to uint32 (larger float -> larger key; NaN payloads sort above +inf).
+__device__ __forceinline__ uint32_t float_key(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 __device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
 __device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, (_Float16)v); }
 

@@ -11,7 +11,7 @@
 namespace exl3 {
 
 constexpr int kGemvKBMax = 8;        // Hadamard blocks (128 k) per workgroup split
-constexpr int kGemvTargetWG = 1024;  // workgroups a dense GEMV launch aims for (256 CUs x 4)
+constexpr int kGemvTargetWG = 1024;  // workgroups a GEMV launch aims for (256 CUs x 4); EXL3MI_TARGET_WG overrides
 constexpr int kGemvMaxRows = 8;      // rows per GEMV pass
 
 // acc[m][h] += sum over tile-rows lt = lt0, lt0 + step, ... < nt of sum_r xs[m * xs_ld + 16 lt + r] * h(16 lt + r, col)
@@ -48,16 +48,27 @@ __device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __r
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
 }
 
+// Issue the first two tile-rows' loads of a strip (so their latency overlaps whatever the caller does next).
+template <int K>
+__device__ __forceinline__ void strip_prefetch(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
+                                               int lane, uint32_t (&A)[K], uint32_t (&B)[K]) {
+    if (lt0 >= nt) return;
+    const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
+    const int n = (nt - lt0 + step - 1) / step;
+    strip_load<K>(A, base, rs * step, 0, n);
+    strip_load<K>(B, base, rs * step, 1, n);
+}
+
+// The strip loop proper, starting from strip_prefetch's A (tile-row lt0) and B (lt0 + step).
 template <int K, int M>
-__device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
-                                           int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2]) {
+__device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
+                                               int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2],
+                                               uint32_t (&A)[K], uint32_t (&B)[K]) {
     if (lt0 >= nt) return;
     const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const size_t rstep = rs * step;
-    uint32_t A[K], B[K], C[K];
-    strip_load<K>(A, base, rstep, 0, n);
-    strip_load<K>(B, base, rstep, 1, n);
+    uint32_t C[K];
     int i = 0;
     for (; i + 3 <= n; i += 3) {                         // branch-free body: loads stay two tile-rows ahead
         strip_load<K>(C, base, rstep, i + 2, n);
@@ -69,6 +80,14 @@ __device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size
     }
     if (i < n) strip_tile_row<K, M>(A, lane, xs + (lt0 + i * step) * 16, xs_ld, acc);
     if (i + 1 < n) strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
+}
+
+template <int K, int M>
+__device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
+                                           int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2]) {
+    uint32_t A[K], B[K];
+    strip_prefetch<K>(sp, rs, lt0, nt, step, lane, A, B);
+    strip_gemv_run<K, M>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, A, B);
 }
 
 // Per-tile K (mixed bitrate): tile i of the projection (row-major over [k/16, n/16]) holds 8 * kmap[i] words at

@@ -121,6 +121,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int strip = blockIdx.x, p = blockIdx.y;
     const int b0 = (int)((int64_t)p * a.nblk / a.P), b1 = (int)((int64_t)(p + 1) * a.nblk / a.P);
     const int kb = b1 - b0;
+    const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
+    const uint32_t* sp = a.tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
+    uint32_t A[K], B[K];
+    strip_prefetch<K>(sp, rs, wave, kb * 8, 4, lane, A, B);          // weight loads in flight during phase 1
 
     // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums
     for (int i = wave; i < M * kb; i += 4) {
@@ -135,9 +139,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     float acc[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.f;
-    const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
-    const uint32_t* sp = a.tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
-    strip_gemv<K, M>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc);
+    strip_gemv_run<K, M>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, A, B);
 
     // phase 3: reduce waves, then splits
 #pragma unroll
@@ -163,6 +165,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if (!splitk_arrive(&a.cnt[strip], a.P, &s_last)) return;
     for (int m = wave; m < M && m < a.m; m += 4) {
         float va = 0.f, vb = 0.f;
+#pragma unroll 8
         for (int pp = 0; pp < a.P; ++pp) {
             const float* q = a.part + (((size_t)strip * a.P + pp) * M + m) * 128;
             va += splitk_load(q + lane);
@@ -222,7 +225,8 @@ static gemv_fn gemv_select(int K, int M, bool f32) {
 
 // Number of k-splits: enough workgroups to cover the chip, at most kGemvKBMax Hadamard blocks per split.
 static int gemv_splits(int strips, int nblk) {
-    int P = (kGemvTargetWG + strips - 1) / strips;
+    const int target = env_int("EXL3MI_TARGET_WG", kGemvTargetWG);
+    int P = (target + strips - 1) / strips;
     int pmin = (nblk + kGemvKBMax - 1) / kGemvKBMax;
     if (P < pmin) P = pmin;
     if (P > nblk) P = nblk;

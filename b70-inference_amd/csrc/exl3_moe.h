@@ -7,18 +7,34 @@ namespace exl3 {
 
 constexpr int kMoeMaxExperts = 3072;   // expert tables per layer (routed + shared); the align kernel keeps 4 ints each in LDS
 
+// One work unit of the GEMV kernels: up to 8 rows (pairs) of one expert, with everything a workgroup needs so that a
+// single uniform load replaces the table lookups. Items past the last real one have cnt == 0.
+struct alignas(256) ItemDesc {
+    int32_t e, p0, cnt, pad;
+    int32_t tok[8];                    // token of each row
+    float w[8];                        // routing weight of each row (1 for the shared expert)
+    int64_t tab[9];                    // the expert's (trellis, suh, svh) addresses for gate, up, down
+    int64_t km[6];                     // (kmap, woff) addresses for gate, up, down when K is per tile
+};
+static_assert(sizeof(ItemDesc) == 256, "item descriptor layout");
+
 struct RouteArgs {
     const int32_t* ids;
     const float* tw;
     int M, topk, slots, E, shared, MR;
     int* counts;                       // optional [E]
     int* n_items;                      // optional: items of <= MR rows
-    int* item_e;
-    int* item_p0;
-    int* item_cnt;
+    ItemDesc* items;                   // optional [max_items]
+    int max_items;
+    const int64_t* tables;             // [9][E] (read when items are built)
+    const int64_t* kmaps;              // [6][E] or null
     int* pair_tok;
     float* pair_w;
     int* pair_of;
+    int* tok_nvalid;                   // optional [M]: valid slots per token; tokens with none get a zero output row
+    void* out;
+    int64_t out_ld;
+    int out_f32, H;
 };
 
 struct MoeArgs {
@@ -36,12 +52,12 @@ struct MoeArgs {
     int MR, max_items;
     // routing (workspace)
     int* n_items;
-    int* item_e;
-    int* item_p0;
-    int* item_cnt;
+    const ItemDesc* items;
     int* pair_tok;
     float* pair_w;
     int* pair_of;
+    int* tok_nvalid;                   // [M] valid slots per token
+    int* cnt_tok;                      // [M][H/128] combine arrival counters
     // intermediates (workspace)
     uint16_t* abuf;                    // [pairs][I] fp16, Hadamard-domain down input
     float* y;                          // [pairs][H] fp32, weighted expert outputs

@@ -75,24 +75,51 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     for (int e = t; e < r.E; e += T) {
         const int c = cnt[e];
         if (r.counts) r.counts[e] = c;
+        if (!r.items) continue;
         for (int q = 0, it = nch[e]; q * r.MR < c; ++q, ++it) {
-            if (r.item_e) {
-                r.item_e[it] = e;
-                r.item_p0[it] = start[e] + q * r.MR;
-                r.item_cnt[it] = min(r.MR, c - q * r.MR);
+            ItemDesc& d = r.items[it];
+            d.e = e;
+            d.p0 = start[e] + q * r.MR;
+            d.cnt = min(r.MR, c - q * r.MR);
+            for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
+            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
+        }
+    }
+    if (r.items)
+        for (int it = nitems + t; it < r.max_items; it += T) r.items[it].cnt = 0;
+    if (t == 0 && r.n_items) r.n_items[0] = nitems;
+    if (r.tok_nvalid) {
+        for (int tok = t; tok < r.M; tok += T) {
+            int nv = 0;
+            for (int j = 0; j < r.slots; ++j) {
+                const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
+                nv += (e >= 0 && e < r.E);
+            }
+            r.tok_nvalid[tok] = nv;
+            if (nv == 0) {
+                for (int c = 0; c < r.H; ++c) {
+                    if (r.out_f32) reinterpret_cast<float*>(r.out)[(int64_t)tok * r.out_ld + c] = 0.f;
+                    else reinterpret_cast<uint16_t*>(r.out)[(int64_t)tok * r.out_ld + c] = 0;
+                }
             }
         }
     }
-    if (t == 0 && r.n_items) r.n_items[0] = nitems;
     __syncthreads();
     for (int i = t; i < np; i += T) {
         const int tok = i / r.slots, j = i - tok * r.slots;
         const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
         if (e >= 0 && e < r.E) {
-            const int pos = start[e] + atomicAdd(&fill[e], 1);
+            const int f = atomicAdd(&fill[e], 1);
+            const int pos = start[e] + f;
+            const float wt = j < r.topk ? r.tw[tok * r.topk + j] : 1.0f;
             r.pair_tok[pos] = tok;
-            r.pair_w[pos] = j < r.topk ? r.tw[tok * r.topk + j] : 1.0f;
+            r.pair_w[pos] = wt;
             r.pair_of[i] = pos;
+            if (r.items) {
+                ItemDesc& d = r.items[nch[e] + f / r.MR];
+                d.tok[f % r.MR] = tok;
+                d.w[f % r.MR] = wt;
+            }
         } else {
             r.pair_of[i] = -1;
         }
@@ -124,37 +151,41 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nbI = a.I / 128;
     const int item = blockIdx.x / nbI, nb = blockIdx.x - item * nbI, p = blockIdx.y;
-    if (item >= a.n_items[0]) return;
-    const int e = a.item_e[item], p0 = a.item_p0[item], cnt = a.item_cnt[item];
-    const int64_t E = a.E;
+    const ItemDesc* d = a.items + item;
+    const int cnt = d->cnt;
+    if (cnt == 0) return;
+    const int p0 = d->p0;
     const int b0 = (int)((int64_t)p * a.nblk_h / a.P_gu), b1 = (int)((int64_t)(p + 1) * a.nblk_h / a.P_gu);
     const int kb = b1 - b0;
+    const int proj = wave >> 1, half = wave & 1;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(d->tab[3 * proj]);
+    const int tn = a.I / 16;
+    constexpr int KL = K > 0 ? K : 1;
+    const size_t rs = (size_t)tn * (8 * KL);
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    uint32_t PA[KL], PB[KL];
+    if (K > 0) strip_prefetch<KL>(sp, rs, half, kb * 8, 2, lane, PA, PB);
 
     // phase 1: both projections' input transforms for the item's rows
     for (int i = wave; i < 2 * MR * kb; i += 4) {
         const int proj = i / (MR * kb), rem = i - proj * MR * kb, m = rem / kb, b = rem - m * kb;
         const int k0 = (b0 + b) * 128;
-        const uint16_t* suh = reinterpret_cast<const uint16_t*>(a.tables[(3 * proj + 1) * E + e]);
-        const uint16_t* xr = m < cnt ? a.x + (int64_t)a.pair_tok[p0 + m] * a.x_ld + k0 : nullptr;
+        const uint16_t* suh = reinterpret_cast<const uint16_t*>(d->tab[3 * proj + 1]);
+        const uint16_t* xr = m < cnt ? a.x + (int64_t)d->tok[m] * a.x_ld + k0 : nullptr;
         float s = had_in_block(xr, suh + k0, &xs[proj][m][b * 128], lane);
         if (lane == 0) bsum[proj][m][b] = s;
     }
     __syncthreads();
 
     // phase 2: waves 0, 1 stream the gate strip, waves 2, 3 the up strip (alternating tile-rows)
-    const int proj = wave >> 1, half = wave & 1;
     float acc[MR][2];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
-    const uint32_t* tr = reinterpret_cast<const uint32_t*>(a.tables[(3 * proj) * E + e]);
-    const int tn = a.I / 16;
     if (K > 0) {
-        const size_t rs = (size_t)tn * (8 * K);
-        strip_gemv<(K > 0 ? K : 1), MR>(tr + (size_t)nb * (64 * K) + (size_t)b0 * 8 * rs, rs, half, kb * 8, 2, lane,
-                                        &xs[proj][0][0], kGemvKBMax * 128, acc);
+        strip_gemv_run<KL, MR>(sp, rs, half, kb * 8, 2, lane, &xs[proj][0][0], kGemvKBMax * 128, acc, PA, PB);
     } else {
-        const uint8_t* km = reinterpret_cast<const uint8_t*>(a.kmaps[(2 * proj) * E + e]);
-        const int32_t* wo = reinterpret_cast<const int32_t*>(a.kmaps[(2 * proj + 1) * E + e]);
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[2 * proj]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[2 * proj + 1]);
         strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &xs[proj][0][0],
                              kGemvKBMax * 128, acc);
     }
@@ -184,11 +215,12 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     if (!splitk_arrive(&a.cnt_gu[slot], a.P_gu, &s_last)) return;
 
     // epilogue (last workgroup of this item / column block)
-    const uint16_t* svg = reinterpret_cast<const uint16_t*>(a.tables[2 * E + e]) + nb * 128;
-    const uint16_t* svu = reinterpret_cast<const uint16_t*>(a.tables[5 * E + e]) + nb * 128;
-    const uint16_t* sud = reinterpret_cast<const uint16_t*>(a.tables[7 * E + e]) + nb * 128;
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(d->tab[2]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(d->tab[5]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(d->tab[7]) + nb * 128;
     for (int m = wave; m < cnt; m += 4) {
         float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+#pragma unroll 4
         for (int pp = 0; pp < a.P_gu; ++pp) {
             const float* q = a.part_gu + ((slot * a.P_gu + pp) * 2) * MR * 128 + m * 128;
             g0 += splitk_load(q + lane);
@@ -214,21 +246,33 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     if (threadIdx.x == 0) a.cnt_gu[slot] = 0;
 }
 
-// ================================================================================================ down
+// ================================================================================================ down (+ combine)
+// The last workgroup of an (item, column block) writes its rows' weighted outputs y, then counts them in per-(token,
+// column block) arrival counters; the workgroup that completes a token's slots sums them in slot order into `out`
+// (the reference's CombineKernel, fused: no separate launch).
 template <int K, int MR>
 __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[MR][kGemvKBMax * 128];
     __shared__ float red[4][MR][2][64];
     __shared__ float bsum[MR][kGemvKBMax];
     __shared__ int s_last;
+    __shared__ int s_comb[MR];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nbH = a.H / 128;
     const int item = blockIdx.x / nbH, nb = blockIdx.x - item * nbH, p = blockIdx.y;
-    if (item >= a.n_items[0]) return;
-    const int e = a.item_e[item], p0 = a.item_p0[item], cnt = a.item_cnt[item];
-    const int64_t E = a.E;
+    const ItemDesc* d = a.items + item;
+    const int cnt = d->cnt;
+    if (cnt == 0) return;
+    const int p0 = d->p0;
     const int b0 = (int)((int64_t)p * a.nblk_i / a.P_d), b1 = (int)((int64_t)(p + 1) * a.nblk_i / a.P_d);
     const int kb = b1 - b0;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(d->tab[6]);
+    const int tn = a.H / 16;
+    constexpr int KL = K > 0 ? K : 1;
+    const size_t rs = (size_t)tn * (8 * KL);
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    uint32_t PA[KL], PB[KL];
+    if (K > 0) strip_prefetch<KL>(sp, rs, wave, kb * 8, 4, lane, PA, PB);
 
     for (int i = wave; i < MR * kb; i += 4) {
         const int m = i / kb, b = i - m * kb;
@@ -241,15 +285,11 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     float acc[MR][2];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
-    const uint32_t* tr = reinterpret_cast<const uint32_t*>(a.tables[6 * E + e]);
-    const int tn = a.H / 16;
     if (K > 0) {
-        const size_t rs = (size_t)tn * (8 * K);
-        strip_gemv<(K > 0 ? K : 1), MR>(tr + (size_t)nb * (64 * K) + (size_t)b0 * 8 * rs, rs, wave, kb * 8, 4, lane,
-                                        &xs[0][0], kGemvKBMax * 128, acc);
+        strip_gemv_run<KL, MR>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, PA, PB);
     } else {
-        const uint8_t* km = reinterpret_cast<const uint8_t*>(a.kmaps[4 * E + e]);
-        const int32_t* wo = reinterpret_cast<const int32_t*>(a.kmaps[5 * E + e]);
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[4]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[5]);
         strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128,
                              acc);
     }
@@ -277,94 +317,109 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     }
     if (!splitk_arrive(&a.cnt_d[slot], a.P_d, &s_last)) return;
 
-    const uint16_t* svd = reinterpret_cast<const uint16_t*>(a.tables[8 * E + e]) + nb * 128;
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(d->tab[8]) + nb * 128;
     for (int m = wave; m < cnt; m += 4) {
         float v0 = 0.f, v1 = 0.f;
+#pragma unroll 4
         for (int pp = 0; pp < a.P_d; ++pp) {
             const float* q = a.part_d + ((slot * a.P_d + pp) * MR + m) * 128;
             v0 += splitk_load(q + lane);
             v1 += splitk_load(q + lane + 64);
         }
         fwht128_wave(v0, v1, lane);
-        const float w = a.pair_w[p0 + m];
+        const float w = d->w[m];
         float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 128;
-        dst[lane] = v0 * kRsqrt128 * h2f(svd[lane]) * w;
-        dst[lane + 64] = v1 * kRsqrt128 * h2f(svd[lane + 64]) * w;
+        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(svd[lane]) * w);
+        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(svd[lane + 64]) * w);
     }
     if (threadIdx.x == 0) a.cnt_d[slot] = 0;
-}
 
-// ================================================================================================ combine
-__global__ __launch_bounds__(64) void combine_kernel(MoeArgs a) {
-    const int lane = threadIdx.x;
-    const int t = blockIdx.x, nb = blockIdx.y;
-    const int c0 = nb * 128 + lane, c1 = c0 + 64;
-    float v0 = 0.f, v1 = 0.f;
-    for (int j = 0; j < a.slots; ++j) {
-        const int pr = a.pair_of[t * a.slots + j];
-        if (pr < 0) continue;
-        const float* y = a.y + (size_t)pr * a.H;
-        v0 += y[c0];
-        v1 += y[c1];
+    // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int m = 0; m < cnt; ++m) {
+            const int t = d->tok[m];
+            const int old = __hip_atomic_fetch_add(&a.cnt_tok[(size_t)t * nbH + nb], 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            s_comb[m] = (old == a.tok_nvalid[t] - 1) ? t : -1;
+        }
     }
-    if (a.out_f32) {
-        float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
-        o[c0] = v0;
-        o[c1] = v1;
-    } else {
-        uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
-        o[c0] = f2h(v0);
-        o[c1] = f2h(v1);
+    __syncthreads();
+    for (int m = wave; m < cnt; m += 4) {
+        const int t = s_comb[m];
+        if (t < 0) continue;
+        const int c0 = nb * 128 + lane, c1 = c0 + 64;
+        float v0 = 0.f, v1 = 0.f;
+        for (int j = 0; j < a.slots; ++j) {
+            const int pr = a.pair_of[t * a.slots + j];
+            if (pr < 0) continue;
+            const float* y = a.y + (size_t)pr * a.H;
+            v0 += splitk_load(y + c0);
+            v1 += splitk_load(y + c1);
+        }
+        if (a.out_f32) {
+            float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
+            o[c0] = v0;
+            o[c1] = v1;
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
+            o[c0] = f2h(v0);
+            o[c1] = f2h(v1);
+        }
+        if (lane == 0) a.cnt_tok[(size_t)t * nbH + nb] = 0;
     }
 }
 
 // ================================================================================================ router
-// One wave per row: softmax statistics over E logits (+ bias), then k rounds of a wave argmax over the key z.
+// One wave per row. The row's keys z = logits + bias sit in LDS; softmax statistics over them, then k rounds of a
+// DPP wave argmax: the largest key (order-preserving uint map) and, among lanes holding it, the lowest expert index.
+// A picked key is overwritten with NaN, which never compares greater or equal, so it is not picked again.
 __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, int64_t ld, int E,
                                                    const float* __restrict__ bias, int k, int32_t* __restrict__ ids,
                                                    float* __restrict__ w) {
+    extern __shared__ float zs[];
     const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
     const float* z = logits + row * ld;
     float mx = -INFINITY;
-    for (int i = lane; i < E; i += 64) mx = fmaxf(mx, z[i] + (bias ? bias[i] : 0.f));
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    for (int i = lane; i < E; i += 64) {
+        const float v = z[i] + (bias ? bias[i] : 0.f);
+        zs[i] = v;
+        mx = fmaxf(mx, v);
+    }
+    const uint32_t mk = wave_max_u32(float_key(mx));
+    mx = __builtin_bit_cast(float, (mk & 0x80000000u) ? (mk & 0x7FFFFFFFu) : ~mk);
     float sum = 0.f;
-    for (int i = lane; i < E; i += 64) sum += expf(z[i] + (bias ? bias[i] : 0.f) - mx);
+    for (int i = lane; i < E; i += 64) sum += expf(zs[i] - mx);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
-    // k rounds of a wave argmax over the key z (ties to the lower index); picks are kept in LDS
-    __shared__ int s_taken[32];
+    __syncthreads();
     float ptaken = 0.f;
     int taken = -1;
     for (int j = 0; j < k; ++j) {
         float best = -INFINITY;
         int bi = 0x7FFFFFFF;
         for (int i = lane; i < E; i += 64) {
-            bool used = false;
-            for (int q = 0; q < j; ++q) used |= (s_taken[q] == i);
-            if (used) continue;
-            const float v = z[i] + (bias ? bias[i] : 0.f);
-            if (v > best || (v == best && i < bi)) {
+            const float v = zs[i];
+            if (v > best) {                      // ascending i: a tie keeps the lower index
                 best = v;
                 bi = i;
             }
         }
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ob = __shfl_xor(best, m);
-            const int oi = __shfl_xor(bi, m);
-            if (ob > best || (ob == best && oi < bi)) {
-                best = ob;
-                bi = oi;
+        if (bi == 0x7FFFFFFF) best = -INFINITY;
+        const uint32_t kmax = wave_max_u32(bi == 0x7FFFFFFF ? 0u : float_key(best));
+        const uint32_t cand = (bi != 0x7FFFFFFF && float_key(best) == kmax) ? (uint32_t)bi : 0xFFFFFFFFu;
+        const int win = (int)wave_min_u32(cand);
+        if (win >= 0 && win < E) {
+            const float vb = zs[win];
+            if (lane == j) {
+                taken = win;
+                ptaken = expf(vb - mx) / sum;
             }
         }
-        if (lane == j) {
-            taken = bi;
-            ptaken = expf(best - mx) / sum;
-        }
-        if (lane == 0) s_taken[j] = bi;
+        __syncthreads();
+        if (lane == 0 && win >= 0 && win < E) zs[win] = __builtin_nanf("");
         __syncthreads();
     }
     float s = lane < k ? ptaken : 0.f;
@@ -403,7 +458,8 @@ int launch_align(const RouteArgs& r, hipStream_t st) {
 }
 
 static int moe_splits(int units, int nblk) {
-    int P = (kGemvTargetWG + units - 1) / (units > 0 ? units : 1);
+    const int target = env_int("EXL3MI_TARGET_WG", kGemvTargetWG);
+    int P = (target + units - 1) / (units > 0 ? units : 1);
     int pmin = (nblk + kGemvKBMax - 1) / kGemvKBMax;
     if (P < pmin) P = pmin;
     if (P > nblk) P = nblk;
@@ -471,21 +527,22 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     const int MR = a.MR;
     Workspace ws;
     const size_t n_gu = (size_t)max_items * nbI, n_d = (size_t)max_items * nbH;
-    size_t bytes = carve_size((size_t)4 * max_items + 1, 4) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
+    size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
+                   carve_size(a.M, 4) +
                    carve_size(npairs * a.I, 2) + carve_size(npairs * a.H, 4) +
                    carve_size(n_gu * a.P_gu * 2 * MR * 128, 4) + carve_size(n_d * a.P_d * MR * 128, 4);
-    int rc = workspace(bytes, n_gu + n_d, &ws);
+    const size_t n_tok = (size_t)a.M * nbH;
+    int rc = workspace(bytes, n_gu + n_d + n_tok, &ws);
     if (rc) return rc;
     Carve c{ws.scratch, ws.scratch_bytes};
-    int* ib = c.take<int>((size_t)4 * max_items + 1);
-    a.n_items = ib;
-    a.item_e = ib + 1;
-    a.item_p0 = ib + 1 + max_items;
-    a.item_cnt = ib + 1 + 2 * max_items;
+    a.n_items = c.take<int>(1);
+    ItemDesc* items = c.take<ItemDesc>(max_items);
+    a.items = items;
     int* pb = c.take<int>(npairs * 2);
     a.pair_tok = pb;
     a.pair_of = pb + npairs;
     a.pair_w = c.take<float>(npairs);
+    a.tok_nvalid = c.take<int>(a.M);
     a.abuf = c.take<uint16_t>(npairs * a.I);
     a.y = c.take<float>(npairs * a.H);
     a.part_gu = c.take<float>(n_gu * a.P_gu * 2 * MR * 128);
@@ -493,6 +550,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     if (!a.part_d) return fail(EXL3_ERR_INVALID, "moe: workspace carve failed");
     a.cnt_gu = ws.counters;
     a.cnt_d = ws.counters + n_gu;
+    a.cnt_tok = ws.counters + n_gu + n_d;
 
     RouteArgs r{};
     r.ids = a.ids;
@@ -504,17 +562,22 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.shared = a.shared;
     r.MR = MR;
     r.n_items = a.n_items;
-    r.item_e = a.item_e;
-    r.item_p0 = a.item_p0;
-    r.item_cnt = a.item_cnt;
+    r.items = items;
+    r.max_items = max_items;
+    r.tables = a.tables;
+    r.kmaps = a.kmaps;
     r.pair_tok = a.pair_tok;
     r.pair_w = a.pair_w;
     r.pair_of = a.pair_of;
+    r.tok_nvalid = a.tok_nvalid;
+    r.out = a.out;
+    r.out_ld = a.out_ld;
+    r.out_f32 = a.out_f32;
+    r.H = a.H;
     rc = launch_align(r, st);
     if (rc) return rc;
     EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
     EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
-    EXL3_LAUNCH("moe_combine", combine_kernel, dim3(a.M, nbH), dim3(64), 0, st, a);
     return EXL3_OK;
 }
 
@@ -620,12 +683,13 @@ int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype
 
 int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
                             int32_t* ids, float* w, void* stream) {
-    EXL3_CHECK_ARG(M >= 0 && E > 0 && k > 0 && k <= 32 && k <= E && ld >= E, "exl3_route_softmax_topk: bad sizes");
+    EXL3_CHECK_ARG(M >= 0 && E > 0 && E <= 8192 && k > 0 && k <= 32 && k <= E && ld >= E,
+                   "exl3_route_softmax_topk: bad sizes");
     if (M == 0) return EXL3_OK;
     EXL3_CHECK_ARG(logits && ids && w, "exl3_route_softmax_topk: null pointer");
     EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_softmax_topk: too many rows");
-    EXL3_LAUNCH("route_softmax_topk", route_kernel, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld,
-                (int)E, bias, (int)k, ids, w);
+    EXL3_LAUNCH("route_softmax_topk", route_kernel, dim3((unsigned)M), dim3(64), (size_t)E * sizeof(float),
+                (hipStream_t)stream, logits, ld, (int)E, bias, (int)k, ids, w);
     return EXL3_OK;
 }
 

@@ -2,6 +2,7 @@
 #include "exl3_runtime.h"
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 
 #include <mutex>
@@ -60,6 +61,13 @@ int workspace(size_t bytes, size_t ncounters, Workspace* out) {
     }
     *out = w;
     return EXL3_OK;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    long x = strtol(v, nullptr, 10);
+    return x > 0 && x < (1L << 30) ? (int)x : dflt;
 }
 
 namespace {

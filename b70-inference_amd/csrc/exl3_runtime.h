@@ -33,6 +33,9 @@ struct Workspace {
 };
 int workspace(size_t bytes, size_t ncounters, Workspace* out);
 
+// Integer tuning knob from the environment (read once per name), `dflt` when unset or not a positive number.
+int env_int(const char* name, int dflt);
+
 // Bump allocator over one workspace request.
 struct Carve {
     char* p;

@@ -112,7 +112,7 @@ int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int64_t M, int6
 
 /* Softmax router: p = softmax(logits + bias) over E experts, top-k by p (ties to the lower index, descending),
  * weights renormalised over the k picks with +1e-20. logits fp32 [M, E] (row stride ld), bias fp32 [E] or NULL;
- * ids int32 [M, k], w fp32 [M, k]. k <= 32.
+ * ids int32 [M, k], w fp32 [M, k]. k <= 32, E <= 8192.
  * Replaces: the fused softmax/top-k router of trellis-serve (trellis-serve.patch:395-441). */
 int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
                             int32_t* ids, float* w, void* stream);

@@ -175,3 +175,17 @@ def test_block_sparse_mlp_forward(exl3, oracle, small):
     rid, rw = oracle.route_softmax_topk(logits.view(2, 11).numpy(), 3)
     ref = oracle.moe_layer(x.view(2, 256).numpy(), orc[:11], rid, rw, 0, 0.0, orc[11])
     assert max_rel(out.view(2, 256).cpu().numpy(), ref) <= MAX_REL
+
+
+def test_moe_token_without_active_slots(exl3, oracle, small):
+    """A token whose slots are all inactive gets a zero row (and its neighbours are unaffected)."""
+    tables, orc = small
+    ids, w = _ids_w(3, 3, 12, 1400)
+    ids[1, :] = -1
+    x = torch.randn(3, 256, generator=torch.Generator().manual_seed(15)).half()
+    out = torch.full((3, 256), 7.0, device="cuda")
+    exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables, out=out)
+    ref = oracle.moe_layer(x.numpy(), orc, ids.numpy(), w.numpy(), 0)
+    got = out.cpu().numpy()
+    assert (got[1] == 0).all()
+    assert max_rel(got, ref) <= MAX_REL
