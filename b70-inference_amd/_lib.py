@@ -78,8 +78,9 @@ def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def profile_enable(on: bool = True):
-    check(lib().exl3_profile_enable(1 if on else 0), "exl3_profile_enable")
+def profile_enable(on: bool = True, repeat: int = 1):
+    """Event-time every library launch on its stream; repeat > 1 runs each launch that many times per event pair."""
+    check(lib().exl3_profile_enable(max(1, int(repeat)) if on else 0), "exl3_profile_enable")
 
 
 def profile_read() -> dict:

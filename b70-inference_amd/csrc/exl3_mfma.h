@@ -1,0 +1,77 @@
+// Trellis decode straight into v_mfma_f32_16x16x32_f16 B fragments.
+//
+// Fragment layout (checked on gfx950): B[k][n] of a 32 x 16 block, lane L holds n = L & 15 and
+// k = 8 (L >> 4) + j for j = 0..7 as four packed fp16 pairs; A[m][k]: m = L & 15, same k; D[m][n]: n = L & 15,
+// m = 4 (L >> 4) + i.
+// One 32 x 16 B block = two vertically adjacent 16x16 tiles (tile-row 2s + (L >> 5)). Lane L needs column
+// n of its tile and rows 8rh .. 8rh + 7 (rh = (L >> 4) & 1): chunk q = n & 7, positions u = o + u' with
+// o = 2 rh + 4 (n >> 3) and u' in {0, 1, 8, 9, 16, 17, 24, 25}. The lane loads the few ring words covering those
+// windows, funnel-shifts them by its (lane-dependent) bit offset so every window sits at a compile-time offset, and
+// decodes its own 8 values: no value is decoded twice and no cross-lane exchange is needed.
+#pragma once
+
+#include "exl3_device.h"
+
+namespace exl3 {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// Window of normalised position u' (bits [u'K, u'K + 16) of R), low 16 bits valid.
+template <int K>
+__device__ __forceinline__ uint32_t frag_window(const uint32_t* R, int up) {
+    const int E = up * K + 16;
+    const int IW = (E - 1) >> 5;
+    const int SH = 32 * (IW + 1) - E;
+    if (SH == 0) return R[IW];
+    if (E - 16 >= 32 * IW) return R[IW] >> SH;
+    return __builtin_amdgcn_alignbit(R[IW - 1], R[IW], SH);
+}
+
+// h values (1024 + bytesum, the codebook affine left out) of lane `lane`'s B fragment for the tile whose 8K ring
+// words start at `tw`. Words are read with in-tile wrap-around, so every access stays inside the tile.
+template <int K>
+__device__ __forceinline__ h8_t frag_decode(const uint32_t* __restrict__ tw, int lane) {
+    constexpr int W = 8 * K;
+    constexpr int NW = (48 + 25 * K + 31) / 32;
+    const int q = lane & 7, h = (lane >> 3) & 1, rh = (lane >> 4) & 1;
+    const int start = (32 * q + 2 * rh + 4 * h + 1) * K - 16;   // first ring bit needed (-15 .. 256K)
+    const int W0 = (start - 1) >> 5;                             // floor((start - 1) / 32), >= -1
+    const uint32_t sh = (uint32_t)(32 - (start - 32 * W0));      // 0 .. 31
+    uint32_t R[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        int w = W0 + i;
+        w = w < 0 ? w + W : (w >= W ? w - W : w);
+        R[i] = __builtin_nontemporal_load(tw + w);
+    }
+#pragma unroll
+    for (int i = 0; i < NW - 1; ++i) R[i] = __builtin_amdgcn_alignbit(R[i], R[i + 1], sh);
+    uint32_t p[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        p[c] = __builtin_bit_cast(uint32_t, mul1_pair_raw(frag_window<K>(R, 8 * c), frag_window<K>(R, 8 * c + 1)));
+    typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+    u4_t v = {p[0], p[1], p[2], p[3]};
+    return __builtin_bit_cast(h8_t, v);
+}
+
+// Per-tile K: dispatch on the tile's bitrate (all lanes of one tile take the same branch).
+__device__ __forceinline__ h8_t frag_decode_k(const uint32_t* __restrict__ tw, int Kt, int lane) {
+    switch (Kt) {
+        case 1: return frag_decode<1>(tw, lane);
+        case 2: return frag_decode<2>(tw, lane);
+        case 3: return frag_decode<3>(tw, lane);
+        case 4: return frag_decode<4>(tw, lane);
+        case 5: return frag_decode<5>(tw, lane);
+        case 6: return frag_decode<6>(tw, lane);
+        case 7: return frag_decode<7>(tw, lane);
+        case 8: return frag_decode<8>(tw, lane);
+        default: {
+            h8_t z = {};
+            return z;
+        }
+    }
+}
+
+}  // namespace exl3

@@ -5,7 +5,9 @@
 
 namespace exl3 {
 
-constexpr int kMoeMaxExperts = 3072;   // expert tables per layer (routed + shared); the align kernel keeps 4 ints each in LDS
+constexpr int kMoeMaxExperts = 2048;   // expert tables per layer (routed + shared); the align kernel keeps 5 ints each in LDS
+constexpr int kMoeSmallRows = 8;       // experts with at most this many rows in a call take the GEMV kernels
+constexpr int kMfmaRows = 64;          // row block of the MFMA grouped GEMM
 
 // One work unit of the GEMV kernels: up to 8 rows (pairs) of one expert, with everything a workgroup needs so that a
 // single uniform load replaces the table lookups. Items past the last real one have cnt == 0.
@@ -28,6 +30,9 @@ struct RouteArgs {
     int max_items;
     const int64_t* tables;             // [9][E] (read when items are built)
     const int64_t* kmaps;              // [6][E] or null
+    int use_mfma, MB;                  // experts with more than MR rows -> blocks of MB rows for the MFMA kernels
+    ItemDesc* blocks;                  // [max_blocks]
+    int max_blocks;
     int* pair_tok;
     float* pair_w;
     int* pair_of;
@@ -53,6 +58,9 @@ struct MoeArgs {
     // routing (workspace)
     int* n_items;
     const ItemDesc* items;
+    const ItemDesc* blocks;            // MFMA row blocks (cnt == 0 past the last)
+    int max_blocks;
+    _Float16* xh;                      // [pairs][2][H] transformed gate / up inputs of MFMA rows
     int* pair_tok;
     float* pair_w;
     int* pair_of;

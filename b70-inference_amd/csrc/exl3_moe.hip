@@ -14,6 +14,7 @@
 #include "exl3_device.h"
 #include "exl3_gemv.h"
 #include "exl3_moe.h"
+#include "exl3_moe_dev.h"
 #include "exl3_runtime.h"
 
 namespace exl3 {
@@ -50,8 +51,9 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     int* cnt = sm;                 // [E]
     int* start = sm + r.E;         // [E]
     int* fill = sm + 2 * r.E;      // [E]
-    int* nch = sm + 3 * r.E;       // [E]
-    int* tmp = sm + 4 * r.E;       // [1024]
+    int* nch = sm + 3 * r.E;       // [E] GEMV items of the expert, then their first index
+    int* nbl = sm + 4 * r.E;       // [E] MFMA blocks of the expert, then their first index
+    int* tmp = sm + 5 * r.E;       // [1024]
     const int t = threadIdx.x, T = blockDim.x;
     const int np = r.M * r.slots;
     for (int e = t; e < r.E; e += T) {
@@ -66,17 +68,30 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     }
     __syncthreads();
     for (int e = t; e < r.E; e += T) {
-        start[e] = cnt[e];
-        nch[e] = (cnt[e] + r.MR - 1) / r.MR;
+        const int c = cnt[e];
+        const bool big = r.use_mfma && c > r.MR;
+        start[e] = c;
+        nch[e] = big ? 0 : (c + r.MR - 1) / r.MR;
+        nbl[e] = big ? (c + r.MB - 1) / r.MB : 0;
     }
     __syncthreads();
     block_scan_exclusive(start, r.E, tmp);
     const int nitems = block_scan_exclusive(nch, r.E, tmp);
+    const int nblocks = block_scan_exclusive(nbl, r.E, tmp);
     for (int e = t; e < r.E; e += T) {
         const int c = cnt[e];
         if (r.counts) r.counts[e] = c;
         if (!r.items) continue;
-        for (int q = 0, it = nch[e]; q * r.MR < c; ++q, ++it) {
+        const bool big = r.use_mfma && c > r.MR;
+        for (int q = 0, b = nbl[e]; big && q * r.MB < c; ++q, ++b) {
+            ItemDesc& d = r.blocks[b];
+            d.e = e;
+            d.p0 = start[e] + q * r.MB;
+            d.cnt = min(r.MB, c - q * r.MB);
+            for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
+            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
+        }
+        for (int q = 0, it = nch[e]; !big && q * r.MR < c; ++q, ++it) {
             ItemDesc& d = r.items[it];
             d.e = e;
             d.p0 = start[e] + q * r.MR;
@@ -87,6 +102,8 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     }
     if (r.items)
         for (int it = nitems + t; it < r.max_items; it += T) r.items[it].cnt = 0;
+    if (r.blocks)
+        for (int b = nblocks + t; b < r.max_blocks; b += T) r.blocks[b].cnt = 0;
     if (t == 0 && r.n_items) r.n_items[0] = nitems;
     if (r.tok_nvalid) {
         for (int tok = t; tok < r.M; tok += T) {
@@ -115,7 +132,7 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             r.pair_tok[pos] = tok;
             r.pair_w[pos] = wt;
             r.pair_of[i] = pos;
-            if (r.items) {
+            if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
                 ItemDesc& d = r.items[nch[e] + f / r.MR];
                 d.tok[f % r.MR] = tok;
                 d.w[f % r.MR] = wt;
@@ -124,21 +141,6 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             r.pair_of[i] = -1;
         }
     }
-}
-
-// ================================================================================================ activation
-__device__ __forceinline__ float act_mul(float g, float u, int act, float L) {
-    if (act == EXL3_ACT_GELU_TANH) {
-        // 0.5 g (1 + tanh(z)) == g * sigmoid(2z): the sigmoid form has no cancellation for negative g
-        const float z2 = 1.5957691216057308f * (g + 0.044715f * g * g * g);   // 2 sqrt(2 / pi) (g + 0.044715 g^3)
-        return g / (1.f + expf(-z2)) * u;
-    }
-    float s = g / (1.f + expf(-g));
-    if (L > 0.f) {
-        s = fminf(s, L);
-        u = fminf(fmaxf(u, -L), L);
-    }
-    return s * u;
 }
 
 // ================================================================================================ gate | up
@@ -234,8 +236,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
         g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(svg[lane + 64]));
         u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(svu[lane]));
         u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(svu[lane + 64]));
-        float a0 = (float)(_Float16)act_mul(g0, u0, a.act, a.limit);
-        float a1 = (float)(_Float16)act_mul(g1, u1, a.act, a.limit);
+        float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
+        float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
         a0 = (float)(_Float16)(a0 * h2f(sud[lane]));
         a1 = (float)(_Float16)(a1 * h2f(sud[lane + 64]));
         fwht128_wave(a0, a1, lane);
@@ -346,29 +348,8 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
         }
     }
     __syncthreads();
-    for (int m = wave; m < cnt; m += 4) {
-        const int t = s_comb[m];
-        if (t < 0) continue;
-        const int c0 = nb * 128 + lane, c1 = c0 + 64;
-        float v0 = 0.f, v1 = 0.f;
-        for (int j = 0; j < a.slots; ++j) {
-            const int pr = a.pair_of[t * a.slots + j];
-            if (pr < 0) continue;
-            const float* y = a.y + (size_t)pr * a.H;
-            v0 += splitk_load(y + c0);
-            v1 += splitk_load(y + c1);
-        }
-        if (a.out_f32) {
-            float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
-            o[c0] = v0;
-            o[c1] = v1;
-        } else {
-            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
-            o[c0] = f2h(v0);
-            o[c1] = f2h(v1);
-        }
-        if (lane == 0) a.cnt_tok[(size_t)t * nbH + nb] = 0;
-    }
+    for (int m = wave; m < cnt; m += 4)
+        if (s_comb[m] >= 0) combine_token(a, s_comb[m], nb, lane);
 }
 
 // ================================================================================================ router
@@ -445,11 +426,11 @@ __global__ __launch_bounds__(256) void act_mul_kernel(const void* __restrict__ x
         g = reinterpret_cast<const float*>(x)[i];
         u = reinterpret_cast<const float*>(y)[i];
     }
-    z[i] = f2h(act_mul(g, u, act, L));
+    z[i] = f2h(act_mul_dev(g, u, act, L));
 }
 
 // ================================================================================================ host
-static size_t align_lds_bytes(int E) { return (size_t)(4 * E + 1024) * sizeof(int); }
+static size_t align_lds_bytes(int E) { return (size_t)(5 * E + 1024) * sizeof(int); }
 
 int launch_align(const RouteArgs& r, hipStream_t st) {
     const size_t lds = align_lds_bytes(r.E);
@@ -516,7 +497,11 @@ static moe_fn down_select(int K, int MR) {
     }
 }
 
-// Decode path: items of <= MR rows through the GEMV kernels. `a` has every field but the route/workspace ones set.
+int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st);   // exl3_mfma.hip
+int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st);
+
+// One layer call: align, then GEMV items (experts with <= MR rows) and MFMA blocks (more rows), gate|up before down.
+// `a` has every field but the route / workspace ones set.
 int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     const int max_items = a.max_items;
     const int nbI = a.I / 128, nbH = a.H / 128;
@@ -527,7 +512,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     const int MR = a.MR;
     Workspace ws;
     const size_t n_gu = (size_t)max_items * nbI, n_d = (size_t)max_items * nbH;
-    size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
+    const bool use_mfma = a.max_blocks > 0;
+    size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) +
+                   carve_size(a.max_blocks, sizeof(ItemDesc)) + (use_mfma ? carve_size(npairs * 2 * a.H, 2) : 0) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
                    carve_size(a.M, 4) +
                    carve_size(npairs * a.I, 2) + carve_size(npairs * a.H, 4) +
                    carve_size(n_gu * a.P_gu * 2 * MR * 128, 4) + carve_size(n_d * a.P_d * MR * 128, 4);
@@ -538,6 +525,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     a.n_items = c.take<int>(1);
     ItemDesc* items = c.take<ItemDesc>(max_items);
     a.items = items;
+    ItemDesc* blocks = a.max_blocks ? c.take<ItemDesc>(a.max_blocks) : nullptr;
+    a.blocks = blocks;
+    a.xh = use_mfma ? c.take<_Float16>(npairs * 2 * a.H) : nullptr;
     int* pb = c.take<int>(npairs * 2);
     a.pair_tok = pb;
     a.pair_of = pb + npairs;
@@ -566,6 +556,10 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.max_items = max_items;
     r.tables = a.tables;
     r.kmaps = a.kmaps;
+    r.use_mfma = use_mfma;
+    r.MB = kMfmaRows;
+    r.blocks = blocks;
+    r.max_blocks = a.max_blocks;
     r.pair_tok = a.pair_tok;
     r.pair_w = a.pair_w;
     r.pair_of = a.pair_of;
@@ -576,7 +570,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.H = a.H;
     rc = launch_align(r, st);
     if (rc) return rc;
+    if (use_mfma && (rc = launch_moe_mfma_gateup(a, st))) return rc;
     EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
+    if (use_mfma && (rc = launch_moe_mfma_down(a, st))) return rc;
     EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
     return EXL3_OK;
 }
@@ -634,10 +630,14 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.out_ld = out_ld;
     a.out_f32 = out_dtype == EXL3_F32;
     const int64_t npairs = M * a.slots;
-    a.MR = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-    int64_t mi = E + npairs / a.MR;
+    a.MR = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
+    // An expert has at most npairs rows; with more than MR possible rows per expert (M > MR or duplicates), experts
+    // with more than MR rows go to the MFMA kernels and every other expert is one GEMV item.
+    const bool mfma = M > kMoeSmallRows;
+    int64_t mi = mfma ? (E < npairs ? E : npairs) : E + npairs / a.MR;
     if (mi > npairs) mi = npairs;
     a.max_items = (int)mi;
+    a.max_blocks = mfma ? (int)(npairs / kMfmaRows + npairs / (a.MR + 1) + 1) : 0;
     EXL3_CHECK_ARG((int64_t)a.max_items * (H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
     return moe_decode_path(a, npairs, (hipStream_t)stream);
 }

@@ -76,6 +76,7 @@ struct ProfRec {
     hipEvent_t a, b;
 };
 bool g_prof_on = false;
+int g_prof_rep = 1;
 std::vector<hipEvent_t> g_pool;
 size_t g_pool_used = 0;
 std::vector<ProfRec> g_recs;
@@ -103,6 +104,8 @@ void prof_start(const char* name, hipStream_t s) {
     g_recs.push_back(r);
 }
 
+int prof_repeat() { return g_prof_on ? g_prof_rep : 1; }
+
 void prof_stop(hipStream_t s) {
     if (!g_prof_on || g_recs.empty() || g_prof_overflow) return;
     hipEventRecord(g_recs.back().b, s);
@@ -114,6 +117,7 @@ extern "C" {
 
 int exl3_profile_enable(int on) {
     exl3::g_prof_on = on != 0;
+    exl3::g_prof_rep = on > 1 ? on : 1;
     exl3::g_recs.clear();
     exl3::g_pool_used = 0;
     exl3::g_prof_overflow = false;
@@ -130,7 +134,7 @@ int exl3_profile_read(char* out, int64_t cap) {
         size_t i = 0;
         while (i < agg.size() && agg[i].first != r.name) ++i;
         if (i == agg.size()) agg.push_back({r.name, {0.0, 0}});
-        agg[i].second.first += ms * 1000.0;
+        agg[i].second.first += ms * 1000.0 / g_prof_rep;
         agg[i].second.second += 1;
     }
     std::string txt;

@@ -56,13 +56,18 @@ inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) =
 
 // Opt-in kernel timing (exl3_profile_enable): a HIP event pair on the launch stream around every library launch,
 // aggregated per kernel name by exl3_profile_read. Off by default; never used under graph capture.
+// With repeat R > 1 every profiled launch runs R times back to back inside its event pair (all library kernels
+// are idempotent: they rewrite their outputs and leave their arrival counters at zero), which amortises the
+// event-record overhead; exl3_profile_read reports the per-launch average.
 void prof_start(const char* name, hipStream_t s);
 void prof_stop(hipStream_t s);
+int prof_repeat();
 
 #define EXL3_LAUNCH(name, kernel, grid, block, lds, stream, ...)                   \
     do {                                                                         \
         ::exl3::prof_start(name, stream);                                        \
-        hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);       \
+        for (int rep_ = ::exl3::prof_repeat(); rep_ > 0; --rep_)                 \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);   \
         ::exl3::prof_stop(stream);                                               \
         EXL3_CHECK_HIP(hipGetLastError());                                       \
     } while (0)

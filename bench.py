@@ -115,7 +115,7 @@ def graph_time(fns, reps=1, wall=False):
 def kernel_profile(fns):
     """Eager run of fns with the library's event profiler: {kernel: (launches, avg us)}."""
     torch.cuda.synchronize()
-    exl3._lib.profile_enable(True)
+    exl3._lib.profile_enable(True, repeat=8)
     for f in fns:
         f()
     torch.cuda.synchronize()

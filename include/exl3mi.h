@@ -40,8 +40,9 @@ int exl3_abi_version(void);
  * e.g. before HIP graph capture. No reference counterpart (the reference grows its scratch inside the op). */
 int exl3_reserve_workspace(int64_t bytes, int64_t ncounters);
 
-/* Kernel timing: while enabled, every kernel the library launches is bracketed by a HIP event pair on its stream.
- * exl3_profile_read writes "name count avg_us" lines (one per kernel) for the launches since the last enable.
+/* Kernel timing: while enabled (on != 0), every kernel the library launches is bracketed by a HIP event pair on its
+ * stream; with on = R > 1 each launch runs R times inside its pair (the kernels are idempotent) to amortise the event
+ * overhead. exl3_profile_read writes "name count avg_us" lines (per-launch averages) since the last enable.
  * Not for use under graph capture. No reference counterpart (the reference times with torch.profiler). */
 int exl3_profile_enable(int on);
 int exl3_profile_read(char* out, int64_t cap);

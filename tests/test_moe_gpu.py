@@ -189,3 +189,76 @@ def test_moe_token_without_active_slots(exl3, oracle, small):
     got = out.cpu().numpy()
     assert (got[1] == 0).all()
     assert max_rel(got, ref) <= MAX_REL
+
+
+def _skewed_ids(M, k, E, seed, hot=(0, 1, 2)):
+    """Routing where the `hot` experts appear in most tokens (many rows -> MFMA blocks) and the rest rarely."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.empty(M, k, dtype=torch.int32)
+    for t in range(M):
+        pool = list(hot) if torch.rand(1, generator=g).item() < 0.85 else []
+        rest = [int(e) for e in torch.randperm(E, generator=g) if int(e) not in pool]
+        row = (pool + rest)[:k]
+        ids[t] = torch.tensor(row, dtype=torch.int32)[torch.randperm(k, generator=g)]
+    w = torch.rand(M, k, generator=g)
+    return ids, (w / w.sum(1, keepdim=True)).float()
+
+
+@pytest.mark.parametrize("M", [12, 80])
+def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
+    """M > 8: experts with more than 8 rows go through the MFMA grouped GEMM (80 tokens: the hot experts cross the
+    64-row block boundary), the rest through the GEMV kernels, in one call."""
+    tables, orc = small
+    ids, w = _skewed_ids(M, 4, 12, 1500 + M)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(16)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    counts = np.bincount(ids.numpy().reshape(-1), minlength=12)
+    assert counts.max() > 8 and (counts[counts > 0] <= 8).any()
+
+
+def test_moe_prefill_per_projection_k_and_gelu(exl3, oracle):
+    tables, orc = make_experts(exl3, oracle, 6, 512, 384, 2, 3, 1600)
+    ids, w = _skewed_ids(40, 3, 6, 1601, hot=(1, 4))
+    x = torch.randn(40, 512, generator=torch.Generator().manual_seed(17)).half()
+    for act in (0, 1):
+        y, ref = _run(exl3, oracle, tables, orc, x, ids, w, act=act)
+        assert max_rel(y, ref) <= MAX_REL
+
+
+def test_moe_prefill_per_tile_k_shared(exl3, oracle):
+    """Per-tile K in {1, 2} (38/62), shared expert on every row (an MFMA expert), routed experts mostly small."""
+    tables, orc = make_experts(exl3, oracle, 7, 256, 256, 0, 0, 1700, per_tile=((1, 2), (0.38, 0.62)))
+    ids, w = _ids_w(20, 2, 6, 1701)
+    x = torch.randn(20, 256, generator=torch.Generator().manual_seed(18)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=6)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_moe_prefill_deterministic_and_token_permutation(exl3, small):
+    """Row results do not depend on which other rows share a block: permuting the tokens permutes the output rows
+    bit for bit, and two calls agree exactly."""
+    tables, _ = small
+    ids, w = _skewed_ids(70, 4, 12, 1800)
+    x = torch.randn(70, 256, generator=torch.Generator().manual_seed(19)).half()
+    perm = torch.randperm(70, generator=torch.Generator().manual_seed(20))
+    a = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables)
+    b = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables)
+    c = exl3.moe_forward(x[perm].cuda(), ids[perm].cuda(), w[perm].cuda(), tables)
+    assert torch.equal(a, b)
+    assert torch.equal(a[perm.cuda()], c)
+
+
+def test_moe_c4_shape_rows_vs_oracle(exl3, oracle):
+    """C4 shapes (H=5120, I=1536, gate/up K=2, down K=3), 64 tokens over 8 experts with Zipf-skewed softmax routing:
+    every row checked against the oracle."""
+    tables, orc = make_experts(exl3, oracle, 8, 5120, 1536, 2, 3, 4000)
+    g = torch.Generator().manual_seed(4001)
+    logits = torch.randn(64, 8, generator=g)
+    bias = -1.1 * torch.log(torch.randperm(8, generator=g).float() + 1)
+    x = torch.randn(64, 5120, generator=g).half()
+    ids, w = exl3.route_softmax_topk(logits.cuda(), 3, bias.cuda())
+    rid, rw = oracle.route_softmax_topk(logits.numpy(), 3, bias.numpy())
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    y, ref = _run(exl3, oracle, tables, orc, x, ids.cpu(), w.cpu())
+    assert max_rel(y, ref) <= MAX_REL
