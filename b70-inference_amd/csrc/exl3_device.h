@@ -24,6 +24,18 @@ typedef float f2_t __attribute__((ext_vector_type(2)));
 constexpr uint32_t kMul1 = 0x83DCD12Du;
 constexpr float kRsqrt128 = 0.08838834764831845f;
 
+// Loads through explicit global (address space 1) pointers. Pointers that reach a kernel through tables or
+// descriptors are generic to the compiler, which would emit flat loads; flat loads also count against the LDS
+// counter, so every wait on them becomes a full drain and software prefetching stops working.
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ T ldg_nt(const T* p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)p);
+}
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
 // ------------------------------------------------------------------------------------------------ windows
@@ -74,7 +86,7 @@ template <int K>
 __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ p, int lane, uint32_t* R) {
     const uint32_t* q = p + lane * K;
 #pragma unroll
-    for (int i = 0; i < K; ++i) R[1 + i] = __builtin_nontemporal_load(q + i);
+    for (int i = 0; i < K; ++i) R[1 + i] = ldg_nt(q + i);
 }
 
 template <int K>

@@ -44,7 +44,7 @@ __device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __r
                                            int nt) {
     const size_t off = (size_t)(lt < nt ? lt : nt - 1) * rs;
 #pragma unroll
-    for (int i = 0; i < K; ++i) D[i] = __builtin_nontemporal_load(base + off + i);
+    for (int i = 0; i < K; ++i) D[i] = ldg_nt(base + off + i);
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
 }
 
@@ -99,7 +99,7 @@ __device__ __forceinline__ void mixed_tile_row(const uint32_t* __restrict__ tw, 
     uint32_t D[K];
     const uint32_t* q = tw + (lane & 7) * K;
 #pragma unroll
-    for (int i = 0; i < K; ++i) D[i] = __builtin_nontemporal_load(q + i);
+    for (int i = 0; i < K; ++i) D[i] = ldg_nt(q + i);
     strip_tile_row<K, M>(D, lane, xr, xs_ld, acc);
 }
 
@@ -110,8 +110,8 @@ __device__ __forceinline__ void strip_gemv_mixed(const uint32_t* __restrict__ wo
                                                  float (&acc)[M][2]) {
     for (int lt = lt0; lt < nt; lt += step) {
         const int tile = (tr0 + lt) * tn + tile_n0 + (lane >> 3);
-        const int Kt = kmap[tile];
-        const uint32_t* tw = words + woff[tile];
+        const int Kt = ldg(kmap + tile);
+        const uint32_t* tw = words + ldg(woff + tile);
         const _Float16* xr = xs + lt * 16;
         switch (Kt) {
             case 1: mixed_tile_row<1, M>(tw, lane, xr, xs_ld, acc); break;
@@ -140,12 +140,14 @@ __device__ __forceinline__ void splitk_store(float* p, float v) {
 #if EXL3_SPLITK_FENCE
     *p = v;
 #else
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((__attribute__((address_space(1))) float*)p, v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 #endif
 }
 
 __device__ __forceinline__ float splitk_load(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((const __attribute__((address_space(1))) float*)p, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Returns true in every thread of the last-arriving workgroup (of `nparts`); that workgroup resets the counter
@@ -176,8 +178,8 @@ __device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, co
                                               _Float16* dst, int lane) {
     float va = 0.f, vb = 0.f;
     if (x) {
-        va = (float)(_Float16)(h2f(x[lane]) * h2f(suh[lane]));
-        vb = (float)(_Float16)(h2f(x[lane + 64]) * h2f(suh[lane + 64]));
+        va = (float)(_Float16)(h2f(ldg(x + lane)) * h2f(ldg(suh + lane)));
+        vb = (float)(_Float16)(h2f(ldg(x + lane + 64)) * h2f(ldg(suh + lane + 64)));
     }
     fwht128_wave(va, vb, lane);
     _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
@@ -193,8 +195,8 @@ __device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, co
 __device__ __forceinline__ float copy_block(const uint16_t* __restrict__ x, _Float16* dst, int lane) {
     _Float16 ha = (_Float16)0.f, hb = (_Float16)0.f;
     if (x) {
-        ha = __builtin_bit_cast(_Float16, x[lane]);
-        hb = __builtin_bit_cast(_Float16, x[lane + 64]);
+        ha = __builtin_bit_cast(_Float16, ldg(x + lane));
+        hb = __builtin_bit_cast(_Float16, ldg(x + lane + 64));
     }
     dst[lane] = ha;
     dst[lane + 64] = hb;

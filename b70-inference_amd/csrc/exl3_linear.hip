@@ -173,8 +173,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
         fwht128_wave(va, vb, lane);
         const int c0 = strip * 128 + lane, c1 = c0 + 64;
-        va *= kRsqrt128 * h2f(a.svh[c0]);
-        vb *= kRsqrt128 * h2f(a.svh[c1]);
+        va *= kRsqrt128 * h2f(ldg(a.svh + c0));
+        vb *= kRsqrt128 * h2f(ldg(a.svh + c1));
         if (F32) {
             float* o = reinterpret_cast<float*>(a.out) + (int64_t)m * a.out_ld;
             o[c0] = va;

@@ -43,7 +43,7 @@ __device__ __forceinline__ h8_t frag_decode(const uint32_t* __restrict__ tw, int
     for (int i = 0; i < NW; ++i) {
         int w = W0 + i;
         w = w < 0 ? w + W : (w >= W ? w - W : w);
-        R[i] = __builtin_nontemporal_load(tw + w);
+        R[i] = ldg_nt(tw + w);
     }
 #pragma unroll
     for (int i = 0; i < NW - 1; ++i) R[i] = __builtin_amdgcn_alignbit(R[i], R[i + 1], sh);
@@ -51,6 +51,53 @@ __device__ __forceinline__ h8_t frag_decode(const uint32_t* __restrict__ tw, int
 #pragma unroll
     for (int c = 0; c < 4; ++c)
         p[c] = __builtin_bit_cast(uint32_t, mul1_pair_raw(frag_window<K>(R, 8 * c), frag_window<K>(R, 8 * c + 1)));
+    typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+    u4_t v = {p[0], p[1], p[2], p[3]};
+    return __builtin_bit_cast(h8_t, v);
+}
+
+// Split form of frag_decode for software pipelining: the ring-word indices a lane reads inside any tile do not
+// depend on the tile, so they are computed once (frag_setup), words are loaded ahead (frag_load), and decoded later
+// (frag_finish).
+template <int K>
+struct FragCfg {
+    static constexpr int NW = (48 + 25 * K + 31) / 32;
+    int widx[NW];
+    uint32_t sh;
+};
+
+template <int K>
+__device__ __forceinline__ void frag_setup(int lane, FragCfg<K>& c) {
+    constexpr int W = 8 * K;
+    const int q = lane & 7, h = (lane >> 3) & 1, rh = (lane >> 4) & 1;
+    const int start = (32 * q + 2 * rh + 4 * h + 1) * K - 16;
+    const int W0 = (start - 1) >> 5;
+    c.sh = (uint32_t)(32 - (start - 32 * W0));
+#pragma unroll
+    for (int i = 0; i < FragCfg<K>::NW; ++i) {
+        int w = W0 + i;
+        c.widx[i] = w < 0 ? w + W : (w >= W ? w - W : w);
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void frag_load(const uint32_t* __restrict__ tw, const FragCfg<K>& c,
+                                          uint32_t (&R)[FragCfg<K>::NW]) {
+#pragma unroll
+    for (int i = 0; i < FragCfg<K>::NW; ++i) R[i] = ldg_nt(tw + c.widx[i]);
+}
+
+template <int K>
+__device__ __forceinline__ h8_t frag_finish(uint32_t (&R)[FragCfg<K>::NW], uint32_t sh) {
+    constexpr int NW = FragCfg<K>::NW;
+    uint32_t N[NW];
+#pragma unroll
+    for (int i = 0; i < NW - 1; ++i) N[i] = __builtin_amdgcn_alignbit(R[i], R[i + 1], sh);
+    N[NW - 1] = R[NW - 1];
+    uint32_t p[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        p[c] = __builtin_bit_cast(uint32_t, mul1_pair_raw(frag_window<K>(N, 8 * c), frag_window<K>(N, 8 * c + 1)));
     typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
     u4_t v = {p[0], p[1], p[2], p[3]};
     return __builtin_bit_cast(h8_t, v);

@@ -43,6 +43,78 @@ __device__ __forceinline__ void xcd_map(int nbc, int& blk, int& nb) {
     nb = j - q * nbc;
 }
 
+// ------------------------------------------------------------------------------------------------ pipelined K loop
+// One wave accumulates T tile columns (tile column t from projection t / (T / NP)) over all 32-k steps for RG row
+// groups of A (NP activation streams, one per projection). Weight words run two steps ahead (ring of 3), A fragments
+// one step ahead (ring of 2); the loop is unrolled 6x so every buffer is consumed where it was filled, and each
+// step issues A(s+1) before W(s+2) so waiting for a step's data never waits for a later prefetch.
+template <int K, int T, int NP, int RG>
+struct MfmaLoop {
+    static constexpr int NW = FragCfg<K>::NW;
+    static constexpr int TPP = T / NP;          // tile columns per projection
+    const uint32_t* wbase[T];                   // tile (tile-row lane >> 5, column) of step 0, per tile column
+    size_t wstep;                               // words between consecutive steps (two tile-rows)
+    const _Float16* abase[NP][RG];              // A row pointer (with this lane's k offset) per projection / group
+    int nsteps;
+    FragCfg<K> cfg;
+
+    __device__ __forceinline__ void load_w(uint32_t (&W)[T][NW], int s) const {
+        const size_t off = (size_t)(s < nsteps ? s : nsteps - 1) * wstep;
+#pragma unroll
+        for (int t = 0; t < T; ++t) frag_load<K>(wbase[t] + off, cfg, W[t]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ void load_a(h8_t (&A)[NP][RG], int s) const {
+        const int ss = (s < nsteps ? s : nsteps - 1) * 32;
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) A[p][rg] = *reinterpret_cast<const h8_t*>(abase[p][rg] + ss);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ void compute(uint32_t (&W)[T][NW], const h8_t (&A)[NP][RG], f4_t (&acc)[T][RG],
+                                            float (&rs)[NP][RG]) const {
+        h8_t bf[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) bf[t] = frag_finish<K>(W[t], cfg.sh);
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+                float sv = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sv += (float)A[p][rg][j];
+                rs[p][rg] += sv;
+#pragma unroll
+                for (int u = 0; u < TPP; ++u)
+                    acc[p * TPP + u][rg] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(A[p][rg], bf[p * TPP + u], acc[p * TPP + u][rg], 0, 0, 0);
+            }
+    }
+    __device__ __forceinline__ void run(f4_t (&acc)[T][RG], float (&rs)[NP][RG]) const {
+        uint32_t W0[T][NW], W1[T][NW], W2[T][NW];
+        h8_t A0[NP][RG], A1[NP][RG];
+        load_a(A0, 0);
+        load_w(W0, 0);
+        load_w(W1, 1);
+        int s = 0;
+        for (; s + 6 <= nsteps; s += 6) {
+            load_a(A1, s + 1); load_w(W2, s + 2); compute(W0, A0, acc, rs);
+            load_a(A0, s + 2); load_w(W0, s + 3); compute(W1, A1, acc, rs);
+            load_a(A1, s + 3); load_w(W1, s + 4); compute(W2, A0, acc, rs);
+            load_a(A0, s + 4); load_w(W2, s + 5); compute(W0, A1, acc, rs);
+            load_a(A1, s + 5); load_w(W0, s + 6); compute(W1, A0, acc, rs);
+            load_a(A0, s + 6); load_w(W1, s + 7); compute(W2, A1, acc, rs);
+        }
+        // tail (< 6 steps): W0 / W1 hold steps s, s + 1 and A0 holds step s
+        if (s < nsteps) { load_a(A1, s + 1); load_w(W2, s + 2); compute(W0, A0, acc, rs); }
+        if (s + 1 < nsteps) { load_a(A0, s + 2); load_w(W0, s + 3); compute(W1, A1, acc, rs); }
+        if (s + 2 < nsteps) { load_a(A1, s + 3); load_w(W1, s + 4); compute(W2, A0, acc, rs); }
+        if (s + 3 < nsteps) { load_a(A0, s + 4); load_w(W2, s + 5); compute(W0, A1, acc, rs); }
+        if (s + 4 < nsteps) { load_a(A1, s + 5); compute(W1, A0, acc, rs); }
+    }
+};
+
 // ------------------------------------------------------------------------------------------------ gate | up
 template <int K, int MB>
 __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
@@ -84,17 +156,30 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
         for (int rg = 0; rg < RG; ++rg) rs[p][rg] = 0.f;
 
     const int nsteps = a.H / 32;
-    for (int s = 0; s < nsteps; ++s) {
+    if (K > 0) {
+        constexpr int KL = K > 0 ? K : 1;
+        MfmaLoop<KL, 4, 2, RG> L;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            L.wbase[t] = trp[t >> 1] + ((size_t)(lane >> 5) * tn + ct0 + (t & 1)) * (8 * KL);
+        L.wstep = (size_t)2 * tn * 8 * KL;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) L.abase[p][rg] = arow[rg] + (size_t)p * a.H;
+        L.nsteps = nsteps;
+        frag_setup<KL>(lane, L.cfg);
+        L.run(acc, rs);
+    }
+    for (int s = 0; K == 0 && s < nsteps; ++s) {
         const int tr = 2 * s + (lane >> 5);
         h8_t bf[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int p = t >> 1, col = ct0 + (t & 1);
-            if (K > 0) {
-                bf[t] = frag_decode<(K > 0 ? K : 1)>(trp[p] + ((size_t)tr * tn + col) * (8 * (K > 0 ? K : 1)), lane);
-            } else {
+            {
                 const int tile = tr * tn + col;
-                bf[t] = frag_decode_k(trp[p] + wop[p][tile], kmp[p][tile], lane);
+                bf[t] = frag_decode_k(trp[p] + ldg(wop[p] + tile), ldg(kmp[p] + tile), lane);
             }
         }
 #pragma unroll
@@ -142,14 +227,14 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
         float u0 = kMul1C1 * C[(MB + m) * 128 + lane] + su, u1 = kMul1C1 * C[(MB + m) * 128 + lane + 64] + su;
         fwht128_wave(g0, g1, lane);
         fwht128_wave(u0, u1, lane);
-        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(svg[lane]));
-        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(svg[lane + 64]));
-        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(svu[lane]));
-        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(svu[lane + 64]));
+        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(ldg(svg + lane)));
+        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(ldg(svg + lane + 64)));
+        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(ldg(svu + lane)));
+        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(ldg(svu + lane + 64)));
         float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
         float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
-        a0 = (float)(_Float16)(a0 * h2f(sud[lane]));
-        a1 = (float)(_Float16)(a1 * h2f(sud[lane + 64]));
+        a0 = (float)(_Float16)(a0 * h2f(ldg(sud + lane)));
+        a1 = (float)(_Float16)(a1 * h2f(ldg(sud + lane + 64)));
         fwht128_wave(a0, a1, lane);
         uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
         dst[lane] = f2h(a0 * kRsqrt128);
@@ -194,17 +279,41 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
         rs[rg] = 0.f;
     }
     const int nsteps = a.I / 32;
-    for (int s = 0; s < nsteps; ++s) {
+    if (K > 0) {
+        constexpr int KL = K > 0 ? K : 1;
+        MfmaLoop<KL, 2, 1, RG> L;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) L.wbase[t] = trd + ((size_t)(lane >> 5) * tn + ct0 + t) * (8 * KL);
+        L.wstep = (size_t)2 * tn * 8 * KL;
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) L.abase[0][rg] = reinterpret_cast<const _Float16*>(arow[rg]);
+        L.nsteps = nsteps;
+        frag_setup<KL>(lane, L.cfg);
+        f4_t acc1[2][RG];
+        float rs1[1][RG];
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            acc1[0][rg] = acc[0][rg];
+            acc1[1][rg] = acc[1][rg];
+            rs1[0][rg] = rs[rg];
+        }
+        L.run(acc1, rs1);
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) {
+            acc[0][rg] = acc1[0][rg];
+            acc[1][rg] = acc1[1][rg];
+            rs[rg] = rs1[0][rg];
+        }
+    }
+    for (int s = 0; K == 0 && s < nsteps; ++s) {
         const int tr = 2 * s + (lane >> 5);
         h8_t bf[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int col = ct0 + t;
-            if (K > 0) {
-                bf[t] = frag_decode<(K > 0 ? K : 1)>(trd + ((size_t)tr * tn + col) * (8 * (K > 0 ? K : 1)), lane);
-            } else {
+            {
                 const int tile = tr * tn + col;
-                bf[t] = frag_decode_k(trd + wod[tile], kmd[tile], lane);
+                bf[t] = frag_decode_k(trd + ldg(wod + tile), ldg(kmd + tile), lane);
             }
         }
 #pragma unroll
@@ -242,8 +351,8 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
         fwht128_wave(v0, v1, lane);
         const float w = a.pair_w[p0 + m];
         float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 128;
-        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(svd[lane]) * w);
-        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(svd[lane + 64]) * w);
+        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(ldg(svd + lane)) * w);
+        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(ldg(svd + lane + 64)) * w);
     }
     // combine: count rows into their tokens, finish tokens whose slots are all in
     __builtin_amdgcn_s_waitcnt(0);

@@ -232,14 +232,14 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
         }
         fwht128_wave(g0, g1, lane);
         fwht128_wave(u0, u1, lane);
-        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(svg[lane]));
-        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(svg[lane + 64]));
-        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(svu[lane]));
-        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(svu[lane + 64]));
+        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(ldg(svg + lane)));
+        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(ldg(svg + lane + 64)));
+        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(ldg(svu + lane)));
+        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(ldg(svu + lane + 64)));
         float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
         float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
-        a0 = (float)(_Float16)(a0 * h2f(sud[lane]));
-        a1 = (float)(_Float16)(a1 * h2f(sud[lane + 64]));
+        a0 = (float)(_Float16)(a0 * h2f(ldg(sud + lane)));
+        a1 = (float)(_Float16)(a1 * h2f(ldg(sud + lane + 64)));
         fwht128_wave(a0, a1, lane);
         uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
         dst[lane] = f2h(a0 * kRsqrt128);
@@ -331,8 +331,8 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
         fwht128_wave(v0, v1, lane);
         const float w = d->w[m];
         float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 128;
-        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(svd[lane]) * w);
-        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(svd[lane + 64]) * w);
+        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(ldg(svd + lane)) * w);
+        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(ldg(svd + lane + 64)) * w);
     }
     if (threadIdx.x == 0) a.cnt_d[slot] = 0;
 
