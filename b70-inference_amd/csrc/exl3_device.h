@@ -31,6 +31,8 @@ template <typename T>
 __device__ __forceinline__ T ldg(const T* p) {
     return *(const __attribute__((address_space(1))) T*)p;
 }
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 template <typename T>
 __device__ __forceinline__ T ldg_nt(const T* p) {
     return __builtin_nontemporal_load((const __attribute__((address_space(1))) T*)p);
@@ -89,10 +91,14 @@ __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ p, int l
     for (int i = 0; i < K; ++i) R[1 + i] = ldg_nt(q + i);
 }
 
+// R[0] = last word of the previous chunk of the lane's tile: lane l - 1, or l + 7 for chunk 0 (the ring wraps inside
+// the 8 lanes of a tile; both stay inside the lane's 16-lane row, so two DPP row shifts do it).
 template <int K>
 __device__ __forceinline__ void chunk_prev(int lane, uint32_t* R) {
-    int src = (lane & 7) ? lane - 1 : lane + 7;
-    R[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)R[K]);
+    const int v = (int)R[K];
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1 (lane - 1)
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x107, 0xF, 0xF, false);   // row_shl:7 (lane + 7)
+    R[0] = (uint32_t)((lane & 7) ? dn : up);
 }
 
 // Decode the lane's 32 positions into 16 packed fp16 pairs: pair j holds positions (2j, 2j+1), i.e. rows
@@ -112,18 +118,50 @@ __device__ __forceinline__ void decode_chunk_raw(const uint32_t* R, h2_t* w) {
 
 // ------------------------------------------------------------------------------------------------ Hadamard
 
+// Value of lane (lane ^ M) (gfx950): DPP quad permutes for 1 and 2, row shifts for 4 (left or right by 4 inside the
+// 16-lane row, by bit 2), a row rotate by 8 for 8, and v_permlane16/32_swap for 16 and 32 (swapping a register with
+// itself: element [0] holds the lower partner row / half in the upper one, [1] the upper partner in the lower one).
+template <int M>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+    const int u = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false));
+    if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false));
+    if constexpr (M == 4) {
+        const int l = __builtin_amdgcn_update_dpp(0, u, 0x104, 0xF, 0xF, false);   // row_shl:4 (lane + 4)
+        const int r = __builtin_amdgcn_update_dpp(0, u, 0x114, 0xF, 0xF, false);   // row_shr:4 (lane - 4)
+        return __builtin_bit_cast(float, (lane & 4) ? r : l);
+    }
+    if constexpr (M == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false));
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+        return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+    }
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+        return __builtin_bit_cast(float, (lane & 32) ? r[0] : r[1]);
+    }
+    return v;
+}
+
+template <int M>
+__device__ __forceinline__ void fwht_stage(float& a, float& b, int lane) {
+    const float pa = lane_xor<M>(a, lane), pb = lane_xor<M>(b, lane);
+    const bool hi = lane & M;
+    a = hi ? pa - a : a + pa;
+    b = hi ? pb - b : b + pb;
+}
+
 // Unnormalised natural-order Sylvester FWHT-128 across a wave: lane l holds elements l (a) and l + 64 (b).
 __device__ __forceinline__ void fwht128_wave(float& a, float& b, int lane) {
-    float s = a + b, d = a - b;
+    const float s = a + b, d = a - b;
     a = s;
     b = d;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        float pa = __shfl_xor(a, m), pb = __shfl_xor(b, m);
-        bool hi = lane & m;
-        a = hi ? pa - a : a + pa;
-        b = hi ? pb - b : b + pb;
-    }
+    fwht_stage<1>(a, b, lane);
+    fwht_stage<2>(a, b, lane);
+    fwht_stage<4>(a, b, lane);
+    fwht_stage<8>(a, b, lane);
+    fwht_stage<16>(a, b, lane);
+    fwht_stage<32>(a, b, lane);
 }
 
 // ------------------------------------------------------------------------------------------------ wave reductions
@@ -153,12 +191,32 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     v = min(v, EXL3_DPP(v, 0x143, 0xC));
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
+
+__device__ __forceinline__ float wave_sum_f32(float f) {
+    const uint32_t ident = 0u;   // +0.0f
+    uint32_t v = __builtin_bit_cast(uint32_t, f);
+#define EXL3_ADD(ctrl, rmask) \
+    v = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, v) + __builtin_bit_cast(float, EXL3_DPP(v, ctrl, rmask)))
+    EXL3_ADD(0xB1, 0xF);
+    EXL3_ADD(0x4E, 0xF);
+    EXL3_ADD(0x141, 0xF);
+    EXL3_ADD(0x140, 0xF);
+    EXL3_ADD(0x142, 0xA);
+    EXL3_ADD(0x143, 0xC);
+#undef EXL3_ADD
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane((int)v, 63));
+}
 #undef EXL3_DPP
 
 // Order-preserving map of a float to uint32 (larger float -> larger key; NaN payloads sort above +inf).
 __device__ __forceinline__ uint32_t float_key(float f) {
     const uint32_t u = __builtin_bit_cast(uint32_t, f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inverse of float_key.
+__device__ __forceinline__ float key_float(uint32_t k) {
+    return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
 __device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }

@@ -13,6 +13,10 @@ namespace exl3 {
 constexpr int kGemvKBMax = 8;        // Hadamard blocks (128 k) per workgroup split
 constexpr int kGemvTargetWG = 1024;  // workgroups a GEMV launch aims for (256 CUs x 4); EXL3MI_TARGET_WG overrides
 constexpr int kGemvMaxRows = 8;      // rows per GEMV pass
+#ifndef EXL3_LINEAR_RING
+#define EXL3_LINEAR_RING 3
+#endif
+constexpr int kLinearRing = EXL3_LINEAR_RING;   // register ring depth of the dense GEMV
 
 // acc[m][h] += sum over tile-rows lt = lt0, lt0 + step, ... < nt of sum_r xs[m * xs_ld + 16 lt + r] * h(16 lt + r, col)
 // where `sp` points at tile-row 0 of the strip, tile-rows are `rs` words apart, and lane l owns columns
@@ -48,46 +52,51 @@ __device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __r
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
 }
 
-// Issue the first two tile-rows' loads of a strip (so their latency overlaps whatever the caller does next).
-template <int K>
+// Ring of R register buffers: buffer r holds tile-row i + r of the wave's rows lt0 + i * step; loads run R - 1 rows
+// ahead of the decode. strip_prefetch issues the first R - 1 rows (so their latency overlaps whatever the caller
+// does next); strip_gemv_run consumes them and streams the rest.
+template <int K, int R>
+struct StripRing {
+    uint32_t D[R][K];
+};
+
+template <int K, int R>
 __device__ __forceinline__ void strip_prefetch(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
-                                               int lane, uint32_t (&A)[K], uint32_t (&B)[K]) {
+                                               int lane, StripRing<K, R>& ring) {
     if (lt0 >= nt) return;
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const int n = (nt - lt0 + step - 1) / step;
-    strip_load<K>(A, base, rs * step, 0, n);
-    strip_load<K>(B, base, rs * step, 1, n);
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r) strip_load<K>(ring.D[r], base, rs * step, r, n);
 }
 
-// The strip loop proper, starting from strip_prefetch's A (tile-row lt0) and B (lt0 + step).
-template <int K, int M>
+template <int K, int M, int R>
 __device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
                                                int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2],
-                                               uint32_t (&A)[K], uint32_t (&B)[K]) {
+                                               StripRing<K, R>& ring) {
     if (lt0 >= nt) return;
     const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const size_t rstep = rs * step;
-    uint32_t C[K];
     int i = 0;
-    for (; i + 3 <= n; i += 3) {                         // branch-free body: loads stay two tile-rows ahead
-        strip_load<K>(C, base, rstep, i + 2, n);
-        strip_tile_row<K, M>(A, lane, xs + (lt0 + i * step) * 16, xs_ld, acc);
-        strip_load<K>(A, base, rstep, i + 3, n);
-        strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
-        strip_load<K>(B, base, rstep, i + 4, n);
-        strip_tile_row<K, M>(C, lane, xs + (lt0 + (i + 2) * step) * 16, xs_ld, acc);
+    for (; i + R <= n; i += R) {                         // branch-free body: loads stay R - 1 tile-rows ahead
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            strip_load<K>(ring.D[(r + R - 1) % R], base, rstep, i + r + R - 1, n);
+            strip_tile_row<K, M>(ring.D[r], lane, xs + (lt0 + (i + r) * step) * 16, xs_ld, acc);
+        }
     }
-    if (i < n) strip_tile_row<K, M>(A, lane, xs + (lt0 + i * step) * 16, xs_ld, acc);
-    if (i + 1 < n) strip_tile_row<K, M>(B, lane, xs + (lt0 + (i + 1) * step) * 16, xs_ld, acc);
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r)
+        if (i + r < n) strip_tile_row<K, M>(ring.D[r], lane, xs + (lt0 + (i + r) * step) * 16, xs_ld, acc);
 }
 
 template <int K, int M>
 __device__ __forceinline__ void strip_gemv(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
                                            int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2]) {
-    uint32_t A[K], B[K];
-    strip_prefetch<K>(sp, rs, lt0, nt, step, lane, A, B);
-    strip_gemv_run<K, M>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, A, B);
+    StripRing<K, 3> ring;
+    strip_prefetch<K, 3>(sp, rs, lt0, nt, step, lane, ring);
+    strip_gemv_run<K, M, 3>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, ring);
 }
 
 // Per-tile K (mixed bitrate): tile i of the projection (row-major over [k/16, n/16]) holds 8 * kmap[i] words at
@@ -185,10 +194,7 @@ __device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, co
     _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
     dst[lane] = ha;
     dst[lane + 64] = hb;
-    float s = (float)ha + (float)hb;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
-    return s;
+    return wave_sum_f32((float)ha + (float)hb);
 }
 
 // Same for an activation block that is already in the Hadamard domain (fp16): copy to LDS and sum.
@@ -200,10 +206,7 @@ __device__ __forceinline__ float copy_block(const uint16_t* __restrict__ x, _Flo
     }
     dst[lane] = ha;
     dst[lane + 64] = hb;
-    float s = (float)ha + (float)hb;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
-    return s;
+    return wave_sum_f32((float)ha + (float)hb);
 }
 
 }  // namespace exl3

@@ -123,8 +123,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int kb = b1 - b0;
     const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
     const uint32_t* sp = a.tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
-    uint32_t A[K], B[K];
-    strip_prefetch<K>(sp, rs, wave, kb * 8, 4, lane, A, B);          // weight loads in flight during phase 1
+    StripRing<K, kLinearRing> ring;
+    strip_prefetch<K, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, ring);   // weight loads in flight during phase 1
 
     // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums
     for (int i = wave; i < M * kb; i += 4) {
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     float acc[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.f;
-    strip_gemv_run<K, M>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, A, B);
+    strip_gemv_run<K, M, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
 
     // phase 3: reduce waves, then splits
 #pragma unroll

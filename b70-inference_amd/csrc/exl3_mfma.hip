@@ -204,8 +204,8 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
             float v = rs[p][rg];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
+            v += lane_xor<16>(v, lane);
+            v += lane_xor<32>(v, lane);
             if (wave == 0 && lane < 16) rsum[p * MB + 16 * rg + lane] = v;
         }
 #pragma unroll
@@ -330,8 +330,8 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
         float v = rs[rg];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
+        v += lane_xor<16>(v, lane);
+        v += lane_xor<32>(v, lane);
         if (wave == 0 && lane < 16) rsum[16 * rg + lane] = v;
     }
 #pragma unroll

@@ -143,6 +143,114 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     }
 }
 
+// Same tables for at most kAlignSmall pairs, one thread per pair: a pair's place in the expert-sorted order is the
+// number of valid pairs with a lower expert plus those of its own expert earlier in flat order; item and block indices
+// are counts of chunk leaders (a pair whose index within its expert is a multiple of MR, or of MB for MFMA blocks)
+// placed at or before it. No scan over E, a handful of barriers.
+constexpr int kAlignSmall = 256;
+
+__global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
+    __shared__ int s_e[kAlignSmall], s_pos[kAlignSmall];
+    __shared__ uint8_t s_lead[kAlignSmall], s_blead[kAlignSmall];
+    const int t = threadIdx.x;
+    const int np = r.M * r.slots;
+    int e = -1, tok = 0;
+    float wt = 0.f;
+    if (t < np) {
+        tok = t / r.slots;
+        const int j = t - tok * r.slots;
+        e = j < r.topk ? ldg(r.ids + tok * r.topk + j) : r.shared;
+        if (e >= r.E) e = -1;
+        wt = j < r.topk ? ldg(r.tw + tok * r.topk + j) : 1.0f;
+    }
+    s_e[t] = e;
+    __syncthreads();
+    int below = 0, before = 0, cnt = 0;
+    if (e >= 0)
+        for (int q = 0; q < np; ++q) {
+            const int eq = s_e[q];
+            below += eq >= 0 && eq < e;
+            before += eq == e && q < t;
+            cnt += eq == e;
+        }
+    const int pos = below + before;
+    const bool big = e >= 0 && r.use_mfma && cnt > r.MR;
+    const bool lead = e >= 0 && !big && before % r.MR == 0;
+    const bool blead = big && before % r.MB == 0;
+    s_pos[t] = e >= 0 ? pos : 0x7FFFFFFF;
+    s_lead[t] = lead;
+    s_blead[t] = blead;
+    __syncthreads();
+    int nitems = 0, nblocks = 0, item = 0, block = 0;
+    for (int q = 0; q < np; ++q) {
+        const int pq = s_pos[q];
+        if (s_lead[q]) {
+            ++nitems;
+            item += pq <= pos;
+        }
+        if (s_blead[q]) {
+            ++nblocks;
+            block += pq <= pos;
+        }
+    }
+    --item;
+    --block;
+    if (t < np) {
+        if (e >= 0) {
+            r.pair_tok[pos] = tok;
+            r.pair_w[pos] = wt;
+            r.pair_of[t] = pos;
+        } else {
+            r.pair_of[t] = -1;
+        }
+    }
+    if (r.items) {
+        if (lead) {
+            ItemDesc& d = r.items[item];
+            d.e = e;
+            d.p0 = pos;
+            d.cnt = min(r.MR, cnt - before);
+            for (int i = 0; i < 9; ++i) d.tab[i] = ldg(r.tables + (int64_t)i * r.E + e);
+            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? ldg(r.kmaps + (int64_t)i * r.E + e) : 0;
+        }
+        if (e >= 0 && !big) {
+            ItemDesc& d = r.items[item];
+            d.tok[before % r.MR] = tok;
+            d.w[before % r.MR] = wt;
+        }
+        for (int it = nitems + t; it < r.max_items; it += kAlignSmall) r.items[it].cnt = 0;
+        if (t == 0 && r.n_items) r.n_items[0] = nitems;
+    }
+    if (r.blocks) {
+        if (blead) {
+            ItemDesc& d = r.blocks[block];
+            d.e = e;
+            d.p0 = pos;
+            d.cnt = min(r.MB, cnt - before);
+            for (int i = 0; i < 9; ++i) d.tab[i] = ldg(r.tables + (int64_t)i * r.E + e);
+            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? ldg(r.kmaps + (int64_t)i * r.E + e) : 0;
+        }
+        for (int b = nblocks + t; b < r.max_blocks; b += kAlignSmall) r.blocks[b].cnt = 0;
+    }
+    if (r.counts)
+        for (int x = t; x < r.E; x += kAlignSmall) {
+            int c = 0;
+            for (int q = 0; q < np; ++q) c += s_e[q] == x;
+            r.counts[x] = c;
+        }
+    if (r.tok_nvalid)
+        for (int tk = t; tk < r.M; tk += kAlignSmall) {
+            int nv = 0;
+            for (int j = 0; j < r.slots; ++j) nv += s_e[tk * r.slots + j] >= 0;
+            r.tok_nvalid[tk] = nv;
+            if (nv == 0)
+                for (int c = 0; c < r.H; ++c) {
+                    if (r.out_f32) reinterpret_cast<float*>(r.out)[(int64_t)tk * r.out_ld + c] = 0.f;
+                    else reinterpret_cast<uint16_t*>(r.out)[(int64_t)tk * r.out_ld + c] = 0;
+                }
+        }
+}
+
 // ================================================================================================ gate | up
 template <int K, int MR>
 __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
@@ -165,8 +273,8 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     constexpr int KL = K > 0 ? K : 1;
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
-    uint32_t PA[KL], PB[KL];
-    if (K > 0) strip_prefetch<KL>(sp, rs, half, kb * 8, 2, lane, PA, PB);
+    StripRing<KL, 3> ring;
+    if (K > 0) strip_prefetch<KL, 3>(sp, rs, half, kb * 8, 2, lane, ring);
 
     // phase 1: both projections' input transforms for the item's rows
     for (int i = wave; i < 2 * MR * kb; i += 4) {
@@ -184,7 +292,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR>(sp, rs, half, kb * 8, 2, lane, &xs[proj][0][0], kGemvKBMax * 128, acc, PA, PB);
+        strip_gemv_run<KL, MR, 3>(sp, rs, half, kb * 8, 2, lane, &xs[proj][0][0], kGemvKBMax * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[2 * proj]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[2 * proj + 1]);
@@ -273,8 +381,8 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     constexpr int KL = K > 0 ? K : 1;
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
-    uint32_t PA[KL], PB[KL];
-    if (K > 0) strip_prefetch<KL>(sp, rs, wave, kb * 8, 4, lane, PA, PB);
+    StripRing<KL, 3> ring;
+    if (K > 0) strip_prefetch<KL, 3>(sp, rs, wave, kb * 8, 4, lane, ring);
 
     for (int i = wave; i < MR * kb; i += 4) {
         const int m = i / kb, b = i - m * kb;
@@ -288,7 +396,7 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, PA, PB);
+        strip_gemv_run<KL, MR, 3>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[4]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[5]);
@@ -353,62 +461,19 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
 }
 
 // ================================================================================================ router
-// One wave per row. The row's keys z = logits + bias sit in LDS; softmax statistics over them, then k rounds of a
-// DPP wave argmax: the largest key (order-preserving uint map) and, among lanes holding it, the lowest expert index.
-// A picked key is overwritten with NaN, which never compares greater or equal, so it is not picked again.
+// One wave per row (route_row).
+template <int V>
 __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, int64_t ld, int E,
                                                    const float* __restrict__ bias, int k, int32_t* __restrict__ ids,
                                                    float* __restrict__ w) {
-    extern __shared__ float zs[];
     const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
-    const float* z = logits + row * ld;
-    float mx = -INFINITY;
-    for (int i = lane; i < E; i += 64) {
-        const float v = z[i] + (bias ? bias[i] : 0.f);
-        zs[i] = v;
-        mx = fmaxf(mx, v);
-    }
-    const uint32_t mk = wave_max_u32(float_key(mx));
-    mx = __builtin_bit_cast(float, (mk & 0x80000000u) ? (mk & 0x7FFFFFFFu) : ~mk);
-    float sum = 0.f;
-    for (int i = lane; i < E; i += 64) sum += expf(zs[i] - mx);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) sum += __shfl_xor(sum, m);
-    __syncthreads();
-    float ptaken = 0.f;
-    int taken = -1;
-    for (int j = 0; j < k; ++j) {
-        float best = -INFINITY;
-        int bi = 0x7FFFFFFF;
-        for (int i = lane; i < E; i += 64) {
-            const float v = zs[i];
-            if (v > best) {                      // ascending i: a tie keeps the lower index
-                best = v;
-                bi = i;
-            }
-        }
-        if (bi == 0x7FFFFFFF) best = -INFINITY;
-        const uint32_t kmax = wave_max_u32(bi == 0x7FFFFFFF ? 0u : float_key(best));
-        const uint32_t cand = (bi != 0x7FFFFFFF && float_key(best) == kmax) ? (uint32_t)bi : 0xFFFFFFFFu;
-        const int win = (int)wave_min_u32(cand);
-        if (win >= 0 && win < E) {
-            const float vb = zs[win];
-            if (lane == j) {
-                taken = win;
-                ptaken = expf(vb - mx) / sum;
-            }
-        }
-        __syncthreads();
-        if (lane == 0 && win >= 0 && win < E) zs[win] = __builtin_nanf("");
-        __syncthreads();
-    }
-    float s = lane < k ? ptaken : 0.f;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    int id;
+    float wt;
+    route_row<V>(logits + row * ld, bias, E, k, lane, id, wt);
     if (lane < k) {
-        ids[row * k + lane] = taken;
-        w[row * k + lane] = ptaken / (s + 1e-20f);
+        ids[row * k + lane] = id;
+        w[row * k + lane] = wt;
     }
 }
 
@@ -433,6 +498,10 @@ __global__ __launch_bounds__(256) void act_mul_kernel(const void* __restrict__ x
 static size_t align_lds_bytes(int E) { return (size_t)(5 * E + 1024) * sizeof(int); }
 
 int launch_align(const RouteArgs& r, hipStream_t st) {
+    if ((int64_t)r.M * r.slots <= kAlignSmall) {
+        EXL3_LAUNCH("moe_align", align_small_kernel, dim3(1), dim3(kAlignSmall), 0, st, r);
+        return EXL3_OK;
+    }
     const size_t lds = align_lds_bytes(r.E);
     EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), lds, st, r);
     return EXL3_OK;
@@ -499,6 +568,8 @@ static moe_fn down_select(int K, int MR) {
 
 int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st);   // exl3_mfma.hip
 int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st);
+bool moe_fused_ok(const MoeArgs& a);                            // exl3_moe_fused.hip
+int moe_fused_path(const MoeArgs& a, hipStream_t st);
 
 // One layer call: align, then GEMV items (experts with <= MR rows) and MFMA blocks (more rows), gate|up before down.
 // `a` has every field but the route / workspace ones set.
@@ -630,6 +701,7 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.out_ld = out_ld;
     a.out_f32 = out_dtype == EXL3_F32;
     const int64_t npairs = M * a.slots;
+    if (moe_fused_ok(a)) return moe_fused_path(a, (hipStream_t)stream);
     a.MR = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
     // An expert has at most npairs rows; with more than MR possible rows per expert (M > MR or duplicates), experts
     // with more than MR rows go to the MFMA kernels and every other expert is one GEMV item.
@@ -688,8 +760,11 @@ int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t 
     if (M == 0) return EXL3_OK;
     EXL3_CHECK_ARG(logits && ids && w, "exl3_route_softmax_topk: null pointer");
     EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_softmax_topk: too many rows");
-    EXL3_LAUNCH("route_softmax_topk", route_kernel, dim3((unsigned)M), dim3(64), (size_t)E * sizeof(float),
-                (hipStream_t)stream, logits, ld, (int)E, bias, (int)k, ids, w);
+    void (*kern)(const float*, int64_t, int, const float*, int, int32_t*, float*) =
+        E <= 64 ? route_kernel<1> : E <= 128 ? route_kernel<2> : E <= 256 ? route_kernel<4> : E <= 512 ? route_kernel<8>
+        : E <= 1024 ? route_kernel<16> : E <= 2048 ? route_kernel<32> : E <= 4096 ? route_kernel<64> : route_kernel<128>;
+    EXL3_LAUNCH("route_softmax_topk", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E,
+                bias, (int)k, ids, w);
     return EXL3_OK;
 }
 

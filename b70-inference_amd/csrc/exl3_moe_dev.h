@@ -47,4 +47,68 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
     if (lane == 0) a.cnt_tok[(size_t)t * (a.H / 128) + nb] = 0;
 }
 
+// Softmax + top-k of one row by one wave (trellis-serve.patch:395-441): z = logits + bias in fp32; experts ranked by
+// z descending, exact ties to the lower index; p = exp(z - max) / sum exp(z - max) over the row; the k picks are
+// renormalised w = p / (sum of picked p + 1e-20). Lane l keeps the order keys of entries l + 64 v (v < V, E <= 64 V)
+// in registers; picked and padding entries hold key 0, NaN logits key 1 (below every number, still pickable, as a
+// stable descending sort places them last). Each round is one DPP wave max, a ballot of the lanes holding it, and a
+// DPP wave min of their lowest indices only when several lanes tie. Lane j < k returns pick j in (id, w).
+template <int V>
+__device__ __forceinline__ void route_row(const float* __restrict__ z, const float* __restrict__ bias, int E, int k,
+                                          int lane, int& id, float& w) {
+    uint32_t key[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int i = lane + 64 * v;
+        uint32_t kk = 0u;
+        if (i < E) {
+            const float f = ldg(z + i) + (bias ? ldg(bias + i) : 0.f);
+            kk = f != f ? 1u : float_key(f);
+        }
+        key[v] = kk;
+    }
+    uint32_t lmax = 0u;
+#pragma unroll
+    for (int v = 0; v < V; ++v) lmax = max(lmax, key[v]);
+    const float mx = key_float(wave_max_u32(lmax));
+    float se = 0.f;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+        if (key[v] != 0u) se += expf(key_float(key[v]) - mx);
+    const float sum = wave_sum_f32(se);
+
+    uint32_t tkey = 0u;
+    id = -1;
+    for (int j = 0; j < k; ++j) {
+        uint32_t best = 0u;
+        int bv = 0;
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+            if (key[v] > best) {          // ascending v: a lane keeps its lowest index among equal keys
+                best = key[v];
+                bv = v;
+            }
+        const uint32_t kmax = wave_max_u32(best);
+        if (kmax == 0u) break;            // fewer than k entries (k <= E is checked on the host)
+        const uint64_t mask = __ballot(best == kmax);
+        const int mine = lane + 64 * bv;
+        int widx;
+        if (__popcll(mask) == 1) widx = __builtin_amdgcn_readlane(mine, __ffsll((unsigned long long)mask) - 1);
+        else widx = (int)wave_min_u32(best == kmax ? (uint32_t)mine : 0xFFFFFFFFu);
+        if (lane == (widx & 63)) {
+            const int vv = widx >> 6;
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                if (v == vv) key[v] = 0u;
+        }
+        if (lane == j) {
+            id = widx;
+            tkey = kmax;
+        }
+    }
+    const float p = id >= 0 ? expf(key_float(tkey) - mx) / sum : 0.f;
+    const float s = wave_sum_f32(p);
+    w = p / (s + 1e-20f);
+}
+
 }  // namespace exl3

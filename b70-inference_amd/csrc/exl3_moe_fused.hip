@@ -1,0 +1,598 @@
+// Fused small-batch MoE layer on gfx950: gate|up, activation, down and combine in ONE launch.
+//
+// For decode batches (at most 8 tokens, at most kFusedMaxPairs (token, slot) pairs) the multi-kernel path is a chain
+// of short latency-bound launches. Here every workgroup:
+//   1. reads the routing ids (pair l in lane l and l + 64 of every wave) and groups the pairs by expert in
+//      registers: a pair's index among its expert's pairs in flat order comes from a readlane sweep, items are
+//      chunks of up to MR such pairs (the reference's per-expert row groups, glm/xpu/csrc/exl3_moe.n128.sycl:691-734)
+//      numbered by a ballot over their first pairs, and the job's item, expert and rows follow from ballots. No align
+//      launch and no barrier; rows keep their flat pair index as row id.
+//   2. runs job blockIdx.x: [0, J_gu) are gate|up jobs (item, 128-column block of I, k-split of H), [J_gu, J_gu + J_d)
+//      down jobs (item, 128-column block of H, k-split of I), item-major. A gate|up job streams both strips and, in
+//      the last split to arrive, applies the reference's GateUpKernel epilogue (Hadamard * svh, act, * suh_d,
+//      Hadamard: exl3_moe.n128.sycl:253-271) and publishes the item's down input. A down job prefetches its first
+//      weight rows, waits until every column block of its item's down input is published, streams, and in the last
+//      split writes the weighted rows y; the workgroup that completes a token's slots sums them in slot order
+//      (exl3_moe.n128.sycl:385-410).
+// Progress: gate|up jobs never wait and have lower workgroup ids than every down job. Workgroups are dispatched in id
+// order within each XCD (ids round-robin over the XCDs), so a waiting down job only waits for gate|up workgroups that
+// its XCD or another has already dispatched or will dispatch before any of its own down jobs. The wait is also
+// bounded: a timeout sets an error word instead of hanging. Cross-workgroup data (partials, down inputs, y) moves
+// with agent-scope stores and loads that write through the XCD-local L2, published by counters after the stores have
+// drained (the split-K handoff). Every counter sits on its own 128-byte line.
+#include "exl3_device.h"
+#include "exl3_gemv.h"
+#include "exl3_moe.h"
+#include "exl3_moe_dev.h"
+#include "exl3_runtime.h"
+
+namespace exl3 {
+
+constexpr int kFusedMaxPairs = 128;
+constexpr int kFusedMaxRows = 8;
+constexpr int kSpinMax = 1 << 18;       // polls of a down job's wait (each backs off up to ~2000 cycles)
+constexpr int kCS = 32;                 // counter stride in ints (one 128-byte line per counter)
+#ifndef EXL3_FUSED_RING
+#define EXL3_FUSED_RING 4
+#endif
+constexpr int kFusedRing = EXL3_FUSED_RING;   // GEMV register ring depth (loads run kFusedRing - 1 tile-rows ahead)
+
+struct FusedArgs {
+    const uint16_t* x;
+    int64_t x_ld;
+    int M, H, I, topk, slots, E, shared, np;
+    const int32_t* ids;
+    const float* tw;
+    const int64_t* tables;              // [9][E]
+    const int64_t* kmaps;               // [6][E] or null
+    int act;
+    float limit;
+    float* abuf;                        // [max_items][MR][I] down input (fp16 values held in fp32)
+    float* y;                           // [np][H] weighted expert outputs
+    float* part_gu;                     // [max_items * nbI][P_gu][2][MR][128]
+    float* part_d;                      // [max_items * nbH][P_d][MR][128]
+    int* cnt_gu;                        // [max_items * nbI] * kCS
+    int* cnt_d;                         // [max_items * nbH] * kCS
+    int* cnt_tok;                       // [M * nbH] * kCS
+    int* cnt_item;                      // [max_items] * kCS
+    int* err;                           // set when a wait times out
+    int P_gu, P_d, nblk_h, nblk_i, J_gu, J_d, max_items;
+    void* out;
+    int64_t out_ld;
+    int out_f32;
+};
+
+__device__ __forceinline__ int atomic_add_agent(int* p, int v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int atomic_load_agent(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_store_agent(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MR>
+struct FusedShared {
+    static constexpr int KBF = MR <= 4 ? 8 : 4;        // k-blocks (128 rows) per job split
+    _Float16 xs[2][MR][KBF * 128];
+    float red[4][MR][2][64];
+    float bsum[2][MR][KBF];
+    _Float16 su[2][KBF * 128];          // gate / up input sign vectors of the job's k range
+    int ge[4][kFusedMaxPairs];          // each wave's copy of the pairs' experts (grouping sweep)
+    int rows[MR];                       // flat pair index of each row of the job's item
+    int comb[MR];
+    int flag;
+};
+
+// The job's item as every wave sees it (uniform values; its rows are in FusedShared::rows).
+struct Item {
+    int e, cnt;                         // expert, rows
+    uint64_t v0, v1;                    // valid pairs (pair l: bit l of v0, pair 64 + l: bit l of v1)
+    int64_t tab[9];                     // the expert's (trellis, suh, svh) addresses for gate, up, down
+    int64_t km[6];                      // (kmap, woff) addresses when K is per tile
+};
+
+// Expert of pair p, -1 for none (p >= np, a negative id, the absent shared expert). The id load is unconditional
+// (clamped index) so that both of a lane's loads are in flight together.
+__device__ __forceinline__ int pair_expert(const FusedArgs& a, int p) {
+    const int pc = p < a.np ? p : a.np - 1;
+    const int tok = pc / a.slots, j = pc - tok * a.slots;
+    const int v = a.topk > 0 ? ldg(a.ids + tok * a.topk + (j < a.topk ? j : a.topk - 1)) : 0;
+    const int e = j < a.topk ? v : a.shared;
+    return p < a.np && e < a.E ? e : -1;
+}
+
+__device__ __forceinline__ float pair_weight(const FusedArgs& a, int p) {
+    const int tok = p / a.slots, j = p - tok * a.slots;
+    return j < a.topk ? ldg(a.tw + tok * a.topk + j) : 1.0f;
+}
+
+__device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
+__device__ __forceinline__ int ctz64(uint64_t m) { return __ffsll((unsigned long long)m) - 1; }
+// set bits of (lo, hi) in [b, b + n) (a 128-bit mask; n <= 64)
+__device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n) {
+    int c = 0;
+    for (int i = b; i < b + n; ++i) c += (int)(((i < 64 ? lo >> i : hi >> (i - 64))) & 1);
+    return c;
+}
+
+// Groups the pairs and returns the number of items; fills `it` and rows[] for item `item` when it exists. Every wave
+// runs it and writes the same rows, so a wave may read rows[] right after without a barrier.
+// `ge` is the wave's own 128-int LDS slice (written and read by this wave only: LDS keeps a wave's accesses in order).
+template <int MR>
+__device__ __forceinline__ int group_pairs(const FusedArgs& a, int item, int lane, Item& it, int* rows, int* ge) {
+    const int np = a.np;
+    const int l1 = lane + 64;
+    const int e0 = pair_expert(a, lane);
+    const int e1 = pair_expert(a, l1);
+    ge[lane] = e0;
+    ge[l1] = e1;
+    int bf0 = 0, bf1 = 0;
+    for (int q4 = 0; q4 < np; q4 += 4) {          // entries past np are -1 and only match lanes without a pair
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ge + q4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int eq = (int)v[k], q = q4 + k;
+            bf0 += (eq == e0) & (q < lane);
+            bf1 += (eq == e1) & (q < l1);
+        }
+    }
+    const uint64_t L0 = __ballot(e0 >= 0 && bf0 % MR == 0), L1 = __ballot(e1 >= 0 && bf1 % MR == 0);
+    it.v0 = __ballot(e0 >= 0);
+    it.v1 = __ballot(e1 >= 0);
+    const int n0 = popc64(L0), nitems = n0 + popc64(L1);
+    if (item >= nitems) return nitems;
+    // first pair of the item: the item-th set bit of (L0, L1)
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    const uint64_t s0 = __ballot(((L0 >> lane) & 1) && popc64(L0 & below) == item);
+    const uint64_t s1 = __ballot(((L1 >> lane) & 1) && n0 + popc64(L1 & below) == item);
+    const int p = s0 ? ctz64(s0) : 64 + ctz64(s1);
+    const int e = p < 64 ? __builtin_amdgcn_readlane(e0, p) : __builtin_amdgcn_readlane(e1, p - 64);
+    const int bfp = p < 64 ? __builtin_amdgcn_readlane(bf0, p) : __builtin_amdgcn_readlane(bf1, p - 64);
+    const int ce = popc64(__ballot(e0 == e)) + popc64(__ballot(e1 == e));
+    it.e = e;
+    it.cnt = min(MR, ce - bfp);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) it.tab[i] = ldg(a.tables + (int64_t)i * a.E + e);
+    if (a.kmaps)
+#pragma unroll
+        for (int i = 0; i < 6; ++i) it.km[i] = ldg(a.kmaps + (int64_t)i * a.E + e);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const uint64_t r0 = __ballot(e0 == e && bf0 == bfp + m), r1 = __ballot(e1 == e && bf1 == bfp + m);
+        if (lane == 0) rows[m] = m < it.cnt ? (r0 ? ctz64(r0) : 64 + ctz64(r1)) : 0;
+    }
+    return nitems;
+}
+
+// sum over pp < P of the partials at base + pp * stride + off (agent-scope loads, issued 16 at a time, added in pp order)
+template <int NV>
+__device__ __forceinline__ void sum_partials(const float* base, size_t stride, const int (&off)[NV], int P,
+                                             float (&acc)[NV]) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] = 0.f;
+    for (int p0 = 0; p0 < P; p0 += 16) {
+        float t[16][NV];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) t[i][v] = p0 + i < P ? splitk_load(base + (size_t)(p0 + i) * stride + off[v]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) acc[v] += t[i][v];
+    }
+}
+
+template <int K, int MR>
+__device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
+                                             int nb, int p) {
+    constexpr int KBF = FusedShared<MR>::KBF;
+    constexpr int KL = K > 0 ? K : 1;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cnt = it.cnt;
+    const int nbI = a.I / 128;
+    const int b0 = (int)((int64_t)p * a.nblk_h / a.P_gu), b1 = (int)((int64_t)(p + 1) * a.nblk_h / a.P_gu);
+    const int kb = b1 - b0;
+    const int proj = wave >> 1, half = wave & 1;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(proj ? it.tab[3] : it.tab[0]);
+    const int tn = a.I / 16;
+    const size_t rs = (size_t)tn * (8 * KL);
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    StripRing<KL, kFusedRing> ring;
+    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, half, kb * 8, 2, lane, ring);
+
+    // stage the k range of the item's x rows (16-byte loads; rows past cnt are zero) in xs[1] and both input sign
+    // vectors in su, all loads of a thread in flight together
+    {
+        const int k0 = b0 * 128, nch = kb * 16;                  // 16-byte chunks per row
+        const uint16_t* sg = reinterpret_cast<const uint16_t*>(it.tab[1]) + k0;
+        const uint16_t* su = reinterpret_cast<const uint16_t*>(it.tab[4]) + k0;
+        for (int c = threadIdx.x; c < MR * nch; c += 256) {
+            const int m = c / nch, o = c - m * nch;
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (m < cnt)
+                v = ldg(reinterpret_cast<const u32x4_t*>(a.x + (int64_t)(s.rows[m] / a.slots) * a.x_ld + k0) + o);
+            *reinterpret_cast<u32x4_t*>(&s.xs[1][m][o * 8]) = v;
+        }
+        for (int c = threadIdx.x; c < kb * 128; c += 256) {
+            s.su[0][c] = __builtin_bit_cast(_Float16, ldg(sg + c));
+            s.su[1][c] = __builtin_bit_cast(_Float16, ldg(su + c));
+        }
+    }
+    __syncthreads();
+    // input transform of block (m, b) for both projections by one wave: xs[0] <- gate, xs[1] <- up (in place)
+    for (int i = wave; i < MR * kb; i += 4) {
+        const int m = i / kb, b = i - m * kb;
+        _Float16* xg = &s.xs[0][m][b * 128];
+        _Float16* xu = &s.xs[1][m][b * 128];
+        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
+        if (m < cnt) {
+            const float xa = (float)xu[lane], xb = (float)xu[lane + 64];
+            ga = (float)(_Float16)(xa * (float)s.su[0][b * 128 + lane]);
+            gb = (float)(_Float16)(xb * (float)s.su[0][b * 128 + lane + 64]);
+            ua = (float)(_Float16)(xa * (float)s.su[1][b * 128 + lane]);
+            ub = (float)(_Float16)(xb * (float)s.su[1][b * 128 + lane + 64]);
+            fwht128_wave(ga, gb, lane);
+            fwht128_wave(ua, ub, lane);
+        }
+        const _Float16 hga = (_Float16)(ga * kRsqrt128), hgb = (_Float16)(gb * kRsqrt128);
+        const _Float16 hua = (_Float16)(ua * kRsqrt128), hub = (_Float16)(ub * kRsqrt128);
+        xg[lane] = hga;
+        xg[lane + 64] = hgb;
+        xu[lane] = hua;
+        xu[lane + 64] = hub;
+        const float sg = wave_sum_f32((float)hga + (float)hgb), su = wave_sum_f32((float)hua + (float)hub);
+        if (lane == 0) {
+            s.bsum[0][m][b] = sg;
+            s.bsum[1][m][b] = su;
+        }
+    }
+    __syncthreads();
+
+    float acc[MR][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
+    if (K > 0) {
+        strip_gemv_run<KL, MR, kFusedRing>(sp, rs, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128, acc, ring);
+    } else {
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(proj ? it.km[2] : it.km[0]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(proj ? it.km[3] : it.km[1]);
+        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128,
+                             acc);
+    }
+
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        s.red[wave][m][0][lane] = acc[m][0];
+        s.red[wave][m][1][lane] = acc[m][1];
+    }
+    __syncthreads();
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    const size_t slot = (size_t)item * nbI + nb;
+    if (half == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float sx = 0.f;
+            for (int b = 0; b < kb; ++b) sx += s.bsum[proj][m][b];
+            float* dst = a.part_gu + (((slot * a.P_gu + p) * 2 + proj) * MR + m) * 128;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float v = s.red[wave][m][h][lane] + s.red[wave + 1][m][h][lane];
+                splitk_store(dst + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+            }
+        }
+    }
+    if (!splitk_arrive(&a.cnt_gu[slot * kCS], a.P_gu, &s.flag)) return;
+
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(it.tab[2]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(it.tab[5]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(it.tab[7]) + nb * 128;
+    const float sg0 = h2f(ldg(svg + lane)), sg1 = h2f(ldg(svg + lane + 64));
+    const float su0 = h2f(ldg(svu + lane)), su1 = h2f(ldg(svu + lane + 64));
+    const float sd0 = h2f(ldg(sud + lane)), sd1 = h2f(ldg(sud + lane + 64));
+    for (int m = wave; m < cnt; m += 4) {
+        const int off[4] = {m * 128 + lane, m * 128 + lane + 64, (MR + m) * 128 + lane, (MR + m) * 128 + lane + 64};
+        float v[4];
+        sum_partials<4>(a.part_gu + slot * a.P_gu * 2 * MR * 128, 2 * MR * 128, off, a.P_gu, v);
+        float g0 = v[0], g1 = v[1], u0 = v[2], u1 = v[3];
+        fwht128_wave(g0, g1, lane);
+        fwht128_wave(u0, u1, lane);
+        g0 = (float)(_Float16)(g0 * kRsqrt128 * sg0);
+        g1 = (float)(_Float16)(g1 * kRsqrt128 * sg1);
+        u0 = (float)(_Float16)(u0 * kRsqrt128 * su0);
+        u1 = (float)(_Float16)(u1 * kRsqrt128 * su1);
+        float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
+        float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
+        a0 = (float)(_Float16)(a0 * sd0);
+        a1 = (float)(_Float16)(a1 * sd1);
+        fwht128_wave(a0, a1, lane);
+        float* dst = a.abuf + ((size_t)item * MR + m) * a.I + nb * 128;
+        splitk_store(dst + lane, (float)(_Float16)(a0 * kRsqrt128));
+        splitk_store(dst + lane + 64, (float)(_Float16)(a1 * kRsqrt128));
+    }
+    __builtin_amdgcn_s_waitcnt(0);      // this wave's down-input stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        a.cnt_gu[slot * kCS] = 0;
+        atomic_add_agent(&a.cnt_item[item * kCS], 1);
+    }
+}
+
+template <int K, int MR>
+__device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
+                                           int nb, int p) {
+    constexpr int KBF = FusedShared<MR>::KBF;
+    constexpr int KL = K > 0 ? K : 1;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cnt = it.cnt;
+    const int nbI = a.I / 128, nbH = a.H / 128;
+    const int b0 = (int)((int64_t)p * a.nblk_i / a.P_d), b1 = (int)((int64_t)(p + 1) * a.nblk_i / a.P_d);
+    const int kb = b1 - b0;
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(it.tab[6]);
+    const int tn = a.H / 16;
+    const size_t rs = (size_t)tn * (8 * KL);
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    StripRing<KL, kFusedRing> ring;
+    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, wave, kb * 8, 4, lane, ring);
+
+    // wait for the item's down input (all nbI column blocks), then count this job as a consumer; the last consumer
+    // clears the item counter for the next call
+    if (threadIdx.x == 0) {
+        int* c = &a.cnt_item[item * kCS];
+        int n = 0, back = 1;
+        while (atomic_load_agent(c) < nbI) {
+            if (++n > kSpinMax) {
+                atomic_store_agent(a.err, 1);
+                break;
+            }
+            for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(4);
+            back = back < 8 ? 2 * back : 8;
+        }
+        const int old = atomic_add_agent(c, 1);
+        if (old == nbI + nbH * a.P_d - 1) atomic_store_agent(c, 0);
+    }
+    __syncthreads();
+
+    // the wave's blocks (m, b) = (i / kb, i % kb), i = wave, wave + 4, ...: every load first, then convert and sum
+    constexpr int NBW = (MR * KBF + 3) / 4;
+    float va[NBW], vb[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const int i = wave + 4 * j, m = i / kb, b = i - m * kb;
+        va[j] = vb[j] = 0.f;
+        if (i < MR * kb && m < cnt) {
+            const float* src = a.abuf + ((size_t)item * MR + m) * a.I + (b0 + b) * 128;
+            va[j] = splitk_load(src + lane);
+            vb[j] = splitk_load(src + lane + 64);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const int i = wave + 4 * j, m = i / kb, b = i - m * kb;
+        if (i < MR * kb) {
+            const _Float16 ha = (_Float16)va[j], hb = (_Float16)vb[j];
+            s.xs[0][m][b * 128 + lane] = ha;
+            s.xs[0][m][b * 128 + lane + 64] = hb;
+            const float bs = wave_sum_f32((float)ha + (float)hb);
+            if (lane == 0) s.bsum[0][m][b] = bs;
+        }
+    }
+    __syncthreads();
+
+    float acc[MR][2];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
+    if (K > 0) {
+        strip_gemv_run<KL, MR, kFusedRing>(sp, rs, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc, ring);
+    } else {
+        const uint8_t* km = reinterpret_cast<const uint8_t*>(it.km[4]);
+        const int32_t* wo = reinterpret_cast<const int32_t*>(it.km[5]);
+        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc);
+    }
+
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        s.red[wave][m][0][lane] = acc[m][0];
+        s.red[wave][m][1][lane] = acc[m][1];
+    }
+    __syncthreads();
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    const size_t slot = (size_t)item * nbH + nb;
+    if (wave == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float sx = 0.f;
+            for (int b = 0; b < kb; ++b) sx += s.bsum[0][m][b];
+            float* dst = a.part_d + ((slot * a.P_d + p) * MR + m) * 128;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float v = s.red[0][m][h][lane] + s.red[1][m][h][lane] + s.red[2][m][h][lane] +
+                                s.red[3][m][h][lane];
+                splitk_store(dst + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+            }
+        }
+    }
+    if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) return;
+
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(it.tab[8]) + nb * 128;
+    const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
+    for (int m = wave; m < cnt; m += 4) {
+        const int pr = s.rows[m];
+        const float w = pair_weight(a, pr);
+        const int off[2] = {m * 128 + lane, m * 128 + lane + 64};
+        float v[2];
+        sum_partials<2>(a.part_d + slot * a.P_d * MR * 128, MR * 128, off, a.P_d, v);
+        float v0 = v[0], v1 = v[1];
+        fwht128_wave(v0, v1, lane);
+        float* dst = a.y + (size_t)pr * a.H + nb * 128;
+        splitk_store(dst + lane, v0 * kRsqrt128 * sd0 * w);
+        splitk_store(dst + lane + 64, v1 * kRsqrt128 * sd1 * w);
+    }
+    if (threadIdx.x == 0) a.cnt_d[slot * kCS] = 0;
+
+    // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int m = 0; m < cnt; ++m) {
+            const int t = s.rows[m] / a.slots;
+            const int nv = popc_range(it.v0, it.v1, t * a.slots, a.slots);
+            const int old = atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
+            s.comb[m] = (old == nv - 1) ? t : -1;
+        }
+    }
+    __syncthreads();
+    for (int m = wave; m < cnt; m += 4) {
+        const int t = s.comb[m];
+        if (t < 0) continue;
+        const int c0 = nb * 128 + lane, c1 = c0 + 64;
+        float v0 = 0.f, v1 = 0.f;
+        for (int j = 0; j < a.slots; ++j) {
+            const int pr = t * a.slots + j;
+            if (!(((pr < 64 ? it.v0 >> pr : it.v1 >> (pr - 64))) & 1)) continue;
+            const float* yr = a.y + (size_t)pr * a.H;
+            v0 += splitk_load(yr + c0);
+            v1 += splitk_load(yr + c1);
+        }
+        if (a.out_f32) {
+            float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
+            o[c0] = v0;
+            o[c1] = v1;
+        } else {
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
+            o[c0] = f2h(v0);
+            o[c1] = f2h(v1);
+        }
+        if (lane == 0) a.cnt_tok[((size_t)t * nbH + nb) * kCS] = 0;
+    }
+}
+
+template <int K, int MR>
+__global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
+    __shared__ __attribute__((aligned(16))) FusedShared<MR> s;
+    const int lane = threadIdx.x & 63;
+    const int job = blockIdx.x;
+    const bool gu = job < a.J_gu;
+    const int jj = gu ? job : job - a.J_gu;
+    const int nbo = gu ? a.I / 128 : a.H / 128, P = gu ? a.P_gu : a.P_d;
+    const int item = jj / (nbo * P), rem = jj - item * (nbo * P), nb = rem / P, p = rem - nb * P;
+    Item it;
+    const int nitems = group_pairs<MR>(a, item, lane, it, s.rows, s.ge[threadIdx.x >> 6]);
+    if (job == 0) {
+        // tokens with no valid slot get a zero output row
+        for (int tk = 0; tk < a.M; ++tk) {
+            if (popc_range(it.v0, it.v1, tk * a.slots, a.slots)) continue;
+            for (int c = threadIdx.x; c < a.H; c += 256) {
+                if (a.out_f32) reinterpret_cast<float*>(a.out)[(int64_t)tk * a.out_ld + c] = 0.f;
+                else reinterpret_cast<uint16_t*>(a.out)[(int64_t)tk * a.out_ld + c] = 0;
+            }
+        }
+    }
+    if (item >= nitems) return;         // uniform
+    if (gu) fused_gateup<K, MR>(a, s, it, item, nb, p);
+    else fused_down<K, MR>(a, s, it, item, nb, p);
+}
+
+typedef void (*fused_fn)(FusedArgs);
+
+template <int MR>
+static fused_fn pick_fused(int K) {
+    switch (K) {
+        case 0: return moe_fused_kernel<0, MR>;
+        case 1: return moe_fused_kernel<1, MR>;
+        case 2: return moe_fused_kernel<2, MR>;
+        case 3: return moe_fused_kernel<3, MR>;
+        case 4: return moe_fused_kernel<4, MR>;
+        case 5: return moe_fused_kernel<5, MR>;
+        case 6: return moe_fused_kernel<6, MR>;
+        case 7: return moe_fused_kernel<7, MR>;
+        default: return moe_fused_kernel<8, MR>;
+    }
+}
+
+static int fused_splits(int units, int nblk, int kbf, int target) {
+    int P = (target + units - 1) / (units > 0 ? units : 1);
+    const int pmin = (nblk + kbf - 1) / kbf;
+    if (P < pmin) P = pmin;
+    if (P > nblk) P = nblk;
+    return P < 1 ? 1 : P;
+}
+
+// Eligible: gate, up and down share one K (or all per-tile), at most 8 tokens and kFusedMaxPairs pairs, x rows
+// 16-byte aligned.
+bool moe_fused_ok(const MoeArgs& a) {
+    return a.Kg == a.Kd && a.M <= kFusedMaxRows && (int64_t)a.M * a.slots <= kFusedMaxPairs &&
+           aligned(a.x, 16) && a.x_ld % 8 == 0 && env_int("EXL3MI_NO_FUSED", 0) == 0;
+}
+
+int moe_fused_path(const MoeArgs& m, hipStream_t st) {
+    FusedArgs a{};
+    a.x = m.x;
+    a.x_ld = m.x_ld;
+    a.M = m.M;
+    a.H = m.H;
+    a.I = m.I;
+    a.topk = m.topk;
+    a.slots = m.slots;
+    a.E = m.E;
+    a.shared = m.shared;
+    a.np = m.M * m.slots;
+    a.ids = m.ids;
+    a.tw = m.tw;
+    a.tables = m.tables;
+    a.kmaps = m.kmaps;
+    a.act = m.act;
+    a.limit = m.limit;
+    a.out = m.out;
+    a.out_ld = m.out_ld;
+    a.out_f32 = m.out_f32;
+    const int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
+    const int kbf = MR <= 4 ? 8 : 4;
+    // items <= sum over active experts of ceil(rows / MR) <= (pairs + active * (MR - 1)) / MR
+    const int active = a.np < a.E ? a.np : a.E;
+    int mi = (a.np + active * (MR - 1)) / MR;
+    a.max_items = mi < a.np ? mi : a.np;
+    const int nbI = a.I / 128, nbH = a.H / 128;
+    a.nblk_h = a.H / 128;
+    a.nblk_i = a.I / 128;
+    const int target = env_int("EXL3MI_FUSED_JOBS", 640);
+    a.P_gu = fused_splits(a.max_items * nbI, a.nblk_h, kbf, target);
+    a.P_d = fused_splits(a.max_items * nbH, a.nblk_i, kbf, target);
+    const int64_t jgu = (int64_t)a.max_items * nbI * a.P_gu, jd = (int64_t)a.max_items * nbH * a.P_d;
+    EXL3_CHECK_ARG(jgu + jd < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
+    a.J_gu = (int)jgu;
+    a.J_d = (int)jd;
+
+    const size_t mx = a.max_items, np = a.np;
+    const size_t bytes = carve_size(mx * MR * a.I, 4) + carve_size(np * a.H, 4) +
+                         carve_size(mx * nbI * a.P_gu * 2 * MR * 128, 4) + carve_size(mx * nbH * a.P_d * MR * 128, 4);
+    const size_t n_cnt = (mx * nbI + mx * nbH + (size_t)a.M * nbH + mx + 1) * kCS;
+    Workspace ws;
+    int rc = workspace(bytes, n_cnt, &ws);
+    if (rc) return rc;
+    Carve c{ws.scratch, ws.scratch_bytes};
+    a.abuf = c.take<float>(mx * MR * a.I);
+    a.y = c.take<float>(np * a.H);
+    a.part_gu = c.take<float>(mx * nbI * a.P_gu * 2 * MR * 128);
+    a.part_d = c.take<float>(mx * nbH * a.P_d * MR * 128);
+    if (!a.part_d) return fail(EXL3_ERR_INVALID, "moe: workspace carve failed");
+    int* cn = ws.counters;
+    a.cnt_gu = cn;
+    a.cnt_d = a.cnt_gu + mx * nbI * kCS;
+    a.cnt_tok = a.cnt_d + mx * nbH * kCS;
+    a.cnt_item = a.cnt_tok + (size_t)a.M * nbH * kCS;
+    a.err = a.cnt_item + mx * kCS;
+    fused_fn fn;
+    switch (MR) {
+        case 1: fn = pick_fused<1>(m.Kg); break;
+        case 2: fn = pick_fused<2>(m.Kg); break;
+        case 4: fn = pick_fused<4>(m.Kg); break;
+        default: fn = pick_fused<8>(m.Kg); break;
+    }
+    EXL3_LAUNCH("moe_fused", fn, dim3((unsigned)(jgu + jd)), dim3(256), 0, st, a);
+    return EXL3_OK;
+}
+
+}  // namespace exl3

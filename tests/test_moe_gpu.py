@@ -64,6 +64,32 @@ def test_moe_gelu_and_clamp(exl3, oracle, small):
     assert max_rel(y, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 8])
+def test_moe_fused_and_multi_kernel_paths(exl3, oracle, small, monkeypatch, M):
+    """Decode batches take the one-launch fused layer; EXL3MI_NO_FUSED=1 forces the align / gate|up / down launches.
+    Both meet the bar, with a shared expert, a repeated expert and an inactive slot."""
+    tables, orc = small
+    ids, w = _ids_w(M, 3, 11, 710 + M, dup=True, inactive=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(70 + M)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=11)
+    assert max_rel(y, ref) <= MAX_REL
+    monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    y2, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=11)
+    assert max_rel(y2, ref) <= MAX_REL
+
+
+def test_moe_fused_counters_reset_between_calls(exl3, small):
+    """The fused layer's job ticket and arrival counters are back at zero after every call: alternating batch sizes
+    and split counts reproduce the first results bit for bit."""
+    tables, _ = small
+    xs = {M: torch.randn(M, 256, generator=torch.Generator().manual_seed(90 + M)).half().cuda() for M in (1, 4, 8)}
+    rw = {M: _ids_w(M, 4, 12, 720 + M) for M in (1, 4, 8)}
+    first = {M: exl3.moe_forward(xs[M], rw[M][0].cuda(), rw[M][1].cuda(), tables) for M in (1, 4, 8)}
+    for M in (8, 1, 4, 4, 1, 8):
+        again = exl3.moe_forward(xs[M], rw[M][0].cuda(), rw[M][1].cuda(), tables)
+        assert torch.equal(again, first[M])
+
+
 def test_moe_deterministic(exl3, small):
     tables, _ = small
     ids, w = _ids_w(4, 4, 12, 703, dup=True)
@@ -135,6 +161,21 @@ def test_router_ties_bias_and_sizes(exl3, oracle):
         rid, rw = oracle.route_softmax_topk(logits.numpy(), 8, None if b is None else b.numpy())
         assert np.array_equal(ids.cpu().numpy(), rid)
         assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+
+
+@pytest.mark.parametrize("M,E,k", [(1, 1, 1), (3, 64, 64 // 2), (4, 100, 7), (4, 512, 10), (2, 1000, 16),
+                                   (2, 2048, 8), (1, 4096, 32), (2, 8192, 10)])
+def test_router_register_sizes(exl3, oracle, M, E, k):
+    """Every values-per-lane variant of the router (E up to 8192, k up to 32), with ties and -inf entries."""
+    g = torch.Generator().manual_seed(E * 31 + k)
+    logits = torch.randn(M, E, generator=g)
+    if E >= 8:
+        logits[0, torch.randperm(E, generator=g)[:3]] = 2.5      # exact ties, lower index first
+        logits[-1, torch.randperm(E, generator=g)[:2]] = float("-inf")
+    ids, w = exl3.route_softmax_topk(logits.cuda(), k, None)
+    rid, rw = oracle.route_softmax_topk(logits.numpy(), k, None)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
 
 
 def test_act_mul_ops(exl3, oracle):
