@@ -43,10 +43,11 @@ __device__ __forceinline__ void strip_tile_row(const uint32_t (&D)[K], int lane,
 }
 
 // Unconditional (the index is clamped to the last tile-row, nt > 0), so the waitcnt pass sees straight-line loads.
+// Offsets are 32-bit word counts (a projection's trellis holds fewer than 2^32 words; the host checks).
 template <int K>
-__device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __restrict__ base, size_t rs, int lt,
+__device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __restrict__ base, uint32_t rs, int lt,
                                            int nt) {
-    const size_t off = (size_t)(lt < nt ? lt : nt - 1) * rs;
+    const uint32_t off = (uint32_t)(lt < nt ? lt : nt - 1) * rs;
 #pragma unroll
     for (int i = 0; i < K; ++i) D[i] = ldg_nt(base + off + i);
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
@@ -67,7 +68,7 @@ __device__ __forceinline__ void strip_prefetch(const uint32_t* __restrict__ sp, 
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const int n = (nt - lt0 + step - 1) / step;
 #pragma unroll
-    for (int r = 0; r < R - 1; ++r) strip_load<K>(ring.D[r], base, rs * step, r, n);
+    for (int r = 0; r < R - 1; ++r) strip_load<K>(ring.D[r], base, (uint32_t)(rs * step), r, n);
 }
 
 template <int K, int M, int R>
@@ -77,7 +78,7 @@ __device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, 
     if (lt0 >= nt) return;
     const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
-    const size_t rstep = rs * step;
+    const uint32_t rstep = (uint32_t)(rs * step);
     int i = 0;
     for (; i + R <= n; i += R) {                         // branch-free body: loads stay R - 1 tile-rows ahead
 #pragma unroll

@@ -328,6 +328,8 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
     EXL3_CHECK_ARG(A && B && C && suh && svh, "exl3_gemm: null pointer");
     EXL3_CHECK_ARG(aligned(B, 4), "exl3_gemm: trellis must be 4-byte aligned");
     EXL3_CHECK_ARG(n / 128 <= 65535, "exl3_gemm: n too large");
+    EXL3_CHECK_ARG(k / 16 * (n / 16) * 8 * (int64_t)(K > 0 ? K : 8) < (1LL << 32),
+                   "exl3_gemm: trellis of %lld x %lld at K=%d exceeds 2^32 words", (long long)k, (long long)n, K);
     return launch_gemv(A, a_ld, m, k, reinterpret_cast<const uint32_t*>(B), n, K, C, c_ld, c_dtype == EXL3_F32, suh,
                        svh, (hipStream_t)stream);
 }

@@ -87,6 +87,15 @@ __device__ __forceinline__ void frag_load(const uint32_t* __restrict__ tw, const
     for (int i = 0; i < FragCfg<K>::NW; ++i) R[i] = ldg_nt(tw + c.widx[i]);
 }
 
+// First ring word (-1 .. 8K - 1) and funnel shift of lane `lane`'s fragment windows (see frag_decode).
+template <int K>
+__device__ __forceinline__ void frag_origin(int lane, int& w0, uint32_t& sh) {
+    const int q = lane & 7, h = (lane >> 3) & 1, rh = (lane >> 4) & 1;
+    const int start = (32 * q + 2 * rh + 4 * h + 1) * K - 16;
+    w0 = (start - 1) >> 5;
+    sh = (uint32_t)(32 - (start - 32 * w0));
+}
+
 template <int K>
 __device__ __forceinline__ h8_t frag_finish(uint32_t (&R)[FragCfg<K>::NW], uint32_t sh) {
     constexpr int NW = FragCfg<K>::NW;

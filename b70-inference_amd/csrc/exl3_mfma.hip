@@ -1,12 +1,17 @@
-// Expert-sorted ragged grouped GEMM on fp16 MFMA for experts with many rows (prefill chunks).
+// Expert-sorted ragged grouped GEMM on fp16 MFMA for prefill-sized calls.
 //
-// Rows (token, expert pairs) are grouped by expert and cut into blocks of MB rows. Per layer call:
-//   pairs_had   transformed gate / up inputs of every block row: xh[pair][proj] = fp16(H128(fp16(x * suh)) / sqrt(128))
-//   gateup      workgroup per (block, 128-column block of I), full H: each wave decodes two gate and two up tile
-//               columns per 32-k step straight into MFMA B fragments (the codebook affine is folded: B holds h values,
-//               the epilogue applies c1 * acc + c2 * rowsum(A)), then the fused activation / down-input epilogue
-//   down        workgroup per (block, 128-column block of H), full I, epilogue Hadamard * svh_d * w and the combine
-// Workgroup ids are laid out so that the column blocks of one expert block run on one XCD (shared L2 for A).
+// Rows (token, expert pairs) are grouped by expert and cut into blocks of up to kMfmaRows rows; in a prefill call
+// every expert with rows gets blocks (no GEMV items). Per layer call:
+//   pairs_had   transformed gate / up inputs of every block row, xh[pair][proj] = fp16(H128(fp16(x * suh)) / sqrt(128)),
+//               and their 128-blocks' sums (the codebook affine term)
+//   gateup      workgroup per (block, 128-column block of I), full H; each wave owns two gate and two up tile columns
+//               and decodes them straight into MFMA B fragments once per 32-k step (B holds h = 1024 + bytesum; the
+//               affine is applied as c1 * acc + c2 * rowsum(A) in the epilogue), then the fused activation / down-input
+//               epilogue (Hadamard * svh, act, * suh_d, Hadamard) per 16-row group
+//   down        workgroup per (block, 256-column block of H), full I, epilogue Hadamard * svh_d * w, then the combine
+// The A rows of the active row groups are staged through a two-stage LDS ring (loaded into registers two steps
+// ahead), weight words three steps ahead; one barrier per step. Workgroup ids are laid out so that the column blocks
+// of one row block run on one XCD (shared L2 for its A rows).
 // Semantics: the reference's GateUpDpasKernel / DownDpasKernel / moe_prefill (glm/xpu/csrc/exl3_moe.n128.sycl:
 // 472-689, 868-916) and exllamav3's exl3_moe (ext-op-inventory.md:1060-1093).
 #include "exl3_device.h"
@@ -26,12 +31,14 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     const int cnt = d->cnt;
     if (cnt == 0) return;
     const int p0 = d->p0;
+    const int nblk = a.H / 128;
     for (int i = wave; i < 2 * cnt; i += 4) {
         const int row = i >> 1, proj = i & 1;
         const int tok = a.pair_tok[p0 + row];
         const uint16_t* suh = reinterpret_cast<const uint16_t*>(d->tab[3 * proj + 1]) + kb * 128;
         _Float16* dst = a.xh + ((size_t)(p0 + row) * 2 + proj) * a.H + kb * 128;
-        had_in_block(a.x + (int64_t)tok * a.x_ld + kb * 128, suh, dst, lane);
+        const float bs = had_in_block(a.x + (int64_t)tok * a.x_ld + kb * 128, suh, dst, lane);
+        if (lane == 0) a.xsum[((size_t)(p0 + row) * 2 + proj) * nblk + kb] = bs;
     }
 }
 
@@ -44,80 +51,363 @@ __device__ __forceinline__ void xcd_map(int nbc, int& blk, int& nb) {
 }
 
 // ------------------------------------------------------------------------------------------------ pipelined K loop
-// One wave accumulates T tile columns (tile column t from projection t / (T / NP)) over all 32-k steps for RG row
-// groups of A (NP activation streams, one per projection). Weight words run two steps ahead (ring of 3), A fragments
-// one step ahead (ring of 2); the loop is unrolled 6x so every buffer is consumed where it was filled, and each
-// step issues A(s+1) before W(s+2) so waiting for a step's data never waits for a later prefetch.
-template <int K, int T, int NP, int RG>
-struct MfmaLoop {
-    static constexpr int NW = FragCfg<K>::NW;
-    static constexpr int TPP = T / NP;          // tile columns per projection
-    const uint32_t* wbase[T];                   // tile (tile-row lane >> 5, column) of step 0, per tile column
-    size_t wstep;                               // words between consecutive steps (two tile-rows)
-    const _Float16* abase[NP][RG];              // A row pointer (with this lane's k offset) per projection / group
-    int nsteps;
-    FragCfg<K> cfg;
+constexpr int kMfT = 4;                              // tile columns per wave
 
-    __device__ __forceinline__ void load_w(uint32_t (&W)[T][NW], int s) const {
-        const size_t off = (size_t)(s < nsteps ? s : nsteps - 1) * wstep;
+// 16-byte unit of (row, chunk) in one staged A plane (16 * RGA rows x four 16-byte chunks = 32 k); the chunk is
+// swizzled by row so that the 16 rows of a fragment read hit distinct banks.
+__device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
+
+// One wave accumulates kMfT tile columns over all 32-k steps for RGA row groups. Tile column t of the wave belongs to
+// column pair t >> 1 (gate|up: the projection; down: columns c0, c0 + 1 or c0 + 2, c0 + 3), whose two adjacent tiles of
+// one tile-row are contiguous in memory.
+//   weights: per step the wave's 8 tiles (2 pairs x 2 tile-rows x 2 tiles) come in with ONE coalesced load of K words
+//            per lane (16 lanes per 2-tile segment), loaded DW - 1 steps ahead into a register ring, and are staged in a
+//            wave-private LDS slot per tile laid out as [w(8K-1), w(0) .. w(8K-1), w(0), w(1), w(2)], so that every
+//            lane's fragment window (first word -1 .. 8K - 1, at most 8K + 2 past) is contiguous: no wrap logic, and
+//            per-lane scattered loads (64-bit addresses per lane into the texture unit) become LDS reads.
+//   A:       staged per step by the whole workgroup: loaded into register slot s % 4 four steps ahead, stored to LDS
+//            stage s % 2 one step ahead; memory-counter waits complete in issue order, so each step issues its A load
+//            before its weight load.
+template <int K, int NP, int RGA>
+struct MfmaPipe {
+    static constexpr int NW = FragCfg<K>::NW;
+    static constexpr int DW = 4;
+    static constexpr int TPP = kMfT / NP;
+    static constexpr int TS = 8 * K + 4;                     // LDS words per staged tile
+    static constexpr int UNITS = NP * RGA * 64;              // 16-byte A units per stage
+    static constexpr int CPT = (UNITS + 255) / 256;          // A units a thread stages per step
+    const uint32_t* wsrc;                                    // this lane's K words at step 0
+    uint32_t wstep;                                          // words between consecutive steps (two tile-rows)
+    int nsteps;
+    uint32_t* wl;                                            // the wave's LDS slots [8][TS]
+    int wdst, wslot;                                         // this lane's staged words: slot wslot, word wdst
+    int w0;                                                  // fragment window origin (ring word, -1 .. 8K - 1)
+    uint32_t sh;
+    const _Float16* asrc[CPT];                               // this thread's staged A units at step 0
+    int adst[CPT];
+    u32x4_t* lds;                                            // [2][UNITS]
+    int lane;
+
+    __device__ __forceinline__ void load_w(uint32_t (&D)[K], int s) const {
+        const uint32_t* p = wsrc + (uint32_t)(s < nsteps ? s : nsteps - 1) * wstep;
 #pragma unroll
-        for (int t = 0; t < T; ++t) frag_load<K>(wbase[t] + off, cfg, W[t]);
+        for (int i = 0; i < K; ++i) D[i] = ldg_nt(p + i);
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ void load_a(h8_t (&A)[NP][RG], int s) const {
+    __device__ __forceinline__ void stage_w(const uint32_t (&D)[K]) const {
+        uint32_t* t = wl + wslot * TS;
+#pragma unroll
+        for (int i = 0; i < K; ++i) t[1 + wdst + i] = D[i];
+        const int q = lane & 7;                              // this lane's eighth of the tile
+        if (q == 7) t[0] = D[K - 1];                          // w(8K - 1) in front
+#pragma unroll
+        for (int u = 0; u < 3; ++u)                          // w(0..2) behind
+            if (q == u / K) t[8 * K + 1 + u] = D[u % K];
+    }
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA]) const {
+        h8_t af[NP][RGA];
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int rg = 0; rg < RGA; ++rg)
+                af[p][rg] = __builtin_bit_cast(
+                    h8_t, lds[stage * UNITS + p * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
+        h8_t bf[kMfT];
+#pragma unroll
+        for (int t = 0; t < kMfT; ++t) {
+            const int slot = 2 * (2 * (t >> 1) + (lane >> 5)) + (t & 1);
+            const uint32_t* r = wl + slot * TS + 1 + w0;
+            uint32_t R[NW];
+#pragma unroll
+            for (int i = 0; i < NW; ++i) R[i] = r[i];
+            bf[t] = frag_finish<K>(R, sh);
+        }
+#pragma unroll
+        for (int t = 0; t < kMfT; ++t)
+#pragma unroll
+            for (int rg = 0; rg < RGA; ++rg)
+                acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t / TPP][rg], bf[t], acc[t][rg], 0, 0, 0);
+    }
+    // step s, with every ring slot known at compile time (R = s mod 4)
+    template <int R>
+    __device__ __forceinline__ void step(int s, uint32_t (&W)[DW][K], u32x4_t (&RA)[4][CPT],
+                                         f4_t (&acc)[kMfT][RGA]) const {
+        load_a(RA[R], s + 4);                            // slot R held A(s), stored to LDS one step ago
+        load_w(W[(R + DW - 1) % DW], s + DW - 1);
+        stage_w(W[R % DW]);
+        compute(R % 2, acc);
+        store_a(RA[(R + 1) % 4], (R + 1) % 2);
+        __syncthreads();
+    }
+    __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
         const int ss = (s < nsteps ? s : nsteps - 1) * 32;
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) A[p][rg] = *reinterpret_cast<const h8_t*>(abase[p][rg] + ss);
+        for (int j = 0; j < CPT; ++j) Ra[j] = ldg(reinterpret_cast<const u32x4_t*>(asrc[j] + ss));
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ void compute(uint32_t (&W)[T][NW], const h8_t (&A)[NP][RG], f4_t (&acc)[T][RG],
-                                            float (&rs)[NP][RG]) const {
-        h8_t bf[T];
+    __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
 #pragma unroll
-        for (int t = 0; t < T; ++t) bf[t] = frag_finish<K>(W[t], cfg.sh);
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-                float sv = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) sv += (float)A[p][rg][j];
-                rs[p][rg] += sv;
-#pragma unroll
-                for (int u = 0; u < TPP; ++u)
-                    acc[p * TPP + u][rg] =
-                        __builtin_amdgcn_mfma_f32_16x16x32_f16(A[p][rg], bf[p * TPP + u], acc[p * TPP + u][rg], 0, 0, 0);
-            }
+        for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
     }
-    __device__ __forceinline__ void run(f4_t (&acc)[T][RG], float (&rs)[NP][RG]) const {
-        uint32_t W0[T][NW], W1[T][NW], W2[T][NW];
-        h8_t A0[NP][RG], A1[NP][RG];
-        load_a(A0, 0);
-        load_w(W0, 0);
-        load_w(W1, 1);
-        int s = 0;
-        for (; s + 6 <= nsteps; s += 6) {
-            load_a(A1, s + 1); load_w(W2, s + 2); compute(W0, A0, acc, rs);
-            load_a(A0, s + 2); load_w(W0, s + 3); compute(W1, A1, acc, rs);
-            load_a(A1, s + 3); load_w(W1, s + 4); compute(W2, A0, acc, rs);
-            load_a(A0, s + 4); load_w(W2, s + 5); compute(W0, A1, acc, rs);
-            load_a(A1, s + 5); load_w(W0, s + 6); compute(W1, A0, acc, rs);
-            load_a(A0, s + 6); load_w(W1, s + 7); compute(W2, A1, acc, rs);
+    __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
+        uint32_t W[DW][K];
+        u32x4_t RA[4][CPT];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            load_a(RA[i], i);
+            if (i < DW - 1) load_w(W[i], i);
         }
-        // tail (< 6 steps): W0 / W1 hold steps s, s + 1 and A0 holds step s
-        if (s < nsteps) { load_a(A1, s + 1); load_w(W2, s + 2); compute(W0, A0, acc, rs); }
-        if (s + 1 < nsteps) { load_a(A0, s + 2); load_w(W0, s + 3); compute(W1, A1, acc, rs); }
-        if (s + 2 < nsteps) { load_a(A1, s + 3); load_w(W1, s + 4); compute(W2, A0, acc, rs); }
-        if (s + 3 < nsteps) { load_a(A0, s + 4); load_w(W2, s + 5); compute(W0, A1, acc, rs); }
-        if (s + 4 < nsteps) { load_a(A1, s + 5); compute(W1, A0, acc, rs); }
+        store_a(RA[0], 0);
+        __syncthreads();
+        int s = 0;
+        for (; s + 4 <= nsteps; s += 4) {
+            step<0>(s, W, RA, acc);
+            step<1>(s + 1, W, RA, acc);
+            step<2>(s + 2, W, RA, acc);
+            step<3>(s + 3, W, RA, acc);
+        }
+        if (s < nsteps) step<0>(s, W, RA, acc);
+        if (s + 1 < nsteps) step<1>(s + 1, W, RA, acc);
+        if (s + 2 < nsteps) step<2>(s + 2, W, RA, acc);
+    }
+    // weight set-up: pair_base(pair) = the pair's first tile (tile-row 0) in words; tile-rows are tn * 8K words apart
+    template <typename F>
+    __device__ __forceinline__ void setup_w(int tn, uint32_t* wave_lds, F pair_base) {
+        const int g = lane >> 4, pair = g >> 1, hr = g & 1;
+        wsrc = pair_base(pair) + (size_t)hr * tn * (8 * K) + (lane & 15) * K;
+        wstep = (uint32_t)(2 * tn * 8 * K);
+        wl = wave_lds;
+        wslot = 2 * g + ((lane & 15) >> 3);
+        wdst = (lane & 7) * K;
+        frag_origin<K>(lane, w0, sh);
+    }
+    // staging set-up: unit u = (tid + 256 j) mod UNITS (UNITS < 256: several threads stage the same unit, writing
+    // the same value, so that the loads and stores stay unconditional: a branch around them would make the compiler
+    // drain every outstanding load, the weight prefetch included) of plane p = u / (RGA * 64): row (u % (RGA * 64)) / 4
+    // (clamped to the block's last row), chunk u % 4, from row pointer rowptr(p, row) (k offset 0)
+    template <typename F>
+    __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int u = (threadIdx.x + 256 * j) % UNITS;
+            const int p = u / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+            asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
+            adst[j] = p * RGA * 64 + a_unit(row, ch);
+        }
     }
 };
 
 // ------------------------------------------------------------------------------------------------ gate | up
-template <int K, int MB>
-__global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
+template <int K, int RGA>
+__device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
+                                                 uint32_t* wlds, float* C, float* rsum) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p0 = d->p0;
+    const int tn = a.I / 16;
+    const uint32_t* trp[2] = {reinterpret_cast<const uint32_t*>(d->tab[0]),
+                              reinterpret_cast<const uint32_t*>(d->tab[3])};
+    const int ct0 = nb * 8 + 2 * wave;
+    MfmaPipe<K, 2, RGA> L;
+    L.nsteps = a.H / 32;
+    L.lds = stage;
+    L.lane = lane;
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) { return trp[pair] + (size_t)ct0 * (8 * K); });
+    L.setup_a(cnt, [&](int p, int row) { return a.xh + ((size_t)(p0 + row) * 2 + p) * a.H; });
+    f4_t acc[kMfT][RGA];
+#pragma unroll
+    for (int t = 0; t < kMfT; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
+    L.run(acc);
+
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(d->tab[2]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(d->tab[5]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(d->tab[7]) + nb * 128;
+    const float sg0 = h2f(ldg(svg + lane)), sg1 = h2f(ldg(svg + lane + 64));
+    const float su0 = h2f(ldg(svu + lane)), su1 = h2f(ldg(svu + lane + 64));
+    const float sd0 = h2f(ldg(sud + lane)), sd1 = h2f(ldg(sud + lane + 64));
+    const int nbI = a.I / 128;
+#pragma unroll
+    for (int rg = 0; rg < RGA; ++rg) {
+        // this row group's gate / up columns of the whole workgroup -> C[2][16][128]
+#pragma unroll
+        for (int t = 0; t < kMfT; ++t) {
+            const int p = t >> 1, col = (2 * wave + (t & 1)) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) C[(p * 16 + 4 * (lane >> 4) + i) * 128 + col] = acc[t][rg][i];
+        }
+        __syncthreads();
+        for (int j = 0; j < 4; ++j) {
+            const int ml = 4 * wave + j, m = 16 * rg + ml;
+            if (m >= cnt) break;
+            const float sg = kMul1C2 * rsum[m], su = kMul1C2 * rsum[64 + m];
+            float g0 = kMul1C1 * C[ml * 128 + lane] + sg, g1 = kMul1C1 * C[ml * 128 + lane + 64] + sg;
+            float u0 = kMul1C1 * C[(16 + ml) * 128 + lane] + su, u1 = kMul1C1 * C[(16 + ml) * 128 + lane + 64] + su;
+            fwht128_wave(g0, g1, lane);
+            fwht128_wave(u0, u1, lane);
+            g0 = (float)(_Float16)(g0 * kRsqrt128 * sg0);
+            g1 = (float)(_Float16)(g1 * kRsqrt128 * sg1);
+            u0 = (float)(_Float16)(u0 * kRsqrt128 * su0);
+            u1 = (float)(_Float16)(u1 * kRsqrt128 * su1);
+            float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
+            float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
+            a0 = (float)(_Float16)(a0 * sd0);
+            a1 = (float)(_Float16)(a1 * sd1);
+            fwht128_wave(a0, a1, lane);
+            const _Float16 h0 = (_Float16)(a0 * kRsqrt128), h1 = (_Float16)(a1 * kRsqrt128);
+            uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
+            dst[lane] = __builtin_bit_cast(uint16_t, h0);
+            dst[lane + 64] = __builtin_bit_cast(uint16_t, h1);
+            const float bs = wave_sum_f32((float)h0 + (float)h1);
+            if (lane == 0) a.asum[(size_t)(p0 + m) * nbI + nb] = bs;
+        }
+        __syncthreads();
+    }
+}
+
+// sum over b < n of q[b], in order, with the loads issued 16 at a time
+__device__ __forceinline__ float sum_ordered(const float* q, int n) {
+    float v = 0.f;
+    for (int b0 = 0; b0 < n; b0 += 16) {
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) t[i] = b0 + i < n ? ldg(q + b0 + i) : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v += t[i];
+    }
+    return v;
+}
+
+template <int K>
+__global__ __launch_bounds__(256, 2) void gateup_mfma_kernel(MoeArgs a) {
+    __shared__ u32x4_t stage[2 * 2 * 4 * 64];          // [2 stages][2 planes][64 rows x 4 units]
+    __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
+    __shared__ float C[2 * 16 * 128];
+    __shared__ float rsum[2 * 64];
+    const int nbI = a.I / 128;
+    int blk, nb;
+    xcd_map(nbI, blk, nb);
+    if (blk >= a.max_blocks) return;
+    const ItemDesc* d = a.blocks + blk;
+    const int cnt = d->cnt;
+    if (cnt == 0) return;
+    // row sums of the block's A rows (block sums in order)
+    const int nblk = a.H / 128;
+    for (int i = threadIdx.x; i < 2 * 64; i += 256) {
+        const int p = i >> 6, m = i & 63;
+        rsum[i] = m < cnt ? sum_ordered(a.xsum + ((size_t)(d->p0 + m) * 2 + p) * nblk, nblk) : 0.f;
+    }
+    __syncthreads();
+    const int rga = (cnt + 15) >> 4;
+    if (rga <= 1) gateup_mfma_body<K, 1>(a, d, nb, cnt, stage, wlds, C, rsum);
+    else if (rga <= 2) gateup_mfma_body<K, 2>(a, d, nb, cnt, stage, wlds, C, rsum);
+    else gateup_mfma_body<K, 4>(a, d, nb, cnt, stage, wlds, C, rsum);
+}
+
+// ------------------------------------------------------------------------------------------------ down
+// 256 output columns per workgroup (two Hadamard blocks): wave w owns tile columns 4w .. 4w + 3.
+template <int K, int RGA>
+__device__ __forceinline__ void down_mfma_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
+                                               uint32_t* wlds, float* C, float* rsum, int* s_comb) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p0 = d->p0;
+    const int tn = a.H / 16, nbH = a.H / 128;
+    const uint32_t* trd = reinterpret_cast<const uint32_t*>(d->tab[6]);
+    MfmaPipe<K, 1, RGA> L;
+    L.nsteps = a.I / 32;
+    L.lds = stage;
+    L.lane = lane;
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) {
+        int ct = nb * 16 + 4 * wave + 2 * pair;
+        ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
+        return trd + (size_t)ct * (8 * K);
+    });
+    L.setup_a(cnt, [&](int, int row) { return reinterpret_cast<const _Float16*>(a.abuf) + (size_t)(p0 + row) * a.I; });
+    f4_t acc[kMfT][RGA];
+#pragma unroll
+    for (int t = 0; t < kMfT; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
+    L.run(acc);
+
+    const int nhalf = 2 * nb + 1 < nbH ? 2 : 1;
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(d->tab[8]) + nb * 256;
+    float sd[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        sd[h][0] = h < nhalf ? h2f(ldg(svd + 128 * h + lane)) : 0.f;
+        sd[h][1] = h < nhalf ? h2f(ldg(svd + 128 * h + lane + 64)) : 0.f;
+    }
+#pragma unroll
+    for (int rg = 0; rg < RGA; ++rg) {
+#pragma unroll
+        for (int t = 0; t < kMfT; ++t) {
+            const int col = (4 * wave + t) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * 256 + col] = acc[t][rg][i];
+        }
+        __syncthreads();
+        for (int j = 0; j < 8; ++j) {                 // (row, half) pairs of this wave
+            const int ml = 4 * wave + (j >> 1), h = j & 1, m = 16 * rg + ml;
+            if (m >= cnt || h >= nhalf) continue;
+            const float sx = kMul1C2 * rsum[m];
+            float v0 = kMul1C1 * C[ml * 256 + 128 * h + lane] + sx, v1 = kMul1C1 * C[ml * 256 + 128 * h + lane + 64] + sx;
+            fwht128_wave(v0, v1, lane);
+            const float w = a.pair_w[p0 + m];
+            float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 256 + 128 * h;
+            splitk_store(dst + lane, v0 * kRsqrt128 * sd[h][0] * w);
+            splitk_store(dst + lane + 64, v1 * kRsqrt128 * sd[h][1] * w);
+        }
+        __syncthreads();
+    }
+    // combine: count rows into their tokens per 128-column block, finish tokens whose slots are all in
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * cnt; i += 256) {
+        const int m = i >> 1, h = i & 1;
+        int r = -1;
+        if (h < nhalf) {
+            const int t = a.pair_tok[p0 + m];
+            const int old = __hip_atomic_fetch_add(&a.cnt_tok[(size_t)t * nbH + 2 * nb + h], 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+            r = (old == a.tok_nvalid[t] - 1) ? t : -1;
+        }
+        s_comb[i] = r;
+    }
+    __syncthreads();
+    for (int i = wave; i < 2 * cnt; i += 4)
+        if (s_comb[i] >= 0) combine_token(a, s_comb[i], 2 * nb + (i & 1), lane);
+}
+
+template <int K>
+__global__ __launch_bounds__(256, 2) void down_mfma_kernel(MoeArgs a) {
+    __shared__ u32x4_t stage[2 * 4 * 64];              // [2 stages][64 rows x 4 units]
+    __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
+    __shared__ float C[16 * 256];
+    __shared__ float rsum[64];
+    __shared__ int s_comb[2 * 64];
+    const int nbH2 = (a.H / 128 + 1) / 2;
+    int blk, nb;
+    xcd_map(nbH2, blk, nb);
+    if (blk >= a.max_blocks) return;
+    const ItemDesc* d = a.blocks + blk;
+    const int cnt = d->cnt;
+    if (cnt == 0) return;
+    const int nbI = a.I / 128;
+    for (int m = threadIdx.x; m < 64; m += 256)
+        rsum[m] = m < cnt ? sum_ordered(a.asum + (size_t)(d->p0 + m) * nbI, nbI) : 0.f;
+    __syncthreads();
+    const int rga = (cnt + 15) >> 4;
+    if (rga <= 1) down_mfma_body<K, 1>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
+    else if (rga <= 2) down_mfma_body<K, 2>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
+    else down_mfma_body<K, 4>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
+}
+
+// ------------------------------------------------------------------------------------------------ per-tile K
+// Per-tile bitrate (K = 0): each wave decodes its tile columns with the tile's own K (lanes 0-31 and 32-63 hold two
+// tile-rows, which may differ), A fragments straight from memory.
+template <int MB>
+__global__ __launch_bounds__(256) void gateup_mfma_mixed_kernel(MoeArgs a) {
     extern __shared__ float smem[];
     constexpr int RG = MB / 16;
     float* C = smem;                         // [2][MB][128]
@@ -145,69 +435,41 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
         arow[rg] = a.xh + (size_t)(p0 + r) * 2 * a.H + 8 * (lane >> 4);
     }
     f4_t acc[4][RG];
-    float rs[2][RG];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) rs[p][rg] = 0.f;
-
     const int nsteps = a.H / 32;
-    if (K > 0) {
-        constexpr int KL = K > 0 ? K : 1;
-        MfmaLoop<KL, 4, 2, RG> L;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            L.wbase[t] = trp[t >> 1] + ((size_t)(lane >> 5) * tn + ct0 + (t & 1)) * (8 * KL);
-        L.wstep = (size_t)2 * tn * 8 * KL;
-#pragma unroll
-        for (int p = 0; p < 2; ++p)
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) L.abase[p][rg] = arow[rg] + (size_t)p * a.H;
-        L.nsteps = nsteps;
-        frag_setup<KL>(lane, L.cfg);
-        L.run(acc, rs);
-    }
-    for (int s = 0; K == 0 && s < nsteps; ++s) {
+    for (int s = 0; s < nsteps; ++s) {
         const int tr = 2 * s + (lane >> 5);
         h8_t bf[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int p = t >> 1, col = ct0 + (t & 1);
-            {
-                const int tile = tr * tn + col;
-                bf[t] = frag_decode_k(trp[p] + ldg(wop[p] + tile), ldg(kmp[p] + tile), lane);
-            }
+            const int tile = tr * tn + col;
+            bf[t] = frag_decode_k(trp[p] + ldg(wop[p] + tile), ldg(kmp[p] + tile), lane);
         }
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const h8_t av = *reinterpret_cast<const h8_t*>(arow[rg] + (size_t)p * a.H + 32 * s);
-                float sv = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) sv += (float)av[j];
-                rs[p][rg] += sv;
                 acc[2 * p][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[2 * p], acc[2 * p][rg], 0, 0, 0);
                 acc[2 * p + 1][rg] =
                     __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[2 * p + 1], acc[2 * p + 1][rg], 0, 0, 0);
             }
         }
     }
-
-    // row sums: lanes L, L ^ 16, L ^ 32, L ^ 48 hold the four k-groups of row L & 15
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            float v = rs[p][rg];
-            v += lane_xor<16>(v, lane);
-            v += lane_xor<32>(v, lane);
-            if (wave == 0 && lane < 16) rsum[p * MB + 16 * rg + lane] = v;
+    const int nblk = a.H / 128;
+    for (int i = threadIdx.x; i < 2 * MB; i += 256) {
+        const int p = i / MB, m = i - p * MB;
+        float v = 0.f;
+        if (m < cnt) {
+            const float* q = a.xsum + ((size_t)(p0 + m) * 2 + p) * nblk;
+            for (int b = 0; b < nblk; ++b) v += q[b];
         }
+        rsum[i] = v;
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int p = t >> 1, col = (2 * wave + (t & 1)) * 16 + (lane & 15);
@@ -236,15 +498,17 @@ __global__ __launch_bounds__(256) void gateup_mfma_kernel(MoeArgs a) {
         a0 = (float)(_Float16)(a0 * h2f(ldg(sud + lane)));
         a1 = (float)(_Float16)(a1 * h2f(ldg(sud + lane + 64)));
         fwht128_wave(a0, a1, lane);
+        const _Float16 h0 = (_Float16)(a0 * kRsqrt128), h1 = (_Float16)(a1 * kRsqrt128);
         uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
-        dst[lane] = f2h(a0 * kRsqrt128);
-        dst[lane + 64] = f2h(a1 * kRsqrt128);
+        dst[lane] = __builtin_bit_cast(uint16_t, h0);
+        dst[lane + 64] = __builtin_bit_cast(uint16_t, h1);
+        const float bs = wave_sum_f32((float)h0 + (float)h1);
+        if (lane == 0) a.asum[(size_t)(p0 + m) * nbI + nb] = bs;
     }
 }
 
-// ------------------------------------------------------------------------------------------------ down
-template <int K, int MB>
-__global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
+template <int MB>
+__global__ __launch_bounds__(256) void down_mfma_mixed_kernel(MoeArgs a) {
     extern __shared__ float smem[];
     constexpr int RG = MB / 16;
     float* C = smem;                         // [MB][128]
@@ -272,67 +536,32 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
         arow[rg] = a.abuf + (size_t)(p0 + r) * a.I + 8 * (lane >> 4);
     }
     f4_t acc[2][RG];
-    float rs[RG];
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-        acc[0][rg] = acc[1][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
-        rs[rg] = 0.f;
-    }
+    for (int rg = 0; rg < RG; ++rg) acc[0][rg] = acc[1][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
     const int nsteps = a.I / 32;
-    if (K > 0) {
-        constexpr int KL = K > 0 ? K : 1;
-        MfmaLoop<KL, 2, 1, RG> L;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) L.wbase[t] = trd + ((size_t)(lane >> 5) * tn + ct0 + t) * (8 * KL);
-        L.wstep = (size_t)2 * tn * 8 * KL;
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) L.abase[0][rg] = reinterpret_cast<const _Float16*>(arow[rg]);
-        L.nsteps = nsteps;
-        frag_setup<KL>(lane, L.cfg);
-        f4_t acc1[2][RG];
-        float rs1[1][RG];
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            acc1[0][rg] = acc[0][rg];
-            acc1[1][rg] = acc[1][rg];
-            rs1[0][rg] = rs[rg];
-        }
-        L.run(acc1, rs1);
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            acc[0][rg] = acc1[0][rg];
-            acc[1][rg] = acc1[1][rg];
-            rs[rg] = rs1[0][rg];
-        }
-    }
-    for (int s = 0; K == 0 && s < nsteps; ++s) {
+    for (int s = 0; s < nsteps; ++s) {
         const int tr = 2 * s + (lane >> 5);
         h8_t bf[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const int col = ct0 + t;
-            {
-                const int tile = tr * tn + col;
-                bf[t] = frag_decode_k(trd + ldg(wod + tile), ldg(kmd + tile), lane);
-            }
+            const int tile = tr * tn + ct0 + t;
+            bf[t] = frag_decode_k(trd + ldg(wod + tile), ldg(kmd + tile), lane);
         }
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) {
             const h8_t av = *reinterpret_cast<const h8_t*>(arow[rg] + 32 * s);
-            float sv = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) sv += (float)av[j];
-            rs[rg] += sv;
             acc[0][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[0], acc[0][rg], 0, 0, 0);
             acc[1][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[1], acc[1][rg], 0, 0, 0);
         }
     }
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-        float v = rs[rg];
-        v += lane_xor<16>(v, lane);
-        v += lane_xor<32>(v, lane);
-        if (wave == 0 && lane < 16) rsum[16 * rg + lane] = v;
+    const int nbI = a.I / 128;
+    for (int m = threadIdx.x; m < MB; m += 256) {
+        float v = 0.f;
+        if (m < cnt) {
+            const float* q = a.asum + (size_t)(p0 + m) * nbI;
+            for (int b = 0; b < nbI; ++b) v += q[b];
+        }
+        rsum[m] = v;
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -354,13 +583,11 @@ __global__ __launch_bounds__(256) void down_mfma_kernel(MoeArgs a) {
         splitk_store(dst + lane, v0 * kRsqrt128 * h2f(ldg(svd + lane)) * w);
         splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(ldg(svd + lane + 64)) * w);
     }
-    // combine: count rows into their tokens, finish tokens whose slots are all in
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const int nbH_ = nbH;
     for (int m = threadIdx.x; m < cnt; m += 256) {
         const int t = a.pair_tok[p0 + m];
-        const int old = __hip_atomic_fetch_add(&a.cnt_tok[(size_t)t * nbH_ + nb], 1, __ATOMIC_RELAXED,
+        const int old = __hip_atomic_fetch_add(&a.cnt_tok[(size_t)t * nbH + nb], 1, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
         s_comb[m] = (old == a.tok_nvalid[t] - 1) ? t : -1;
     }
@@ -383,57 +610,57 @@ static hipError_t set_max_lds(const void* fn, int bytes) {
     return e;
 }
 
-template <int MB>
 static mfma_fn pick_gu(int K) {
     switch (K) {
-        case 0: return gateup_mfma_kernel<0, MB>;
-        case 1: return gateup_mfma_kernel<1, MB>;
-        case 2: return gateup_mfma_kernel<2, MB>;
-        case 3: return gateup_mfma_kernel<3, MB>;
-        case 4: return gateup_mfma_kernel<4, MB>;
-        case 5: return gateup_mfma_kernel<5, MB>;
-        case 6: return gateup_mfma_kernel<6, MB>;
-        case 7: return gateup_mfma_kernel<7, MB>;
-        default: return gateup_mfma_kernel<8, MB>;
+        case 0: return gateup_mfma_mixed_kernel<kMfmaRows>;
+        case 1: return gateup_mfma_kernel<1>;
+        case 2: return gateup_mfma_kernel<2>;
+        case 3: return gateup_mfma_kernel<3>;
+        case 4: return gateup_mfma_kernel<4>;
+        case 5: return gateup_mfma_kernel<5>;
+        case 6: return gateup_mfma_kernel<6>;
+        case 7: return gateup_mfma_kernel<7>;
+        default: return gateup_mfma_kernel<8>;
     }
 }
 
-template <int MB>
 static mfma_fn pick_dn(int K) {
     switch (K) {
-        case 0: return down_mfma_kernel<0, MB>;
-        case 1: return down_mfma_kernel<1, MB>;
-        case 2: return down_mfma_kernel<2, MB>;
-        case 3: return down_mfma_kernel<3, MB>;
-        case 4: return down_mfma_kernel<4, MB>;
-        case 5: return down_mfma_kernel<5, MB>;
-        case 6: return down_mfma_kernel<6, MB>;
-        case 7: return down_mfma_kernel<7, MB>;
-        default: return down_mfma_kernel<8, MB>;
+        case 0: return down_mfma_mixed_kernel<kMfmaRows>;
+        case 1: return down_mfma_kernel<1>;
+        case 2: return down_mfma_kernel<2>;
+        case 3: return down_mfma_kernel<3>;
+        case 4: return down_mfma_kernel<4>;
+        case 5: return down_mfma_kernel<5>;
+        case 6: return down_mfma_kernel<6>;
+        case 7: return down_mfma_kernel<7>;
+        default: return down_mfma_kernel<8>;
     }
 }
 
-int mfma_lds_gu(int MB) { return (2 * MB * 128 + 2 * MB) * (int)sizeof(float); }
-int mfma_lds_dn(int MB) { return (MB * 128 + MB) * (int)sizeof(float); }
-
 int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
-    constexpr int MB = kMfmaRows;
     const int nxb = (a.max_blocks + 7) / 8 * 8;
     EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
-    mfma_fn fn = pick_gu<MB>(a.Kg);
-    const int lds = mfma_lds_gu(MB);
-    EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
+    mfma_fn fn = pick_gu(a.Kg);
+    int lds = 0;
+    if (a.Kg == 0) {
+        lds = (2 * kMfmaRows * 128 + 2 * kMfmaRows) * (int)sizeof(float);
+        EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
+    }
     EXL3_LAUNCH("moe_gateup_mfma", fn, dim3(nxb * (a.I / 128)), dim3(256), lds, st, a);
     return EXL3_OK;
 }
 
 int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st) {
-    constexpr int MB = kMfmaRows;
     const int nxb = (a.max_blocks + 7) / 8 * 8;
-    mfma_fn fn = pick_dn<MB>(a.Kd);
-    const int lds = mfma_lds_dn(MB);
-    EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
-    EXL3_LAUNCH("moe_down_mfma", fn, dim3(nxb * (a.H / 128)), dim3(256), lds, st, a);
+    mfma_fn fn = pick_dn(a.Kd);
+    int lds = 0, ncb = (a.H / 128 + 1) / 2;
+    if (a.Kd == 0) {
+        lds = (kMfmaRows * 128 + kMfmaRows) * (int)sizeof(float);
+        EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
+        ncb = a.H / 128;
+    }
+    EXL3_LAUNCH("moe_down_mfma", fn, dim3(nxb * ncb), dim3(256), lds, st, a);
     return EXL3_OK;
 }
 

@@ -61,6 +61,8 @@ struct MoeArgs {
     const ItemDesc* blocks;            // MFMA row blocks (cnt == 0 past the last)
     int max_blocks;
     _Float16* xh;                      // [pairs][2][H] transformed gate / up inputs of MFMA rows
+    float* xsum;                       // [pairs][2][H / 128] block sums of xh (the MFMA rows' affine term)
+    float* asum;                       // [pairs][I / 128] block sums of abuf (MFMA rows)
     int* pair_tok;
     float* pair_w;
     int* pair_of;

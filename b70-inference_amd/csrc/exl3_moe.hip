@@ -56,6 +56,7 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     int* tmp = sm + 5 * r.E;       // [1024]
     const int t = threadIdx.x, T = blockDim.x;
     const int np = r.M * r.slots;
+    const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
     for (int e = t; e < r.E; e += T) {
         cnt[e] = 0;
         fill[e] = 0;
@@ -71,7 +72,7 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         const int c = cnt[e];
         const bool big = r.use_mfma && c > r.MR;
         start[e] = c;
-        nch[e] = big ? 0 : (c + r.MR - 1) / r.MR;
+        nch[e] = big ? 0 : (c + mr - 1) / mr;
         nbl[e] = big ? (c + r.MB - 1) / r.MB : 0;
     }
     __syncthreads();
@@ -91,11 +92,11 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
             for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
         }
-        for (int q = 0, it = nch[e]; !big && q * r.MR < c; ++q, ++it) {
+        for (int q = 0, it = nch[e]; !big && q * mr < c; ++q, ++it) {
             ItemDesc& d = r.items[it];
             d.e = e;
-            d.p0 = start[e] + q * r.MR;
-            d.cnt = min(r.MR, c - q * r.MR);
+            d.p0 = start[e] + q * mr;
+            d.cnt = min(mr, c - q * mr);
             for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
             for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
         }
@@ -133,9 +134,9 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             r.pair_w[pos] = wt;
             r.pair_of[i] = pos;
             if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
-                ItemDesc& d = r.items[nch[e] + f / r.MR];
-                d.tok[f % r.MR] = tok;
-                d.w[f % r.MR] = wt;
+                ItemDesc& d = r.items[nch[e] + f / mr];
+                d.tok[f % mr] = tok;
+                d.w[f % mr] = wt;
             }
         } else {
             r.pair_of[i] = -1;
@@ -154,6 +155,7 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
     __shared__ uint8_t s_lead[kAlignSmall], s_blead[kAlignSmall];
     const int t = threadIdx.x;
     const int np = r.M * r.slots;
+    const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
     int e = -1, tok = 0;
     float wt = 0.f;
     if (t < np) {
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
         }
     const int pos = below + before;
     const bool big = e >= 0 && r.use_mfma && cnt > r.MR;
-    const bool lead = e >= 0 && !big && before % r.MR == 0;
+    const bool lead = e >= 0 && !big && before % mr == 0;
     const bool blead = big && before % r.MB == 0;
     s_pos[t] = e >= 0 ? pos : 0x7FFFFFFF;
     s_lead[t] = lead;
@@ -209,14 +211,14 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
             ItemDesc& d = r.items[item];
             d.e = e;
             d.p0 = pos;
-            d.cnt = min(r.MR, cnt - before);
+            d.cnt = min(mr, cnt - before);
             for (int i = 0; i < 9; ++i) d.tab[i] = ldg(r.tables + (int64_t)i * r.E + e);
             for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? ldg(r.kmaps + (int64_t)i * r.E + e) : 0;
         }
         if (e >= 0 && !big) {
             ItemDesc& d = r.items[item];
-            d.tok[before % r.MR] = tok;
-            d.w[before % r.MR] = wt;
+            d.tok[before % mr] = tok;
+            d.w[before % mr] = wt;
         }
         for (int it = nitems + t; it < r.max_items; it += kAlignSmall) r.items[it].cnt = 0;
         if (t == 0 && r.n_items) r.n_items[0] = nitems;
@@ -580,12 +582,16 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     a.nblk_i = a.I / 128;
     a.P_gu = moe_splits(max_items < 16 ? max_items * nbI : 16 * nbI, a.nblk_h);
     a.P_d = moe_splits(max_items < 16 ? max_items * nbH : 16 * nbH, a.nblk_i);
-    const int MR = a.MR;
+    const int MR = a.MR > 0 ? a.MR : 1;
     Workspace ws;
     const size_t n_gu = (size_t)max_items * nbI, n_d = (size_t)max_items * nbH;
     const bool use_mfma = a.max_blocks > 0;
     size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) +
-                   carve_size(a.max_blocks, sizeof(ItemDesc)) + (use_mfma ? carve_size(npairs * 2 * a.H, 2) : 0) + carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
+                   carve_size(a.max_blocks, sizeof(ItemDesc)) +
+                   (use_mfma ? carve_size(npairs * 2 * a.H, 2) + carve_size(npairs * 2 * (a.H / 128), 4) +
+                                   carve_size(npairs * (a.I / 128), 4)
+                             : 0) +
+                   carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
                    carve_size(a.M, 4) +
                    carve_size(npairs * a.I, 2) + carve_size(npairs * a.H, 4) +
                    carve_size(n_gu * a.P_gu * 2 * MR * 128, 4) + carve_size(n_d * a.P_d * MR * 128, 4);
@@ -599,6 +605,8 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     ItemDesc* blocks = a.max_blocks ? c.take<ItemDesc>(a.max_blocks) : nullptr;
     a.blocks = blocks;
     a.xh = use_mfma ? c.take<_Float16>(npairs * 2 * a.H) : nullptr;
+    a.xsum = use_mfma ? c.take<float>(npairs * 2 * (a.H / 128)) : nullptr;
+    a.asum = use_mfma ? c.take<float>(npairs * (a.I / 128)) : nullptr;
     int* pb = c.take<int>(npairs * 2);
     a.pair_tok = pb;
     a.pair_of = pb + npairs;
@@ -621,7 +629,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.slots = a.slots;
     r.E = a.E;
     r.shared = a.shared;
-    r.MR = MR;
+    r.MR = a.MR;
     r.n_items = a.n_items;
     r.items = items;
     r.max_items = max_items;
@@ -642,9 +650,11 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     rc = launch_align(r, st);
     if (rc) return rc;
     if (use_mfma && (rc = launch_moe_mfma_gateup(a, st))) return rc;
-    EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
+    if (max_items > 0)
+        EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
     if (use_mfma && (rc = launch_moe_mfma_down(a, st))) return rc;
-    EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
+    if (max_items > 0)
+        EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
     return EXL3_OK;
 }
 
@@ -673,6 +683,8 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
                    "exl3_moe_forward: M=%lld topk=%lld E=%lld out of range", (long long)M, (long long)topk,
                    (long long)E);
     EXL3_CHECK_ARG(H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0, "exl3_moe_forward: H and I must be multiples of 128");
+    EXL3_CHECK_ARG(H / 16 * (I / 16) * 64 < (1LL << 32), "exl3_moe_forward: projection of %lld x %lld exceeds 2^32 words",
+                   (long long)H, (long long)I);
     EXL3_CHECK_ARG(x_ld >= H && out_ld >= H, "exl3_moe_forward: row strides must cover H");
     EXL3_CHECK_ARG(shared < E, "exl3_moe_forward: shared expert index %lld >= E", (long long)shared);
     if (M == 0) return EXL3_OK;
@@ -702,14 +714,14 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.out_f32 = out_dtype == EXL3_F32;
     const int64_t npairs = M * a.slots;
     if (moe_fused_ok(a)) return moe_fused_path(a, (hipStream_t)stream);
-    a.MR = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
-    // An expert has at most npairs rows; with more than MR possible rows per expert (M > MR or duplicates), experts
-    // with more than MR rows go to the MFMA kernels and every other expert is one GEMV item.
+    // Decode batches (M <= 8): GEMV items of up to MR rows per expert. Prefill batches: every expert with rows goes to
+    // the MFMA kernels in blocks of up to kMfmaRows rows (MR = 0: no GEMV items).
     const bool mfma = M > kMoeSmallRows;
-    int64_t mi = mfma ? (E < npairs ? E : npairs) : E + npairs / a.MR;
+    a.MR = mfma ? 0 : M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
+    int64_t mi = mfma ? 0 : E + npairs / a.MR;
     if (mi > npairs) mi = npairs;
     a.max_items = (int)mi;
-    a.max_blocks = mfma ? (int)(npairs / kMfmaRows + npairs / (a.MR + 1) + 1) : 0;
+    a.max_blocks = mfma ? (int)(npairs / kMfmaRows + (E < npairs ? E : npairs) + 1) : 0;
     EXL3_CHECK_ARG((int64_t)a.max_items * (H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
     return moe_decode_path(a, npairs, (hipStream_t)stream);
 }

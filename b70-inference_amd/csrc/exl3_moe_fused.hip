@@ -80,6 +80,7 @@ struct FusedShared {
     float bsum[2][MR][KBF];
     _Float16 su[2][KBF * 128];          // gate / up input sign vectors of the job's k range
     int ge[4][kFusedMaxPairs];          // each wave's copy of the pairs' experts (grouping sweep)
+    int64_t tab[9];                     // the item's (trellis, suh, svh) addresses for gate, up, down
     int rows[MR];                       // flat pair index of each row of the job's item
     int comb[MR];
     int flag;
@@ -89,7 +90,6 @@ struct FusedShared {
 struct Item {
     int e, cnt;                         // expert, rows
     uint64_t v0, v1;                    // valid pairs (pair l: bit l of v0, pair 64 + l: bit l of v1)
-    int64_t tab[9];                     // the expert's (trellis, suh, svh) addresses for gate, up, down
     int64_t km[6];                      // (kmap, woff) addresses when K is per tile
 };
 
@@ -117,11 +117,12 @@ __device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n
     return c;
 }
 
-// Groups the pairs and returns the number of items; fills `it` and rows[] for item `item` when it exists. Every wave
-// runs it and writes the same rows, so a wave may read rows[] right after without a barrier.
+// Groups the pairs and returns the number of items; fills `it`, rows[] and tab[] for item `item` when it exists. Every
+// wave runs it and writes the same rows and table entries, so a wave may read them right after without a barrier.
 // `ge` is the wave's own 128-int LDS slice (written and read by this wave only: LDS keeps a wave's accesses in order).
-template <int MR>
-__device__ __forceinline__ int group_pairs(const FusedArgs& a, int item, int lane, Item& it, int* rows, int* ge) {
+template <int K, int MR>
+__device__ __forceinline__ int group_pairs(const FusedArgs& a, int item, int lane, Item& it, int* rows, int64_t* tab,
+                                           int* ge) {
     const int np = a.np;
     const int l1 = lane + 64;
     const int e0 = pair_expert(a, lane);
@@ -153,9 +154,8 @@ __device__ __forceinline__ int group_pairs(const FusedArgs& a, int item, int lan
     const int ce = popc64(__ballot(e0 == e)) + popc64(__ballot(e1 == e));
     it.e = e;
     it.cnt = min(MR, ce - bfp);
-#pragma unroll
-    for (int i = 0; i < 9; ++i) it.tab[i] = ldg(a.tables + (int64_t)i * a.E + e);
-    if (a.kmaps)
+    if (lane < 9) tab[lane] = ldg(a.tables + (int64_t)lane * a.E + e);
+    if (K == 0)
 #pragma unroll
         for (int i = 0; i < 6; ++i) it.km[i] = ldg(a.kmaps + (int64_t)i * a.E + e);
 #pragma unroll
@@ -196,7 +196,7 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     const int b0 = (int)((int64_t)p * a.nblk_h / a.P_gu), b1 = (int)((int64_t)(p + 1) * a.nblk_h / a.P_gu);
     const int kb = b1 - b0;
     const int proj = wave >> 1, half = wave & 1;
-    const uint32_t* tr = reinterpret_cast<const uint32_t*>(proj ? it.tab[3] : it.tab[0]);
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(proj ? s.tab[3] : s.tab[0]);
     const int tn = a.I / 16;
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
@@ -207,8 +207,8 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     // vectors in su, all loads of a thread in flight together
     {
         const int k0 = b0 * 128, nch = kb * 16;                  // 16-byte chunks per row
-        const uint16_t* sg = reinterpret_cast<const uint16_t*>(it.tab[1]) + k0;
-        const uint16_t* su = reinterpret_cast<const uint16_t*>(it.tab[4]) + k0;
+        const uint16_t* sg = reinterpret_cast<const uint16_t*>(s.tab[1]) + k0;
+        const uint16_t* su = reinterpret_cast<const uint16_t*>(s.tab[4]) + k0;
         for (int c = threadIdx.x; c < MR * nch; c += 256) {
             const int m = c / nch, o = c - m * nch;
             u32x4_t v = {0u, 0u, 0u, 0u};
@@ -286,9 +286,9 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     }
     if (!splitk_arrive(&a.cnt_gu[slot * kCS], a.P_gu, &s.flag)) return;
 
-    const uint16_t* svg = reinterpret_cast<const uint16_t*>(it.tab[2]) + nb * 128;
-    const uint16_t* svu = reinterpret_cast<const uint16_t*>(it.tab[5]) + nb * 128;
-    const uint16_t* sud = reinterpret_cast<const uint16_t*>(it.tab[7]) + nb * 128;
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(s.tab[2]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(s.tab[5]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(s.tab[7]) + nb * 128;
     const float sg0 = h2f(ldg(svg + lane)), sg1 = h2f(ldg(svg + lane + 64));
     const float su0 = h2f(ldg(svu + lane)), su1 = h2f(ldg(svu + lane + 64));
     const float sd0 = h2f(ldg(sud + lane)), sd1 = h2f(ldg(sud + lane + 64));
@@ -330,7 +330,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     const int nbI = a.I / 128, nbH = a.H / 128;
     const int b0 = (int)((int64_t)p * a.nblk_i / a.P_d), b1 = (int)((int64_t)(p + 1) * a.nblk_i / a.P_d);
     const int kb = b1 - b0;
-    const uint32_t* tr = reinterpret_cast<const uint32_t*>(it.tab[6]);
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(s.tab[6]);
     const int tn = a.H / 16;
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
@@ -416,7 +416,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     }
     if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) return;
 
-    const uint16_t* svd = reinterpret_cast<const uint16_t*>(it.tab[8]) + nb * 128;
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(s.tab[8]) + nb * 128;
     const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
     for (int m = wave; m < cnt; m += 4) {
         const int pr = s.rows[m];
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const int nbo = gu ? a.I / 128 : a.H / 128, P = gu ? a.P_gu : a.P_d;
     const int item = jj / (nbo * P), rem = jj - item * (nbo * P), nb = rem / P, p = rem - nb * P;
     Item it;
-    const int nitems = group_pairs<MR>(a, item, lane, it, s.rows, s.ge[threadIdx.x >> 6]);
+    const int nitems = group_pairs<K, MR>(a, item, lane, it, s.rows, s.tab, s.ge[threadIdx.x >> 6]);
     if (job == 0) {
         // tokens with no valid slot get a zero output row
         for (int tk = 0; tk < a.M; ++tk) {
