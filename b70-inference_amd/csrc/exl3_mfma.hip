@@ -278,19 +278,21 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
     return v;
 }
 
-template <int K>
-__global__ __launch_bounds__(256, 2) void gateup_mfma_kernel(MoeArgs a) {
-    __shared__ u32x4_t stage[2 * 2 * 4 * 64];          // [2 stages][2 planes][64 rows x 4 units]
+// One instance per row class (RGA row groups of 16): workgroup (list index, column block); indices past the class's
+// block count exit at once.
+template <int K, int RGA>
+__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_mfma_kernel(MoeArgs a) {
+    constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
+    __shared__ u32x4_t stage[2 * 2 * RGA * 64];        // [2 stages][2 planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
     const int nbI = a.I / 128;
-    int blk, nb;
-    xcd_map(nbI, blk, nb);
-    if (blk >= a.max_blocks) return;
-    const ItemDesc* d = a.blocks + blk;
+    int idx, nb;
+    xcd_map(nbI, idx, nb);
+    if (idx >= a.cls_cnt[CL]) return;
+    const ItemDesc* d = a.blocks + a.cls_list[CL * a.max_blocks + idx];
     const int cnt = d->cnt;
-    if (cnt == 0) return;
     // row sums of the block's A rows (block sums in order)
     const int nblk = a.H / 128;
     for (int i = threadIdx.x; i < 2 * 64; i += 256) {
@@ -298,10 +300,7 @@ __global__ __launch_bounds__(256, 2) void gateup_mfma_kernel(MoeArgs a) {
         rsum[i] = m < cnt ? sum_ordered(a.xsum + ((size_t)(d->p0 + m) * 2 + p) * nblk, nblk) : 0.f;
     }
     __syncthreads();
-    const int rga = (cnt + 15) >> 4;
-    if (rga <= 1) gateup_mfma_body<K, 1>(a, d, nb, cnt, stage, wlds, C, rsum);
-    else if (rga <= 2) gateup_mfma_body<K, 2>(a, d, nb, cnt, stage, wlds, C, rsum);
-    else gateup_mfma_body<K, 4>(a, d, nb, cnt, stage, wlds, C, rsum);
+    gateup_mfma_body<K, RGA>(a, d, nb, cnt, stage, wlds, C, rsum);
 }
 
 // ------------------------------------------------------------------------------------------------ down
@@ -379,28 +378,25 @@ __device__ __forceinline__ void down_mfma_body(const MoeArgs& a, const ItemDesc*
         if (s_comb[i] >= 0) combine_token(a, s_comb[i], 2 * nb + (i & 1), lane);
 }
 
-template <int K>
-__global__ __launch_bounds__(256, 2) void down_mfma_kernel(MoeArgs a) {
-    __shared__ u32x4_t stage[2 * 4 * 64];              // [2 stages][64 rows x 4 units]
+template <int K, int RGA>
+__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mfma_kernel(MoeArgs a) {
+    constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
+    __shared__ u32x4_t stage[2 * RGA * 64];            // [2 stages][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
     __shared__ int s_comb[2 * 64];
     const int nbH2 = (a.H / 128 + 1) / 2;
-    int blk, nb;
-    xcd_map(nbH2, blk, nb);
-    if (blk >= a.max_blocks) return;
-    const ItemDesc* d = a.blocks + blk;
+    int idx, nb;
+    xcd_map(nbH2, idx, nb);
+    if (idx >= a.cls_cnt[CL]) return;
+    const ItemDesc* d = a.blocks + a.cls_list[CL * a.max_blocks + idx];
     const int cnt = d->cnt;
-    if (cnt == 0) return;
     const int nbI = a.I / 128;
     for (int m = threadIdx.x; m < 64; m += 256)
         rsum[m] = m < cnt ? sum_ordered(a.asum + (size_t)(d->p0 + m) * nbI, nbI) : 0.f;
     __syncthreads();
-    const int rga = (cnt + 15) >> 4;
-    if (rga <= 1) down_mfma_body<K, 1>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
-    else if (rga <= 2) down_mfma_body<K, 2>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
-    else down_mfma_body<K, 4>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
+    down_mfma_body<K, RGA>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
 }
 
 // ------------------------------------------------------------------------------------------------ per-tile K
@@ -610,57 +606,86 @@ static hipError_t set_max_lds(const void* fn, int bytes) {
     return e;
 }
 
+template <int RGA>
 static mfma_fn pick_gu(int K) {
     switch (K) {
-        case 0: return gateup_mfma_mixed_kernel<kMfmaRows>;
-        case 1: return gateup_mfma_kernel<1>;
-        case 2: return gateup_mfma_kernel<2>;
-        case 3: return gateup_mfma_kernel<3>;
-        case 4: return gateup_mfma_kernel<4>;
-        case 5: return gateup_mfma_kernel<5>;
-        case 6: return gateup_mfma_kernel<6>;
-        case 7: return gateup_mfma_kernel<7>;
-        default: return gateup_mfma_kernel<8>;
+        case 1: return gateup_mfma_kernel<1, RGA>;
+        case 2: return gateup_mfma_kernel<2, RGA>;
+        case 3: return gateup_mfma_kernel<3, RGA>;
+        case 4: return gateup_mfma_kernel<4, RGA>;
+        case 5: return gateup_mfma_kernel<5, RGA>;
+        case 6: return gateup_mfma_kernel<6, RGA>;
+        case 7: return gateup_mfma_kernel<7, RGA>;
+        default: return gateup_mfma_kernel<8, RGA>;
     }
 }
 
+template <int RGA>
 static mfma_fn pick_dn(int K) {
     switch (K) {
-        case 0: return down_mfma_mixed_kernel<kMfmaRows>;
-        case 1: return down_mfma_kernel<1>;
-        case 2: return down_mfma_kernel<2>;
-        case 3: return down_mfma_kernel<3>;
-        case 4: return down_mfma_kernel<4>;
-        case 5: return down_mfma_kernel<5>;
-        case 6: return down_mfma_kernel<6>;
-        case 7: return down_mfma_kernel<7>;
-        default: return down_mfma_kernel<8>;
+        case 1: return down_mfma_kernel<1, RGA>;
+        case 2: return down_mfma_kernel<2, RGA>;
+        case 3: return down_mfma_kernel<3, RGA>;
+        case 4: return down_mfma_kernel<4, RGA>;
+        case 5: return down_mfma_kernel<5, RGA>;
+        case 6: return down_mfma_kernel<6, RGA>;
+        case 7: return down_mfma_kernel<7, RGA>;
+        default: return down_mfma_kernel<8, RGA>;
     }
 }
 
 int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
     EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
-    mfma_fn fn = pick_gu(a.Kg);
-    int lds = 0;
     if (a.Kg == 0) {
-        lds = (2 * kMfmaRows * 128 + 2 * kMfmaRows) * (int)sizeof(float);
+        mfma_fn fn = gateup_mfma_mixed_kernel<kMfmaRows>;
+        const int lds = (2 * kMfmaRows * 128 + 2 * kMfmaRows) * (int)sizeof(float);
         EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
+        EXL3_LAUNCH("moe_gateup_mfma", fn, dim3(nxb * (a.I / 128)), dim3(256), lds, st, a);
+        return EXL3_OK;
     }
-    EXL3_LAUNCH("moe_gateup_mfma", fn, dim3(nxb * (a.I / 128)), dim3(256), lds, st, a);
+    // the three row classes run concurrently: 4 row groups on the caller's stream, 2 and 1 on the side streams
+    AuxStreams ax;
+    int rc = aux_streams(&ax);
+    if (rc) return rc;
+    const dim3 grid(nxb * (a.I / 128));
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[0], st));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[0], ax.ev[0], 0));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[1], ax.ev[0], 0));
+    EXL3_LAUNCH("moe_gateup_mfma_r4", pick_gu<4>(a.Kg), grid, dim3(256), 0, st, a);
+    EXL3_LAUNCH("moe_gateup_mfma_r2", pick_gu<2>(a.Kg), grid, dim3(256), 0, ax.s[0], a);
+    EXL3_LAUNCH("moe_gateup_mfma_r1", pick_gu<1>(a.Kg), grid, dim3(256), 0, ax.s[1], a);
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[1], ax.s[0]));
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[2], ax.s[1]));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[1], 0));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[2], 0));
     return EXL3_OK;
 }
 
 int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
-    mfma_fn fn = pick_dn(a.Kd);
-    int lds = 0, ncb = (a.H / 128 + 1) / 2;
     if (a.Kd == 0) {
-        lds = (kMfmaRows * 128 + kMfmaRows) * (int)sizeof(float);
+        mfma_fn fn = down_mfma_mixed_kernel<kMfmaRows>;
+        const int lds = (kMfmaRows * 128 + kMfmaRows) * (int)sizeof(float);
         EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
-        ncb = a.H / 128;
+        EXL3_LAUNCH("moe_down_mfma", fn, dim3(nxb * (a.H / 128)), dim3(256), lds, st, a);
+        return EXL3_OK;
     }
-    EXL3_LAUNCH("moe_down_mfma", fn, dim3(nxb * ncb), dim3(256), lds, st, a);
+    // the three row classes run concurrently: 4 row groups on the caller's stream, 2 and 1 on the side streams
+    AuxStreams ax;
+    int rc = aux_streams(&ax);
+    if (rc) return rc;
+    const dim3 grid(nxb * ((a.H / 128 + 1) / 2));
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[0], st));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[0], ax.ev[0], 0));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[1], ax.ev[0], 0));
+    EXL3_LAUNCH("moe_down_mfma_r4", pick_dn<4>(a.Kd), grid, dim3(256), 0, st, a);
+    EXL3_LAUNCH("moe_down_mfma_r2", pick_dn<2>(a.Kd), grid, dim3(256), 0, ax.s[0], a);
+    EXL3_LAUNCH("moe_down_mfma_r1", pick_dn<1>(a.Kd), grid, dim3(256), 0, ax.s[1], a);
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[1], ax.s[0]));
+    EXL3_CHECK_HIP(hipEventRecord(ax.ev[2], ax.s[1]));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[1], 0));
+    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[2], 0));
     return EXL3_OK;
 }
 

@@ -9,6 +9,10 @@ constexpr int kMoeMaxExperts = 2048;   // expert tables per layer (routed + shar
 constexpr int kMoeSmallRows = 8;       // experts with at most this many rows in a call take the GEMV kernels
 constexpr int kMfmaRows = 64;          // row block of the MFMA grouped GEMM
 
+// Row class of an MFMA block (0: <= 16 rows, 1: <= 32, 2: <= 64): each class runs its own kernel instance sized for
+// its row groups, so that small blocks get the register budget (and occupancy) of a small block.
+__host__ __device__ constexpr int mfma_row_class(int cnt) { return cnt <= 16 ? 0 : cnt <= 32 ? 1 : 2; }
+
 // One work unit of the GEMV kernels: up to 8 rows (pairs) of one expert, with everything a workgroup needs so that a
 // single uniform load replaces the table lookups. Items past the last real one have cnt == 0.
 struct alignas(256) ItemDesc {
@@ -33,6 +37,8 @@ struct RouteArgs {
     int use_mfma, MB;                  // experts with more than MR rows -> blocks of MB rows for the MFMA kernels
     ItemDesc* blocks;                  // [max_blocks]
     int max_blocks;
+    int* cls_list;                     // optional [3][max_blocks]: block indices by row class (<= 16, 32, 64 rows)
+    int* cls_cnt;                      // [3]
     int* pair_tok;
     float* pair_w;
     int* pair_of;
@@ -60,6 +66,8 @@ struct MoeArgs {
     const ItemDesc* items;
     const ItemDesc* blocks;            // MFMA row blocks (cnt == 0 past the last)
     int max_blocks;
+    const int* cls_list;               // [3][max_blocks] block indices by row class (<= 16, <= 32, <= 64 rows)
+    const int* cls_cnt;                // [3] blocks per class
     _Float16* xh;                      // [pairs][2][H] transformed gate / up inputs of MFMA rows
     float* xsum;                       // [pairs][2][H / 128] block sums of xh (the MFMA rows' affine term)
     float* asum;                       // [pairs][I / 128] block sums of abuf (MFMA rows)

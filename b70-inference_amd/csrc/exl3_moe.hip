@@ -54,7 +54,9 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     int* nch = sm + 3 * r.E;       // [E] GEMV items of the expert, then their first index
     int* nbl = sm + 4 * r.E;       // [E] MFMA blocks of the expert, then their first index
     int* tmp = sm + 5 * r.E;       // [1024]
+    __shared__ int s_cls[3];
     const int t = threadIdx.x, T = blockDim.x;
+    if (t < 3) s_cls[t] = 0;
     const int np = r.M * r.slots;
     const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
     for (int e = t; e < r.E; e += T) {
@@ -91,6 +93,10 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             d.cnt = min(r.MB, c - q * r.MB);
             for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
             for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
+            if (r.cls_list) {
+                const int cl = mfma_row_class(d.cnt);
+                r.cls_list[cl * r.max_blocks + atomicAdd(&s_cls[cl], 1)] = b;
+            }
         }
         for (int q = 0, it = nch[e]; !big && q * mr < c; ++q, ++it) {
             ItemDesc& d = r.items[it];
@@ -106,6 +112,8 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     if (r.blocks)
         for (int b = nblocks + t; b < r.max_blocks; b += T) r.blocks[b].cnt = 0;
     if (t == 0 && r.n_items) r.n_items[0] = nitems;
+    __syncthreads();
+    if (t < 3 && r.cls_cnt) r.cls_cnt[t] = s_cls[t];
     if (r.tok_nvalid) {
         for (int tok = t; tok < r.M; tok += T) {
             int nv = 0;
@@ -153,7 +161,9 @@ constexpr int kAlignSmall = 256;
 __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
     __shared__ int s_e[kAlignSmall], s_pos[kAlignSmall];
     __shared__ uint8_t s_lead[kAlignSmall], s_blead[kAlignSmall];
+    __shared__ int s_cls[3];
     const int t = threadIdx.x;
+    if (t < 3) s_cls[t] = 0;
     const int np = r.M * r.slots;
     const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
     int e = -1, tok = 0;
@@ -231,9 +241,15 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
             d.cnt = min(r.MB, cnt - before);
             for (int i = 0; i < 9; ++i) d.tab[i] = ldg(r.tables + (int64_t)i * r.E + e);
             for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? ldg(r.kmaps + (int64_t)i * r.E + e) : 0;
+            if (r.cls_list) {
+                const int cl = mfma_row_class(d.cnt);
+                r.cls_list[cl * r.max_blocks + atomicAdd(&s_cls[cl], 1)] = block;
+            }
         }
         for (int b = nblocks + t; b < r.max_blocks; b += kAlignSmall) r.blocks[b].cnt = 0;
     }
+    __syncthreads();
+    if (t < 3 && r.cls_cnt) r.cls_cnt[t] = s_cls[t];
     if (r.counts)
         for (int x = t; x < r.E; x += kAlignSmall) {
             int c = 0;
@@ -589,7 +605,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) +
                    carve_size(a.max_blocks, sizeof(ItemDesc)) +
                    (use_mfma ? carve_size(npairs * 2 * a.H, 2) + carve_size(npairs * 2 * (a.H / 128), 4) +
-                                   carve_size(npairs * (a.I / 128), 4)
+                                   carve_size(npairs * (a.I / 128), 4) + carve_size(3 * (size_t)a.max_blocks + 3, 4)
                              : 0) +
                    carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
                    carve_size(a.M, 4) +
@@ -607,6 +623,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     a.xh = use_mfma ? c.take<_Float16>(npairs * 2 * a.H) : nullptr;
     a.xsum = use_mfma ? c.take<float>(npairs * 2 * (a.H / 128)) : nullptr;
     a.asum = use_mfma ? c.take<float>(npairs * (a.I / 128)) : nullptr;
+    int* cls = use_mfma ? c.take<int>(3 * (size_t)a.max_blocks + 3) : nullptr;
+    a.cls_list = cls;
+    a.cls_cnt = cls ? cls + 3 * (size_t)a.max_blocks : nullptr;
     int* pb = c.take<int>(npairs * 2);
     a.pair_tok = pb;
     a.pair_of = pb + npairs;
@@ -639,6 +658,8 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.MB = kMfmaRows;
     r.blocks = blocks;
     r.max_blocks = a.max_blocks;
+    r.cls_list = cls;
+    r.cls_cnt = cls ? cls + 3 * (size_t)a.max_blocks : nullptr;
     r.pair_tok = a.pair_tok;
     r.pair_w = a.pair_w;
     r.pair_of = a.pair_of;

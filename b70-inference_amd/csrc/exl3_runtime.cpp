@@ -28,6 +28,27 @@ std::mutex g_ws_mu;
 Workspace g_ws[kMaxDevices];
 }  // namespace
 
+namespace {
+AuxStreams g_aux[kMaxDevices];
+bool g_aux_ok[kMaxDevices];
+}  // namespace
+
+int aux_streams(AuxStreams* out) {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (!g_aux_ok[dev]) {
+        AuxStreams a{};
+        for (int i = 0; i < 2; ++i) EXL3_CHECK_HIP(hipStreamCreateWithFlags(&a.s[i], hipStreamNonBlocking));
+        for (int i = 0; i < 3; ++i) EXL3_CHECK_HIP(hipEventCreateWithFlags(&a.ev[i], hipEventDisableTiming));
+        g_aux[dev] = a;
+        g_aux_ok[dev] = true;
+    }
+    *out = g_aux[dev];
+    return EXL3_OK;
+}
+
 int workspace(size_t bytes, size_t ncounters, Workspace* out) {
     int dev = 0;
     EXL3_CHECK_HIP(hipGetDevice(&dev));

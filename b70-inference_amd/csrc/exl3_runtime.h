@@ -33,6 +33,14 @@ struct Workspace {
 };
 int workspace(size_t bytes, size_t ncounters, Workspace* out);
 
+// Two library-owned side streams (default priority) and three events of the current device, created on first use:
+// a launch sequence forks onto them with events and joins back, which also works under stream capture.
+struct AuxStreams {
+    hipStream_t s[2];
+    hipEvent_t ev[3];
+};
+int aux_streams(AuxStreams* out);
+
 // Integer tuning knob from the environment (read once per name), `dflt` when unset or not a positive number.
 int env_int(const char* name, int dflt);
 
