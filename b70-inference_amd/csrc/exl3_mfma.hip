@@ -198,6 +198,13 @@ struct MfmaPipe {
 };
 
 // ------------------------------------------------------------------------------------------------ gate | up
+template <int RGA>
+__device__ __forceinline__ void gateup_epilogue(const MoeArgs& a, const ItemDesc* d, int nb, int cnt,
+                                                const f4_t (&acc)[kMfT][RGA], float* C, const float* rsum);
+template <int RGA>
+__device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* d, int nb, int cnt,
+                                              const f4_t (&acc)[kMfT][RGA], float* C, const float* rsum, int* s_comb);
+
 template <int K, int RGA>
 __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
                                                  uint32_t* wlds, float* C, float* rsum) {
@@ -219,7 +226,16 @@ __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDes
 #pragma unroll
         for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
     L.run(acc);
+    gateup_epilogue<RGA>(a, d, nb, cnt, acc, C, rsum);
+}
 
+// Affine, Hadamard * svh, act(g, u) * suh_d, Hadamard of the workgroup's 128 columns per 16-row group -> abuf (fp16)
+// and its block sums (the down GEMM's affine term).
+template <int RGA>
+__device__ __forceinline__ void gateup_epilogue(const MoeArgs& a, const ItemDesc* d, int nb, int cnt,
+                                                const f4_t (&acc)[kMfT][RGA], float* C, const float* rsum) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p0 = d->p0;
     const uint16_t* svg = reinterpret_cast<const uint16_t*>(d->tab[2]) + nb * 128;
     const uint16_t* svu = reinterpret_cast<const uint16_t*>(d->tab[5]) + nb * 128;
     const uint16_t* sud = reinterpret_cast<const uint16_t*>(d->tab[7]) + nb * 128;
@@ -310,7 +326,7 @@ __device__ __forceinline__ void down_mfma_body(const MoeArgs& a, const ItemDesc*
                                                uint32_t* wlds, float* C, float* rsum, int* s_comb) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
-    const int tn = a.H / 16, nbH = a.H / 128;
+    const int tn = a.H / 16;
     const uint32_t* trd = reinterpret_cast<const uint32_t*>(d->tab[6]);
     MfmaPipe<K, 1, RGA> L;
     L.nsteps = a.I / 32;
@@ -328,7 +344,16 @@ __device__ __forceinline__ void down_mfma_body(const MoeArgs& a, const ItemDesc*
 #pragma unroll
         for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
     L.run(acc);
+    down_epilogue<RGA>(a, d, nb, cnt, acc, C, rsum, s_comb);
+}
 
+// Affine, Hadamard * svh_d * w of the workgroup's 256 columns per 16-row group -> y rows, then the combine.
+template <int RGA>
+__device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* d, int nb, int cnt,
+                                              const f4_t (&acc)[kMfT][RGA], float* C, const float* rsum, int* s_comb) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p0 = d->p0;
+    const int nbH = a.H / 128;
     const int nhalf = 2 * nb + 1 < nbH ? 2 : 1;
     const uint16_t* svd = reinterpret_cast<const uint16_t*>(d->tab[8]) + nb * 256;
     float sd[2][2];
@@ -400,196 +425,275 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mfm
 }
 
 // ------------------------------------------------------------------------------------------------ per-tile K
-// Per-tile bitrate (K = 0): each wave decodes its tile columns with the tile's own K (lanes 0-31 and 32-63 hold two
-// tile-rows, which may differ), A fragments straight from memory.
-template <int MB>
-__global__ __launch_bounds__(256) void gateup_mfma_mixed_kernel(MoeArgs a) {
-    extern __shared__ float smem[];
-    constexpr int RG = MB / 16;
-    float* C = smem;                         // [2][MB][128]
-    float* rsum = smem + 2 * MB * 128;       // [2][MB]
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nbI = a.I / 128;
-    int blk, nb;
-    xcd_map(nbI, blk, nb);
-    if (blk >= a.max_blocks) return;
-    const ItemDesc* d = a.blocks + blk;
-    const int cnt = d->cnt;
-    if (cnt == 0) return;
-    const int p0 = d->p0;
-    const int tn = a.I / 16;
-    const uint32_t* trp[2] = {reinterpret_cast<const uint32_t*>(d->tab[0]),
-                              reinterpret_cast<const uint32_t*>(d->tab[3])};
-    const uint8_t* kmp[2] = {reinterpret_cast<const uint8_t*>(d->km[0]), reinterpret_cast<const uint8_t*>(d->km[2])};
-    const int32_t* wop[2] = {reinterpret_cast<const int32_t*>(d->km[1]), reinterpret_cast<const int32_t*>(d->km[3])};
-    const int ct0 = nb * 8 + 2 * wave;
-    const _Float16* arow[RG];
-#pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-        int r = 16 * rg + (lane & 15);
-        r = r < cnt ? r : cnt - 1;
-        arow[rg] = a.xh + (size_t)(p0 + r) * 2 * a.H + 8 * (lane >> 4);
+// Per-tile bitrate (K = 0: tile i of a projection holds 8 kmap[i] words at woff[i]). MFMA 16x16x16 per tile-row, so
+// the 64 lanes of a wave always share one tile and branch uniformly on its K. Fragment layout: B[k][n] lane L holds
+// n = L & 15, k = 4 (L >> 4) + j, j < 4, i.e. tile rows 4g .. 4g + 3 (g = L >> 4) of column n = chunk positions
+// u0 + {0, 1, 8, 9}, u0 = 4 (n >> 3) + 2 (g >> 1) + 16 (g & 1); A[m][k] lane L holds m = L & 15, same k.
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+constexpr int kMixKMax = 8;
+constexpr int kMixTS = 8 * kMixKMax + 4;                    // LDS words per staged tile (w(-1), 8K words, w(0), pad)
+
+// Lane's four h values of a staged tile of bitrate K (1 .. 8, any lane value): slot[1 + w] = ring word w for
+// w = -1 .. 8K. Positions u0, u0 + 1 and u0 + 8, u0 + 9 of chunk q, u0 = 4 h + 2 (g >> 1) + 16 (g & 1), form two window
+// pairs. A pair whose first window starts at ring bit `start` reads words floor((start - 1) / 32) and the next one,
+// funnel-shifted by 32 - (start - 32 floor((start - 1) / 32)); its windows then sit at bits 0 and K from the top. With
+// t = start + 31 (> 0): the slot index is t >> 5 and the shift 31 - (t & 31), the low bits of ~t. cA = 32 q + u0 + 1.
+__device__ __forceinline__ h4_t decode4_rt(const uint32_t* slot, int K, uint32_t cA) {
+    const uint32_t tA = cA * (uint32_t)K + 15u;                // start = (32 q + u0 + 1) K - 16
+    const uint32_t tB = tA + 8u * (uint32_t)K;                 // positions u0 + 8, u0 + 9
+    const uint32_t s1 = 16u - (uint32_t)K;
+    const uint32_t* pa = slot + (tA >> 5);
+    const uint32_t* pb = slot + (tB >> 5);
+    const uint32_t na = __builtin_amdgcn_alignbit(pa[0], pa[1], ~tA);
+    const uint32_t nb = __builtin_amdgcn_alignbit(pb[0], pb[1], ~tB);
+    const uint32_t p0 = __builtin_bit_cast(uint32_t, mul1_pair_raw(na >> 16, na >> s1));
+    const uint32_t p1 = __builtin_bit_cast(uint32_t, mul1_pair_raw(nb >> 16, nb >> s1));
+    typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+    const u2_t v = {p0, p1};
+    return __builtin_bit_cast(h4_t, v);
+}
+
+// One wave, kMfT tile columns (column pair t >> 1: gate|up projection, or down columns c0 + 2 (t >> 1)), RGA row
+// groups, 32 k per step = two tile-rows. Per step the wave's 8 tiles (slot 2t + tile-row half) are fetched by 8 lanes
+// each with two clamped 16-byte loads (any K <= 8, every address inside the tile), after their (kmap, woff) one step
+// earlier; staged in LDS like MfmaPipe with the tile's K beside it, then decoded per tile-row with that K. Rings of 4
+// (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4 steps ahead) make the loop a 4-step unroll;
+// the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A as in MfmaPipe.
+template <int NP, int RGA>
+struct MfmaPipeMix {
+    static constexpr int DW = 3;
+    static constexpr int UNITS = NP * RGA * 64;
+    static constexpr int CPT = (UNITS + 255) / 256;
+    static constexpr int TPP = kMfT / NP;
+    const uint32_t* words[2];                                // per column pair: the projection's words
+    const uint8_t* kmap[2];
+    const int32_t* woff[2];
+    int col[2];                                              // per column pair: its first tile column
+    int tn, nsteps;
+    uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
+    int* kt;                                                 // the wave's staged K per slot [8]
+    uint32_t cA;                                             // 32 q + u0 + 1 of the lane's fragment positions
+    const _Float16* asrc[CPT];
+    int adst[CPT];
+    u32x4_t* lds;
+    int lane;
+
+    // this lane's tile of step s: slot lane >> 3 = 2 t + hr, tile (2 s + hr, column of t)
+    __device__ __forceinline__ int tile_of(int s) const {
+        const int sl = lane >> 3, t = sl >> 1, hr = sl & 1;
+        const int ss = s < nsteps ? s : nsteps - 1;
+        return (2 * ss + hr) * tn + ((t >> 1) ? col[1] : col[0]) + (t & 1);
     }
-    f4_t acc[4][RG];
+    __device__ __forceinline__ void load_meta(int (&M)[2], int s) const {
+        const int pr = (lane >> 4) >> 1, tile = tile_of(s);
+        M[0] = ldg((pr ? kmap[1] : kmap[0]) + tile);
+        M[1] = ldg((pr ? woff[1] : woff[0]) + tile);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ void load_w(u32x4_t (&D)[2], const int (&M)[2]) const {
+        const int pr = (lane >> 4) >> 1, i = lane & 7, last = 8 * M[0] - 4;
+        const uint32_t* t = (pr ? words[1] : words[0]) + M[1];
+        const int a0 = 4 * i < last ? 4 * i : last, a1 = 32 + 4 * i < last ? 32 + 4 * i : last;
+        D[0] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (a0 > 0 ? a0 : 0)));
+        D[1] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (a1 > 0 ? a1 : 0)));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ void stage_w(const u32x4_t (&D)[2], const int (&M)[2]) const {
+        const int sl = lane >> 3, i = lane & 7, K = M[0], last = 8 * K - 4;
+        uint32_t* t = wl + sl * kMixTS;
+        const int a0 = 4 * i < last ? 4 * i : last, a1 = 32 + 4 * i < last ? 32 + 4 * i : last;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
-    const int nsteps = a.H / 32;
-    for (int s = 0; s < nsteps; ++s) {
-        const int tr = 2 * s + (lane >> 5);
-        h8_t bf[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int p = t >> 1, col = ct0 + (t & 1);
-            const int tile = tr * tn + col;
-            bf[t] = frag_decode_k(trp[p] + ldg(wop[p] + tile), ldg(kmp[p] + tile), lane);
+        for (int j = 0; j < 4; ++j) {
+            t[1 + a0 + j] = D[0][j];
+            t[1 + a1 + j] = D[1][j];
         }
+        if (a1 + 4 == 8 * K) t[0] = D[1][3];                 // w(8K - 1) in front (a1 = 8K - 4 for K <= 4)
+        if (i == 0) {
+            t[8 * K + 1] = D[0][0];                          // w(0) behind
+            kt[sl] = K;
+        }
+    }
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA]) const {
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
+        for (int sr = 0; sr < 2; ++sr) {
+            h4_t af[NP][RGA];
+            const int ch = 2 * sr + ((lane >> 4) >> 1), hf = (lane >> 4) & 1;
 #pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                const h8_t av = *reinterpret_cast<const h8_t*>(arow[rg] + (size_t)p * a.H + 32 * s);
-                acc[2 * p][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[2 * p], acc[2 * p][rg], 0, 0, 0);
-                acc[2 * p + 1][rg] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[2 * p + 1], acc[2 * p + 1][rg], 0, 0, 0);
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int rg = 0; rg < RGA; ++rg) {
+                    const u32x4_t* u = lds + stage * UNITS + p * RGA * 64 + a_unit(16 * rg + (lane & 15), ch);
+                    af[p][rg] = *(reinterpret_cast<const h4_t*>(u) + hf);
+                }
+#pragma unroll
+            for (int t = 0; t < kMfT; ++t) {
+                const int sl = 2 * t + sr;
+                const h4_t bf = decode4_rt(wl + sl * kMixTS, kt[sl], cA);
+#pragma unroll
+                for (int rg = 0; rg < RGA; ++rg)
+                    acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
             }
         }
     }
-    const int nblk = a.H / 128;
-    for (int i = threadIdx.x; i < 2 * MB; i += 256) {
-        const int p = i / MB, m = i - p * MB;
-        float v = 0.f;
-        if (m < cnt) {
-            const float* q = a.xsum + ((size_t)(p0 + m) * 2 + p) * nblk;
-            for (int b = 0; b < nblk; ++b) v += q[b];
+    __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
+        const int ss = (s < nsteps ? s : nsteps - 1) * 32;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) Ra[j] = ldg(reinterpret_cast<const u32x4_t*>(asrc[j] + ss));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
+    }
+    // step s, R = s mod 4
+    template <int R>
+    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
+                                         f4_t (&acc)[kMfT][RGA]) const {
+        load_a(RA[R], s + 4);
+        load_meta(M[(R + DW) % 4], s + DW);
+        load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
+        stage_w(W[R], M[R]);
+        compute(R % 2, acc);
+        store_a(RA[(R + 1) % 4], (R + 1) % 2);
+        __syncthreads();
+    }
+    __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
+        u32x4_t W[4][2];
+        int M[4][2];
+        u32x4_t RA[4][CPT];
+#pragma unroll
+        for (int i = 0; i < DW; ++i) load_meta(M[i], i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            load_a(RA[i], i);
+            if (i < DW - 1) load_w(W[i], M[i]);
         }
-        rsum[i] = v;
+        store_a(RA[0], 0);
+        __syncthreads();
+        for (int s = 0; s < nsteps; s += 4) {
+            step<0>(s, W, M, RA, acc);
+            step<1>(s + 1, W, M, RA, acc);
+            step<2>(s + 2, W, M, RA, acc);
+            step<3>(s + 3, W, M, RA, acc);
+        }
     }
+    template <typename F>
+    __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int p = t >> 1, col = (2 * wave + (t & 1)) * 16 + (lane & 15);
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) C[(p * MB + 16 * rg + 4 * (lane >> 4) + i) * 128 + col] = acc[t][rg][i];
+        for (int j = 0; j < CPT; ++j) {
+            const int u = (threadIdx.x + 256 * j) % UNITS;
+            const int p = u / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+            asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
+            adst[j] = p * RGA * 64 + a_unit(row, ch);
+        }
+        const int q = lane & 7, h = (lane >> 3) & 1, g = lane >> 4;
+        cA = (uint32_t)(32 * q + 4 * h + 2 * (g >> 1) + 16 * (g & 1) + 1);
     }
-    __syncthreads();
+};
 
-    const uint16_t* svg = reinterpret_cast<const uint16_t*>(d->tab[2]) + nb * 128;
-    const uint16_t* svu = reinterpret_cast<const uint16_t*>(d->tab[5]) + nb * 128;
-    const uint16_t* sud = reinterpret_cast<const uint16_t*>(d->tab[7]) + nb * 128;
-    for (int m = wave; m < cnt; m += 4) {
-        const float sg = kMul1C2 * rsum[m], su = kMul1C2 * rsum[MB + m];
-        float g0 = kMul1C1 * C[m * 128 + lane] + sg, g1 = kMul1C1 * C[m * 128 + lane + 64] + sg;
-        float u0 = kMul1C1 * C[(MB + m) * 128 + lane] + su, u1 = kMul1C1 * C[(MB + m) * 128 + lane + 64] + su;
-        fwht128_wave(g0, g1, lane);
-        fwht128_wave(u0, u1, lane);
-        g0 = (float)(_Float16)(g0 * kRsqrt128 * h2f(ldg(svg + lane)));
-        g1 = (float)(_Float16)(g1 * kRsqrt128 * h2f(ldg(svg + lane + 64)));
-        u0 = (float)(_Float16)(u0 * kRsqrt128 * h2f(ldg(svu + lane)));
-        u1 = (float)(_Float16)(u1 * kRsqrt128 * h2f(ldg(svu + lane + 64)));
-        float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
-        float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
-        a0 = (float)(_Float16)(a0 * h2f(ldg(sud + lane)));
-        a1 = (float)(_Float16)(a1 * h2f(ldg(sud + lane + 64)));
-        fwht128_wave(a0, a1, lane);
-        const _Float16 h0 = (_Float16)(a0 * kRsqrt128), h1 = (_Float16)(a1 * kRsqrt128);
-        uint16_t* dst = a.abuf + (size_t)(p0 + m) * a.I + nb * 128;
-        dst[lane] = __builtin_bit_cast(uint16_t, h0);
-        dst[lane + 64] = __builtin_bit_cast(uint16_t, h1);
-        const float bs = wave_sum_f32((float)h0 + (float)h1);
-        if (lane == 0) a.asum[(size_t)(p0 + m) * nbI + nb] = bs;
+template <int RGA>
+__device__ __forceinline__ void gateup_mix_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
+                                                uint32_t* wlds, int* kts, float* C, float* rsum) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p0 = d->p0;
+    MfmaPipeMix<2, RGA> L;
+    L.tn = a.I / 16;
+    L.nsteps = a.H / 32;
+    L.lds = stage;
+    L.lane = lane;
+    L.wl = wlds + wave * 8 * kMixTS;
+    L.kt = kts + wave * 8;
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+        L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[3 * pr]);
+        L.kmap[pr] = reinterpret_cast<const uint8_t*>(d->km[2 * pr]);
+        L.woff[pr] = reinterpret_cast<const int32_t*>(d->km[2 * pr + 1]);
+        L.col[pr] = nb * 8 + 2 * wave;
     }
+    L.setup_a(cnt, [&](int p, int row) { return a.xh + ((size_t)(p0 + row) * 2 + p) * a.H; });
+    f4_t acc[kMfT][RGA];
+#pragma unroll
+    for (int t = 0; t < kMfT; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
+    L.run(acc);
+    gateup_epilogue<RGA>(a, d, nb, cnt, acc, C, rsum);
 }
 
-template <int MB>
-__global__ __launch_bounds__(256) void down_mfma_mixed_kernel(MoeArgs a) {
-    extern __shared__ float smem[];
-    constexpr int RG = MB / 16;
-    float* C = smem;                         // [MB][128]
-    float* rsum = smem + MB * 128;           // [MB]
-    __shared__ int s_comb[MB];
+template <int RGA>
+__device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
+                                              uint32_t* wlds, int* kts, float* C, float* rsum, int* s_comb) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nbH = a.H / 128;
-    int blk, nb;
-    xcd_map(nbH, blk, nb);
-    if (blk >= a.max_blocks) return;
-    const ItemDesc* d = a.blocks + blk;
-    const int cnt = d->cnt;
-    if (cnt == 0) return;
     const int p0 = d->p0;
     const int tn = a.H / 16;
-    const uint32_t* trd = reinterpret_cast<const uint32_t*>(d->tab[6]);
-    const uint8_t* kmd = reinterpret_cast<const uint8_t*>(d->km[4]);
-    const int32_t* wod = reinterpret_cast<const int32_t*>(d->km[5]);
-    const int ct0 = nb * 8 + 2 * wave;
-    const uint16_t* arow[RG];
+    MfmaPipeMix<1, RGA> L;
+    L.tn = tn;
+    L.nsteps = a.I / 32;
+    L.lds = stage;
+    L.lane = lane;
+    L.wl = wlds + wave * 8 * kMixTS;
+    L.kt = kts + wave * 8;
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-        int r = 16 * rg + (lane & 15);
-        r = r < cnt ? r : cnt - 1;
-        arow[rg] = a.abuf + (size_t)(p0 + r) * a.I + 8 * (lane >> 4);
+    for (int pr = 0; pr < 2; ++pr) {
+        L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[6]);
+        L.kmap[pr] = reinterpret_cast<const uint8_t*>(d->km[4]);
+        L.woff[pr] = reinterpret_cast<const int32_t*>(d->km[5]);
+        int ct = nb * 16 + 4 * wave + 2 * pr;
+        L.col[pr] = ct < tn ? ct : tn - 2;             // a last half block: in-bounds loads, results unused
     }
-    f4_t acc[2][RG];
+    L.setup_a(cnt, [&](int, int row) { return reinterpret_cast<const _Float16*>(a.abuf) + (size_t)(p0 + row) * a.I; });
+    f4_t acc[kMfT][RGA];
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) acc[0][rg] = acc[1][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
-    const int nsteps = a.I / 32;
-    for (int s = 0; s < nsteps; ++s) {
-        const int tr = 2 * s + (lane >> 5);
-        h8_t bf[2];
+    for (int t = 0; t < kMfT; ++t)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int tile = tr * tn + ct0 + t;
-            bf[t] = frag_decode_k(trd + ldg(wod + tile), ldg(kmd + tile), lane);
-        }
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-            const h8_t av = *reinterpret_cast<const h8_t*>(arow[rg] + 32 * s);
-            acc[0][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[0], acc[0][rg], 0, 0, 0);
-            acc[1][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[1], acc[1][rg], 0, 0, 0);
-        }
-    }
-    const int nbI = a.I / 128;
-    for (int m = threadIdx.x; m < MB; m += 256) {
-        float v = 0.f;
-        if (m < cnt) {
-            const float* q = a.asum + (size_t)(p0 + m) * nbI;
-            for (int b = 0; b < nbI; ++b) v += q[b];
-        }
-        rsum[m] = v;
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int col = (2 * wave + t) * 16 + (lane & 15);
-#pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) C[(16 * rg + 4 * (lane >> 4) + i) * 128 + col] = acc[t][rg][i];
-    }
-    __syncthreads();
+        for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
+    L.run(acc);
+    down_epilogue<RGA>(a, d, nb, cnt, acc, C, rsum, s_comb);
+}
 
-    const uint16_t* svd = reinterpret_cast<const uint16_t*>(d->tab[8]) + nb * 128;
-    for (int m = wave; m < cnt; m += 4) {
-        const float sx = kMul1C2 * rsum[m];
-        float v0 = kMul1C1 * C[m * 128 + lane] + sx, v1 = kMul1C1 * C[m * 128 + lane + 64] + sx;
-        fwht128_wave(v0, v1, lane);
-        const float w = a.pair_w[p0 + m];
-        float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 128;
-        splitk_store(dst + lane, v0 * kRsqrt128 * h2f(ldg(svd + lane)) * w);
-        splitk_store(dst + lane + 64, v1 * kRsqrt128 * h2f(ldg(svd + lane + 64)) * w);
+template <int RGA>
+__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_mix_kernel(MoeArgs a) {
+    constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
+    __shared__ u32x4_t stage[2 * 2 * RGA * 64];
+    __shared__ uint32_t wlds[4 * 8 * kMixTS];
+    __shared__ int kts[4 * 8];
+    __shared__ float C[2 * 16 * 128];
+    __shared__ float rsum[2 * 64];
+    const int nbI = a.I / 128;
+    int idx, nb;
+    xcd_map(nbI, idx, nb);
+    if (idx >= a.cls_cnt[CL]) return;
+    const ItemDesc* d = a.blocks + a.cls_list[CL * a.max_blocks + idx];
+    const int cnt = d->cnt;
+    const int nblk = a.H / 128;
+    for (int i = threadIdx.x; i < 2 * 64; i += 256) {
+        const int p = i >> 6, m = i & 63;
+        rsum[i] = m < cnt ? sum_ordered(a.xsum + ((size_t)(d->p0 + m) * 2 + p) * nblk, nblk) : 0.f;
     }
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int m = threadIdx.x; m < cnt; m += 256) {
-        const int t = a.pair_tok[p0 + m];
-        const int old = __hip_atomic_fetch_add(&a.cnt_tok[(size_t)t * nbH + nb], 1, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_comb[m] = (old == a.tok_nvalid[t] - 1) ? t : -1;
-    }
+    gateup_mix_body<RGA>(a, d, nb, cnt, stage, wlds, kts, C, rsum);
+}
+
+template <int RGA>
+__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix_kernel(MoeArgs a) {
+    constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
+    __shared__ u32x4_t stage[2 * RGA * 64];
+    __shared__ uint32_t wlds[4 * 8 * kMixTS];
+    __shared__ int kts[4 * 8];
+    __shared__ float C[16 * 256];
+    __shared__ float rsum[64];
+    __shared__ int s_comb[2 * 64];
+    const int nbH2 = (a.H / 128 + 1) / 2;
+    int idx, nb;
+    xcd_map(nbH2, idx, nb);
+    if (idx >= a.cls_cnt[CL]) return;
+    const ItemDesc* d = a.blocks + a.cls_list[CL * a.max_blocks + idx];
+    const int cnt = d->cnt;
+    const int nbI = a.I / 128;
+    for (int m = threadIdx.x; m < 64; m += 256)
+        rsum[m] = m < cnt ? sum_ordered(a.asum + (size_t)(d->p0 + m) * nbI, nbI) : 0.f;
     __syncthreads();
-    for (int m = wave; m < cnt; m += 4)
-        if (s_comb[m] >= 0) combine_token(a, s_comb[m], nb, lane);
+    down_mix_body<RGA>(a, d, nb, cnt, stage, wlds, kts, C, rsum, s_comb);
 }
 
 // ------------------------------------------------------------------------------------------------ host
@@ -634,27 +738,16 @@ static mfma_fn pick_dn(int K) {
     }
 }
 
-int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
-    const int nxb = (a.max_blocks + 7) / 8 * 8;
-    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
-    if (a.Kg == 0) {
-        mfma_fn fn = gateup_mfma_mixed_kernel<kMfmaRows>;
-        const int lds = (2 * kMfmaRows * 128 + 2 * kMfmaRows) * (int)sizeof(float);
-        EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
-        EXL3_LAUNCH("moe_gateup_mfma", fn, dim3(nxb * (a.I / 128)), dim3(256), lds, st, a);
-        return EXL3_OK;
-    }
+template <typename F>
+static int fork3(hipStream_t st, F launch) {
     // the three row classes run concurrently: 4 row groups on the caller's stream, 2 and 1 on the side streams
     AuxStreams ax;
     int rc = aux_streams(&ax);
     if (rc) return rc;
-    const dim3 grid(nxb * (a.I / 128));
     EXL3_CHECK_HIP(hipEventRecord(ax.ev[0], st));
     EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[0], ax.ev[0], 0));
     EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[1], ax.ev[0], 0));
-    EXL3_LAUNCH("moe_gateup_mfma_r4", pick_gu<4>(a.Kg), grid, dim3(256), 0, st, a);
-    EXL3_LAUNCH("moe_gateup_mfma_r2", pick_gu<2>(a.Kg), grid, dim3(256), 0, ax.s[0], a);
-    EXL3_LAUNCH("moe_gateup_mfma_r1", pick_gu<1>(a.Kg), grid, dim3(256), 0, ax.s[1], a);
+    if ((rc = launch(4, st)) || (rc = launch(2, ax.s[0])) || (rc = launch(1, ax.s[1]))) return rc;
     EXL3_CHECK_HIP(hipEventRecord(ax.ev[1], ax.s[0]));
     EXL3_CHECK_HIP(hipEventRecord(ax.ev[2], ax.s[1]));
     EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[1], 0));
@@ -662,31 +755,29 @@ int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
     return EXL3_OK;
 }
 
+int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
+    const int nxb = (a.max_blocks + 7) / 8 * 8;
+    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
+    const dim3 grid(nxb * (a.I / 128));
+    return fork3(st, [&](int rga, hipStream_t s) -> int {
+        mfma_fn fn = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)
+                               : (rga == 4 ? pick_gu<4>(a.Kg) : rga == 2 ? pick_gu<2>(a.Kg) : pick_gu<1>(a.Kg));
+        const char* nm = rga == 4 ? "moe_gateup_mfma_r4" : rga == 2 ? "moe_gateup_mfma_r2" : "moe_gateup_mfma_r1";
+        EXL3_LAUNCH(nm, fn, grid, dim3(256), 0, s, a);
+        return EXL3_OK;
+    });
+}
+
 int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
-    if (a.Kd == 0) {
-        mfma_fn fn = down_mfma_mixed_kernel<kMfmaRows>;
-        const int lds = (kMfmaRows * 128 + kMfmaRows) * (int)sizeof(float);
-        EXL3_CHECK_HIP(set_max_lds((const void*)fn, lds));
-        EXL3_LAUNCH("moe_down_mfma", fn, dim3(nxb * (a.H / 128)), dim3(256), lds, st, a);
-        return EXL3_OK;
-    }
-    // the three row classes run concurrently: 4 row groups on the caller's stream, 2 and 1 on the side streams
-    AuxStreams ax;
-    int rc = aux_streams(&ax);
-    if (rc) return rc;
     const dim3 grid(nxb * ((a.H / 128 + 1) / 2));
-    EXL3_CHECK_HIP(hipEventRecord(ax.ev[0], st));
-    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[0], ax.ev[0], 0));
-    EXL3_CHECK_HIP(hipStreamWaitEvent(ax.s[1], ax.ev[0], 0));
-    EXL3_LAUNCH("moe_down_mfma_r4", pick_dn<4>(a.Kd), grid, dim3(256), 0, st, a);
-    EXL3_LAUNCH("moe_down_mfma_r2", pick_dn<2>(a.Kd), grid, dim3(256), 0, ax.s[0], a);
-    EXL3_LAUNCH("moe_down_mfma_r1", pick_dn<1>(a.Kd), grid, dim3(256), 0, ax.s[1], a);
-    EXL3_CHECK_HIP(hipEventRecord(ax.ev[1], ax.s[0]));
-    EXL3_CHECK_HIP(hipEventRecord(ax.ev[2], ax.s[1]));
-    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[1], 0));
-    EXL3_CHECK_HIP(hipStreamWaitEvent(st, ax.ev[2], 0));
-    return EXL3_OK;
+    return fork3(st, [&](int rga, hipStream_t s) -> int {
+        mfma_fn fn = a.Kd == 0 ? (rga == 4 ? down_mix_kernel<4> : rga == 2 ? down_mix_kernel<2> : down_mix_kernel<1>)
+                               : (rga == 4 ? pick_dn<4>(a.Kd) : rga == 2 ? pick_dn<2>(a.Kd) : pick_dn<1>(a.Kd));
+        const char* nm = rga == 4 ? "moe_down_mfma_r4" : rga == 2 ? "moe_down_mfma_r2" : "moe_down_mfma_r1";
+        EXL3_LAUNCH(nm, fn, grid, dim3(256), 0, s, a);
+        return EXL3_OK;
+    });
 }
 
 }  // namespace exl3

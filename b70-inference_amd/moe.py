@@ -31,6 +31,16 @@ class MixedEXL3:
         self.in_features, self.out_features = suh.numel(), svh.numel()
         if kmap.numel() != (self.in_features // 16) * (self.out_features // 16) or woff.numel() != kmap.numel() + 1:
             raise Exl3Error("MixedEXL3: kmap / woff sizes do not match the shape")
+        # the kernels stage a tile in 8 * kmap words and fetch it with 16-byte loads at words + woff: K in 1..8,
+        # woff the running sum of 8 * kmap from 0, words 16-byte aligned and long enough
+        km = kmap.to(torch.int64)
+        if kmap.numel() and (int(km.min()) < 1 or int(km.max()) > 8):
+            raise Exl3Error("MixedEXL3: every kmap entry must be in 1..8")
+        wo = woff.to(torch.int64)
+        if int(wo[0]) != 0 or not torch.equal(wo[1:] - wo[:-1], 8 * km):
+            raise Exl3Error("MixedEXL3: woff must be the running sum of 8 * kmap starting at 0")
+        if words.numel() * words.element_size() < 4 * int(wo[-1]) or words.data_ptr() % 16:
+            raise Exl3Error("MixedEXL3: words must hold woff[-1] uint32 words and be 16-byte aligned")
         self.K = 0
         self.trellis = words
 

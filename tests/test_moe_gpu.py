@@ -276,6 +276,19 @@ def test_moe_prefill_per_tile_k_shared(exl3, oracle):
     assert max_rel(y, ref) <= MAX_REL
 
 
+def test_moe_prefill_per_tile_k_all_bitrates(exl3, oracle):
+    """Per-tile K over 1..8 on the MFMA path in all three row classes: the hot experts take about 85 rows each (a
+    64-row block plus a 17..32-row block), the rest at most 16; H = 384 leaves the down kernel a half column block."""
+    tables, orc = make_experts(exl3, oracle, 10, 384, 256, 0, 0, 1750, per_tile=(tuple(range(1, 9)), (0.125,) * 8))
+    ids, w = _skewed_ids(100, 4, 10, 1751)
+    counts = np.bincount(ids.numpy().reshape(-1), minlength=10)
+    assert counts.max() > 64 and any(16 < c <= 32 for c in counts % 64) and counts.min() <= 16
+    x = torch.randn(100, 384, generator=torch.Generator().manual_seed(1752)).half()
+    for act in (0, 1):
+        y, ref = _run(exl3, oracle, tables, orc, x, ids, w, act=act)
+        assert max_rel(y, ref) <= MAX_REL
+
+
 def test_moe_prefill_deterministic_and_token_permutation(exl3, small):
     """Row results do not depend on which other rows share a block: permuting the tokens permutes the output rows
     bit for bit, and two calls agree exactly."""
