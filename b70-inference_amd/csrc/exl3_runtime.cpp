@@ -113,24 +113,19 @@ hipEvent_t take_event() {
 }
 }  // namespace
 
-void prof_start(const char* name, hipStream_t s) {
-    if (!g_prof_on) return;
+ProfEvents prof_begin(const char* name) {
+    if (!g_prof_on) return {nullptr, nullptr};
     if (g_recs.size() >= 100000) {
         g_prof_overflow = true;
-        return;
+        return {nullptr, nullptr};
     }
     ProfRec r{name, take_event(), take_event()};
-    if (!r.a || !r.b) return;
-    hipEventRecord(r.a, s);
+    if (!r.a || !r.b) return {nullptr, nullptr};
     g_recs.push_back(r);
+    return {r.a, r.b};
 }
 
 int prof_repeat() { return g_prof_on ? g_prof_rep : 1; }
-
-void prof_stop(hipStream_t s) {
-    if (!g_prof_on || g_recs.empty() || g_prof_overflow) return;
-    hipEventRecord(g_recs.back().b, s);
-}
 
 }  // namespace exl3
 

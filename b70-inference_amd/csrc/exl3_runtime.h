@@ -2,6 +2,7 @@
 // per-device workspace (split-K partials, arrival counters, routing tables, intermediate activations).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -62,22 +63,30 @@ inline size_t carve_size(size_t n, size_t elem) { return (n * elem + 255) & ~(si
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-// Opt-in kernel timing (exl3_profile_enable): a HIP event pair on the launch stream around every library launch,
+// Opt-in kernel timing (exl3_profile_enable): every library launch gets a HIP event pair that the runtime records
+// with the dispatch itself (hipExtLaunchKernel start/stop events: the kernel's own begin and end, no queue gaps),
 // aggregated per kernel name by exl3_profile_read. Off by default; never used under graph capture.
-// With repeat R > 1 every profiled launch runs R times back to back inside its event pair (all library kernels
-// are idempotent: they rewrite their outputs and leave their arrival counters at zero), which amortises the
-// event-record overhead; exl3_profile_read reports the per-launch average.
-void prof_start(const char* name, hipStream_t s);
-void prof_stop(hipStream_t s);
+// With repeat R > 1 every profiled launch runs R times back to back, the first carrying the start event and the
+// last the stop event (all library kernels are idempotent: they rewrite their outputs and leave their arrival
+// counters at zero); exl3_profile_read reports the per-launch average.
+struct ProfEvents {
+    hipEvent_t a, b;                    // both null when profiling is off
+};
+ProfEvents prof_begin(const char* name);
 int prof_repeat();
 
-#define EXL3_LAUNCH(name, kernel, grid, block, lds, stream, ...)                   \
-    do {                                                                         \
-        ::exl3::prof_start(name, stream);                                        \
-        for (int rep_ = ::exl3::prof_repeat(); rep_ > 0; --rep_)                 \
-            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);   \
-        ::exl3::prof_stop(stream);                                               \
-        EXL3_CHECK_HIP(hipGetLastError());                                       \
+#define EXL3_LAUNCH(name, kernel, grid, block, lds, stream, ...)                                          \
+    do {                                                                                                \
+        const ::exl3::ProfEvents pe_ = ::exl3::prof_begin(name);                                        \
+        if (pe_.a) {                                                                                    \
+            const int reps_ = ::exl3::prof_repeat();                                                    \
+            for (int rep_ = 0; rep_ < reps_; ++rep_)                                                    \
+                hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, rep_ == 0 ? pe_.a : nullptr,    \
+                                      rep_ == reps_ - 1 ? pe_.b : nullptr, 0u, __VA_ARGS__);            \
+        } else {                                                                                        \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                          \
+        }                                                                                               \
+        EXL3_CHECK_HIP(hipGetLastError());                                                              \
     } while (0)
 
 }  // namespace exl3

@@ -112,10 +112,11 @@ def graph_time(fns, reps=1, wall=False):
     return e0.elapsed_time(e1) * 1e3 / (reps * len(fns)), t1 - t0
 
 
-def kernel_profile(fns):
-    """Eager run of fns with the library's event profiler: {kernel: (launches, avg us)}."""
+def kernel_profile(fns, repeat=1):
+    """Eager run of fns with the library's event profiler (a HIP event pair around each launch on its own stream):
+    {kernel: (launches, avg us)}. repeat > 1 re-runs each launch between its events (weights then partly cached)."""
     torch.cuda.synchronize()
-    exl3._lib.profile_enable(True, repeat=8)
+    exl3._lib.profile_enable(True, repeat=repeat)
     for f in fns:
         f()
     torch.cuda.synchronize()
@@ -236,6 +237,21 @@ def zipf_bias(E, s, seed):
     return (-s * torch.log(rank + 1)).cuda()
 
 
+def recorded_traffic(kname):
+    """HBM bytes per launch of the headline kernel from its committed rocprofv3 counter summary (FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain copy of known size); None without
+    one. The counters need a profiler run of their own, so the figure is the recorded one, not a live one."""
+    path = os.path.join(ROOT, "profiles", f"{kname}_c3_m4_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 def cpu_baseline(wl, seconds=12.0):
     """The oracle (NumPy, fp32 accumulation) on a bounded sample of the headline workload: whole layer calls on the
@@ -276,6 +292,8 @@ def main():
     ap.add_argument("--configs", default="all", help="comma list of c1..c5 to report next to the headline, or none")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 3 plain device copies of MIB MiB each (the HBM counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (every expert resident on one MI355X); "
@@ -284,6 +302,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(2)
+    if args.copy_probe > 0:
+        n = args.copy_probe << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 3}), flush=True)
+        return
     torch.manual_seed(0)
     K, W = args.steps, args.warmup
     log("device", torch.cuda.get_device_name(0))
@@ -309,14 +337,23 @@ def main():
     byts = sum(wl.bytes_per_step(j) for j in range(K)) / K
     us_tok = ms_step * 1e3 / M
 
-    # dominant kernel (gate|up: two thirds of the weight bytes), timed live with HIP events on its stream
-    prof = kernel_profile([wl.step_fn(j) for j in range(64)])
-    gu_n, gu_us = prof.get("moe_gateup", (0, float("nan")))
-    gu_bytes = sum(wl.unique(j) * wl.gu_bytes + 2 * M * H + 2 * M * 10 * I for j in range(64)) / 64
-    achieved = gu_bytes / gu_us / 1e3
+    # dominant kernel, timed live with HIP events on the stream it is launched on: the one-launch fused layer kernel
+    # (every touched expert's gate, up and down weights, x in, combined rows out) where the layer takes it, else the
+    # gate|up GEMV kernel (gate and up weights of every touched expert, x in, activations out)
+    nprof = 64
+    prof = kernel_profile([wl.step_fn(j) for j in range(nprof)])
+    if "moe_fused" in prof:
+        kname = "moe_fused"
+        k_bytes = sum(wl.bytes_per_step(j) for j in range(nprof)) / nprof
+    else:
+        kname = "moe_gateup"
+        k_bytes = sum(wl.unique(j) * wl.gu_bytes + 2 * M * H + 2 * M * 10 * I for j in range(nprof)) / nprof
+    k_n, k_us = prof.get(kname, (0, float("nan")))
+    traffic = recorded_traffic(kname)
+    achieved = k_bytes / k_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "moe_gateup",
-                "kernel_us": round(gu_us, 3), "launches": gu_n,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
+                "kernel_us": round(k_us, 3), "launches": k_n, "bytes_per_launch": int(k_bytes),
                 "layer_gbps": round(byts / (ms_step * 1e3) / 1e3, 1)}
     log("kernel profile", prof)
 
