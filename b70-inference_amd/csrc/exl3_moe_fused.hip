@@ -185,6 +185,61 @@ __device__ __forceinline__ void sum_partials(const float* base, size_t stride, c
     }
 }
 
+// The strip GEMV sized to the item's row count (wave-uniform): most decode items hold one row, and at 4 rows the dot
+// products are a third of the GEMV's VALU work. Rows past the variant's size keep their zero accumulators.
+template <int KL, int MR>
+__device__ __forceinline__ void item_gemv(int cnt, const uint32_t* sp, size_t rs, int lt0, int nt, int step, int lane,
+                                          const _Float16* xs, int xs_ld, float (&acc)[MR][2],
+                                          StripRing<KL, kFusedRing>& ring) {
+    cnt = __builtin_amdgcn_readfirstlane(cnt);
+    if constexpr (MR >= 2)
+        if (cnt == 1) {
+            strip_gemv_run<KL, 1, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+                                              reinterpret_cast<float(&)[1][2]>(acc), ring);
+            return;
+        }
+    if constexpr (MR >= 4)
+        if (cnt == 2) {
+            strip_gemv_run<KL, 2, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+                                              reinterpret_cast<float(&)[2][2]>(acc), ring);
+            return;
+        }
+    if constexpr (MR >= 8)
+        if (cnt <= 4) {
+            strip_gemv_run<KL, 4, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+                                              reinterpret_cast<float(&)[4][2]>(acc), ring);
+            return;
+        }
+    strip_gemv_run<KL, MR, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, ring);
+}
+
+template <int MR>
+__device__ __forceinline__ void item_gemv_mixed(int cnt, const uint32_t* words, const uint8_t* kmap,
+                                                const int32_t* woff, int tn, int tile_n0, int tr0, int lt0, int nt,
+                                                int step, int lane, const _Float16* xs, int xs_ld,
+                                                float (&acc)[MR][2]) {
+    cnt = __builtin_amdgcn_readfirstlane(cnt);
+    if constexpr (MR >= 2)
+        if (cnt == 1) {
+            strip_gemv_mixed<1>(words, kmap, woff, tn, tile_n0, tr0, lt0, nt, step, lane, xs, xs_ld,
+                                reinterpret_cast<float(&)[1][2]>(acc));
+            return;
+        }
+    if constexpr (MR >= 4)
+        if (cnt == 2) {
+            strip_gemv_mixed<2>(words, kmap, woff, tn, tile_n0, tr0, lt0, nt, step, lane, xs, xs_ld,
+                                reinterpret_cast<float(&)[2][2]>(acc));
+            return;
+        }
+    if constexpr (MR >= 8)
+        if (cnt <= 4) {
+            strip_gemv_mixed<4>(words, kmap, woff, tn, tile_n0, tr0, lt0, nt, step, lane, xs, xs_ld,
+                                reinterpret_cast<float(&)[4][2]>(acc));
+            return;
+        }
+    strip_gemv_mixed<MR>(words, kmap, woff, tn, tile_n0, tr0, lt0, nt, step, lane, xs, xs_ld, acc);
+}
+
 template <int K, int MR>
 __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
                                              int nb, int p) {
@@ -255,12 +310,12 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR, kFusedRing>(sp, rs, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128, acc, ring);
+        item_gemv<KL, MR>(cnt, sp, rs, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(proj ? it.km[2] : it.km[0]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(proj ? it.km[3] : it.km[1]);
-        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128,
-                             acc);
+        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &s.xs[proj][0][0],
+                            KBF * 128, acc);
     }
 
 #pragma unroll
@@ -385,11 +440,12 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR, kFusedRing>(sp, rs, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc, ring);
+        item_gemv<KL, MR>(cnt, sp, rs, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(it.km[4]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(it.km[5]);
-        strip_gemv_mixed<MR>(tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc);
+        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128,
+                            acc);
     }
 
 #pragma unroll
