@@ -103,17 +103,43 @@ __device__ __forceinline__ void chunk_prev(int lane, uint32_t* R) {
 
 // Decode the lane's 32 positions into 16 packed fp16 pairs: pair j holds positions (2j, 2j+1), i.e. rows
 // (pos_row(2j), pos_row(2j)+1) of column half pos_half(2j).
+// Window of position u (low 16 bits valid) given the funnel-shifted words N[j] = bits [32 j + 16, 32 j + 48) of R's
+// bit string: a window inside one word of R is a shift of it; one that crosses the boundary at bit 32 IW lies inside
+// N[IW - 1]. Either way one shift-and-mask (v_bfe_u32), the funnel shift being shared by every window crossing that
+// boundary (about 16 / K of them) instead of one v_alignbit plus a mask per window.
+// At K = 8 every window is byte-aligned and a crossing one is a single v_perm_b32 already: window_raw is kept there.
+template <int K>
+__device__ __forceinline__ uint32_t window_norm(const uint32_t* R, const uint32_t* N, int u) {
+    if constexpr (K == 8) return window_raw<K>(R, u);
+    const int E = 32 + (u + 1) * K;        // exclusive end bit
+    const int IW = (E - 1) >> 5;           // word holding the last bit
+    const int SH = 32 * (IW + 1) - E;
+    if (E - 16 >= 32 * IW) return SH == 0 ? R[IW] : R[IW] >> SH;
+    return N[IW - 1] >> (32 * IW + 16 - E);
+}
+
+template <int K>
+__device__ __forceinline__ void funnel_words(const uint32_t* R, uint32_t* N) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) N[j] = __builtin_amdgcn_alignbit(R[j], R[j + 1], 16);
+}
+
 template <int K>
 __device__ __forceinline__ void decode_chunk(const uint32_t* R, h2_t* w) {
+    uint32_t N[K];
+    funnel_words<K>(R, N);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) w[j] = mul1_pair(window_raw<K>(R, 2 * j), window_raw<K>(R, 2 * j + 1));
+    for (int j = 0; j < 16; ++j) w[j] = mul1_pair(window_norm<K>(R, N, 2 * j), window_norm<K>(R, N, 2 * j + 1));
 }
 
 // Same positions, codebook affine left out (h = 1024 + bytesum).
 template <int K>
 __device__ __forceinline__ void decode_chunk_raw(const uint32_t* R, h2_t* w) {
+    uint32_t N[K];
+    funnel_words<K>(R, N);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) w[j] = mul1_pair_raw(window_raw<K>(R, 2 * j), window_raw<K>(R, 2 * j + 1));
+    for (int j = 0; j < 16; ++j)
+        w[j] = mul1_pair_raw(window_norm<K>(R, N, 2 * j), window_norm<K>(R, N, 2 * j + 1));
 }
 
 // ------------------------------------------------------------------------------------------------ Hadamard

@@ -2,23 +2,26 @@
 //
 // For decode batches (at most 8 tokens, at most kFusedMaxPairs (token, slot) pairs) the multi-kernel path is a chain
 // of short latency-bound launches. Here every workgroup:
-//   1. reads the routing ids (pair l in lane l and l + 64 of every wave) and groups the pairs by expert in
-//      registers: a pair's index among its expert's pairs in flat order comes from a readlane sweep, items are
+//   1. reads the routing ids (pair l in lanes l and l + 64 of wave 0) and groups the pairs by expert in
+//      registers, once: a pair's index among its expert's pairs in flat order comes from an LDS sweep, items are
 //      chunks of up to MR such pairs (the reference's per-expert row groups, glm/xpu/csrc/exl3_moe.n128.sycl:691-734)
-//      numbered by a ballot over their first pairs, and the job's item, expert and rows follow from ballots. No align
-//      launch and no barrier; rows keep their flat pair index as row id.
-//   2. runs job blockIdx.x: [0, J_gu) are gate|up jobs (item, 128-column block of I, k-split of H), [J_gu, J_gu + J_d)
-//      down jobs (item, 128-column block of H, k-split of I), item-major. A gate|up job streams both strips and, in
-//      the last split to arrive, applies the reference's GateUpKernel epilogue (Hadamard * svh, act, * suh_d,
+//      numbered by a ballot over their first pairs, and an item's expert and rows follow from ballots. No align
+//      launch; rows keep their flat pair index as row id.
+//   2. runs gate|up job blockIdx.x (item i = blockIdx.x / GU; GU jobs per item = 128-column blocks of I x k-splits of
+//      H in tile-rows), then the down jobs of item i - 1 (DN per item = 128-column blocks of H x k-splits of I; job
+//      r of that item on the workgroup with r = blockIdx.x - i GU (mod GU)). A gate|up job streams both strips and,
+//      in the last split to arrive, applies the reference's GateUpKernel epilogue (Hadamard * svh, act, * suh_d,
 //      Hadamard: exl3_moe.n128.sycl:253-271) and publishes the item's down input. A down job prefetches its first
-//      weight rows, waits until every column block of its item's down input is published, streams, and in the last
-//      split writes the weighted rows y; the workgroup that completes a token's slots sums them in slot order
-//      (exl3_moe.n128.sycl:385-410).
-// Progress: gate|up jobs never wait and have lower workgroup ids than every down job. Workgroups are dispatched in id
-// order within each XCD (ids round-robin over the XCDs), so a waiting down job only waits for gate|up workgroups that
-// its XCD or another has already dispatched or will dispatch before any of its own down jobs. The wait is also
-// bounded: a timeout sets an error word instead of hanging. Cross-workgroup data (partials, down inputs, y) moves
-// with agent-scope stores and loads that write through the XCD-local L2, published by counters after the stores have
+//      weight rows, waits until every column block of its item's down input is published, streams, and writes the
+//      weighted rows y (directly when I is not split, else in the last split); the workgroup that completes a token's
+//      slots sums them in slot order (exl3_moe.n128.sycl:385-410).
+// Progress: gate|up jobs never wait, and a down job of item i only waits for the gate|up jobs of item i, which run on
+// workgroups with lower ids ([i GU, (i + 1) GU) against >= (i + 1) GU). Workgroups are dispatched in id order within
+// each XCD (ids round-robin over the XCDs), and every workgroup finishes its gate|up job before it can wait, so the
+// lowest waiting workgroup always has its inputs coming: no co-residency is assumed. The grid is sized to what the
+// device holds at once, so in practice every workgroup is resident from the start. The wait is also bounded: a
+// timeout sets an error word instead of hanging. Cross-workgroup data (partials, down inputs, y) moves with
+// agent-scope stores and loads that write through the XCD-local L2, published by counters after the stores have
 // drained (the split-K handoff). Every counter sits on its own 128-byte line.
 #include "exl3_device.h"
 #include "exl3_gemv.h"
@@ -50,13 +53,15 @@ struct FusedArgs {
     float* abuf;                        // [max_items][MR][I] down input (fp16 values held in fp32)
     float* y;                           // [np][H] weighted expert outputs
     float* part_gu;                     // [max_items * nbI][P_gu][2][MR][128]
-    float* part_d;                      // [max_items * nbH][P_d][MR][128]
+    float* part_d;                      // [max_items * nbH][P_d][MR][128] (P_d > 1)
     int* cnt_gu;                        // [max_items * nbI] * kCS
     int* cnt_d;                         // [max_items * nbH] * kCS
     int* cnt_tok;                       // [M * nbH] * kCS
     int* cnt_item;                      // [max_items] * kCS
     int* err;                           // set when a wait times out
-    int P_gu, P_d, nblk_h, nblk_i, J_gu, J_d, max_items;
+    int P_gu, P_d;                      // k-splits (in tile-rows) of H for gate|up and of I for down
+    int GU, DN;                         // gate|up jobs (I / 128 * P_gu) and down jobs (H / 128 * P_d) per item
+    int J_gu, max_items;
     void* out;
     int64_t out_ld;
     int out_f32;
@@ -74,22 +79,50 @@ __device__ __forceinline__ void atomic_store_agent(int* p, int v) {
 
 template <int MR>
 struct FusedShared {
-    static constexpr int KBF = MR <= 4 ? 8 : 4;        // k-blocks (128 rows) per job split
+    static constexpr int KBF = MR <= 4 ? 8 : 4;        // 128-blocks of x a job stages (its k range, block-aligned)
     _Float16 xs[2][MR][KBF * 128];
     float red[4][MR][2][64];
-    float bsum[2][MR][KBF];
-    _Float16 su[2][KBF * 128];          // gate / up input sign vectors of the job's k range
-    int ge[4][kFusedMaxPairs];          // each wave's copy of the pairs' experts (grouping sweep)
+    float cv[MR][128];                  // down outputs of an unsplit down job, natural column order
+    float ksum[2][MR];                  // per projection and row: sum of the transformed x over the job's k range
+    _Float16 su[2][KBF * 128];          // gate / up input sign vectors of the staged blocks
+    int ge[kFusedMaxPairs];             // the pairs' experts (grouping sweep of wave 0)
     int64_t tab[9];                     // the item's (trellis, suh, svh) addresses for gate, up, down
+    int64_t km[6];                      // the item's (kmap, woff) addresses when K is per tile
+    uint64_t valid[2];                  // valid pairs
     int rows[MR];                       // flat pair index of each row of the job's item
     int comb[MR];
+    int nitems, it_e, it_cnt;
     int flag;
 };
 
-// The job's item as every wave sees it (uniform values; its rows are in FusedShared::rows).
+// k range of split p of P over T tile-rows, and the 128-blocks that cover it
+struct KRange {
+    int t0, nt;                         // first tile-row, tile-rows
+    int b0, kbs;                        // first staged block, staged blocks
+    int xo;                             // offset of tile-row t0 in the staged blocks (elements)
+};
+__device__ __forceinline__ KRange k_range(int p, int P, int T) {
+    KRange r;
+    r.t0 = (int)((int64_t)p * T / P);
+    const int t1 = (int)((int64_t)(p + 1) * T / P);
+    r.nt = t1 - r.t0;
+    r.b0 = r.t0 >> 3;
+    r.kbs = ((t1 + 7) >> 3) - r.b0;
+    r.xo = 16 * r.t0 - 128 * r.b0;
+    return r;
+}
+
+// The pair grouping as the grouping wave holds it (per-lane values for pairs lane and lane + 64, uniform masks).
+struct Groups {
+    int e0, e1, bf0, bf1;               // expert and index among its expert's pairs of pairs lane, lane + 64
+    uint64_t L0, L1;                    // pairs that start an item
+    uint64_t v0, v1;                    // valid pairs
+    int n0, nitems;
+};
+
+// The job's item as every wave reads it from LDS (uniform values; its rows are in FusedShared::rows).
 struct Item {
     int e, cnt;                         // expert, rows
-    uint64_t v0, v1;                    // valid pairs (pair l: bit l of v0, pair 64 + l: bit l of v1)
     int64_t km[6];                      // (kmap, woff) addresses when K is per tile
 };
 
@@ -117,53 +150,71 @@ __device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n
     return c;
 }
 
-// Groups the pairs and returns the number of items; fills `it`, rows[] and tab[] for item `item` when it exists. Every
-// wave runs it and writes the same rows and table entries, so a wave may read them right after without a barrier.
-// `ge` is the wave's own 128-int LDS slice (written and read by this wave only: LDS keeps a wave's accesses in order).
-template <int K, int MR>
-__device__ __forceinline__ int group_pairs(const FusedArgs& a, int item, int lane, Item& it, int* rows, int64_t* tab,
-                                           int* ge) {
+// Groups the pairs (one wave; `ge` is a 128-int LDS array written and read by this wave only: LDS keeps a wave's
+// accesses in order).
+template <int MR>
+__device__ __forceinline__ void group_pairs(const FusedArgs& a, int lane, Groups& g, int* ge) {
     const int np = a.np;
     const int l1 = lane + 64;
-    const int e0 = pair_expert(a, lane);
-    const int e1 = pair_expert(a, l1);
-    ge[lane] = e0;
-    ge[l1] = e1;
+    g.e0 = pair_expert(a, lane);
+    g.e1 = pair_expert(a, l1);
+    ge[lane] = g.e0;
+    ge[l1] = g.e1;
     int bf0 = 0, bf1 = 0;
     for (int q4 = 0; q4 < np; q4 += 4) {          // entries past np are -1 and only match lanes without a pair
         const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ge + q4);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int eq = (int)v[k], q = q4 + k;
-            bf0 += (eq == e0) & (q < lane);
-            bf1 += (eq == e1) & (q < l1);
+            bf0 += (eq == g.e0) & (q < lane);
+            bf1 += (eq == g.e1) & (q < l1);
         }
     }
-    const uint64_t L0 = __ballot(e0 >= 0 && bf0 % MR == 0), L1 = __ballot(e1 >= 0 && bf1 % MR == 0);
-    it.v0 = __ballot(e0 >= 0);
-    it.v1 = __ballot(e1 >= 0);
-    const int n0 = popc64(L0), nitems = n0 + popc64(L1);
-    if (item >= nitems) return nitems;
+    g.bf0 = bf0;
+    g.bf1 = bf1;
+    g.L0 = __ballot(g.e0 >= 0 && bf0 % MR == 0);
+    g.L1 = __ballot(g.e1 >= 0 && bf1 % MR == 0);
+    g.v0 = __ballot(g.e0 >= 0);
+    g.v1 = __ballot(g.e1 >= 0);
+    g.n0 = popc64(g.L0);
+    g.nitems = g.n0 + popc64(g.L1);
+}
+
+// Expert, row count, rows, tables (and kmaps) of item `item` (< nitems) into LDS, by the wave that grouped the pairs;
+// the other waves read them after a barrier (read_item).
+template <int K, int MR>
+__device__ __forceinline__ void item_info(const FusedArgs& a, const Groups& g, int item, int lane,
+                                          FusedShared<MR>& s) {
     // first pair of the item: the item-th set bit of (L0, L1)
     const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    const uint64_t s0 = __ballot(((L0 >> lane) & 1) && popc64(L0 & below) == item);
-    const uint64_t s1 = __ballot(((L1 >> lane) & 1) && n0 + popc64(L1 & below) == item);
+    const uint64_t s0 = __ballot(((g.L0 >> lane) & 1) && popc64(g.L0 & below) == item);
+    const uint64_t s1 = __ballot(((g.L1 >> lane) & 1) && g.n0 + popc64(g.L1 & below) == item);
     const int p = s0 ? ctz64(s0) : 64 + ctz64(s1);
-    const int e = p < 64 ? __builtin_amdgcn_readlane(e0, p) : __builtin_amdgcn_readlane(e1, p - 64);
-    const int bfp = p < 64 ? __builtin_amdgcn_readlane(bf0, p) : __builtin_amdgcn_readlane(bf1, p - 64);
-    const int ce = popc64(__ballot(e0 == e)) + popc64(__ballot(e1 == e));
-    it.e = e;
-    it.cnt = min(MR, ce - bfp);
-    if (lane < 9) tab[lane] = ldg(a.tables + (int64_t)lane * a.E + e);
-    if (K == 0)
-#pragma unroll
-        for (int i = 0; i < 6; ++i) it.km[i] = ldg(a.kmaps + (int64_t)i * a.E + e);
+    const int e = p < 64 ? __builtin_amdgcn_readlane(g.e0, p) : __builtin_amdgcn_readlane(g.e1, p - 64);
+    const int bfp = p < 64 ? __builtin_amdgcn_readlane(g.bf0, p) : __builtin_amdgcn_readlane(g.bf1, p - 64);
+    const int ce = popc64(__ballot(g.e0 == e)) + popc64(__ballot(g.e1 == e));
+    const int cnt = min(MR, ce - bfp);
+    if (lane == 0) {
+        s.it_e = e;
+        s.it_cnt = cnt;
+    }
+    if (lane < 9) s.tab[lane] = ldg(a.tables + (int64_t)lane * a.E + e);
+    if (K == 0 && lane < 6) s.km[lane] = ldg(a.kmaps + (int64_t)lane * a.E + e);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        const uint64_t r0 = __ballot(e0 == e && bf0 == bfp + m), r1 = __ballot(e1 == e && bf1 == bfp + m);
-        if (lane == 0) rows[m] = m < it.cnt ? (r0 ? ctz64(r0) : 64 + ctz64(r1)) : 0;
+        const uint64_t r0 = __ballot(g.e0 == e && g.bf0 == bfp + m), r1 = __ballot(g.e1 == e && g.bf1 == bfp + m);
+        if (lane == 0) s.rows[m] = m < cnt ? (r0 ? ctz64(r0) : 64 + ctz64(r1)) : 0;
     }
-    return nitems;
+}
+
+template <int K, int MR>
+__device__ __forceinline__ Item read_item(const FusedShared<MR>& s) {
+    Item it;
+    it.e = s.it_e;
+    it.cnt = s.it_cnt;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) it.km[i] = K == 0 ? s.km[i] : 0;
+    return it;
 }
 
 // sum over pp < P of the partials at base + pp * stride + off (agent-scope loads, issued 16 at a time, added in pp order)
@@ -240,6 +291,20 @@ __device__ __forceinline__ void item_gemv_mixed(int cnt, const uint32_t* words, 
     strip_gemv_mixed<MR>(words, kmap, woff, tn, tile_n0, tr0, lt0, nt, step, lane, xs, xs_ld, acc);
 }
 
+// sum over the job's k range of the staged, transformed rows: ksum[proj][m] for the first `nproj` projections
+template <int MR>
+__device__ __forceinline__ void range_sums(FusedShared<MR>& s, int nproj, int cnt, const KRange& kr, int wave,
+                                           int lane) {
+    for (int i = wave; i < nproj * MR; i += 4) {
+        const int pj = i / MR, m = i - pj * MR;
+        float t = 0.f;
+        if (m < cnt)
+            for (int k = lane; k < 16 * kr.nt; k += 64) t += (float)s.xs[pj][m][kr.xo + k];
+        t = wave_sum_f32(t);
+        if (lane == 0) s.ksum[pj][m] = t;
+    }
+}
+
 template <int K, int MR>
 __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
                                              int nb, int p) {
@@ -248,20 +313,19 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cnt = it.cnt;
     const int nbI = a.I / 128;
-    const int b0 = (int)((int64_t)p * a.nblk_h / a.P_gu), b1 = (int)((int64_t)(p + 1) * a.nblk_h / a.P_gu);
-    const int kb = b1 - b0;
+    const KRange kr = k_range(p, a.P_gu, a.H / 16);
     const int proj = wave >> 1, half = wave & 1;
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(proj ? s.tab[3] : s.tab[0]);
     const int tn = a.I / 16;
     const size_t rs = (size_t)tn * (8 * KL);
-    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
-    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, half, kb * 8, 2, lane, ring);
+    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, half, kr.nt, 2, lane, ring);
 
-    // stage the k range of the item's x rows (16-byte loads; rows past cnt are zero) in xs[1] and both input sign
-    // vectors in su, all loads of a thread in flight together
+    // stage the blocks covering the k range of the item's x rows (16-byte loads; rows past cnt are zero) in xs[1]
+    // and both input sign vectors in su, all loads of a thread in flight together
     {
-        const int k0 = b0 * 128, nch = kb * 16;                  // 16-byte chunks per row
+        const int k0 = kr.b0 * 128, nch = kr.kbs * 16;           // 16-byte chunks per row
         const uint16_t* sg = reinterpret_cast<const uint16_t*>(s.tab[1]) + k0;
         const uint16_t* su = reinterpret_cast<const uint16_t*>(s.tab[4]) + k0;
         for (int c = threadIdx.x; c < MR * nch; c += 256) {
@@ -271,50 +335,42 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
                 v = ldg(reinterpret_cast<const u32x4_t*>(a.x + (int64_t)(s.rows[m] / a.slots) * a.x_ld + k0) + o);
             *reinterpret_cast<u32x4_t*>(&s.xs[1][m][o * 8]) = v;
         }
-        for (int c = threadIdx.x; c < kb * 128; c += 256) {
+        for (int c = threadIdx.x; c < kr.kbs * 128; c += 256) {
             s.su[0][c] = __builtin_bit_cast(_Float16, ldg(sg + c));
             s.su[1][c] = __builtin_bit_cast(_Float16, ldg(su + c));
         }
     }
     __syncthreads();
     // input transform of block (m, b) for both projections by one wave: xs[0] <- gate, xs[1] <- up (in place)
-    for (int i = wave; i < MR * kb; i += 4) {
-        const int m = i / kb, b = i - m * kb;
+    for (int i = wave; i < cnt * kr.kbs; i += 4) {
+        const int m = i / kr.kbs, b = i - m * kr.kbs;
         _Float16* xg = &s.xs[0][m][b * 128];
         _Float16* xu = &s.xs[1][m][b * 128];
-        float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
-        if (m < cnt) {
-            const float xa = (float)xu[lane], xb = (float)xu[lane + 64];
-            ga = (float)(_Float16)(xa * (float)s.su[0][b * 128 + lane]);
-            gb = (float)(_Float16)(xb * (float)s.su[0][b * 128 + lane + 64]);
-            ua = (float)(_Float16)(xa * (float)s.su[1][b * 128 + lane]);
-            ub = (float)(_Float16)(xb * (float)s.su[1][b * 128 + lane + 64]);
-            fwht128_wave(ga, gb, lane);
-            fwht128_wave(ua, ub, lane);
-        }
-        const _Float16 hga = (_Float16)(ga * kRsqrt128), hgb = (_Float16)(gb * kRsqrt128);
-        const _Float16 hua = (_Float16)(ua * kRsqrt128), hub = (_Float16)(ub * kRsqrt128);
-        xg[lane] = hga;
-        xg[lane + 64] = hgb;
-        xu[lane] = hua;
-        xu[lane + 64] = hub;
-        const float sg = wave_sum_f32((float)hga + (float)hgb), su = wave_sum_f32((float)hua + (float)hub);
-        if (lane == 0) {
-            s.bsum[0][m][b] = sg;
-            s.bsum[1][m][b] = su;
-        }
+        const float xa = (float)xu[lane], xb = (float)xu[lane + 64];
+        float ga = (float)(_Float16)(xa * (float)s.su[0][b * 128 + lane]);
+        float gb = (float)(_Float16)(xb * (float)s.su[0][b * 128 + lane + 64]);
+        float ua = (float)(_Float16)(xa * (float)s.su[1][b * 128 + lane]);
+        float ub = (float)(_Float16)(xb * (float)s.su[1][b * 128 + lane + 64]);
+        fwht128_wave(ga, gb, lane);
+        fwht128_wave(ua, ub, lane);
+        xg[lane] = (_Float16)(ga * kRsqrt128);
+        xg[lane + 64] = (_Float16)(gb * kRsqrt128);
+        xu[lane] = (_Float16)(ua * kRsqrt128);
+        xu[lane + 64] = (_Float16)(ub * kRsqrt128);
     }
+    // rows past cnt are never read: the GEMV variant matches cnt (and reads row m < its size only)
     __syncthreads();
+    range_sums(s, 2, cnt, kr, wave, lane);
 
     float acc[MR][2];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        item_gemv<KL, MR>(cnt, sp, rs, half, kb * 8, 2, lane, &s.xs[proj][0][0], KBF * 128, acc, ring);
+        item_gemv<KL, MR>(cnt, sp, rs, half, kr.nt, 2, lane, &s.xs[proj][0][kr.xo], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(proj ? it.km[2] : it.km[0]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(proj ? it.km[3] : it.km[1]);
-        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, b0 * 8, half, kb * 8, 2, lane, &s.xs[proj][0][0],
+        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, kr.t0, half, kr.nt, 2, lane, &s.xs[proj][0][kr.xo],
                             KBF * 128, acc);
     }
 
@@ -327,10 +383,8 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     const int cbase = 16 * (lane >> 3) + (lane & 7);
     const size_t slot = (size_t)item * nbI + nb;
     if (half == 0) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float sx = 0.f;
-            for (int b = 0; b < kb; ++b) sx += s.bsum[proj][m][b];
+        for (int m = 0; m < cnt; ++m) {
+            const float sx = s.ksum[proj][m];
             float* dst = a.part_gu + (((slot * a.P_gu + p) * 2 + proj) * MR + m) * 128;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -376,21 +430,20 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
 }
 
 template <int K, int MR>
-__device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
-                                           int nb, int p) {
+__device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& s, uint64_t vm0, uint64_t vm1,
+                                           const Item& it, int item, int nb, int p) {
     constexpr int KBF = FusedShared<MR>::KBF;
     constexpr int KL = K > 0 ? K : 1;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cnt = it.cnt;
     const int nbI = a.I / 128, nbH = a.H / 128;
-    const int b0 = (int)((int64_t)p * a.nblk_i / a.P_d), b1 = (int)((int64_t)(p + 1) * a.nblk_i / a.P_d);
-    const int kb = b1 - b0;
+    const KRange kr = k_range(p, a.P_d, a.I / 16);
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(s.tab[6]);
     const int tn = a.H / 16;
     const size_t rs = (size_t)tn * (8 * KL);
-    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
+    const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
-    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, wave, kb * 8, 4, lane, ring);
+    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, wave, kr.nt, 4, lane, ring);
 
     // wait for the item's down input (all nbI column blocks), then count this job as a consumer; the last consumer
     // clears the item counter for the next call
@@ -406,46 +459,44 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
             back = back < 8 ? 2 * back : 8;
         }
         const int old = atomic_add_agent(c, 1);
-        if (old == nbI + nbH * a.P_d - 1) atomic_store_agent(c, 0);
+        if (old == nbI + a.DN - 1) atomic_store_agent(c, 0);
     }
     __syncthreads();
 
-    // the wave's blocks (m, b) = (i / kb, i % kb), i = wave, wave + 4, ...: every load first, then convert and sum
+    // the wave's blocks (m, b) = (i / kbs, i % kbs), i = wave, wave + 4, ...: every load first, then convert
     constexpr int NBW = (MR * KBF + 3) / 4;
     float va[NBW], vb[NBW];
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-        const int i = wave + 4 * j, m = i / kb, b = i - m * kb;
+        const int i = wave + 4 * j, m = i / kr.kbs, b = i - m * kr.kbs;
         va[j] = vb[j] = 0.f;
-        if (i < MR * kb && m < cnt) {
-            const float* src = a.abuf + ((size_t)item * MR + m) * a.I + (b0 + b) * 128;
+        if (m < cnt) {
+            const float* src = a.abuf + ((size_t)item * MR + m) * a.I + (kr.b0 + b) * 128;
             va[j] = splitk_load(src + lane);
             vb[j] = splitk_load(src + lane + 64);
         }
     }
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
-        const int i = wave + 4 * j, m = i / kb, b = i - m * kb;
-        if (i < MR * kb) {
-            const _Float16 ha = (_Float16)va[j], hb = (_Float16)vb[j];
-            s.xs[0][m][b * 128 + lane] = ha;
-            s.xs[0][m][b * 128 + lane + 64] = hb;
-            const float bs = wave_sum_f32((float)ha + (float)hb);
-            if (lane == 0) s.bsum[0][m][b] = bs;
+        const int i = wave + 4 * j, m = i / kr.kbs, b = i - m * kr.kbs;
+        if (m < cnt) {
+            s.xs[0][m][b * 128 + lane] = (_Float16)va[j];
+            s.xs[0][m][b * 128 + lane + 64] = (_Float16)vb[j];
         }
     }
     __syncthreads();
+    range_sums(s, 1, cnt, kr, wave, lane);
 
     float acc[MR][2];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        item_gemv<KL, MR>(cnt, sp, rs, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128, acc, ring);
+        item_gemv<KL, MR>(cnt, sp, rs, wave, kr.nt, 4, lane, &s.xs[0][0][kr.xo], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(it.km[4]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(it.km[5]);
-        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, b0 * 8, wave, kb * 8, 4, lane, &s.xs[0][0][0], KBF * 128,
-                            acc);
+        item_gemv_mixed<MR>(cnt, tr, km, wo, tn, nb * 8, kr.t0, wave, kr.nt, 4, lane, &s.xs[0][0][kr.xo],
+                            KBF * 128, acc);
     }
 
 #pragma unroll
@@ -456,37 +507,48 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     __syncthreads();
     const int cbase = 16 * (lane >> 3) + (lane & 7);
     const size_t slot = (size_t)item * nbH + nb;
+    const bool split = a.P_d > 1;
     if (wave == 0) {
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float sx = 0.f;
-            for (int b = 0; b < kb; ++b) sx += s.bsum[0][m][b];
+        for (int m = 0; m < cnt; ++m) {
+            const float sx = s.ksum[0][m];
             float* dst = a.part_d + ((slot * a.P_d + p) * MR + m) * 128;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const float v = s.red[0][m][h][lane] + s.red[1][m][h][lane] + s.red[2][m][h][lane] +
-                                s.red[3][m][h][lane];
-                splitk_store(dst + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
+                const float v = kMul1C1 * (s.red[0][m][h][lane] + s.red[1][m][h][lane] + s.red[2][m][h][lane] +
+                                           s.red[3][m][h][lane]) + kMul1C2 * sx;
+                if (split) splitk_store(dst + cbase + 8 * h, v);
+                else s.cv[m][cbase + 8 * h] = v;
             }
         }
     }
-    if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) return;
+    if (split) {
+        if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) return;
+    } else {
+        __syncthreads();
+    }
 
     const uint16_t* svd = reinterpret_cast<const uint16_t*>(s.tab[8]) + nb * 128;
     const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
     for (int m = wave; m < cnt; m += 4) {
         const int pr = s.rows[m];
         const float w = pair_weight(a, pr);
-        const int off[2] = {m * 128 + lane, m * 128 + lane + 64};
-        float v[2];
-        sum_partials<2>(a.part_d + slot * a.P_d * MR * 128, MR * 128, off, a.P_d, v);
-        float v0 = v[0], v1 = v[1];
+        float v0, v1;
+        if (split) {
+            const int off[2] = {m * 128 + lane, m * 128 + lane + 64};
+            float v[2];
+            sum_partials<2>(a.part_d + slot * a.P_d * MR * 128, MR * 128, off, a.P_d, v);
+            v0 = v[0];
+            v1 = v[1];
+        } else {
+            v0 = s.cv[m][lane];
+            v1 = s.cv[m][lane + 64];
+        }
         fwht128_wave(v0, v1, lane);
         float* dst = a.y + (size_t)pr * a.H + nb * 128;
         splitk_store(dst + lane, v0 * kRsqrt128 * sd0 * w);
         splitk_store(dst + lane + 64, v1 * kRsqrt128 * sd1 * w);
     }
-    if (threadIdx.x == 0) a.cnt_d[slot * kCS] = 0;
+    if (split && threadIdx.x == 0) a.cnt_d[slot * kCS] = 0;
 
     // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in
     __builtin_amdgcn_s_waitcnt(0);
@@ -494,7 +556,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     if (threadIdx.x == 0) {
         for (int m = 0; m < cnt; ++m) {
             const int t = s.rows[m] / a.slots;
-            const int nv = popc_range(it.v0, it.v1, t * a.slots, a.slots);
+            const int nv = popc_range(vm0, vm1, t * a.slots, a.slots);
             const int old = atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
             s.comb[m] = (old == nv - 1) ? t : -1;
         }
@@ -507,7 +569,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         float v0 = 0.f, v1 = 0.f;
         for (int j = 0; j < a.slots; ++j) {
             const int pr = t * a.slots + j;
-            if (!(((pr < 64 ? it.v0 >> pr : it.v1 >> (pr - 64))) & 1)) continue;
+            if (!(((pr < 64 ? vm0 >> pr : vm1 >> (pr - 64))) & 1)) continue;
             const float* yr = a.y + (size_t)pr * a.H;
             v0 += splitk_load(yr + c0);
             v1 += splitk_load(yr + c1);
@@ -528,27 +590,45 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
 template <int K, int MR>
 __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(16))) FusedShared<MR> s;
-    const int lane = threadIdx.x & 63;
-    const int job = blockIdx.x;
-    const bool gu = job < a.J_gu;
-    const int jj = gu ? job : job - a.J_gu;
-    const int nbo = gu ? a.I / 128 : a.H / 128, P = gu ? a.P_gu : a.P_d;
-    const int item = jj / (nbo * P), rem = jj - item * (nbo * P), nb = rem / P, p = rem - nb * P;
-    Item it;
-    const int nitems = group_pairs<K, MR>(a, item, lane, it, s.rows, s.tab, s.ge[threadIdx.x >> 6]);
-    if (job == 0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = blockIdx.x;
+    const int gi = g / a.GU, gr0 = g - gi * a.GU;
+    // wave 0 groups the pairs and describes the gate|up job's item; the others wait at the barrier
+    Groups gr;
+    if (wave == 0) {
+        group_pairs<MR>(a, lane, gr, s.ge);
+        if (lane == 0) {
+            s.valid[0] = gr.v0;
+            s.valid[1] = gr.v1;
+            s.nitems = gr.nitems;
+        }
+        if (g < a.J_gu && gi < gr.nitems) item_info<K, MR>(a, gr, gi, lane, s);
+    }
+    __syncthreads();
+    const int nitems = s.nitems;
+    const uint64_t v0 = s.valid[0], v1 = s.valid[1];
+    if (g == 0) {
         // tokens with no valid slot get a zero output row
         for (int tk = 0; tk < a.M; ++tk) {
-            if (popc_range(it.v0, it.v1, tk * a.slots, a.slots)) continue;
+            if (popc_range(v0, v1, tk * a.slots, a.slots)) continue;
             for (int c = threadIdx.x; c < a.H; c += 256) {
                 if (a.out_f32) reinterpret_cast<float*>(a.out)[(int64_t)tk * a.out_ld + c] = 0.f;
                 else reinterpret_cast<uint16_t*>(a.out)[(int64_t)tk * a.out_ld + c] = 0;
             }
         }
     }
-    if (item >= nitems) return;         // uniform
-    if (gu) fused_gateup<K, MR>(a, s, it, item, nb, p);
-    else fused_down<K, MR>(a, s, it, item, nb, p);
+    if (g < a.J_gu && gi < nitems) fused_gateup<K, MR>(a, s, read_item<K, MR>(s), gi, gr0 / a.P_gu, gr0 % a.P_gu);
+    // the down jobs of the previous item (uniform branch)
+    const int di = gi - 1;
+    if (di < 0 || di >= nitems || gr0 >= a.DN) return;
+    __syncthreads();                    // the gate|up job's LDS (rows, tab, xs) is free again
+    if (wave == 0) item_info<K, MR>(a, gr, di, lane, s);
+    __syncthreads();
+    const Item it = read_item<K, MR>(s);
+    for (int r = gr0; r < a.DN; r += a.GU) {
+        fused_down<K, MR>(a, s, v0, v1, it, di, r / a.P_d, r % a.P_d);
+        __syncthreads();
+    }
 }
 
 typedef void (*fused_fn)(FusedArgs);
@@ -568,12 +648,25 @@ static fused_fn pick_fused(int K) {
     }
 }
 
-static int fused_splits(int units, int nblk, int kbf, int target) {
-    int P = (target + units - 1) / (units > 0 ? units : 1);
-    const int pmin = (nblk + kbf - 1) / kbf;
-    if (P < pmin) P = pmin;
-    if (P > nblk) P = nblk;
-    return P < 1 ? 1 : P;
+// largest number of 128-blocks that one of P tile-row splits of T tile-rows touches
+static int max_staged_blocks(int P, int T) {
+    int mx = 0;
+    for (int p = 0; p < P; ++p) {
+        const int t0 = (int)((int64_t)p * T / P), t1 = (int)((int64_t)(p + 1) * T / P);
+        const int n = ((t1 + 7) >> 3) - (t0 >> 3);
+        mx = n > mx ? n : mx;
+    }
+    return mx;
+}
+
+// k-split count: `want` clamped to [1, T / 8] (jobs of at least 8 tile-rows), raised until every split's staged blocks
+// fit the kbf LDS blocks
+static int fused_splits(int want, int T, int kbf) {
+    int P = want;
+    const int pmax = T / 8 > 1 ? T / 8 : 1;
+    P = P < 1 ? 1 : (P > pmax ? pmax : P);
+    while (P < T && max_staged_blocks(P, T) > kbf) ++P;
+    return P;
 }
 
 // Eligible: gate, up and down share one K (or all per-tile), at most 8 tokens and kFusedMaxPairs pairs, x rows
@@ -606,40 +699,6 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.out_f32 = m.out_f32;
     const int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
     const int kbf = MR <= 4 ? 8 : 4;
-    // items <= sum over active experts of ceil(rows / MR) <= (pairs + active * (MR - 1)) / MR
-    const int active = a.np < a.E ? a.np : a.E;
-    int mi = (a.np + active * (MR - 1)) / MR;
-    a.max_items = mi < a.np ? mi : a.np;
-    const int nbI = a.I / 128, nbH = a.H / 128;
-    a.nblk_h = a.H / 128;
-    a.nblk_i = a.I / 128;
-    const int target = env_int("EXL3MI_FUSED_JOBS", 640);
-    a.P_gu = fused_splits(a.max_items * nbI, a.nblk_h, kbf, target);
-    a.P_d = fused_splits(a.max_items * nbH, a.nblk_i, kbf, target);
-    const int64_t jgu = (int64_t)a.max_items * nbI * a.P_gu, jd = (int64_t)a.max_items * nbH * a.P_d;
-    EXL3_CHECK_ARG(jgu + jd < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
-    a.J_gu = (int)jgu;
-    a.J_d = (int)jd;
-
-    const size_t mx = a.max_items, np = a.np;
-    const size_t bytes = carve_size(mx * MR * a.I, 4) + carve_size(np * a.H, 4) +
-                         carve_size(mx * nbI * a.P_gu * 2 * MR * 128, 4) + carve_size(mx * nbH * a.P_d * MR * 128, 4);
-    const size_t n_cnt = (mx * nbI + mx * nbH + (size_t)a.M * nbH + mx + 1) * kCS;
-    Workspace ws;
-    int rc = workspace(bytes, n_cnt, &ws);
-    if (rc) return rc;
-    Carve c{ws.scratch, ws.scratch_bytes};
-    a.abuf = c.take<float>(mx * MR * a.I);
-    a.y = c.take<float>(np * a.H);
-    a.part_gu = c.take<float>(mx * nbI * a.P_gu * 2 * MR * 128);
-    a.part_d = c.take<float>(mx * nbH * a.P_d * MR * 128);
-    if (!a.part_d) return fail(EXL3_ERR_INVALID, "moe: workspace carve failed");
-    int* cn = ws.counters;
-    a.cnt_gu = cn;
-    a.cnt_d = a.cnt_gu + mx * nbI * kCS;
-    a.cnt_tok = a.cnt_d + mx * nbH * kCS;
-    a.cnt_item = a.cnt_tok + (size_t)a.M * nbH * kCS;
-    a.err = a.cnt_item + mx * kCS;
     fused_fn fn;
     switch (MR) {
         case 1: fn = pick_fused<1>(m.Kg); break;
@@ -647,7 +706,47 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
         case 4: fn = pick_fused<4>(m.Kg); break;
         default: fn = pick_fused<8>(m.Kg); break;
     }
-    EXL3_LAUNCH("moe_fused", fn, dim3((unsigned)(jgu + jd)), dim3(256), 0, st, a);
+    // items <= sum over active experts of ceil(rows / MR) <= (pairs + active * (MR - 1)) / MR
+    const int active = a.np < a.E ? a.np : a.E;
+    int mi = (a.np + active * (MR - 1)) / MR;
+    a.max_items = mi < a.np ? mi : a.np;
+    const int nbI = a.I / 128, nbH = a.H / 128;
+    // gate|up jobs: about one per workgroup the device holds at once (EXL3MI_FUSED_JOBS overrides); the grid adds one
+    // item's worth of workgroups for the last item's down jobs. Down jobs split I only as far as the staged blocks
+    // need: an unsplit down job writes its rows directly, with no partial-sum round trip.
+    int resident = 0;
+    int rc = resident_blocks(reinterpret_cast<const void*>(fn), 256, &resident);
+    if (rc) return rc;
+    const int target = env_int("EXL3MI_FUSED_JOBS", resident);
+    a.P_gu = fused_splits(target / (a.max_items * nbI), a.H / 16, kbf);
+    a.GU = nbI * a.P_gu;
+    a.P_d = fused_splits(1, a.I / 16, kbf);
+    a.DN = nbH * a.P_d;
+    const int64_t jgu = (int64_t)a.max_items * a.GU, grid = jgu + a.GU;
+    EXL3_CHECK_ARG(grid < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
+    a.J_gu = (int)jgu;
+
+    const size_t mx = a.max_items, np = a.np;
+    const size_t pd = a.P_d > 1 ? mx * nbH * a.P_d * MR * 128 : 1;
+    const size_t bytes = carve_size(mx * MR * a.I, 4) + carve_size(np * a.H, 4) +
+                         carve_size(mx * nbI * a.P_gu * 2 * MR * 128, 4) + carve_size(pd, 4);
+    const size_t n_cnt = (mx * nbI + mx * nbH + (size_t)a.M * nbH + mx + 1) * kCS;
+    Workspace ws;
+    rc = workspace(bytes, n_cnt, &ws);
+    if (rc) return rc;
+    Carve c{ws.scratch, ws.scratch_bytes};
+    a.abuf = c.take<float>(mx * MR * a.I);
+    a.y = c.take<float>(np * a.H);
+    a.part_gu = c.take<float>(mx * nbI * a.P_gu * 2 * MR * 128);
+    a.part_d = c.take<float>(pd);
+    if (!a.part_d) return fail(EXL3_ERR_INVALID, "moe: workspace carve failed");
+    int* cn = ws.counters;
+    a.cnt_gu = cn;
+    a.cnt_d = a.cnt_gu + mx * nbI * kCS;
+    a.cnt_tok = a.cnt_d + mx * nbH * kCS;
+    a.cnt_item = a.cnt_tok + (size_t)a.M * nbH * kCS;
+    a.err = a.cnt_item + mx * kCS;
+    EXL3_LAUNCH("moe_fused", fn, dim3((unsigned)grid), dim3(256), 0, st, a);
     return EXL3_OK;
 }
 

@@ -49,6 +49,33 @@ int aux_streams(AuxStreams* out) {
     return EXL3_OK;
 }
 
+namespace {
+struct ResidentRec {
+    int dev;
+    const void* fn;
+    int threads, blocks;
+};
+std::vector<ResidentRec> g_resident;
+}  // namespace
+
+int resident_blocks(const void* fn, int threads, int* out) {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (const ResidentRec& r : g_resident)
+        if (r.dev == dev && r.fn == fn && r.threads == threads) {
+            *out = r.blocks;
+            return EXL3_OK;
+        }
+    int per_cu = 0, cus = 0;
+    EXL3_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0));
+    EXL3_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int blocks = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+    g_resident.push_back({dev, fn, threads, blocks});
+    *out = blocks;
+    return EXL3_OK;
+}
+
 int workspace(size_t bytes, size_t ncounters, Workspace* out) {
     int dev = 0;
     EXL3_CHECK_HIP(hipGetDevice(&dev));

@@ -42,7 +42,11 @@ struct AuxStreams {
 };
 int aux_streams(AuxStreams* out);
 
-// Integer tuning knob from the environment (read once per name), `dflt` when unset or not a positive number.
+// Workgroups of `threads` threads of kernel `fn` that the current device holds at once (occupancy x CUs), cached
+// per device and kernel.
+int resident_blocks(const void* fn, int threads, int* out);
+
+// Integer tuning knob from the environment (read at every call), `dflt` when unset or not a positive number.
 int env_int(const char* name, int dflt);
 
 // Bump allocator over one workspace request.
