@@ -688,12 +688,10 @@ static int check_K(int K, const char* what) {
 
 using namespace exl3;
 
-extern "C" {
-
-int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
-                     const float* topk_w, int64_t topk, int64_t E, const int64_t* tables, const int64_t* kmaps,
-                     int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
-                     int64_t out_ld, int out_dtype, void* stream) {
+// Argument checks and MoeArgs shared by the two layer entry points (ids / weights may still be unset).
+static int moe_setup(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, int64_t topk, int64_t E,
+                     const int64_t* tables, const int64_t* kmaps, int K_gate, int K_up, int K_down, int act,
+                     float act_limit, int64_t shared, void* out, int64_t out_ld, int out_dtype, MoeArgs& a) {
     int rc;
     if ((rc = check_K(K_gate, "gate")) || (rc = check_K(K_up, "up")) || (rc = check_K(K_down, "down"))) return rc;
     if (K_gate != K_up)
@@ -708,11 +706,10 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
                    (long long)H, (long long)I);
     EXL3_CHECK_ARG(x_ld >= H && out_ld >= H, "exl3_moe_forward: row strides must cover H");
     EXL3_CHECK_ARG(shared < E, "exl3_moe_forward: shared expert index %lld >= E", (long long)shared);
-    if (M == 0) return EXL3_OK;
-    EXL3_CHECK_ARG(x && tables && out && (topk == 0 || (topk_ids && topk_w)), "exl3_moe_forward: null pointer");
+    EXL3_CHECK_ARG(M == 0 || (x && tables && out), "exl3_moe_forward: null pointer");
     EXL3_CHECK_ARG(K_gate != 0 && K_down != 0 ? true : kmaps != nullptr,
                    "exl3_moe_forward: per-tile K (K=0) needs the kmaps table");
-    MoeArgs a{};
+    a = MoeArgs{};
     a.x = x;
     a.x_ld = x_ld;
     a.M = (int)M;
@@ -721,8 +718,6 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.topk = (int)topk;
     a.slots = (int)topk + (shared >= 0 ? 1 : 0);
     a.E = (int)E;
-    a.ids = topk_ids;
-    a.tw = topk_w;
     a.tables = tables;
     a.kmaps = kmaps;
     a.Kg = K_gate;
@@ -733,18 +728,59 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.out = out;
     a.out_ld = out_ld;
     a.out_f32 = out_dtype == EXL3_F32;
-    const int64_t npairs = M * a.slots;
-    if (moe_fused_ok(a)) return moe_fused_path(a, (hipStream_t)stream);
+    return EXL3_OK;
+}
+
+static int moe_run(MoeArgs& a, hipStream_t st) {
+    if (moe_fused_ok(a)) return moe_fused_path(a, st);
     // Decode batches (M <= 8): GEMV items of up to MR rows per expert. Prefill batches: every expert with rows goes to
     // the MFMA kernels in blocks of up to kMfmaRows rows (MR = 0: no GEMV items).
+    const int64_t M = a.M, E = a.E, npairs = M * a.slots;
     const bool mfma = M > kMoeSmallRows;
     a.MR = mfma ? 0 : M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
     int64_t mi = mfma ? 0 : E + npairs / a.MR;
     if (mi > npairs) mi = npairs;
     a.max_items = (int)mi;
     a.max_blocks = mfma ? (int)(npairs / kMfmaRows + (E < npairs ? E : npairs) + 1) : 0;
-    EXL3_CHECK_ARG((int64_t)a.max_items * (H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
-    return moe_decode_path(a, npairs, (hipStream_t)stream);
+    EXL3_CHECK_ARG((int64_t)a.max_items * (a.H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
+    return moe_decode_path(a, npairs, st);
+}
+
+extern "C" {
+
+int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
+                     const float* topk_w, int64_t topk, int64_t E, const int64_t* tables, const int64_t* kmaps,
+                     int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
+                     int64_t out_ld, int out_dtype, void* stream) {
+    MoeArgs a;
+    int rc = moe_setup(x, x_ld, M, H, I, topk, E, tables, kmaps, K_gate, K_up, K_down, act, act_limit, shared, out,
+                       out_ld, out_dtype, a);
+    if (rc) return rc;
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(topk == 0 || (topk_ids && topk_w), "exl3_moe_forward: null pointer");
+    a.ids = topk_ids;
+    a.tw = topk_w;
+    return moe_run(a, (hipStream_t)stream);
+}
+
+int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const float* logits,
+                            int64_t logits_ld, int64_t n_logits, const float* bias, int64_t topk, int64_t E,
+                            const int64_t* tables, const int64_t* kmaps, int K_gate, int K_up, int K_down, int act,
+                            float act_limit, int64_t shared, int32_t* ids_out, float* w_out, void* out,
+                            int64_t out_ld, int out_dtype, void* stream) {
+    MoeArgs a;
+    int rc = moe_setup(x, x_ld, M, H, I, topk, E, tables, kmaps, K_gate, K_up, K_down, act, act_limit, shared, out,
+                       out_ld, out_dtype, a);
+    if (rc) return rc;
+    EXL3_CHECK_ARG(topk > 0 && topk <= 32 && n_logits >= topk && n_logits <= E && n_logits <= 8192 &&
+                   logits_ld >= n_logits, "exl3_moe_forward_logits: bad router sizes (topk %lld, %lld logits, E %lld)",
+                   (long long)topk, (long long)n_logits, (long long)E);
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(logits && ids_out && w_out, "exl3_moe_forward_logits: null pointer");
+    a.ids = ids_out;
+    a.tw = w_out;
+    if ((rc = exl3_route_softmax_topk(logits, logits_ld, M, n_logits, bias, topk, ids_out, w_out, stream))) return rc;
+    return moe_run(a, (hipStream_t)stream);
 }
 
 int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int64_t M, int64_t topk, int64_t E, int64_t shared,

@@ -131,6 +131,38 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, t
     return out
 
 
+def moe_forward_logits(x: torch.Tensor, logits: torch.Tensor, k: int, tables: ExpertTables, act=ACT_SILU,
+                       act_limit: float = 0.0, shared: int = -1, bias: torch.Tensor | None = None,
+                       out: torch.Tensor | None = None, out_dtype=torch.float32, return_routing: bool = False):
+    """route_softmax_topk(logits, k, bias) then moe_forward, as one library call. logits fp32 [M, n] over the routed
+    experts 0 .. n - 1 of `tables`. Returns out, or (out, ids, w) with return_routing."""
+    require_device(x, logits, bias)
+    if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1 or x.shape[1] != tables.H:
+        raise Exl3Error(f"moe_forward_logits: x must be fp16 [M, {tables.H}] with contiguous rows")
+    M = x.shape[0]
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1 or logits.shape[0] != M:
+        raise Exl3Error("moe_forward_logits: logits must be fp32 [M, n] with contiguous rows")
+    n = logits.shape[1]
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != n or not bias.is_contiguous()):
+        raise Exl3Error("moe_forward_logits: bias must be fp32 [n]")
+    if out is None:
+        out = torch.empty(M, tables.H, dtype=out_dtype, device=x.device)
+    if out.dtype not in (torch.float16, torch.float32) or out.stride(1) != 1 or tuple(out.shape) != (M, tables.H):
+        raise Exl3Error("moe_forward_logits: out must be fp16/fp32 [M, H] with contiguous rows")
+    a = ACTS.get(act)
+    if a is None:
+        raise NotImplementedError(f"moe_forward_logits: activation {act!r}")
+    ids = torch.empty(M, k, dtype=torch.int32, device=x.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=x.device)
+    check(lib().exl3_moe_forward_logits(ptr(x), x.stride(0), M, tables.H, tables.I, ptr(logits), logits.stride(0), n,
+                                        ptr(bias), k, tables.E, ptr(tables.tables), ptr(tables.kmaps), tables.K_gate,
+                                        tables.K_up, tables.K_down, a, float(act_limit), int(shared), ptr(ids),
+                                        ptr(w), ptr(out), out.stride(0),
+                                        EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, stream_of(x)),
+          "moe_forward_logits")
+    return (out, ids, w) if return_routing else out
+
+
 def moe_align(topk_ids: torch.Tensor, topk_w: torch.Tensor, E: int, shared: int = -1):
     """(counts int32 [E], pair_tok int32 [P], pair_w fp32 [P], pair_of int32 [M*slots]) as the kernels build them."""
     require_device(topk_ids, topk_w)
@@ -241,21 +273,22 @@ class BlockSparseMLP:
         self.selection_bias = selection_bias
 
     def route(self, x2: torch.Tensor, params=None):
+        return route_softmax_topk(self.router_logits(x2, params), self.num_experts_per_tok, self.selection_bias)
+
+    def router_logits(self, x2: torch.Tensor, params=None) -> torch.Tensor:
         logits = None if params is None else params.get("router_logits")
         if logits is None:
             if self.router_weight is None:
                 raise Exl3Error("BlockSparseMLP: no router weight and no params['router_logits']")
             logits = x2.float() @ self.router_weight.float()
-        logits = logits.reshape(-1, self.num_experts).float().contiguous()
-        return route_softmax_topk(logits, self.num_experts_per_tok, self.selection_bias)
+        return logits.reshape(-1, self.num_experts).float().contiguous()
 
     def forward(self, x: torch.Tensor, params=None, out_dtype=None) -> torch.Tensor:
         x2 = x.reshape(-1, x.shape[-1])
         if x2.dtype != torch.float16:
             x2 = x2.half()
         x2 = x2.contiguous()
-        ids, w = self.route(x2, params)
-        out = moe_forward(x2, ids, w, self.experts, self.act, self.act_limit, self.shared,
-                          out_dtype=torch.float32)
+        out = moe_forward_logits(x2, self.router_logits(x2, params), self.num_experts_per_tok, self.experts,
+                                 self.act, self.act_limit, self.shared, self.selection_bias, out_dtype=torch.float32)
         out = out.view(x.shape[:-1] + (self.experts.H,))
         return out if out_dtype is None else out.to(out_dtype)

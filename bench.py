@@ -2,7 +2,7 @@
 """Benchmark of the EXL3 quantized-linear + MoE-expert hot path on one MI355X.
 
 One step = one layer call of the headline workload (C3 below) on 4 decode tokens: softmax/top-10 routing from fp32
-logits, then the grouped MoE layer (align, gate|up + activation, down, combine). Timed as HIP-graph replay of exactly
+logits and the grouped MoE layer (gate|up + activation, down, combine) in one library call (moe_forward_logits). Timed as HIP-graph replay of exactly
 --steps steps (warmup steps run eagerly first); every step uses a fresh routing and cycles through layer copies so the
 expert weights come from HBM, not the 256 MB Infinity Cache. Prints one JSON line.
 
@@ -155,8 +155,7 @@ class MoEWorkload:
         x, lg = self.x[r], self.logits[r]
 
         def f():
-            ids, w = exl3.route_softmax_topk(lg, self.topk, self.bias)
-            exl3.moe_forward(x, ids, w, lay, self.act, 0.0, self.shared)
+            exl3.moe_forward_logits(x, lg, self.topk, lay, self.act, 0.0, self.shared, bias=self.bias)
         return f
 
     def experts_used(self, j):

@@ -118,6 +118,35 @@ def test_moe_per_tile_k(exl3, oracle, Ks, probs):
     assert max_rel(y, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("M,n_logits,bias", [(1, 11, False), (2, 11, True), (4, 11, False), (7, 11, True),
+                                               (8, 11, False), (20, 11, True)])
+def test_moe_forward_logits_matches_route_then_forward(exl3, small, M, n_logits, bias):
+    """The routed entry point returns exactly route_softmax_topk followed by moe_forward: same picks, same weights,
+    bit-identical rows (fused decode layer and multi-kernel paths)."""
+    tables, _ = small
+    g = torch.Generator().manual_seed(1900 + M)
+    x = torch.randn(M, 256, generator=g).half().cuda()
+    logits = torch.randn(M, n_logits, generator=g).cuda()
+    b = (0.3 * torch.randn(n_logits, generator=g)).cuda() if bias else None
+    out, ids, w = exl3.moe_forward_logits(x, logits, 3, tables, shared=11, bias=b, return_routing=True)
+    rid, rw = exl3.route_softmax_topk(logits, 3, b)
+    ref = exl3.moe_forward(x, rid, rw, tables, shared=11)
+    assert torch.equal(ids, rid) and torch.equal(w, rw)
+    assert torch.equal(out, ref)
+
+
+def test_moe_forward_logits_many_experts(exl3, oracle):
+    """600 routed experts (the router's 16-register-per-lane variant), top-8: same result as the two calls."""
+    tables, _ = make_experts(exl3, oracle, 600, 128, 128, 2, 2, 1950, oracle=False)
+    g = torch.Generator().manual_seed(1951)
+    x = torch.randn(2, 128, generator=g).half().cuda()
+    logits = torch.randn(2, 600, generator=g).cuda()
+    out, ids, w = exl3.moe_forward_logits(x, logits, 8, tables, return_routing=True)
+    rid, rw = exl3.route_softmax_topk(logits, 8)
+    assert torch.equal(ids, rid) and torch.equal(w, rw)
+    assert torch.equal(out, exl3.moe_forward(x, rid, rw, tables))
+
+
 def test_moe_c3_full_size(exl3, oracle):
     """Fine-grained MoE decode layer: H=2048, 512 experts of I=512, K=3, top-10 softmax routing, M = 1, 2, 4."""
     tables, orc = make_experts(exl3, oracle, 512, 2048, 512, 3, 3, 3000)
@@ -131,6 +160,8 @@ def test_moe_c3_full_size(exl3, oracle):
         assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
         y, ref = _run(exl3, oracle, tables, orc, x, ids.cpu(), w.cpu())
         assert max_rel(y, ref) <= MAX_REL, (M, max_rel(y, ref))
+        y2 = exl3.moe_forward_logits(x.cuda(), logits.cuda(), 10, tables)
+        assert max_rel(y2.cpu().numpy(), ref) <= MAX_REL, M
 
 
 def test_align_tables(exl3, oracle):
