@@ -61,10 +61,12 @@ struct StripRing {
     uint32_t D[R][K];
 };
 
-template <int K, int R>
+// With CHECK false the caller guarantees lt0 < nt: the loads are then issued without a branch, so the wait counts of
+// loads issued before them stay exact (a branch around them makes the compiler drain every load at the join).
+template <int K, int R, bool CHECK = true>
 __device__ __forceinline__ void strip_prefetch(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
                                                int lane, StripRing<K, R>& ring) {
-    if (lt0 >= nt) return;
+    if (CHECK && lt0 >= nt) return;
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const int n = (nt - lt0 + step - 1) / step;
 #pragma unroll

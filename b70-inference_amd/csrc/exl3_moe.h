@@ -56,6 +56,8 @@ struct MoeArgs {
     const float* tw;
     const int64_t* tables;             // [9][E]
     const int64_t* kmaps;              // [6][E] or null
+    int uniform;                       // tables[i][e] == tb[i] + e * ts[i] for every entry (host-known layout)
+    int64_t tb[9], ts[9];
     int Kg, Kd;                        // gate/up K, down K (0 = per-tile)
     int act;
     float limit;

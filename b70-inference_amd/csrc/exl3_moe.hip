@@ -766,8 +766,8 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
 int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const float* logits,
                             int64_t logits_ld, int64_t n_logits, const float* bias, int64_t topk, int64_t E,
                             const int64_t* tables, const int64_t* kmaps, int K_gate, int K_up, int K_down, int act,
-                            float act_limit, int64_t shared, int32_t* ids_out, float* w_out, void* out,
-                            int64_t out_ld, int out_dtype, void* stream) {
+                            float act_limit, int64_t shared, const int64_t* table_layout, int32_t* ids_out,
+                            float* w_out, void* out, int64_t out_ld, int out_dtype, void* stream) {
     MoeArgs a;
     int rc = moe_setup(x, x_ld, M, H, I, topk, E, tables, kmaps, K_gate, K_up, K_down, act, act_limit, shared, out,
                        out_ld, out_dtype, a);
@@ -779,6 +779,13 @@ int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t 
     EXL3_CHECK_ARG(logits && ids_out && w_out, "exl3_moe_forward_logits: null pointer");
     a.ids = ids_out;
     a.tw = w_out;
+    if (table_layout) {
+        a.uniform = 1;
+        for (int i = 0; i < 9; ++i) {
+            a.tb[i] = table_layout[i];
+            a.ts[i] = table_layout[9 + i];
+        }
+    }
     if ((rc = exl3_route_softmax_topk(logits, logits_ld, M, n_logits, bias, topk, ids_out, w_out, stream))) return rc;
     return moe_run(a, (hipStream_t)stream);
 }

@@ -33,7 +33,7 @@ namespace exl3 {
 
 constexpr int kFusedMaxPairs = 128;
 constexpr int kFusedMaxRows = 8;
-constexpr int kSpinMax = 1 << 18;       // polls of a down job's wait (each backs off up to ~2000 cycles)
+constexpr int kSpinMax = 1 << 20;       // polls of a down job's wait (each backs off up to ~512 cycles)
 constexpr int kCS = 32;                 // counter stride in ints (one 128-byte line per counter)
 #ifndef EXL3_FUSED_RING
 #define EXL3_FUSED_RING 4
@@ -60,6 +60,9 @@ struct FusedArgs {
     int* cnt_item;                      // [max_items] * kCS
     int* err;                           // set when a wait times out
     int P_gu, P_d;                      // k-splits (in tile-rows) of H for gate|up and of I for down
+    int direct;                         // down jobs build their inputs from the gate|up partials (no epilogue stage)
+    int uniform;                        // expert e's table entry i is tb[i] + e * ts[i] (no table loads)
+    int64_t tb[9], ts[9];
     int GU, DN;                         // gate|up jobs (I / 128 * P_gu) and down jobs (H / 128 * P_d) per item
     int J_gu, max_items;
     void* out;
@@ -142,6 +145,7 @@ __device__ __forceinline__ float pair_weight(const FusedArgs& a, int p) {
 }
 
 __device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
+
 __device__ __forceinline__ int ctz64(uint64_t m) { return __ffsll((unsigned long long)m) - 1; }
 // set bits of (lo, hi) in [b, b + n) (a 128-bit mask; n <= 64)
 __device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n) {
@@ -198,7 +202,17 @@ __device__ __forceinline__ void item_info(const FusedArgs& a, const Groups& g, i
         s.it_e = e;
         s.it_cnt = cnt;
     }
-    if (lane < 9) s.tab[lane] = ldg(a.tables + (int64_t)lane * a.E + e);
+    if (lane < 9) {
+        // uniform expert layout: entry i of expert e is at tb[i] + e * ts[i], no table load
+        int64_t b = 0, st = 0;
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            if (lane == i) {
+                b = a.tb[i];
+                st = a.ts[i];
+            }
+        s.tab[lane] = a.uniform ? b + (int64_t)e * st : ldg(a.tables + (int64_t)lane * a.E + e);
+    }
     if (K == 0 && lane < 6) s.km[lane] = ldg(a.kmaps + (int64_t)lane * a.E + e);
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
@@ -217,20 +231,22 @@ __device__ __forceinline__ Item read_item(const FusedShared<MR>& s) {
     return it;
 }
 
-// sum over pp < P of the partials at base + pp * stride + off (agent-scope loads, issued 16 at a time, added in pp order)
+// sum over pp < P of the partials at base + pp * stride + off (agent-scope loads, issued 32 at a time, added in pp
+// order)
 template <int NV>
 __device__ __forceinline__ void sum_partials(const float* base, size_t stride, const int (&off)[NV], int P,
                                              float (&acc)[NV]) {
+    constexpr int B = 32 / NV;
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc[v] = 0.f;
-    for (int p0 = 0; p0 < P; p0 += 16) {
-        float t[16][NV];
+    for (int p0 = 0; p0 < P; p0 += B) {
+        float t[B][NV];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < B; ++i)
 #pragma unroll
             for (int v = 0; v < NV; ++v) t[i][v] = p0 + i < P ? splitk_load(base + (size_t)(p0 + i) * stride + off[v]) : 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < B; ++i)
 #pragma unroll
             for (int v = 0; v < NV; ++v) acc[v] += t[i][v];
     }
@@ -305,6 +321,37 @@ __device__ __forceinline__ void range_sums(FusedShared<MR>& s, int nproj, int cn
     }
 }
 
+// Down input of row m, column block nb of I, from the gate|up partials of `slot` (the reference's GateUpKernel
+// epilogue, exl3_moe.n128.sycl:253-271): sum of the P_gu partials in split order, Hadamard * svh for gate and up (fp16),
+// act (fp16), * suh_d (fp16), Hadamard / sqrt(128) (fp16). Returns elements lane and lane + 64 (fp16 values in fp32).
+template <int MR>
+__device__ __forceinline__ void down_input(const FusedArgs& a, const int64_t* tab, size_t slot, int nb, int m, int lane,
+                                           float& r0, float& r1) {
+    const uint16_t* svg = reinterpret_cast<const uint16_t*>(tab[2]) + nb * 128;
+    const uint16_t* svu = reinterpret_cast<const uint16_t*>(tab[5]) + nb * 128;
+    const uint16_t* sud = reinterpret_cast<const uint16_t*>(tab[7]) + nb * 128;
+    const float sg0 = h2f(ldg(svg + lane)), sg1 = h2f(ldg(svg + lane + 64));
+    const float su0 = h2f(ldg(svu + lane)), su1 = h2f(ldg(svu + lane + 64));
+    const float sd0 = h2f(ldg(sud + lane)), sd1 = h2f(ldg(sud + lane + 64));
+    const int off[4] = {m * 128 + lane, m * 128 + lane + 64, (MR + m) * 128 + lane, (MR + m) * 128 + lane + 64};
+    float v[4];
+    sum_partials<4>(a.part_gu + slot * a.P_gu * 2 * MR * 128, 2 * MR * 128, off, a.P_gu, v);
+    float g0 = v[0], g1 = v[1], u0 = v[2], u1 = v[3];
+    fwht128_wave(g0, g1, lane);
+    fwht128_wave(u0, u1, lane);
+    g0 = (float)(_Float16)(g0 * kRsqrt128 * sg0);
+    g1 = (float)(_Float16)(g1 * kRsqrt128 * sg1);
+    u0 = (float)(_Float16)(u0 * kRsqrt128 * su0);
+    u1 = (float)(_Float16)(u1 * kRsqrt128 * su1);
+    float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
+    float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
+    a0 = (float)(_Float16)(a0 * sd0);
+    a1 = (float)(_Float16)(a1 * sd1);
+    fwht128_wave(a0, a1, lane);
+    r0 = (float)(_Float16)(a0 * kRsqrt128);
+    r1 = (float)(_Float16)(a1 * kRsqrt128);
+}
+
 template <int K, int MR>
 __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
                                              int nb, int p) {
@@ -320,24 +367,48 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
-    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, half, kr.nt, 2, lane, ring);
 
     // stage the blocks covering the k range of the item's x rows (16-byte loads; rows past cnt are zero) in xs[1]
-    // and both input sign vectors in su, all loads of a thread in flight together
+    // and both input sign vectors in su. The loads are issued before the first weight rows (every address clamped
+    // in range, no branch), so waiting for them does not wait for the weights.
     {
+        constexpr int XI = (MR * KBF * 16 + 255) / 256, SI = (KBF * 128 + 255) / 256;
         const int k0 = kr.b0 * 128, nch = kr.kbs * 16;           // 16-byte chunks per row
         const uint16_t* sg = reinterpret_cast<const uint16_t*>(s.tab[1]) + k0;
         const uint16_t* su = reinterpret_cast<const uint16_t*>(s.tab[4]) + k0;
-        for (int c = threadIdx.x; c < MR * nch; c += 256) {
-            const int m = c / nch, o = c - m * nch;
-            u32x4_t v = {0u, 0u, 0u, 0u};
-            if (m < cnt)
-                v = ldg(reinterpret_cast<const u32x4_t*>(a.x + (int64_t)(s.rows[m] / a.slots) * a.x_ld + k0) + o);
-            *reinterpret_cast<u32x4_t*>(&s.xs[1][m][o * 8]) = v;
+        u32x4_t xv[XI];
+        uint16_t gv[SI], uv[SI];
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            int c = threadIdx.x + 256 * j;
+            c = c < MR * nch ? c : MR * nch - 1;
+            const int m = c / nch, o = c - m * nch, mm = m < cnt ? m : 0;
+            xv[j] = ldg(reinterpret_cast<const u32x4_t*>(a.x + (int64_t)(s.rows[mm] / a.slots) * a.x_ld + k0) + o);
         }
-        for (int c = threadIdx.x; c < kr.kbs * 128; c += 256) {
-            s.su[0][c] = __builtin_bit_cast(_Float16, ldg(sg + c));
-            s.su[1][c] = __builtin_bit_cast(_Float16, ldg(su + c));
+#pragma unroll
+        for (int j = 0; j < SI; ++j) {
+            int c = threadIdx.x + 256 * j;
+            c = c < kr.kbs * 128 ? c : kr.kbs * 128 - 1;
+            gv[j] = ldg(sg + c);
+            uv[j] = ldg(su + c);
+        }
+        if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, half, kr.nt, 2, lane, ring);   // nt >= 8 > half
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            if (c < MR * nch) {
+                const int m = c / nch, o = c - m * nch;
+                const u32x4_t z = {0u, 0u, 0u, 0u};
+                *reinterpret_cast<u32x4_t*>(&s.xs[1][m][o * 8]) = m < cnt ? xv[j] : z;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SI; ++j) {
+            const int c = threadIdx.x + 256 * j;
+            if (c < kr.kbs * 128) {
+                s.su[0][c] = __builtin_bit_cast(_Float16, gv[j]);
+                s.su[1][c] = __builtin_bit_cast(_Float16, uv[j]);
+            }
         }
     }
     __syncthreads();
@@ -393,33 +464,21 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
             }
         }
     }
+    if (a.direct) {
+        // the down jobs build their inputs from the partials themselves: publish this split to the item counter
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+        __syncthreads();
+        if (threadIdx.x == 0) atomic_add_agent(&a.cnt_item[item * kCS], 1);
+        return;
+    }
     if (!splitk_arrive(&a.cnt_gu[slot * kCS], a.P_gu, &s.flag)) return;
 
-    const uint16_t* svg = reinterpret_cast<const uint16_t*>(s.tab[2]) + nb * 128;
-    const uint16_t* svu = reinterpret_cast<const uint16_t*>(s.tab[5]) + nb * 128;
-    const uint16_t* sud = reinterpret_cast<const uint16_t*>(s.tab[7]) + nb * 128;
-    const float sg0 = h2f(ldg(svg + lane)), sg1 = h2f(ldg(svg + lane + 64));
-    const float su0 = h2f(ldg(svu + lane)), su1 = h2f(ldg(svu + lane + 64));
-    const float sd0 = h2f(ldg(sud + lane)), sd1 = h2f(ldg(sud + lane + 64));
     for (int m = wave; m < cnt; m += 4) {
-        const int off[4] = {m * 128 + lane, m * 128 + lane + 64, (MR + m) * 128 + lane, (MR + m) * 128 + lane + 64};
-        float v[4];
-        sum_partials<4>(a.part_gu + slot * a.P_gu * 2 * MR * 128, 2 * MR * 128, off, a.P_gu, v);
-        float g0 = v[0], g1 = v[1], u0 = v[2], u1 = v[3];
-        fwht128_wave(g0, g1, lane);
-        fwht128_wave(u0, u1, lane);
-        g0 = (float)(_Float16)(g0 * kRsqrt128 * sg0);
-        g1 = (float)(_Float16)(g1 * kRsqrt128 * sg1);
-        u0 = (float)(_Float16)(u0 * kRsqrt128 * su0);
-        u1 = (float)(_Float16)(u1 * kRsqrt128 * su1);
-        float a0 = (float)(_Float16)act_mul_dev(g0, u0, a.act, a.limit);
-        float a1 = (float)(_Float16)act_mul_dev(g1, u1, a.act, a.limit);
-        a0 = (float)(_Float16)(a0 * sd0);
-        a1 = (float)(_Float16)(a1 * sd1);
-        fwht128_wave(a0, a1, lane);
+        float r0, r1;
+        down_input<MR>(a, s.tab, slot, nb, m, lane, r0, r1);
         float* dst = a.abuf + ((size_t)item * MR + m) * a.I + nb * 128;
-        splitk_store(dst + lane, (float)(_Float16)(a0 * kRsqrt128));
-        splitk_store(dst + lane + 64, (float)(_Float16)(a1 * kRsqrt128));
+        splitk_store(dst + lane, r0);
+        splitk_store(dst + lane + 64, r1);
     }
     __builtin_amdgcn_s_waitcnt(0);      // this wave's down-input stores have completed
     __syncthreads();
@@ -443,26 +502,37 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
-    if (K > 0) strip_prefetch<KL, kFusedRing>(sp, rs, wave, kr.nt, 4, lane, ring);
+    if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, wave, kr.nt, 4, lane, ring);   // nt >= 8 > wave
 
-    // wait for the item's down input (all nbI column blocks), then count this job as a consumer; the last consumer
-    // clears the item counter for the next call
+    // wait for the item's down input (all nbI column blocks published, or in direct mode all nbI * P_gu gate|up
+    // splits), then count this job as a consumer; the last consumer clears the item counter for the next call
+    const int need = a.direct ? nbI * a.P_gu : nbI;
     if (threadIdx.x == 0) {
         int* c = &a.cnt_item[item * kCS];
         int n = 0, back = 1;
-        while (atomic_load_agent(c) < nbI) {
+        while (atomic_load_agent(c) < need) {
             if (++n > kSpinMax) {
                 atomic_store_agent(a.err, 1);
                 break;
             }
-            for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(4);
-            back = back < 8 ? 2 * back : 8;
+            for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(2);
+            back = back < 4 ? 2 * back : 4;
         }
         const int old = atomic_add_agent(c, 1);
-        if (old == nbI + a.DN - 1) atomic_store_agent(c, 0);
+        if (old == need + a.DN - 1) atomic_store_agent(c, 0);
     }
     __syncthreads();
 
+    if (a.direct) {
+        // block (m, b) of the down input straight from the gate|up partials, one wave each
+        for (int i = wave; i < cnt * kr.kbs; i += 4) {
+            const int m = i / kr.kbs, b = i - m * kr.kbs, bi = kr.b0 + b;
+            float r0, r1;
+            down_input<MR>(a, s.tab, (size_t)item * nbI + bi, bi, m, lane, r0, r1);
+            s.xs[0][m][b * 128 + lane] = (_Float16)r0;
+            s.xs[0][m][b * 128 + lane + 64] = (_Float16)r1;
+        }
+    } else {
     // the wave's blocks (m, b) = (i / kbs, i % kbs), i = wave, wave + 4, ...: every load first, then convert
     constexpr int NBW = (MR * KBF + 3) / 4;
     float va[NBW], vb[NBW];
@@ -483,6 +553,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
             s.xs[0][m][b * 128 + lane] = (_Float16)va[j];
             s.xs[0][m][b * 128 + lane + 64] = (_Float16)vb[j];
         }
+    }
     }
     __syncthreads();
     range_sums(s, 1, cnt, kr, wave, lane);
@@ -678,6 +749,13 @@ bool moe_fused_ok(const MoeArgs& a) {
 
 int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     FusedArgs a{};
+    if (m.uniform) {
+        a.uniform = 1;
+        for (int i = 0; i < 9; ++i) {
+            a.tb[i] = m.tb[i];
+            a.ts[i] = m.ts[i];
+        }
+    }
     a.x = m.x;
     a.x_ld = m.x_ld;
     a.M = m.M;
@@ -722,6 +800,10 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.GU = nbI * a.P_gu;
     a.P_d = fused_splits(1, a.I / 16, kbf);
     a.DN = nbH * a.P_d;
+    // unsplit down jobs compute their whole input from the partials (each column block of I is then rebuilt by the
+    // item's nbH down jobs instead of once by a gate|up epilogue, saving that stage's round trips); with many
+    // gate|up splits the partial loads cost more than the stage saves
+    a.direct = a.P_d == 1 && a.P_gu <= 8 && nbH <= 64 && env_int("EXL3MI_FUSED_EPILOGUE", 0) == 0;
     const int64_t jgu = (int64_t)a.max_items * a.GU, grid = jgu + a.GU;
     EXL3_CHECK_ARG(grid < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
     a.J_gu = (int)jgu;

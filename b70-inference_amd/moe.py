@@ -11,6 +11,8 @@ Interfaces mirror the reference boundary:
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from ._lib import ACT_GELU_TANH, ACT_SILU, EXL3_F16, EXL3_F32, Exl3Error, check, lib, ptr, require_device, stream_of
@@ -90,6 +92,35 @@ class ExpertTables:
                 krows.append([p.kmap.data_ptr() if isinstance(p, MixedEXL3) else 0 for p in plist])
                 krows.append([p.woff.data_ptr() if isinstance(p, MixedEXL3) else 0 for p in plist])
             self.kmaps = torch.tensor(krows, dtype=torch.int64).to(dev)
+        # uniform layout (every table row an arithmetic progression over the experts, no per-tile K): the decode
+        # kernels then compute an expert's addresses (base + e * stride) instead of loading them
+        self.layout = None
+        if self.kmaps is None:
+            bases, strides = [], []
+            for r in rows:
+                st = r[1] - r[0] if self.E > 1 else 0
+                if any(r[e] - r[0] != e * st for e in range(self.E)):
+                    break
+                bases.append(r[0])
+                strides.append(st)
+            else:
+                self.layout = (ctypes.c_int64 * 18)(*bases, *strides)
+
+    @classmethod
+    def packed(cls, gates, ups, downs):
+        """The same experts copied into one contiguous allocation per projection and tensor kind ([E, ...] trellis, suh,
+        svh), so every table row is base + e * stride (the layout the decode kernels address without table loads).
+        Projections must share K (BC_LinearEXL3)."""
+        out = []
+        for plist in (gates, ups, downs):
+            if any(isinstance(p, MixedEXL3) for p in plist):
+                raise NotImplementedError("ExpertTables.packed: per-tile-K projections are not packed")
+            tr = torch.stack([p.trellis for p in plist])
+            su = torch.stack([p.suh for p in plist])
+            sv = torch.stack([p.svh for p in plist])
+            out.append([BC_LinearEXL3(tr[e], su[e], sv[e], plist[e].K, None, False, True, None)
+                        for e in range(len(plist))])
+        return cls(*out)
 
     def weight_bytes(self, experts) -> int:
         """Trellis + sign-vector bytes of the given expert indices (the algorithmic HBM bytes of reading them)."""
@@ -154,9 +185,10 @@ def moe_forward_logits(x: torch.Tensor, logits: torch.Tensor, k: int, tables: Ex
         raise NotImplementedError(f"moe_forward_logits: activation {act!r}")
     ids = torch.empty(M, k, dtype=torch.int32, device=x.device)
     w = torch.empty(M, k, dtype=torch.float32, device=x.device)
+    layout = ctypes.cast(tables.layout, ctypes.c_void_p) if tables.layout is not None else None
     check(lib().exl3_moe_forward_logits(ptr(x), x.stride(0), M, tables.H, tables.I, ptr(logits), logits.stride(0), n,
                                         ptr(bias), k, tables.E, ptr(tables.tables), ptr(tables.kmaps), tables.K_gate,
-                                        tables.K_up, tables.K_down, a, float(act_limit), int(shared), ptr(ids),
+                                        tables.K_up, tables.K_down, a, float(act_limit), int(shared), layout, ptr(ids),
                                         ptr(w), ptr(out), out.stride(0),
                                         EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, stream_of(x)),
           "moe_forward_logits")

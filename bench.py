@@ -72,14 +72,26 @@ def dev_mixed(k, n, g, Ks=(1, 2), probs=(0.38, 0.62)):
     return exl3.MixedEXL3(words, kmap, woff.to(torch.int32), suh, svh)
 
 
+def dev_packed(E, k, n, K, g):
+    """E projections k -> n generated straight into one [E, ...] allocation per tensor kind (uniform strides)."""
+    tr = torch.randint(-32768, 32768, (E, k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
+    suh = (torch.randint(0, 2, (E, k), device="cuda", generator=g).float() * 2 - 1).half()
+    svh = ((torch.randint(0, 2, (E, n), device="cuda", generator=g).float() * 2 - 1) *
+           float(torch.tensor(1.0 / math.sqrt(k)).half())).half()
+    return [exl3.BC_LinearEXL3(tr[e], suh[e], svh[e], K, None, False, True, None) for e in range(E)]
+
+
 def dev_experts(E, H, I, Kgu, Kd, seed, mixed=False):
+    """Expert tables with random weights: uniform K packed per projection as a model loader lays them out
+    (ExpertTables.packed), per-tile K one allocation per projection."""
     g = dev_gen(seed)
-    mk = (lambda k, n, K: dev_mixed(k, n, g)) if mixed else (lambda k, n, K: dev_linear(k, n, K, g))
+    if not mixed:
+        return exl3.ExpertTables(dev_packed(E, H, I, Kgu, g), dev_packed(E, H, I, Kgu, g), dev_packed(E, I, H, Kd, g))
     gates, ups, downs = [], [], []
     for _ in range(E):
-        gates.append(mk(H, I, Kgu))
-        ups.append(mk(H, I, Kgu))
-        downs.append(mk(I, H, Kd))
+        gates.append(dev_mixed(H, I, g))
+        ups.append(dev_mixed(H, I, g))
+        downs.append(dev_mixed(I, H, g))
     return exl3.ExpertTables(gates, ups, downs)
 
 

@@ -108,13 +108,16 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
  * routing launch, then the layer's launches on the same stream). logits fp32 [M, n_logits] (row stride logits_ld),
  * bias fp32 [n_logits] or NULL; the routed experts are table entries 0 .. n_logits - 1 (n_logits <= E; the shared
  * expert, if any, is another entry). ids_out int32 [M, topk] and w_out fp32 [M, topk] receive the routing.
- * topk <= 32, n_logits <= 8192. Replaces: the router + BlockSparseMLP.forward pair (glm/xpu/glm_xpu/moe_patch.py:68-94 with the
- * trellis-serve fused router, trellis-serve.patch:395-441). */
+ * topk <= 32, n_logits <= 8192. table_layout: NULL, or a HOST array of 18 int64 (base[9], stride[9]) with
+ * tables[i][e] == base[i] + e * stride[i] for every expert e < E (experts packed at uniform strides, as
+ * ExpertTables.packed builds them): the decode kernels then compute an expert's addresses instead of loading them.
+ * Replaces: the router + BlockSparseMLP.forward pair (glm/xpu/glm_xpu/moe_patch.py:68-94 with the trellis-serve fused
+ * router, trellis-serve.patch:395-441). */
 int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const float* logits,
                             int64_t logits_ld, int64_t n_logits, const float* bias, int64_t topk, int64_t E,
                             const int64_t* tables, const int64_t* kmaps, int K_gate, int K_up, int K_down, int act,
-                            float act_limit, int64_t shared, int32_t* ids_out, float* w_out, void* out,
-                            int64_t out_ld, int out_dtype, void* stream);
+                            float act_limit, int64_t shared, const int64_t* table_layout, int32_t* ids_out,
+                            float* w_out, void* out, int64_t out_ld, int out_dtype, void* stream);
 
 /* Routing tables as the MoE kernels build them (pairs grouped by expert), for tests and debugging.
  * Writes counts int32 [E], pair_tok int32 [M*slots], pair_w fp32 [M*slots], pair_of int32 [M*slots]

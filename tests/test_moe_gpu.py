@@ -135,6 +135,21 @@ def test_moe_forward_logits_matches_route_then_forward(exl3, small, M, n_logits,
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("M", [1, 4, 12])
+def test_moe_packed_tables_same_rows(exl3, small, M):
+    """ExpertTables.packed (uniform strides: the decode kernels compute expert addresses instead of loading them)
+    gives bit-identical rows to the same experts addressed through their pointer tables."""
+    tables, _ = small
+    packed = exl3.ExpertTables.packed(*tables.projs)
+    assert packed.layout is not None and list(packed.layout)[9] > 0
+    g = torch.Generator().manual_seed(1960 + M)
+    x = torch.randn(M, 256, generator=g).half().cuda()
+    logits = torch.randn(M, 11, generator=g).cuda()
+    a = exl3.moe_forward_logits(x, logits, 3, tables, shared=11)
+    b = exl3.moe_forward_logits(x, logits, 3, packed, shared=11)
+    assert torch.equal(a, b)
+
+
 def test_moe_forward_logits_many_experts(exl3, oracle):
     """600 routed experts (the router's 16-register-per-lane variant), top-8: same result as the two calls."""
     tables, _ = make_experts(exl3, oracle, 600, 128, 128, 2, 2, 1950, oracle=False)
