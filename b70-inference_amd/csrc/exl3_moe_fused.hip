@@ -482,10 +482,15 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     }
     __builtin_amdgcn_s_waitcnt(0);      // this wave's down-input stores have completed
     __syncthreads();
-    if (threadIdx.x == 0) {
-        a.cnt_gu[slot * kCS] = 0;
-        atomic_add_agent(&a.cnt_item[item * kCS], 1);
-    }
+    // P_gu + 1: block nb of the item's down input is published (its consumers count on from there and the last one
+    // clears it)
+    if (threadIdx.x == 0) atomic_add_agent(&a.cnt_gu[slot * kCS], 1);
+}
+
+// split of P over T tile-rows that holds tile-row t (splits start at floor(p T / P))
+__device__ __forceinline__ int split_of(int t, int P, int T) {
+    const int p = (int)(((int64_t)(t + 1) * P - 1) / T);
+    return p < P - 1 ? p : P - 1;
 }
 
 template <int K, int MR>
@@ -504,22 +509,36 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     StripRing<KL, kFusedRing> ring;
     if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, wave, kr.nt, 4, lane, ring);   // nt >= 8 > wave
 
-    // wait for the item's down input (all nbI column blocks published, or in direct mode all nbI * P_gu gate|up
-    // splits), then count this job as a consumer; the last consumer clears the item counter for the next call
-    const int need = a.direct ? nbI * a.P_gu : nbI;
-    if (threadIdx.x == 0) {
-        int* c = &a.cnt_item[item * kCS];
+    // wait for the down input this job reads, then count the job as a consumer (the last consumer clears the counter
+    // for the next call). Direct mode: every gate|up split of the item (nbI * P_gu arrivals on the item counter).
+    // Otherwise: just the column blocks of I in this job's k range, each published by its gate|up epilogue (counter
+    // P_gu + 1), so a down job starts as soon as its own blocks are in; lane b of wave 0 watches block b0 + b.
+    if (threadIdx.x < 64) {
+        const int lane0 = threadIdx.x;
+        const bool mine = a.direct ? lane0 == 0 : lane0 < kr.kbs;
+        int* c = a.direct ? &a.cnt_item[item * kCS] : &a.cnt_gu[((size_t)item * nbI + kr.b0 + (mine ? lane0 : 0)) * kCS];
+        const int need = a.direct ? nbI * a.P_gu : a.P_gu + 1;
         int n = 0, back = 1;
-        while (atomic_load_agent(c) < need) {
+        while (__ballot(mine && atomic_load_agent(c) < need)) {
             if (++n > kSpinMax) {
-                atomic_store_agent(a.err, 1);
+                if (lane0 == 0) atomic_store_agent(a.err, 1);
                 break;
             }
             for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(2);
             back = back < 4 ? 2 * back : 4;
         }
-        const int old = atomic_add_agent(c, 1);
-        if (old == need + a.DN - 1) atomic_store_agent(c, 0);
+        if (mine) {
+            const int old = atomic_add_agent(c, 1);
+            int last;
+            if (a.direct) {
+                last = need + a.DN - 1;
+            } else {
+                // consumers of block bi: every column block of H times the k splits whose range touches it
+                const int bi = kr.b0 + lane0, T = a.I / 16;
+                last = a.P_gu + nbH * (split_of(8 * bi + 7, a.P_d, T) - split_of(8 * bi, a.P_d, T) + 1);
+            }
+            if (old == last) atomic_store_agent(c, 0);
+        }
     }
     __syncthreads();
 
@@ -697,7 +716,8 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     __syncthreads();
     const Item it = read_item<K, MR>(s);
     for (int r = gr0; r < a.DN; r += a.GU) {
-        fused_down<K, MR>(a, s, v0, v1, it, di, r / a.P_d, r % a.P_d);
+        // k-split major: the down jobs reading the first column blocks of I (published first) come first
+        fused_down<K, MR>(a, s, v0, v1, it, di, r % (a.H / 128), r / (a.H / 128));
         __syncthreads();
     }
 }

@@ -78,6 +78,19 @@ def test_moe_fused_and_multi_kernel_paths(exl3, oracle, small, monkeypatch, M):
     assert max_rel(y2, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("I,M", [(2048, 1), (2560, 2), (2560, 4)])
+def test_moe_fused_split_down_blocks(exl3, oracle, I, M):
+    """Wide intermediate (I = 2048: two k splits of the down projection; I = 2560: three, whose staged ranges share
+    column blocks of I): each down job waits for just its own blocks of the down input; two calls in a row agree."""
+    tables, orc = make_experts(exl3, oracle, 4, 256, I, 3, 3, 1970 + I)
+    ids, w = _ids_w(M, 2, 4, 1971 + M, dup=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(1972 + M)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    y2, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert np.array_equal(y, y2)
+
+
 def test_moe_fused_counters_reset_between_calls(exl3, small):
     """The fused layer's job ticket and arrival counters are back at zero after every call: alternating batch sizes
     and split counts reproduce the first results bit for bit."""
