@@ -56,16 +56,28 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
 template <int V>
 __device__ __forceinline__ void route_row(const float* __restrict__ z, const float* __restrict__ bias, int E, int k,
                                           int lane, int& id, float& w) {
+    // every load issued before any is used (clamped indices, no per-element branch): one memory round trip
+    float f[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int i = lane + 64 * v;
+        f[v] = ldg(z + (i < E ? i : E - 1));
+    }
+    if (bias) {
+        float b[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int i = lane + 64 * v;
+            b[v] = ldg(bias + (i < E ? i : E - 1));
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) f[v] += b[v];
+    }
     uint32_t key[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const int i = lane + 64 * v;
-        uint32_t kk = 0u;
-        if (i < E) {
-            const float f = ldg(z + i) + (bias ? ldg(bias + i) : 0.f);
-            kk = f != f ? 1u : float_key(f);
-        }
-        key[v] = kk;
+        key[v] = i < E ? (f[v] != f[v] ? 1u : float_key(f[v])) : 0u;
     }
     uint32_t lmax = 0u;
 #pragma unroll
