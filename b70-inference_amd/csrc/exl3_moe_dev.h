@@ -28,12 +28,24 @@ __device__ __forceinline__ float act_mul_dev(float g, float u, int act, float L)
 __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, int lane) {
     const int c0 = nb * 128 + lane, c1 = c0 + 64;
     float v0 = 0.f, v1 = 0.f;
-    for (int j = 0; j < a.slots; ++j) {
-        const int pr = a.pair_of[t * a.slots + j];
-        if (pr < 0) continue;
-        const float* y = a.y + (size_t)pr * a.H;
-        v0 += splitk_load(y + c0);
-        v1 += splitk_load(y + c1);
+    // slots in order, 8 at a time: every load of a group issued before the first add (a missing slot reads pair 0's
+    // row and adds zero)
+    for (int j0 = 0; j0 < a.slots; j0 += 8) {
+        int pr[8];
+        float y0[8], y1[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pr[j] = j0 + j < a.slots ? a.pair_of[t * a.slots + j0 + j] : -1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float* y = a.y + (size_t)(pr[j] >= 0 ? pr[j] : 0) * a.H;
+            y0[j] = splitk_load(y + c0);
+            y1[j] = splitk_load(y + c1);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v0 += pr[j] >= 0 ? y0[j] : 0.f;
+            v1 += pr[j] >= 0 ? y1[j] : 0.f;
+        }
     }
     if (a.out_f32) {
         float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;

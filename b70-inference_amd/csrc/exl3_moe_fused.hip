@@ -508,6 +508,13 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
     if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, wave, kr.nt, 4, lane, ring);   // nt >= 8 > wave
+    // the epilogue's output signs and row weights, loaded now so the epilogue waits for nothing
+    constexpr int RW = (MR + 3) / 4;                     // rows m = wave + 4 j of this wave
+    const uint16_t* svd = reinterpret_cast<const uint16_t*>(s.tab[8]) + nb * 128;
+    const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
+    float wrow[RW];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) wrow[j] = pair_weight(a, s.rows[wave + 4 * j < MR ? wave + 4 * j : 0]);
 
     // wait for the down input this job reads, then count the job as a consumer (the last consumer clears the counter
     // for the next call). Direct mode: every gate|up split of the item (nbI * P_gu arrivals on the item counter).
@@ -617,11 +624,12 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         __syncthreads();
     }
 
-    const uint16_t* svd = reinterpret_cast<const uint16_t*>(s.tab[8]) + nb * 128;
-    const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
-    for (int m = wave; m < cnt; m += 4) {
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int m = wave + 4 * j;
+        if (m >= cnt) break;
         const int pr = s.rows[m];
-        const float w = pair_weight(a, pr);
+        const float w = wrow[j];
         float v0, v1;
         if (split) {
             const int off[2] = {m * 128 + lane, m * 128 + lane + 64};
@@ -643,13 +651,12 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int m = 0; m < cnt; ++m) {
-            const int t = s.rows[m] / a.slots;
-            const int nv = popc_range(vm0, vm1, t * a.slots, a.slots);
-            const int old = atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
-            s.comb[m] = (old == nv - 1) ? t : -1;
-        }
+    if (threadIdx.x < cnt) {                 // lane m counts row m (rows of one item belong to different tokens)
+        const int m = threadIdx.x;
+        const int t = s.rows[m] / a.slots;
+        const int nv = popc_range(vm0, vm1, t * a.slots, a.slots);
+        const int old = atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
+        s.comb[m] = (old == nv - 1) ? t : -1;
     }
     __syncthreads();
     for (int m = wave; m < cnt; m += 4) {
@@ -657,12 +664,24 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         if (t < 0) continue;
         const int c0 = nb * 128 + lane, c1 = c0 + 64;
         float v0 = 0.f, v1 = 0.f;
-        for (int j = 0; j < a.slots; ++j) {
-            const int pr = t * a.slots + j;
-            if (!(((pr < 64 ? vm0 >> pr : vm1 >> (pr - 64))) & 1)) continue;
-            const float* yr = a.y + (size_t)pr * a.H;
-            v0 += splitk_load(yr + c0);
-            v1 += splitk_load(yr + c1);
+        // slots in order, 8 at a time: every load of a group issued before the first add (invalid slots read a
+        // valid row and add zero)
+        for (int j0 = 0; j0 < a.slots; j0 += 8) {
+            float y0[8], y1[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int jj = j0 + j < a.slots ? j0 + j : a.slots - 1;
+                const float* yr = a.y + (size_t)(t * a.slots + jj) * a.H;
+                y0[j] = splitk_load(yr + c0);
+                y1[j] = splitk_load(yr + c1);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int pr = t * a.slots + j0 + j;
+                const bool ok = j0 + j < a.slots && (((pr < 64 ? vm0 >> pr : vm1 >> (pr - 64))) & 1);
+                v0 += ok ? y0[j] : 0.f;
+                v1 += ok ? y1[j] : 0.f;
+            }
         }
         if (a.out_f32) {
             float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
