@@ -240,15 +240,18 @@ __device__ __forceinline__ void sum_partials(const float* base, size_t stride, c
 #pragma unroll
     for (int v = 0; v < NV; ++v) acc[v] = 0.f;
     for (int p0 = 0; p0 < P; p0 += B) {
+        // unconditional loads (split index clamped to P - 1), so the whole batch is in flight before the first add
         float t[B][NV];
 #pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int pp = p0 + i < P ? p0 + i : P - 1;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) t[i][v] = splitk_load(base + (size_t)pp * stride + off[v]);
+        }
+#pragma unroll
         for (int i = 0; i < B; ++i)
 #pragma unroll
-            for (int v = 0; v < NV; ++v) t[i][v] = p0 + i < P ? splitk_load(base + (size_t)(p0 + i) * stride + off[v]) : 0.f;
-#pragma unroll
-        for (int i = 0; i < B; ++i)
-#pragma unroll
-            for (int v = 0; v < NV; ++v) acc[v] += t[i][v];
+            for (int v = 0; v < NV; ++v) acc[v] += p0 + i < P ? t[i][v] : 0.f;
     }
 }
 
@@ -565,12 +568,10 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
         const int i = wave + 4 * j, m = i / kr.kbs, b = i - m * kr.kbs;
-        va[j] = vb[j] = 0.f;
-        if (m < cnt) {
-            const float* src = a.abuf + ((size_t)item * MR + m) * a.I + (kr.b0 + b) * 128;
-            va[j] = splitk_load(src + lane);
-            vb[j] = splitk_load(src + lane + 64);
-        }
+        const int mm = m < cnt ? m : 0;                  // unconditional load (rows past cnt read row 0, unused)
+        const float* src = a.abuf + ((size_t)item * MR + mm) * a.I + (kr.b0 + b) * 128;
+        va[j] = splitk_load(src + lane);
+        vb[j] = splitk_load(src + lane + 64);
     }
 #pragma unroll
     for (int j = 0; j < NBW; ++j) {
