@@ -24,7 +24,11 @@
 namespace exl3 {
 
 // ------------------------------------------------------------------------------------------------ input transform
+// Workgroup (row block, 128-column block kb of H): every row's x block times suh_gate and suh_up, Hadamard, fp16
+// (the GEMM inputs xh) and their block sums (xsum). The block's token list and both sign vectors are loaded once;
+// each wave then takes 4 rows at a time with all their x loads in flight before the first transform.
 __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
+    __shared__ int s_tok[kMfmaRows];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int blk = blockIdx.x, kb = blockIdx.y;
     const ItemDesc* d = a.blocks + blk;
@@ -32,13 +36,39 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     if (cnt == 0) return;
     const int p0 = d->p0;
     const int nblk = a.H / 128;
-    for (int i = wave; i < 2 * cnt; i += 4) {
-        const int row = i >> 1, proj = i & 1;
-        const int tok = a.pair_tok[p0 + row];
-        const uint16_t* suh = reinterpret_cast<const uint16_t*>(d->tab[3 * proj + 1]) + kb * 128;
-        _Float16* dst = a.xh + ((size_t)(p0 + row) * 2 + proj) * a.H + kb * 128;
-        const float bs = had_in_block(a.x + (int64_t)tok * a.x_ld + kb * 128, suh, dst, lane);
-        if (lane == 0) a.xsum[((size_t)(p0 + row) * 2 + proj) * nblk + kb] = bs;
+    if (threadIdx.x < cnt) s_tok[threadIdx.x] = a.pair_tok[p0 + threadIdx.x];
+    const uint16_t* sg = reinterpret_cast<const uint16_t*>(d->tab[1]) + kb * 128;
+    const uint16_t* su = reinterpret_cast<const uint16_t*>(d->tab[4]) + kb * 128;
+    const float g0 = h2f(ldg(sg + lane)), g1 = h2f(ldg(sg + lane + 64));
+    const float u0 = h2f(ldg(su + lane)), u1 = h2f(ldg(su + lane + 64));
+    __syncthreads();
+    constexpr int RB = 4;
+    for (int r0 = wave; r0 < cnt; r0 += 4 * RB) {
+        float xa[RB], xb[RB];
+#pragma unroll
+        for (int k = 0; k < RB; ++k) {
+            const int row = r0 + 4 * k < cnt ? r0 + 4 * k : r0;   // unconditional load (repeats row r0, unused)
+            const uint16_t* x = a.x + (int64_t)s_tok[row] * a.x_ld + kb * 128;
+            xa[k] = h2f(ldg(x + lane));
+            xb[k] = h2f(ldg(x + lane + 64));
+        }
+#pragma unroll
+        for (int k = 0; k < RB; ++k) {
+            const int row = r0 + 4 * k;
+            if (row >= cnt) break;
+#pragma unroll
+            for (int proj = 0; proj < 2; ++proj) {
+                float va = (float)(_Float16)(xa[k] * (proj ? u0 : g0));
+                float vb = (float)(_Float16)(xb[k] * (proj ? u1 : g1));
+                fwht128_wave(va, vb, lane);
+                const _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
+                _Float16* dst = a.xh + ((size_t)(p0 + row) * 2 + proj) * a.H + kb * 128;
+                dst[lane] = ha;
+                dst[lane + 64] = hb;
+                const float bs = wave_sum_f32((float)ha + (float)hb);
+                if (lane == 0) a.xsum[((size_t)(p0 + row) * 2 + proj) * nblk + kb] = bs;
+            }
+        }
     }
 }
 
@@ -281,15 +311,16 @@ __device__ __forceinline__ void gateup_epilogue(const MoeArgs& a, const ItemDesc
     }
 }
 
-// sum over b < n of q[b], in order, with the loads issued 16 at a time
+// sum over b < n of q[b] (n >= 1), in order, with the loads issued 16 at a time (unconditionally: indices clamped to
+// n - 1, so no branch splits a batch into separate round trips)
 __device__ __forceinline__ float sum_ordered(const float* q, int n) {
     float v = 0.f;
     for (int b0 = 0; b0 < n; b0 += 16) {
         float t[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) t[i] = b0 + i < n ? ldg(q + b0 + i) : 0.f;
+        for (int i = 0; i < 16; ++i) t[i] = ldg(q + (b0 + i < n ? b0 + i : n - 1));
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v += t[i];
+        for (int i = 0; i < 16; ++i) v += b0 + i < n ? t[i] : 0.f;
     }
     return v;
 }
@@ -359,9 +390,19 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
     float sd[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        sd[h][0] = h < nhalf ? h2f(ldg(svd + 128 * h + lane)) : 0.f;
-        sd[h][1] = h < nhalf ? h2f(ldg(svd + 128 * h + lane + 64)) : 0.f;
+        const int hh = h < nhalf ? h : 0;                // unconditional load, unused past nhalf
+        sd[h][0] = h2f(ldg(svd + 128 * hh + lane));
+        sd[h][1] = h2f(ldg(svd + 128 * hh + lane + 64));
     }
+    // row weights of this wave's rows 16 rg + 4 wave + r, all loaded before the first is needed
+    float wr[RGA][4];
+#pragma unroll
+    for (int rg = 0; rg < RGA; ++rg)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 16 * rg + 4 * wave + r;
+            wr[rg][r] = a.pair_w[p0 + (m < cnt ? m : cnt - 1)];
+        }
 #pragma unroll
     for (int rg = 0; rg < RGA; ++rg) {
 #pragma unroll
@@ -371,13 +412,14 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
             for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * 256 + col] = acc[t][rg][i];
         }
         __syncthreads();
+#pragma unroll
         for (int j = 0; j < 8; ++j) {                 // (row, half) pairs of this wave
             const int ml = 4 * wave + (j >> 1), h = j & 1, m = 16 * rg + ml;
             if (m >= cnt || h >= nhalf) continue;
             const float sx = kMul1C2 * rsum[m];
             float v0 = kMul1C1 * C[ml * 256 + 128 * h + lane] + sx, v1 = kMul1C1 * C[ml * 256 + 128 * h + lane + 64] + sx;
             fwht128_wave(v0, v1, lane);
-            const float w = a.pair_w[p0 + m];
+            const float w = wr[rg][j >> 1];
             float* dst = a.y + (size_t)(p0 + m) * a.H + nb * 256 + 128 * h;
             splitk_store(dst + lane, v0 * kRsqrt128 * sd[h][0] * w);
             splitk_store(dst + lane + 64, v1 * kRsqrt128 * sd[h][1] * w);

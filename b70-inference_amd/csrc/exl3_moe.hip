@@ -46,6 +46,38 @@ __device__ int block_scan_exclusive(int* a, int n, int* tmp /* [1024] */) {
     return total;
 }
 
+// Experts and weights of pairs i0 + k * stride, k < B (-1 / 0 past np or for an invalid id), every load issued
+// before any is used: indices are clamped instead of branched on, so a batch costs one memory round trip.
+template <int B>
+__device__ __forceinline__ void load_pairs(const RouteArgs& r, int i0, int stride, int np, int (&e)[B],
+                                           float (&w)[B]) {
+    int v[B];
+    float wv[B];
+    if (r.topk > 0) {
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            const int i = i0 + k * stride, ic = i < np ? i : np - 1;
+            const int tok = ic / r.slots, j = ic - tok * r.slots, jj = j < r.topk ? j : r.topk - 1;
+            v[k] = ldg(r.ids + tok * r.topk + jj);
+            wv[k] = ldg(r.tw + tok * r.topk + jj);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            v[k] = 0;
+            wv[k] = 1.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+        const int i = i0 + k * stride, ic = i < np ? i : np - 1;
+        const int tok = ic / r.slots, j = ic - tok * r.slots;
+        const int ek = j < r.topk ? v[k] : r.shared;
+        e[k] = i < np && ek >= 0 && ek < r.E ? ek : -1;
+        w[k] = j < r.topk ? wv[k] : 1.0f;
+    }
+}
+
 __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     extern __shared__ int sm[];
     int* cnt = sm;                 // [E]
@@ -64,10 +96,13 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         fill[e] = 0;
     }
     __syncthreads();
-    for (int i = t; i < np; i += T) {
-        const int tok = i / r.slots, j = i - tok * r.slots;
-        const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
-        if (e >= 0 && e < r.E) atomicAdd(&cnt[e], 1);
+    for (int i0 = t; i0 < np; i0 += 8 * T) {
+        int ev[8];
+        float wv[8];
+        load_pairs<8>(r, i0, T, np, ev, wv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (ev[k] >= 0) atomicAdd(&cnt[ev[k]], 1);
     }
     __syncthreads();
     for (int e = t; e < r.E; e += T) {
@@ -84,15 +119,26 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     for (int e = t; e < r.E; e += T) {
         const int c = cnt[e];
         if (r.counts) r.counts[e] = c;
-        if (!r.items) continue;
+        if (!r.items || c == 0) continue;
         const bool big = r.use_mfma && c > r.MR;
+        // the expert's table entries, loaded once for all of its blocks / items
+        int64_t tb[9], km[6];
+#pragma unroll
+        for (int i = 0; i < 9; ++i) tb[i] = ldg(r.tables + (int64_t)i * r.E + e);
+        if (r.kmaps) {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) km[i] = ldg(r.kmaps + (int64_t)i * r.E + e);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) km[i] = 0;
+        }
         for (int q = 0, b = nbl[e]; big && q * r.MB < c; ++q, ++b) {
             ItemDesc& d = r.blocks[b];
             d.e = e;
             d.p0 = start[e] + q * r.MB;
             d.cnt = min(r.MB, c - q * r.MB);
-            for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
-            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
+            for (int i = 0; i < 9; ++i) d.tab[i] = tb[i];
+            for (int i = 0; i < 6; ++i) d.km[i] = km[i];
             if (r.cls_list) {
                 const int cl = mfma_row_class(d.cnt);
                 r.cls_list[cl * r.max_blocks + atomicAdd(&s_cls[cl], 1)] = b;
@@ -103,8 +149,8 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             d.e = e;
             d.p0 = start[e] + q * mr;
             d.cnt = min(mr, c - q * mr);
-            for (int i = 0; i < 9; ++i) d.tab[i] = r.tables[(int64_t)i * r.E + e];
-            for (int i = 0; i < 6; ++i) d.km[i] = r.kmaps ? r.kmaps[(int64_t)i * r.E + e] : 0;
+            for (int i = 0; i < 9; ++i) d.tab[i] = tb[i];
+            for (int i = 0; i < 6; ++i) d.km[i] = km[i];
         }
     }
     if (r.items)
@@ -117,9 +163,12 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     if (r.tok_nvalid) {
         for (int tok = t; tok < r.M; tok += T) {
             int nv = 0;
-            for (int j = 0; j < r.slots; ++j) {
-                const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
-                nv += (e >= 0 && e < r.E);
+            for (int j0 = 0; j0 < r.slots; j0 += 8) {
+                int ev[8];
+                float wv[8];
+                load_pairs<8>(r, tok * r.slots + j0, 1, tok * r.slots + r.slots, ev, wv);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) nv += ev[k] >= 0;
             }
             r.tok_nvalid[tok] = nv;
             if (nv == 0) {
@@ -131,23 +180,30 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         }
     }
     __syncthreads();
-    for (int i = t; i < np; i += T) {
-        const int tok = i / r.slots, j = i - tok * r.slots;
-        const int e = j < r.topk ? r.ids[tok * r.topk + j] : r.shared;
-        if (e >= 0 && e < r.E) {
-            const int f = atomicAdd(&fill[e], 1);
-            const int pos = start[e] + f;
-            const float wt = j < r.topk ? r.tw[tok * r.topk + j] : 1.0f;
-            r.pair_tok[pos] = tok;
-            r.pair_w[pos] = wt;
-            r.pair_of[i] = pos;
-            if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
-                ItemDesc& d = r.items[nch[e] + f / mr];
-                d.tok[f % mr] = tok;
-                d.w[f % mr] = wt;
+    for (int i0 = t; i0 < np; i0 += 8 * T) {
+        int ev[8];
+        float wv[8];
+        load_pairs<8>(r, i0, T, np, ev, wv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = i0 + k * T;
+            if (i >= np) break;
+            const int tok = i / r.slots, e = ev[k];
+            if (e >= 0) {
+                const int f = atomicAdd(&fill[e], 1);
+                const int pos = start[e] + f;
+                const float wt = wv[k];
+                r.pair_tok[pos] = tok;
+                r.pair_w[pos] = wt;
+                r.pair_of[i] = pos;
+                if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
+                    ItemDesc& d = r.items[nch[e] + f / mr];
+                    d.tok[f % mr] = tok;
+                    d.w[f % mr] = wt;
+                }
+            } else {
+                r.pair_of[i] = -1;
             }
-        } else {
-            r.pair_of[i] = -1;
         }
     }
 }
