@@ -233,6 +233,11 @@ static int gemv_splits(int strips, int nblk) {
     return P < 1 ? 1 : P;
 }
 
+// Dense linear on MFMA (exl3_mfma.hip), used from kLinearMfmaMinRows rows on.
+int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K,
+                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st);
+constexpr int kLinearMfmaMinRows = 9;
+
 int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
                 int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st) {
     const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
@@ -330,8 +335,10 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
     EXL3_CHECK_ARG(n / 128 <= 65535, "exl3_gemm: n too large");
     EXL3_CHECK_ARG(k / 16 * (n / 16) * 8 * (int64_t)(K > 0 ? K : 8) < (1LL << 32),
                    "exl3_gemm: trellis of %lld x %lld at K=%d exceeds 2^32 words", (long long)k, (long long)n, K);
-    return launch_gemv(A, a_ld, m, k, reinterpret_cast<const uint32_t*>(B), n, K, C, c_ld, c_dtype == EXL3_F32, suh,
-                       svh, (hipStream_t)stream);
+    const uint32_t* tr = reinterpret_cast<const uint32_t*>(B);
+    if (m >= env_int("EXL3MI_MFMA_MIN_ROWS", kLinearMfmaMinRows))
+        return launch_linear_mfma(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, svh, (hipStream_t)stream);
+    return launch_gemv(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, svh, (hipStream_t)stream);
 }
 
 }  // extern "C"

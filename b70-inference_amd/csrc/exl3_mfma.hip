@@ -738,6 +738,147 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix
     down_mix_body<RGA>(a, d, nb, cnt, stage, wlds, kts, C, rsum, s_comb);
 }
 
+// ------------------------------------------------------------------------------------------------ dense linear
+// exl3_gemm for more rows than the GEMV takes per pass: y = Hn(Hk(x * suh) @ W_hat) * svh with the trellis decoded
+// straight into MFMA B fragments once per row block (up to 64 rows), as in the reference's large-M linear
+// (glm/xpu/csrc/exl3_ops.sycl:643-757), which reconstructs 16384-column fp16 slices and runs a GEMM instead.
+//   linear_had   xh[m][k] = fp16(H128(fp16(x * suh)) / sqrt(128)) and the 128-blocks' sums xsum[m][k / 128]
+//   linear_mfma  workgroup per (row block, k-split, 256-column block); a wave owns four tile columns. With one split
+//                the epilogue writes y; otherwise it writes fp32 partials (affine applied)
+//   linear_reduce (k-split only) wave per (row, 128 columns): partials in split order, Hadamard, * svh -> y
+struct LinArgs {
+    const _Float16* xh;
+    const float* xsum;
+    const uint32_t* tr;
+    const uint16_t* svh;
+    void* out;
+    int64_t out_ld;
+    float* part;                                     // [P][m][n] when P > 1
+    int m, k, n, nblk;
+    int nrb, ncb, P, bps;                            // row blocks, 256-column blocks, k-splits, 128-blocks per split
+    int f32;
+};
+
+__global__ __launch_bounds__(256) void linear_had_kernel(const uint16_t* __restrict__ x, int64_t x_ld, int m, int k,
+                                                         const uint16_t* __restrict__ suh, _Float16* xh, float* xsum) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kb = blockIdx.y, nblk = k / 128;
+    const int r0 = blockIdx.x * 16 + wave;
+    const float s0 = h2f(ldg(suh + kb * 128 + lane)), s1 = h2f(ldg(suh + kb * 128 + lane + 64));
+    constexpr int RB = 4;
+    float xa[RB], xb[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+        const int row = r0 + 4 * j < m ? r0 + 4 * j : m - 1;     // unconditional loads (clamped, unused past m)
+        const uint16_t* xr = x + (int64_t)row * x_ld + kb * 128;
+        xa[j] = h2f(ldg(xr + lane));
+        xb[j] = h2f(ldg(xr + lane + 64));
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+        const int row = r0 + 4 * j;
+        if (row >= m) break;
+        float va = (float)(_Float16)(xa[j] * s0), vb = (float)(_Float16)(xb[j] * s1);
+        fwht128_wave(va, vb, lane);
+        const _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
+        _Float16* dst = xh + (size_t)row * k + kb * 128;
+        dst[lane] = ha;
+        dst[lane + 64] = hb;
+        const float bs = wave_sum_f32((float)ha + (float)hb);
+        if (lane == 0) xsum[(size_t)row * nblk + kb] = bs;
+    }
+}
+
+__device__ __forceinline__ void linear_store(const LinArgs& a, int row, int col, float v0, float v1) {
+    if (a.f32) {
+        float* o = reinterpret_cast<float*>(a.out) + (int64_t)row * a.out_ld + col;
+        o[0] = v0;
+        o[64] = v1;
+    } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)row * a.out_ld + col;
+        o[0] = f2h(v0);
+        o[64] = f2h(v1);
+    }
+}
+
+template <int K, int RGA>
+__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_mfma_kernel(LinArgs a) {
+    __shared__ u32x4_t stage[2 * RGA * 64];            // [2 stages][16 RGA rows x 4 units]
+    __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
+    __shared__ float C[16 * 256];
+    __shared__ float rsum[16 * RGA];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int blk, nb;
+    xcd_map(a.ncb, blk, nb);
+    if (blk >= a.nrb * a.P) return;
+    const int rb = blk / a.P, p = blk - rb * a.P;
+    const int r0 = rb * 16 * RGA;
+    const int cnt = a.m - r0 < 16 * RGA ? a.m - r0 : 16 * RGA;
+    const int kb0 = p * a.bps, nkb = a.nblk - kb0 < a.bps ? a.nblk - kb0 : a.bps;
+    const int tn = a.n / 16;
+    const int nhalf = 2 * nb + 1 < a.n / 128 ? 2 : 1;
+    // output scales of the two 128-column halves (unconditional loads, unused past nhalf)
+    const uint16_t* sv = a.svh + nb * 256;
+    float sd[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int hh = h < nhalf ? h : 0;
+        sd[h][0] = h2f(ldg(sv + 128 * hh + lane)) * kRsqrt128;
+        sd[h][1] = h2f(ldg(sv + 128 * hh + lane + 64)) * kRsqrt128;
+    }
+    if (threadIdx.x < 16 * RGA) {                      // the rows' sums over this split's 128-blocks
+        const int r = threadIdx.x;
+        rsum[r] = sum_ordered(a.xsum + (size_t)(r0 + (r < cnt ? r : cnt - 1)) * a.nblk + kb0, nkb);
+    }
+    __syncthreads();
+    MfmaPipe<K, 1, RGA> L;
+    L.nsteps = nkb * 4;
+    L.lds = stage;
+    L.lane = lane;
+    const uint32_t* trk = a.tr + (size_t)kb0 * 8 * tn * (8 * K);
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) {
+        int ct = nb * 16 + 4 * wave + 2 * pair;
+        ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
+        return trk + (size_t)ct * (8 * K);
+    });
+    L.setup_a(cnt, [&](int, int row) { return a.xh + (size_t)(r0 + row) * a.k + kb0 * 128; });
+    f4_t acc[kMfT][RGA];
+#pragma unroll
+    for (int t = 0; t < kMfT; ++t)
+#pragma unroll
+        for (int rg = 0; rg < RGA; ++rg) acc[t][rg] = f4_t{0.f, 0.f, 0.f, 0.f};
+    L.run(acc);
+    const bool single = a.P == 1;
+    float* part = a.part + (size_t)p * a.m * a.n;
+#pragma unroll
+    for (int rg = 0; rg < RGA; ++rg) {
+#pragma unroll
+        for (int t = 0; t < kMfT; ++t) {
+            const int col = (4 * wave + t) * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) C[(4 * (lane >> 4) + i) * 256 + col] = acc[t][rg][i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {                 // (row, half) pairs of this wave
+            const int ml = 4 * wave + (j >> 1), h = j & 1, m = 16 * rg + ml;
+            if (m >= cnt || h >= nhalf) continue;
+            const float sx = kMul1C2 * rsum[m];
+            float v0 = kMul1C1 * C[ml * 256 + 128 * h + lane] + sx, v1 = kMul1C1 * C[ml * 256 + 128 * h + lane + 64] + sx;
+            const int col = nb * 256 + 128 * h + lane;
+            if (single) {
+                fwht128_wave(v0, v1, lane);
+                linear_store(a, r0 + m, col, v0 * sd[h][0], v1 * sd[h][1]);
+            } else {
+                float* dst = part + (size_t)(r0 + m) * a.n + col;
+                dst[0] = v0;
+                dst[64] = v1;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ host
 typedef void (*mfma_fn)(MoeArgs);
 
@@ -820,6 +961,106 @@ int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st) {
         EXL3_LAUNCH(nm, fn, grid, dim3(256), 0, s, a);
         return EXL3_OK;
     });
+}
+
+// Split-K finish: wave per (row, 128-column block): the split partials summed in split order (eight splits' loads in
+// flight at a time), Hadamard, * svh / sqrt(128).
+__global__ __launch_bounds__(256) void linear_reduce_kernel(LinArgs a) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= a.m) return;
+    const int col = blockIdx.y * 128 + lane;
+    const float s0 = h2f(ldg(a.svh + col)) * kRsqrt128, s1 = h2f(ldg(a.svh + col + 64)) * kRsqrt128;
+    const float* q = a.part + (size_t)row * a.n + col;
+    const size_t ps = (size_t)a.m * a.n;
+    float v0 = 0.f, v1 = 0.f;
+    for (int p0 = 0; p0 < a.P; p0 += 8) {
+        float t0[8], t1[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int pp = p0 + i < a.P ? p0 + i : a.P - 1;
+            t0[i] = ldg(q + pp * ps);
+            t1[i] = ldg(q + pp * ps + 64);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (p0 + i < a.P) {
+                v0 += t0[i];
+                v1 += t1[i];
+            }
+    }
+    fwht128_wave(v0, v1, lane);
+    linear_store(a, row, col, v0 * s0, v1 * s1);
+}
+
+typedef void (*lin_fn)(LinArgs);
+
+template <int RGA>
+static lin_fn pick_lin(int K) {
+    switch (K) {
+        case 1: return linear_mfma_kernel<1, RGA>;
+        case 2: return linear_mfma_kernel<2, RGA>;
+        case 3: return linear_mfma_kernel<3, RGA>;
+        case 4: return linear_mfma_kernel<4, RGA>;
+        case 5: return linear_mfma_kernel<5, RGA>;
+        case 6: return linear_mfma_kernel<6, RGA>;
+        case 7: return linear_mfma_kernel<7, RGA>;
+        default: return linear_mfma_kernel<8, RGA>;
+    }
+}
+
+// Dense linear on MFMA (m > the GEMV's rows per pass). Row blocks of 16, 32 or 64 rows (by m); k-splits so that the
+// grid covers about the workgroups the device holds at once, each split at least two 128-blocks of k.
+int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K,
+                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st) {
+    const int RGA = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+    const int R = 16 * RGA;
+    const int nblk = (int)(k / 128);
+    if (m > 0x7FFFFFFF / 64 || k > 0x7FFFFFFF || n > 0x7FFFFFFF)
+        return fail(EXL3_ERR_INVALID, "exl3_gemm: shape too large");
+    LinArgs a;
+    a.m = (int)m;
+    a.k = (int)k;
+    a.n = (int)n;
+    a.nblk = nblk;
+    a.nrb = (int)((m + R - 1) / R);
+    a.ncb = (int)((n + 255) / 256);
+    lin_fn fn = RGA == 4 ? pick_lin<4>(K) : RGA == 2 ? pick_lin<2>(K) : pick_lin<1>(K);
+    int resident = 0;
+    int rc = resident_blocks((const void*)fn, 256, &resident);
+    if (rc) return rc;
+    const int target = env_int("EXL3MI_LINEAR_JOBS", resident);
+    const int64_t tiles = (int64_t)a.nrb * a.ncb;
+    int P = (int)((target + tiles - 1) / tiles);
+    const int pmax = nblk / 2 > 1 ? nblk / 2 : 1;
+    P = P < 1 ? 1 : (P > pmax ? pmax : P);
+    a.bps = (nblk + P - 1) / P;
+    a.P = (nblk + a.bps - 1) / a.bps;
+    const size_t xh_b = carve_size((size_t)m * k, 2), xs_b = carve_size((size_t)m * nblk, 4);
+    const size_t part_b = a.P > 1 ? carve_size((size_t)a.P * m * n, 4) : 0;
+    Workspace ws;
+    rc = workspace(xh_b + xs_b + part_b, 0, &ws);
+    if (rc) return rc;
+    Carve cv{ws.scratch, ws.scratch_bytes};
+    _Float16* xh = cv.take<_Float16>((size_t)m * k);
+    float* xsum = cv.take<float>((size_t)m * nblk);
+    a.part = a.P > 1 ? cv.take<float>((size_t)a.P * m * n) : nullptr;
+    a.xh = xh;
+    a.xsum = xsum;
+    a.tr = tr;
+    a.svh = svh;
+    a.out = C;
+    a.out_ld = c_ld;
+    a.f32 = f32 ? 1 : 0;
+    EXL3_LAUNCH("linear_had", linear_had_kernel, dim3((unsigned)((m + 15) / 16), (unsigned)nblk), dim3(256), 0, st, A,
+                a_ld, (int)m, (int)k, suh, xh, xsum);
+    const int64_t nx = ((int64_t)a.nrb * a.P + 7) / 8 * 8 * a.ncb;
+    if (nx > 0x7FFFFFFF) return fail(EXL3_ERR_INVALID, "exl3_gemm: grid too large");
+    EXL3_LAUNCH("linear_mfma", fn, dim3((unsigned)nx), dim3(256), 0, st, a);
+    if (a.P > 1)
+        EXL3_LAUNCH("linear_reduce", linear_reduce_kernel, dim3((unsigned)((m + 3) / 4), (unsigned)(n / 128)),
+                    dim3(256), 0, st, a);
+    return EXL3_OK;
 }
 
 }  // namespace exl3

@@ -65,7 +65,9 @@ int exl3_had_r_128(const void* in, int64_t in_ld, void* out, int64_t out_ld, int
 
 /* EXL3 linear: C[m, n] = Hn( Hk(A * suh) @ W_hat ) * svh for A fp16 [m, k] (row stride a_ld), C fp16 or fp32
  * [m, n] (row stride c_ld). A_had (fp16 scratch, >= m*k elements) is accepted for signature compatibility and not
- * used: the input transform is fused. cb must be 2 (mul1).
+ * used: the input transform is fused. cb must be 2 (mul1). Up to 8 rows: decode GEMV; 9 rows and more: the trellis
+ * decoded into fp16 MFMA fragments once per row block of up to 64 rows (the reference's large-M linear,
+ * exl3_ops.sycl:742-756, reconstructs fp16 slices and calls a GEMM instead; same results within the tolerance).
  * Replaces: exllamav3 ext exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1, force_num_sms)
  *           (ext-op-inventory.md:498-557) and exl3xpu_C::exl3_gemm_small / linear (glm/xpu/csrc/exl3_ops.sycl:258-321,
  *           643-757). */

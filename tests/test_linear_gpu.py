@@ -122,3 +122,60 @@ def test_gemm_deterministic_and_bias(exl3):
     y4 = torch.empty(1, 3, 1024, dtype=torch.float16, device="cuda")
     lin.run(x.view(1, 3, 2048), y4)
     assert torch.allclose(y4.view(3, 1024).float(), y1, rtol=2e-3, atol=2e-3)
+
+
+# Rows >= 9 run on the MFMA path (row blocks of 16 / 32 / 64, k-split with partials summed by the last workgroup).
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("M", [9, 24, 40, 64])
+def test_gemm_mfma_rows_all_bitrates(exl3, oracle, K, M):
+    y, ref = _linear_case(exl3, oracle, 512, 384, K, M, torch.float32, 4000 + 10 * K + M)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("jobs", [1, 64, 4096])
+@pytest.mark.parametrize("M,out_dtype", [(16, torch.float16), (100, torch.float32), (130, torch.float16)])
+def test_gemm_mfma_splits(exl3, oracle, monkeypatch, jobs, M, out_dtype):
+    """Forced grid targets: one k-split (epilogue straight from the accumulators), and several (fp32 partials)."""
+    monkeypatch.setenv("EXL3MI_LINEAR_JOBS", str(jobs))
+    y, ref = _linear_case(exl3, oracle, 2048, 640, 3, M, out_dtype, 4500 + M + jobs)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("M", [64, 300])
+def test_gemm_mfma_c1_full_size(exl3, oracle, M):
+    """4096 -> 4096, K=4 with a prefill-sized batch."""
+    y, ref = _linear_case(exl3, oracle, 4096, 4096, 4, M, torch.float16, 1000 + M)
+    assert max_rel(y, ref) <= MAX_REL
+
+
+def test_gemm_mfma_strided_rows_and_determinism(exl3, oracle):
+    """Through the C ABI: row strides wider than k / n on input and output (the columns past n untouched); repeated
+    calls bit-identical; a 20-row call agrees with the same rows of the 70-row call."""
+    from importlib import import_module
+    L_ = import_module("b70-inference_amd._lib")
+    S = synth()
+    k, n, M, K = 1024, 512, 70, 2
+    tr, suh, svh = S.linear(k, n, K, 4700)
+    x = S.activations(M, k, 4701)
+    xb = torch.zeros(M, k + 256, dtype=torch.float16)
+    xb[:, :k] = x
+    xb = xb.cuda()
+    yb = torch.full((M, n + 128), 7.0, dtype=torch.float32, device="cuda")
+    trc, suhc, svhc = tr.cuda(), suh.cuda(), svh.cuda()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(rows, y):
+        L_.check(L_.lib().exl3_gemm(L_.ptr(xb), k + 256, rows, k, L_.ptr(trc), n, K, L_.ptr(y), y.stride(0), 1,
+                                    L_.ptr(suhc), None, L_.ptr(svhc), 2, st), "exl3_gemm")
+
+    run(M, yb)
+    y1 = yb[:, :n].clone()
+    run(M, yb)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, yb[:, :n])
+    assert (yb[:, n:] == 7.0).all()
+    ref = oracle.exl3_linear(x.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), K, np.float32)
+    assert max_rel(y1.cpu().numpy(), ref) <= MAX_REL
+    y20 = torch.empty(20, n, dtype=torch.float32, device="cuda")
+    run(20, y20)
+    assert max_rel(y20.cpu().numpy(), ref[:20]) <= MAX_REL
