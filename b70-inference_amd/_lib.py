@@ -36,6 +36,8 @@ SIGNATURES = {
                                 _i32, _i32, _f32, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "exl3_moe_align": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp],
     "exl3_route_softmax_topk": [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp],
+    "exl3_route_topk": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _f32, _vp, _vp, _vp],
+    "exl3_router_logits": [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp],
 }
 _RESTYPE = {"exl3_last_error": ctypes.c_char_p}
 

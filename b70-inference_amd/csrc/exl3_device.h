@@ -32,6 +32,7 @@ __device__ __forceinline__ T ldg(const T* p) {
     return *(const __attribute__((address_space(1))) T*)p;
 }
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 
 template <typename T>
 __device__ __forceinline__ T ldg_nt(const T* p) {

@@ -14,7 +14,6 @@
 
 namespace exl3 {
 
-typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 // Window of normalised position u' (bits [u'K, u'K + 16) of R), low 16 bits valid.

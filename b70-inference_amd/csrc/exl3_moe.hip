@@ -536,18 +536,151 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
 
 // ================================================================================================ router
 // One wave per row (route_row).
-template <int V>
+template <int V, int SC>
 __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ logits, int64_t ld, int E,
-                                                   const float* __restrict__ bias, int k, int32_t* __restrict__ ids,
-                                                   float* __restrict__ w) {
+                                                   const float* __restrict__ bias, int k, int flags, float scaling,
+                                                   int32_t* __restrict__ ids, float* __restrict__ w) {
     const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
     int id;
     float wt;
-    route_row<V>(logits + row * ld, bias, E, k, lane, id, wt);
+    route_row<V, SC>(logits + row * ld, bias, E, k, lane, !(flags & EXL3_ROUTE_BIAS_SELECT_ONLY),
+                     (flags & EXL3_ROUTE_RENORM) != 0, scaling, id, wt);
     if (lane < k) {
         ids[row * k + lane] = id;
         w[row * k + lane] = wt;
+    }
+}
+
+typedef void (*route_fn)(const float*, int64_t, int, const float*, int, int, float, int32_t*, float*);
+
+template <int SC>
+static route_fn route_pick(int64_t E) {
+    return E <= 64 ? route_kernel<1, SC> : E <= 128 ? route_kernel<2, SC> : E <= 256 ? route_kernel<4, SC>
+         : E <= 512 ? route_kernel<8, SC> : E <= 1024 ? route_kernel<16, SC> : E <= 2048 ? route_kernel<32, SC>
+         : E <= 4096 ? route_kernel<64, SC> : route_kernel<128, SC>;
+}
+
+// Router logits, W [H][E] (the reference's gate_tensor): workgroup of 16 waves per (64 expert columns, MR rows).
+// Lane 8 r + c of wave q reads W rows h = h0 + 8 i + r (h0: the wave's 1/16 of H, 128 rows per batch) at columns
+// 8c .. 8c + 7 with one 16-byte load each, the batch's x values staged in LDS; products accumulate in fp32 per lane,
+// then over r (lane shuffles) and over the 16 waves (LDS, in wave order).
+constexpr int kRtWaves = 16;
+template <int MR>
+__global__ __launch_bounds__(1024) void router_cols_kernel(const uint16_t* __restrict__ x, int64_t x_ld, int M, int H,
+                                                           const uint16_t* __restrict__ W, int64_t w_ld, int E,
+                                                           int round16, float* __restrict__ out, int64_t out_ld) {
+    __shared__ _Float16 xs[kRtWaves][MR][128];
+    __shared__ float red[kRtWaves][MR][64];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane >> 3, c = lane & 7;
+    const int e0 = blockIdx.x * 64, m0 = blockIdx.y * MR;
+    const int ce = e0 + 8 * c < E ? e0 + 8 * c : E - 8;          // in-bounds chunk (results past E unused)
+    const int hw = H / kRtWaves, h0 = wave * hw;                 // hw: a multiple of 8
+    float acc[MR][8];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[m][j] = 0.f;
+    for (int hb = 0; hb < hw; hb += 128) {
+        // stage x[m0 + m][h0 + hb + (0 .. 127)] (zeros past the wave's rows or past M)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int row = m0 + m < M ? m0 + m : M - 1;
+            const int hh = hb + 2 * lane;
+            const uint32_t v = ldg(reinterpret_cast<const uint32_t*>(x + (int64_t)row * x_ld + h0 + (hh < hw ? hh : 0)));
+            const bool ok = m0 + m < M && hh < hw;
+            *reinterpret_cast<uint32_t*>(&xs[wave][m][2 * lane]) = ok ? v : 0u;
+        }
+        __syncthreads();
+        u32x4_t wv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int hh = hb + 8 * i + r;
+            wv[i] = ldg(reinterpret_cast<const u32x4_t*>(W + (int64_t)(h0 + (hh < hw ? hh : hw - 1)) * w_ld + ce));
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const h8_t wh = __builtin_bit_cast(h8_t, wv[i]);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const float xv = (float)xs[wave][m][8 * i + r];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(xv, (float)wh[j], acc[m][j]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float v = acc[m][j];
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[m][j] = v;
+        }
+    if (r == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) red[wave][m][8 * c + j] = acc[m][j];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < MR * 64) {
+        const int m = t >> 6, col = t & 63;
+        float v = 0.f;
+#pragma unroll
+        for (int q = 0; q < kRtWaves; ++q) v += red[q][m][col];
+        if (m0 + m < M && e0 + col < E) out[(int64_t)(m0 + m) * out_ld + e0 + col] = round16 ? (float)(_Float16)v : v;
+    }
+}
+
+// Router logits, W [E][H] (a linear layer's weight): wave per expert, lanes along H with 16-byte loads of W and of
+// the MR x rows, fp32 products, one wave sum per row.
+template <int MR>
+__global__ __launch_bounds__(256) void router_rows_kernel(const uint16_t* __restrict__ x, int64_t x_ld, int M, int H,
+                                                          const uint16_t* __restrict__ W, int64_t w_ld, int E,
+                                                          int round16, float* __restrict__ out, int64_t out_ld) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = blockIdx.x * 4 + wave, m0 = blockIdx.y * MR;
+    if (e >= E) return;
+    const uint16_t* wr = W + (int64_t)e * w_ld;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    for (int h0 = 8 * lane; h0 < H; h0 += 4 * 512) {
+        u32x4_t wv[4], xv[4][MR];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int h = h0 + 512 * i < H ? h0 + 512 * i : h0;      // unconditional (repeats h0, unused)
+            wv[i] = ldg(reinterpret_cast<const u32x4_t*>(wr + h));
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const int row = m0 + m < M ? m0 + m : M - 1;
+                xv[i][m] = ldg(reinterpret_cast<const u32x4_t*>(x + (int64_t)row * x_ld + h));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (h0 + 512 * i >= H) break;
+            const h8_t wh = __builtin_bit_cast(h8_t, wv[i]);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const h8_t xh = __builtin_bit_cast(h8_t, xv[i][m]);
+                float t = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) t = fmaf((float)xh[j], (float)wh[j], t);
+                acc[m] += t;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const float v = wave_sum_f32(acc[m]);
+        if (lane == 0 && m0 + m < M) out[(int64_t)(m0 + m) * out_ld + e] = round16 ? (float)(_Float16)v : v;
     }
 }
 
@@ -885,18 +1018,61 @@ int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype
     return EXL3_OK;
 }
 
+int exl3_route_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k, int score,
+                    int flags, float scaling, int32_t* ids, float* w, void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && E > 0 && E <= 8192 && k > 0 && k <= 32 && k <= E && ld >= E,
+                   "exl3_route_topk: bad sizes (M %lld, E %lld, k %lld, ld %lld)", (long long)M, (long long)E,
+                   (long long)k, (long long)ld);
+    if (score != EXL3_SCORE_SOFTMAX && score != EXL3_SCORE_SIGMOID && score != EXL3_SCORE_SQRT_SOFTPLUS)
+        return fail(EXL3_ERR_UNSUPPORTED, "exl3_route_topk: scoring %d not supported", score);
+    EXL3_CHECK_ARG((flags & ~(EXL3_ROUTE_RENORM | EXL3_ROUTE_BIAS_SELECT_ONLY)) == 0, "exl3_route_topk: bad flags %d",
+                   flags);
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(logits && ids && w, "exl3_route_topk: null pointer");
+    EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_topk: too many rows");
+    route_fn kern = score == EXL3_SCORE_SOFTMAX ? route_pick<EXL3_SCORE_SOFTMAX>(E)
+                  : score == EXL3_SCORE_SIGMOID ? route_pick<EXL3_SCORE_SIGMOID>(E)
+                  : route_pick<EXL3_SCORE_SQRT_SOFTPLUS>(E);
+    EXL3_LAUNCH("route_topk", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
+                (int)k, flags, scaling, ids, w);
+    return EXL3_OK;
+}
+
 int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
                             int32_t* ids, float* w, void* stream) {
-    EXL3_CHECK_ARG(M >= 0 && E > 0 && E <= 8192 && k > 0 && k <= 32 && k <= E && ld >= E,
-                   "exl3_route_softmax_topk: bad sizes");
+    return exl3_route_topk(logits, ld, M, E, bias, k, EXL3_SCORE_SOFTMAX, EXL3_ROUTE_RENORM, 1.0f, ids, w, stream);
+}
+
+int exl3_router_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, const uint16_t* W, int64_t w_ld,
+                       int64_t E, int w_layout, int round_fp16, float* logits, int64_t logits_ld, void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && H > 0 && H % 128 == 0 && E > 0 && E <= 65536 && x_ld >= H && logits_ld >= E,
+                   "exl3_router_logits: bad sizes (M %lld, H %lld, E %lld)", (long long)M, (long long)H, (long long)E);
+    EXL3_CHECK_ARG(w_layout == EXL3_ROUTER_W_HE || w_layout == EXL3_ROUTER_W_EH, "exl3_router_logits: bad w_layout %d",
+                   w_layout);
     if (M == 0) return EXL3_OK;
-    EXL3_CHECK_ARG(logits && ids && w, "exl3_route_softmax_topk: null pointer");
-    EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_softmax_topk: too many rows");
-    void (*kern)(const float*, int64_t, int, const float*, int, int32_t*, float*) =
-        E <= 64 ? route_kernel<1> : E <= 128 ? route_kernel<2> : E <= 256 ? route_kernel<4> : E <= 512 ? route_kernel<8>
-        : E <= 1024 ? route_kernel<16> : E <= 2048 ? route_kernel<32> : E <= 4096 ? route_kernel<64> : route_kernel<128>;
-    EXL3_LAUNCH("route_softmax_topk", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E,
-                bias, (int)k, ids, w);
+    EXL3_CHECK_ARG(x && W && logits, "exl3_router_logits: null pointer");
+    EXL3_CHECK_ARG(M <= 4 * 65535 && H <= 0x7FFFFFFF, "exl3_router_logits: shape too large");
+    EXL3_CHECK_ARG(aligned(W, 16) && w_ld % 8 == 0, "exl3_router_logits: W must be 16-byte aligned, row stride a multiple of 8");
+    hipStream_t st = (hipStream_t)stream;
+    const int MR = M >= 8 ? 8 : M >= 4 ? 4 : M >= 2 ? 2 : 1;       // rows per workgroup ([H, E]: at most 4)
+    typedef void (*rfn)(const uint16_t*, int64_t, int, int, const uint16_t*, int64_t, int, int, float*, int64_t);
+    if (w_layout == EXL3_ROUTER_W_HE) {
+        EXL3_CHECK_ARG(E % 8 == 0 && w_ld >= E && aligned(x, 4) && x_ld % 2 == 0,
+                       "exl3_router_logits: [H, E] weights need E a multiple of 8, w_ld >= E and a 4-byte aligned x");
+        const int mr = MR > 4 ? 4 : MR;
+        rfn fn = mr == 4 ? router_cols_kernel<4> : mr == 2 ? router_cols_kernel<2> : router_cols_kernel<1>;
+        const unsigned gy = (unsigned)((M + mr - 1) / mr);
+        EXL3_LAUNCH("router_logits", fn, dim3((unsigned)((E + 63) / 64), gy), dim3(1024), 0, st, x, x_ld, (int)M,
+                    (int)H, W, w_ld, (int)E, round_fp16 ? 1 : 0, logits, logits_ld);
+    } else {
+        EXL3_CHECK_ARG(w_ld >= H && aligned(x, 16) && x_ld % 8 == 0,
+                       "exl3_router_logits: [E, H] weights need w_ld >= H and a 16-byte aligned x (row stride a multiple of 8)");
+        rfn fn = MR == 8 ? router_rows_kernel<8> : MR == 4 ? router_rows_kernel<4> : MR == 2 ? router_rows_kernel<2>
+                                                                                          : router_rows_kernel<1>;
+        const unsigned gy = (unsigned)((M + MR - 1) / MR);
+        EXL3_LAUNCH("router_logits", fn, dim3((unsigned)((E + 3) / 4), gy), dim3(256), 0, st, x, x_ld, (int)M, (int)H,
+                    W, w_ld, (int)E, round_fp16 ? 1 : 0, logits, logits_ld);
+    }
     return EXL3_OK;
 }
 

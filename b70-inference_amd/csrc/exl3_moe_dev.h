@@ -59,58 +59,84 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
     if (lane == 0) a.cnt_tok[(size_t)t * (a.H / 128) + nb] = 0;
 }
 
-// Softmax + top-k of one row by one wave (trellis-serve.patch:395-441): z = logits + bias in fp32; experts ranked by
-// z descending, exact ties to the lower index; p = exp(z - max) / sum exp(z - max) over the row; the k picks are
-// renormalised w = p / (sum of picked p + 1e-20). Lane l keeps the order keys of entries l + 64 v (v < V, E <= 64 V)
-// in registers; picked and padding entries hold key 0, NaN logits key 1 (below every number, still pickable, as a
-// stable descending sort places them last). Each round is one DPP wave max, a ballot of the lanes holding it, and a
-// DPP wave min of their lowest indices only when several lanes tie. Lane j < k returns pick j in (id, w).
-template <int V>
+// Top-k routing of one row by one wave. Scoring SC (EXL3_SCORE_*), per entry with logit f and bias b (0 without one):
+//   softmax (trellis-serve.patch:395-441): rank by f + b; weight source g = f + b (bias_both) or f (selection-only
+//            bias, the reference's `cold` term); p = exp(g - max g) / sum exp(g - max g) over the row
+//   sigmoid (routing_ds3_nogroup, glm/xpu/glm_xpu/ops.py:177-193): s = sigmoid(f); rank by s + b, or by f without a
+//            bias; weight source s
+//   sqrt-softplus (dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193): s = sqrt(softplus(f)) (f itself above 20); rank by s + b;
+//            weight source s
+// Exact ties rank to the lower index. The k picks' weights are w = v * scaling / (sum of picked v + 1e-20) with
+// renorm, v * scaling without (v = p or s). Lane l keeps the order keys of entries l + 64 v (v < V, E <= 64 V) in
+// registers; picked and padding entries hold key 0, NaN keys 1 (below every number, still pickable, as a stable
+// descending sort places them last). Each round is one DPP wave max, a ballot of the lanes holding it, and a DPP wave
+// min of their lowest indices only when several lanes tie. Lane j < k returns pick j in (id, w).
+template <int V, int SC>
 __device__ __forceinline__ void route_row(const float* __restrict__ z, const float* __restrict__ bias, int E, int k,
-                                          int lane, int& id, float& w) {
+                                          int lane, bool bias_both, bool renorm, float scaling, int& id, float& w) {
     // every load issued before any is used (clamped indices, no per-element branch): one memory round trip
-    float f[V];
+    float f[V], b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const int i = lane + 64 * v;
         f[v] = ldg(z + (i < E ? i : E - 1));
     }
     if (bias) {
-        float b[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int i = lane + 64 * v;
             b[v] = ldg(bias + (i < E ? i : E - 1));
         }
-#pragma unroll
-        for (int v = 0; v < V; ++v) f[v] += b[v];
     }
+    float g[V];                          // weight source per entry
     uint32_t key[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
+        float r;
+        if (SC == EXL3_SCORE_SOFTMAX) {
+            r = bias ? f[v] + b[v] : f[v];
+            g[v] = bias_both ? r : f[v];
+        } else {
+            float s;
+            if (SC == EXL3_SCORE_SIGMOID) {
+                s = 1.f / (1.f + expf(-f[v]));
+            } else {
+                s = sqrtf(f[v] > 20.f ? f[v] : log1pf(expf(f[v])));
+            }
+            g[v] = s;
+            r = bias ? s + b[v] : (SC == EXL3_SCORE_SIGMOID ? f[v] : s);
+        }
         const int i = lane + 64 * v;
-        key[v] = i < E ? (f[v] != f[v] ? 1u : float_key(f[v])) : 0u;
+        key[v] = i < E ? (r != r ? 1u : float_key(r)) : 0u;
     }
-    uint32_t lmax = 0u;
+    float mx = 0.f, sum = 1.f;
+    if (SC == EXL3_SCORE_SOFTMAX) {
+        uint32_t lmax = 0u;
 #pragma unroll
-    for (int v = 0; v < V; ++v) lmax = max(lmax, key[v]);
-    const float mx = key_float(wave_max_u32(lmax));
-    float se = 0.f;
+        for (int v = 0; v < V; ++v) {
+            const int i = lane + 64 * v;
+            lmax = max(lmax, i < E ? (g[v] != g[v] ? 1u : float_key(g[v])) : 0u);
+        }
+        mx = key_float(wave_max_u32(lmax));
+        float se = 0.f;
 #pragma unroll
-    for (int v = 0; v < V; ++v)
-        if (key[v] != 0u) se += expf(key_float(key[v]) - mx);
-    const float sum = wave_sum_f32(se);
+        for (int v = 0; v < V; ++v)
+            if (lane + 64 * v < E) se += expf(g[v] - mx);
+        sum = wave_sum_f32(se);
+    }
 
-    uint32_t tkey = 0u;
+    float gv = 0.f;
     id = -1;
     for (int j = 0; j < k; ++j) {
         uint32_t best = 0u;
         int bv = 0;
+        float gb = 0.f;
 #pragma unroll
         for (int v = 0; v < V; ++v)
             if (key[v] > best) {          // ascending v: a lane keeps its lowest index among equal keys
                 best = key[v];
                 bv = v;
+                gb = g[v];
             }
         const uint32_t kmax = wave_max_u32(best);
         if (kmax == 0u) break;            // fewer than k entries (k <= E is checked on the host)
@@ -119,6 +145,8 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
         int widx;
         if (__popcll(mask) == 1) widx = __builtin_amdgcn_readlane(mine, __ffsll((unsigned long long)mask) - 1);
         else widx = (int)wave_min_u32(best == kmax ? (uint32_t)mine : 0xFFFFFFFFu);
+        // the winner's lane holds it as its own best (bv = widx >> 6): its weight source comes from there
+        const float gw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gb), widx & 63));
         if (lane == (widx & 63)) {
             const int vv = widx >> 6;
 #pragma unroll
@@ -127,12 +155,12 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
         }
         if (lane == j) {
             id = widx;
-            tkey = kmax;
+            gv = gw;
         }
     }
-    const float p = id >= 0 ? expf(key_float(tkey) - mx) / sum : 0.f;
+    const float p = id >= 0 ? (SC == EXL3_SCORE_SOFTMAX ? expf(gv - mx) / sum : gv) : 0.f;
     const float s = wave_sum_f32(p);
-    w = p / (s + 1e-20f);
+    w = renorm ? p * scaling / (s + 1e-20f) : p * scaling;
 }
 
 }  // namespace exl3

@@ -8,6 +8,9 @@ Interfaces mirror the reference boundary:
     glm/xpu/glm_xpu/moe_patch.py:68-94 and dsv41/xpu/dsv_xpu/moe.py:1563-1630
   * BC_GatedMLP(...).run_bszN(x, d) (glm/xpu/glm_xpu/ops.py:157-172), silu_mul / gelu_mul (ext-op-inventory.md:944-956)
   * route_softmax_topk: the fused softmax/top-k router of trellis-serve (trellis-serve.patch:395-441)
+  * route_topk / router_logits / routing_ds3_nogroup: scored top-k routing (softmax, sigmoid + bias, sqrt-softplus)
+    and the router GEMV from hidden states (glm/xpu/glm_xpu/ops.py:177-193; dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193,
+    442-470)
 """
 from __future__ import annotations
 
@@ -225,6 +228,85 @@ def route_softmax_topk(logits: torch.Tensor, k: int, bias: torch.Tensor | None =
     return ids, w
 
 
+SCORES = {"softmax": 0, "sigmoid": 1, "sqrt_softplus": 2}
+ROUTE_RENORM, ROUTE_BIAS_SELECT_ONLY = 1, 2
+ROUTER_W = {"he": 0, "eh": 1}
+
+
+def route_topk(logits: torch.Tensor, k: int, bias: torch.Tensor | None = None, score: str = "softmax",
+               renorm: bool = True, scaling: float = 1.0, bias_select_only: bool = False):
+    """Top-k routing with a scoring function (exl3_route_topk): softmax (bias ranks, and feeds the weights unless
+    bias_select_only), sigmoid (rank by sigmoid + bias, or by the logit without a bias) or sqrt_softplus (rank by
+    sqrt(softplus) + bias); weights v * scaling / (sum of picked v + 1e-20) with renorm. Returns (ids int32 [M, k],
+    w fp32 [M, k]), picks in descending rank, ties to the lower index."""
+    require_device(logits, bias)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise Exl3Error("route_topk: logits must be fp32 [M, E] with contiguous rows")
+    if score not in SCORES:
+        raise NotImplementedError(f"route_topk: scoring {score!r}")
+    M, E = logits.shape
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != E or not bias.is_contiguous()):
+        raise Exl3Error("route_topk: bias must be fp32 [E]")
+    ids = torch.empty(M, k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=logits.device)
+    flags = (ROUTE_RENORM if renorm else 0) | (ROUTE_BIAS_SELECT_ONLY if bias_select_only else 0)
+    check(lib().exl3_route_topk(ptr(logits), logits.stride(0), M, E, ptr(bias), k, SCORES[score], flags,
+                                float(scaling), ptr(ids), ptr(w), stream_of(logits)), "route_topk")
+    return ids, w
+
+
+def router_logits(x: torch.Tensor, weight: torch.Tensor, E: int | None = None, layout: str = "he",
+                  round_fp16: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Router logits fp32 [M, E] = x @ W on the router GEMV (exl3_router_logits). layout "he": weight fp16 [H, >= E]
+    (the reference's gate_tensor, columns :E used); "eh": weight fp16 [>= E, H] (a linear layer's weight, rows :E).
+    round_fp16 rounds each logit to fp16 precision, as a matmul of two fp16 tensors returns it."""
+    require_device(x, weight, out)
+    if layout not in ROUTER_W:
+        raise Exl3Error(f"router_logits: layout {layout!r}")
+    if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1:
+        raise Exl3Error("router_logits: x must be fp16 [M, H] with contiguous rows")
+    if weight.dim() != 2 or weight.dtype != torch.float16 or weight.stride(1) != 1:
+        raise Exl3Error("router_logits: weight must be fp16 2-D with contiguous rows")
+    M, H = x.shape
+    if layout == "he":
+        if weight.shape[0] != H:
+            raise Exl3Error(f"router_logits: weight must be [{H}, E]")
+        E = weight.shape[1] if E is None else E
+    else:
+        if weight.shape[1] != H:
+            raise Exl3Error(f"router_logits: weight must be [E, {H}]")
+        E = weight.shape[0] if E is None else E
+    if out is None:
+        out = torch.empty(M, E, dtype=torch.float32, device=x.device)
+    if out.dtype != torch.float32 or out.stride(1) != 1 or tuple(out.shape) != (M, E):
+        raise Exl3Error("router_logits: out must be fp32 [M, E] with contiguous rows")
+    check(lib().exl3_router_logits(ptr(x), x.stride(0), M, H, ptr(weight), weight.stride(0), E, ROUTER_W[layout],
+                                   1 if round_fp16 else 0, ptr(out), out.stride(0), stream_of(x)), "router_logits")
+    return out
+
+
+def routing_ds3_nogroup(hidden, gate, scores, bias, topk_indices, topk_weights, scaling_factor, gate_t, act_fn,
+                        gate_i8, gate_sb):
+    """Sigmoid / noaux_tc top-k routing without groups, in place, as glm/xpu/glm_xpu/ops.py:177-193: logits =
+    hidden @ gate[:, :E] rounded to fp16 -> scores; selection by sigmoid + bias (by the logits without a bias); weights
+    from the unbiased sigmoid, normalised over the picks (+1e-20) and scaled. gate_t, gate_i8 and gate_sb feed only the
+    reference's CUDA deterministic GEMM and are ignored. Inputs other than fp16 are converted to fp16 (the reference
+    multiplies them in fp32, then rounds the logits to fp16)."""
+    if act_fn != 0:
+        raise NotImplementedError("routing_ds3_nogroup: sigmoid routing only (act_fn 0)")
+    E = scores.shape[-1]
+    k = topk_indices.shape[-1]
+    h = hidden.reshape(-1, hidden.shape[-1])
+    h = (h if h.dtype == torch.float16 else h.half()).contiguous()
+    g = gate if gate.dtype == torch.float16 and gate.stride(-1) == 1 else gate.half().contiguous()
+    logits = router_logits(h, g, E=E, layout="he", round_fp16=True)
+    scores.copy_(logits.view(scores.shape))
+    b = None if bias is None else bias.float().contiguous()
+    ids, w = route_topk(logits, k, b, "sigmoid", renorm=True, scaling=float(scaling_factor))
+    topk_indices.copy_(ids.view(topk_indices.shape))
+    topk_weights.copy_(w.view(topk_weights.shape))
+
+
 def _act_mul(x, y, z, act, act_limit):
     require_device(x, y, z)
     if x.shape != y.shape or x.numel() != z.numel() or x.dtype != y.dtype or z.dtype != torch.float16:
@@ -286,15 +368,21 @@ class BC_GatedMLP:
 
 
 class BlockSparseMLP:
-    """Routed MoE layer: route (softmax / top-k over router logits, optional per-expert selection bias), grouped
-    routed experts, plus the shared expert (weight 1, added after the routed slots). forward returns fp32.
+    """Routed MoE layer: route (top-k over router logits, optional per-expert bias), grouped routed experts, plus the
+    shared expert (weight 1, added after the routed slots). forward returns fp32.
 
     `experts` holds the routed experts first and, when `has_shared`, the shared expert as the last table entry.
-    Router logits come from `router_weight` (fp16 [H, E]: logits = x @ W in fp32) or from params["router_logits"]."""
+    Router logits come from params["router_logits"] or from `router_weight` on the router GEMV: fp16 [H, E] (layout
+    "he", the reference's gate_tensor) or [E, H] ("eh"), optionally rounded to fp16 like a half matmul. Scoring:
+    "softmax" (default; the bias ranks and, unless bias_select_only, shifts the softmax), "sigmoid" or
+    "sqrt_softplus" (rank by score + bias, weights from the score), renormalised (+1e-20) and scaled by
+    routed_scaling."""
 
     def __init__(self, experts: ExpertTables, num_experts_per_tok: int, has_shared: bool = False, act="silu",
                  act_limit: float = 0.0, router_weight: torch.Tensor | None = None,
-                 selection_bias: torch.Tensor | None = None):
+                 selection_bias: torch.Tensor | None = None, scoring: str = "softmax", routed_scaling: float = 1.0,
+                 renormalize: bool = True, bias_select_only: bool = False, router_layout: str = "he",
+                 router_round_fp16: bool = False):
         self.experts = experts
         self.num_experts = experts.E - (1 if has_shared else 0)
         self.num_experts_per_tok = num_experts_per_tok
@@ -303,16 +391,30 @@ class BlockSparseMLP:
         self.act_limit = act_limit
         self.router_weight = router_weight
         self.selection_bias = selection_bias
+        if scoring not in SCORES:
+            raise NotImplementedError(f"BlockSparseMLP: scoring {scoring!r}")
+        self.scoring = scoring
+        self.routed_scaling = float(routed_scaling)
+        self.renormalize = renormalize
+        self.bias_select_only = bias_select_only
+        self.router_layout = router_layout
+        self.router_round_fp16 = router_round_fp16
+
+    def _fused_router(self) -> bool:
+        # the one-call path covers softmax ranked and weighted with the bias, renormalised, unscaled
+        return (self.scoring == "softmax" and self.renormalize and self.routed_scaling == 1.0 and
+                not (self.bias_select_only and self.selection_bias is not None))
 
     def route(self, x2: torch.Tensor, params=None):
-        return route_softmax_topk(self.router_logits(x2, params), self.num_experts_per_tok, self.selection_bias)
+        return route_topk(self.router_logits(x2, params), self.num_experts_per_tok, self.selection_bias, self.scoring,
+                          self.renormalize, self.routed_scaling, self.bias_select_only)
 
     def router_logits(self, x2: torch.Tensor, params=None) -> torch.Tensor:
         logits = None if params is None else params.get("router_logits")
         if logits is None:
             if self.router_weight is None:
                 raise Exl3Error("BlockSparseMLP: no router weight and no params['router_logits']")
-            logits = x2.float() @ self.router_weight.float()
+            return router_logits(x2, self.router_weight, self.num_experts, self.router_layout, self.router_round_fp16)
         return logits.reshape(-1, self.num_experts).float().contiguous()
 
     def forward(self, x: torch.Tensor, params=None, out_dtype=None) -> torch.Tensor:
@@ -320,7 +422,12 @@ class BlockSparseMLP:
         if x2.dtype != torch.float16:
             x2 = x2.half()
         x2 = x2.contiguous()
-        out = moe_forward_logits(x2, self.router_logits(x2, params), self.num_experts_per_tok, self.experts,
-                                 self.act, self.act_limit, self.shared, self.selection_bias, out_dtype=torch.float32)
+        if self._fused_router():
+            out = moe_forward_logits(x2, self.router_logits(x2, params), self.num_experts_per_tok, self.experts,
+                                     self.act, self.act_limit, self.shared, self.selection_bias,
+                                     out_dtype=torch.float32)
+        else:
+            ids, w = self.route(x2, params)
+            out = moe_forward(x2, ids, w, self.experts, self.act, self.act_limit, self.shared)
         out = out.view(x.shape[:-1] + (self.experts.H,))
         return out if out_dtype is None else out.to(out_dtype)

@@ -31,6 +31,9 @@ enum exl3_status {
 
 enum exl3_dtype { EXL3_F16 = 0, EXL3_F32 = 1 };
 enum exl3_act { EXL3_ACT_SILU = 0, EXL3_ACT_GELU_TANH = 1 };
+enum exl3_score { EXL3_SCORE_SOFTMAX = 0, EXL3_SCORE_SIGMOID = 1, EXL3_SCORE_SQRT_SOFTPLUS = 2 };
+enum exl3_route_flags { EXL3_ROUTE_RENORM = 1, EXL3_ROUTE_BIAS_SELECT_ONLY = 2 };
+enum exl3_router_w { EXL3_ROUTER_W_HE = 0, EXL3_ROUTER_W_EH = 1 };
 
 /* Message for the last non-zero status returned on the calling thread. */
 const char* exl3_last_error(void);
@@ -130,10 +133,34 @@ int exl3_moe_align(const int32_t* topk_ids, const float* topk_w, int64_t M, int6
 
 /* Softmax router: p = softmax(logits + bias) over E experts, top-k by p (ties to the lower index, descending),
  * weights renormalised over the k picks with +1e-20. logits fp32 [M, E] (row stride ld), bias fp32 [E] or NULL;
- * ids int32 [M, k], w fp32 [M, k]. k <= 32, E <= 8192.
+ * ids int32 [M, k], w fp32 [M, k]. k <= 32, E <= 8192. Same as exl3_route_topk(..., EXL3_SCORE_SOFTMAX,
+ * EXL3_ROUTE_RENORM, 1.0f, ...).
  * Replaces: the fused softmax/top-k router of trellis-serve (trellis-serve.patch:395-441). */
 int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k,
                             int32_t* ids, float* w, void* stream);
+
+/* Top-k router with a choice of scoring, one row per wave. Per expert e with logit f and bias b (bias NULL: b = 0):
+ *   EXL3_SCORE_SOFTMAX        rank by f + b; weights from p = softmax(f + b), or softmax(f) with
+ *                             EXL3_ROUTE_BIAS_SELECT_ONLY (the bias only ranks: trellis-serve's `cold` term)
+ *   EXL3_SCORE_SIGMOID        s = sigmoid(f); rank by s + b (by f without a bias); weights from s
+ *   EXL3_SCORE_SQRT_SOFTPLUS  s = sqrt(softplus(f)) (softplus(f) = f above 20); rank by s + b; weights from s
+ * Picks in descending rank order, exact ties to the lower index. Weight of a pick: v * scaling / (sum of the picks'
+ * v + 1e-20) with EXL3_ROUTE_RENORM, v * scaling without. Sizes as exl3_route_softmax_topk.
+ * Replaces: routing_ds3_nogroup's selection and weights (glm/xpu/glm_xpu/ops.py:177-193), the dsv Route kernel
+ * (dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193, without its residency terms), trellis-serve's router with `cold`
+ * (trellis-serve.patch:395-441). */
+int exl3_route_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k, int score,
+                    int flags, float scaling, int32_t* ids, float* w, void* stream);
+
+/* Router logits from hidden states: logits[m, e] = sum_h x[m, h] * W(h, e) in fp32 (fixed summation order), x fp16
+ * [M, H] (row stride x_ld), logits fp32 [M, E] (row stride logits_ld), rounded to fp16 precision when round_fp16 != 0
+ * (what a matmul of two fp16 tensors returns). w_layout EXL3_ROUTER_W_HE: W fp16 [H, E] (row stride w_ld >= E,
+ * E % 8 == 0: the reference's gate_tensor[:, :E]); EXL3_ROUTER_W_EH: W fp16 [E, H] (row stride w_ld >= H, a linear
+ * layer's weight). H % 128 == 0; W 16-byte aligned, w_ld % 8 == 0.
+ * Replaces: torch.matmul(hidden, gate[:, :E]) of routing_ds3_nogroup (glm/xpu/glm_xpu/ops.py:183-184) and the GemvH
+ * router GEMV of route_fused / gemv_h (dsv41/xpu/csrc/dsv_moe_glue.sycl:442-470, 520-530). */
+int exl3_router_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, const uint16_t* W, int64_t w_ld,
+                       int64_t E, int w_layout, int round_fp16, float* logits, int64_t logits_ld, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,9 @@ Sources restated (paths relative to the reference root):
   * expert math / MoE      ext-op-inventory.md:923-942; glm/xpu/csrc/exl3_moe.n128.sycl:253-271, 370-379, 405-408;
                            dsv41/xpu/dsv_xpu/moe.py:967-994
   * activations            ext-op-inventory.md:944-956 (SiLU, act_limit clamp); GELU-tanh = torch gelu(approximate='tanh')
-  * routing                trellis-serve.patch:395-441 (softmax -> top-k -> renormalise, +1e-20)
+  * routing                trellis-serve.patch:395-441 (softmax -> top-k -> renormalise, +1e-20); sigmoid + bias,
+                           glm/xpu/glm_xpu/ops.py:177-193; sqrt-softplus, dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193
+  * router logits          glm/xpu/glm_xpu/ops.py:183-184 (x @ gate[:, :E]); dsv_moe_glue.sycl:442-470 (x @ W^T)
   * align / pair lists     glm/xpu/csrc/exl3_moe.n128.sycl:691-734
 
 Every floating-point reduction here runs in float64 unless a caller asks for float32 (`acc`), so the oracle is at
@@ -316,6 +318,53 @@ def route_softmax_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = Non
     pw = np.take_along_axis(p, ids, -1)
     w = pw / (pw.sum(-1, keepdims=True) + 1e-20)
     return ids.astype(np.int32), w.astype(np.float32)
+
+
+SCORES = ("softmax", "sigmoid", "sqrt_softplus")
+
+
+def route_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None, score: str = "softmax",
+               renorm: bool = True, scaling: float = 1.0, bias_select_only: bool = False):
+    """Top-k routing with a scoring function; ranking values in float32 (as the kernel ranks), weights in float64.
+      softmax        rank by f + b; weights from softmax(f + b), or softmax(f) when the bias only selects
+                     (trellis-serve.patch:395-441, its `cold` term)
+      sigmoid        s = sigmoid(f); rank by s + b, by f without a bias; weights from s (glm/xpu/glm_xpu/ops.py:186-191)
+      sqrt_softplus  s = sqrt(softplus(f)), softplus(f) = f above 20; rank by s + b; weights from s
+                     (dsv41/xpu/csrc/dsv_moe_glue.sycl:163-193)
+    A pick's weight is v * scaling / (sum of picked v + 1e-20) with renorm, v * scaling without.
+    Returns ids int32 [M, k] (descending rank, exact ties to the lower index) and w float32 [M, k]."""
+    if score not in SCORES:
+        raise ValueError(score)
+    f = logits.astype(np.float32)
+    b = None if bias is None else bias.astype(np.float32)[None, :]
+    f64 = f.astype(np.float64)
+    if score == "softmax":
+        r = f if b is None else f + b
+        g = r.astype(np.float64) if not bias_select_only else f64
+        v = np.exp(g - g.max(-1, keepdims=True))
+        v = v / v.sum(-1, keepdims=True)
+    else:
+        if score == "sigmoid":
+            s32 = (np.float32(1) / (np.float32(1) + np.exp(-f))).astype(np.float32)
+            v = 1.0 / (1.0 + np.exp(-f64))
+        else:
+            sp32 = np.where(f > 20, f, np.log1p(np.exp(np.minimum(f, 20)))).astype(np.float32)
+            s32 = np.sqrt(sp32).astype(np.float32)
+            v = np.sqrt(np.where(f64 > 20, f64, np.log1p(np.exp(np.minimum(f64, 20)))))
+        r = (s32 + b) if b is not None else (f if score == "sigmoid" else s32)
+    ids = topk_lowest_index(r, k)
+    pv = np.take_along_axis(v, ids, -1)
+    w = pv * scaling / (pv.sum(-1, keepdims=True) + 1e-20) if renorm else pv * scaling
+    return ids.astype(np.int32), w.astype(np.float32)
+
+
+def router_logits(x: np.ndarray, W: np.ndarray, layout: str = "he", round_fp16: bool = False) -> np.ndarray:
+    """logits[m, e] = sum_h x[m, h] W(h, e) in float64, returned as float32, or rounded to fp16 precision (the result of
+    a matmul of two fp16 tensors, glm/xpu/glm_xpu/ops.py:183-184). layout "he": W [H, E] (gate_tensor); "eh": W [E, H]
+    (a linear layer's weight, dsv41/xpu/csrc/dsv_moe_glue.sycl:442-470)."""
+    Wm = W.astype(np.float64) if layout == "he" else W.astype(np.float64).T
+    y = x.astype(np.float64) @ Wm
+    return y.astype(np.float16).astype(np.float32) if round_fp16 else y.astype(np.float32)
 
 
 def align(ids: np.ndarray, w: np.ndarray, E: int, pad: int = 1):

@@ -241,6 +241,73 @@ def test_route_softmax_topk():
     assert (ids_b[:, 0] == 50).all() and (w_b[:, 0] > 0.99).all()
 
 
+@pytest.mark.parametrize("score", ["softmax", "sigmoid", "sqrt_softplus"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_route_topk_scorings_against_torch(score, with_bias):
+    """Each scoring against an independent torch statement of the reference formula (torch.sigmoid / softplus /
+    softmax and torch.topk): trellis-serve.patch:403-424 (softmax, `cold` as a selection-only bias),
+    glm/xpu/glm_xpu/ops.py:186-191 (sigmoid), dsv41/xpu/csrc/dsv_moe_glue.sycl:163-193 (sqrt-softplus)."""
+    import torch
+    g = torch.Generator().manual_seed(11 + 3 * with_bias + len(score))
+    logits = torch.randn(9, 96, generator=g) * 3
+    bias = torch.randn(96, generator=g) * 0.5 if with_bias else None
+    k, scaling = 6, 2.5
+    f = logits.double()
+    if score == "softmax":
+        v = torch.softmax(f, -1)
+        key = f + bias.double() if with_bias else f
+    elif score == "sigmoid":
+        v = torch.sigmoid(f)
+        key = v + bias.double() if with_bias else f
+    else:
+        v = torch.sqrt(torch.nn.functional.softplus(f, threshold=20))
+        key = v + bias.double() if with_bias else v
+    idx = torch.topk(key, k, dim=-1, sorted=True).indices
+    pv = v.gather(-1, idx)
+    w_ref = pv * scaling / (pv.sum(-1, keepdim=True) + 1e-20)
+    ids, w = O.route_topk(logits.numpy(), k, None if bias is None else bias.numpy(), score, True, scaling,
+                          bias_select_only=True)
+    assert np.array_equal(ids, idx.numpy())
+    assert np.abs(w - w_ref.numpy()).max() <= 1e-6 * scaling
+    # without renormalisation the weights are the scores themselves (times scaling)
+    _, w_raw = O.route_topk(logits.numpy(), k, None if bias is None else bias.numpy(), score, False, scaling,
+                            bias_select_only=True)
+    assert np.abs(w_raw - (pv * scaling).numpy()).max() <= 1e-6 * float(pv.max()) * scaling
+
+
+def test_route_topk_softmax_bias_both_is_route_softmax_topk():
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((7, 200)).astype(np.float32)
+    bias = rng.standard_normal(200).astype(np.float32)
+    a = O.route_softmax_topk(logits, 8, bias)
+    b = O.route_topk(logits, 8, bias, "softmax")
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    # selection-only bias: same picks, weights from the unbiased softmax
+    c = O.route_topk(logits, 8, bias, "softmax", bias_select_only=True)
+    assert np.array_equal(a[0], c[0])
+    p = np.exp(logits.astype(np.float64))
+    p /= p.sum(-1, keepdims=True)
+    pv = np.take_along_axis(p, c[0].astype(np.int64), -1)
+    assert np.allclose(c[1], pv / pv.sum(-1, keepdims=True), rtol=1e-6)
+
+
+def test_router_logits_layouts_and_fp16_rounding():
+    import torch
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(5, 256, generator=g).half()
+    W = (torch.randn(256, 40, generator=g) * 0.1).half()
+    ref = (x.double() @ W.double()).numpy()
+    he = O.router_logits(x.numpy(), W.numpy(), "he")
+    eh = O.router_logits(x.numpy(), W.T.contiguous().numpy(), "eh")
+    assert np.array_equal(he, eh) and np.abs(he - ref).max() <= 1e-6 * np.abs(ref).max()
+    r16 = O.router_logits(x.numpy(), W.numpy(), "he", round_fp16=True)
+    assert np.array_equal(r16, ref.astype(np.float16).astype(np.float32))
+    # torch's own fp16 matmul (fp32 accumulation, one rounding) agrees within one fp16 ulp
+    t16 = torch.matmul(x, W).float().numpy()
+    d = np.abs(t16.astype(np.float16).view(np.int16).astype(np.int32) - r16.astype(np.float16).view(np.int16))
+    assert d.max() <= 1
+
+
 def test_align_invariants():
     rng = np.random.default_rng(12)
     ids = rng.integers(0, 16, size=(9, 4)).astype(np.int32)
