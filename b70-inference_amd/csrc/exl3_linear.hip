@@ -101,7 +101,9 @@ struct GemvArgs {
     int m;
     const uint32_t* tr;
     int tn;
-    const uint16_t* suh;
+    const uint16_t* suh;                             // [S][k]
+    const int32_t* sonb;                             // shard of each 128-column strip (S > 1), else null
+    int S;
     const uint16_t* svh;
     void* out;
     int64_t out_ld;
@@ -126,11 +128,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     StripRing<K, kLinearRing> ring;
     strip_prefetch<K, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, ring);   // weight loads in flight during phase 1
 
-    // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums
+    // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums; the
+    // strip's shard selects the sign vector (clamped into [0, S))
+    int shard = 0;
+    if (a.sonb) {
+        shard = a.sonb[strip];
+        shard = shard < 0 ? 0 : (shard >= a.S ? a.S - 1 : shard);
+    }
+    const uint16_t* suh = a.suh + (size_t)shard * (a.nblk * 128);
     for (int i = wave; i < M * kb; i += 4) {
         const int m = i / kb, b = i - m * kb;
         const int k0 = (b0 + b) * 128;
-        float s = had_in_block(m < a.m ? a.x + (int64_t)m * a.x_ld + k0 : nullptr, a.suh + k0, &xs[m][b * 128], lane);
+        float s = had_in_block(m < a.m ? a.x + (int64_t)m * a.x_ld + k0 : nullptr, suh + k0, &xs[m][b * 128], lane);
         if (lane == 0) bsum[m][b] = s;
     }
     __syncthreads();
@@ -235,11 +244,13 @@ static int gemv_splits(int strips, int nblk) {
 
 // Dense linear on MFMA (exl3_mfma.hip), used from kLinearMfmaMinRows rows on.
 int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K,
-                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st);
+                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb,
+                       const uint16_t* svh, hipStream_t st);
 constexpr int kLinearMfmaMinRows = 9;
 
 int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
-                int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st) {
+                int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh,
+                hipStream_t st) {
     const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
     const int P = gemv_splits(strips, nblk);
     const int Mmax = kGemvMaxRows;
@@ -255,6 +266,8 @@ int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uin
         ga.tr = tr;
         ga.tn = tn;
         ga.suh = suh;
+        ga.S = S;
+        ga.sonb = S > 1 ? sonb : nullptr;
         ga.svh = svh;
         ga.out = f32 ? (void*)(reinterpret_cast<float*>(C) + m0 * c_ld) : (void*)(reinterpret_cast<uint16_t*>(C) + m0 * c_ld);
         ga.out_ld = c_ld;
@@ -319,16 +332,18 @@ int exl3_had_r_128(const void* in, int64_t in_ld, void* out, int64_t out_ld, int
     return EXL3_OK;
 }
 
-int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K, void* C,
-              int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
-              void* stream) {
-    (void)A_had;
+int exl3_linear_sharded(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K,
+                        void* C, int64_t c_ld, int c_dtype, const uint16_t* suh, int64_t n_shards,
+                        const int32_t* shard_of_nb, const uint16_t* svh, int cb, void* stream) {
     if (cb != 2) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm: codebook %d not supported (mul1 = 2 only)", cb);
     if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm: K=%d not in 1..8", K);
     EXL3_CHECK_ARG(c_dtype == EXL3_F16 || c_dtype == EXL3_F32, "exl3_gemm: C must be fp16 or fp32");
     EXL3_CHECK_ARG(m >= 0 && k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0,
                    "exl3_gemm: k=%lld and n=%lld must be positive multiples of 128", (long long)k, (long long)n);
     EXL3_CHECK_ARG(a_ld >= k && c_ld >= n, "exl3_gemm: row strides must cover k / n");
+    EXL3_CHECK_ARG(n_shards >= 1 && n_shards <= 64, "exl3_linear_sharded: n_shards=%lld not in 1..64",
+                   (long long)n_shards);
+    EXL3_CHECK_ARG(n_shards == 1 || shard_of_nb, "exl3_linear_sharded: shard_of_nb required for several shards");
     if (m == 0) return EXL3_OK;
     EXL3_CHECK_ARG(A && B && C && suh && svh, "exl3_gemm: null pointer");
     EXL3_CHECK_ARG(aligned(B, 4), "exl3_gemm: trellis must be 4-byte aligned");
@@ -336,9 +351,19 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
     EXL3_CHECK_ARG(k / 16 * (n / 16) * 8 * (int64_t)(K > 0 ? K : 8) < (1LL << 32),
                    "exl3_gemm: trellis of %lld x %lld at K=%d exceeds 2^32 words", (long long)k, (long long)n, K);
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(B);
+    const int S = (int)n_shards;
     if (m >= env_int("EXL3MI_MFMA_MIN_ROWS", kLinearMfmaMinRows))
-        return launch_linear_mfma(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, svh, (hipStream_t)stream);
-    return launch_gemv(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, svh, (hipStream_t)stream);
+        return launch_linear_mfma(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, S, shard_of_nb, svh,
+                                  (hipStream_t)stream);
+    return launch_gemv(A, a_ld, m, k, tr, n, K, C, c_ld, c_dtype == EXL3_F32, suh, S, shard_of_nb, svh,
+                       (hipStream_t)stream);
+}
+
+int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K, void* C,
+              int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
+              void* stream) {
+    (void)A_had;
+    return exl3_linear_sharded(A, a_ld, m, k, B, n, K, C, c_ld, c_dtype, suh, 1, nullptr, svh, cb, stream);
 }
 
 }  // extern "C"

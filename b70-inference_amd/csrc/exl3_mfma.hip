@@ -98,13 +98,13 @@ __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ 
 //   A:       staged per step by the whole workgroup: loaded into register slot s % 4 four steps ahead, stored to LDS
 //            stage s % 2 one step ahead; memory-counter waits complete in issue order, so each step issues its A load
 //            before its weight load.
-template <int K, int NP, int RGA>
+template <int K, int NP, int RGA, int NPS = NP>
 struct MfmaPipe {
     static constexpr int NW = FragCfg<K>::NW;
     static constexpr int DW = 4;
     static constexpr int TPP = kMfT / NP;
     static constexpr int TS = 8 * K + 4;                     // LDS words per staged tile
-    static constexpr int UNITS = NP * RGA * 64;              // 16-byte A units per stage
+    static constexpr int UNITS = NPS * RGA * 64;             // 16-byte A units per stage (NPS staged planes)
     static constexpr int CPT = (UNITS + 255) / 256;          // A units a thread stages per step
     const uint32_t* wsrc;                                    // this lane's K words at step 0
     uint32_t wstep;                                          // words between consecutive steps (two tile-rows)
@@ -117,6 +117,7 @@ struct MfmaPipe {
     int adst[CPT];
     u32x4_t* lds;                                            // [2][UNITS]
     int lane;
+    int apl = 0;                                             // first staged plane this wave reads (NPS > NP)
 
     __device__ __forceinline__ void load_w(uint32_t (&D)[K], int s) const {
         const uint32_t* p = wsrc + (uint32_t)(s < nsteps ? s : nsteps - 1) * wstep;
@@ -141,7 +142,7 @@ struct MfmaPipe {
 #pragma unroll
             for (int rg = 0; rg < RGA; ++rg)
                 af[p][rg] = __builtin_bit_cast(
-                    h8_t, lds[stage * UNITS + p * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
+                    h8_t, lds[stage * UNITS + (p + apl) * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
         h8_t bf[kMfT];
 #pragma unroll
         for (int t = 0; t < kMfT; ++t) {
@@ -742,13 +743,17 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix
 // exl3_gemm for more rows than the GEMV takes per pass: y = Hn(Hk(x * suh) @ W_hat) * svh with the trellis decoded
 // straight into MFMA B fragments once per row block (up to 64 rows), as in the reference's large-M linear
 // (glm/xpu/csrc/exl3_ops.sycl:643-757), which reconstructs 16384-column fp16 slices and runs a GEMM instead.
-//   linear_had   xh[m][k] = fp16(H128(fp16(x * suh)) / sqrt(128)) and the 128-blocks' sums xsum[m][k / 128]
+//   linear_had   xh[s][m][k] = fp16(H128(fp16(x * suh[s])) / sqrt(128)) and the 128-blocks' sums xsum[s][m][k / 128]
+//                for every shard s (a fused multi-projection linear: output column blocks of S projections that share
+//                the input, each with its own input signs suh[s]; shard_of_nb maps 128-column blocks to shards)
 //   linear_mfma  workgroup per (row block, k-split, 256-column block); a wave owns four tile columns. With one split
 //                the epilogue writes y; otherwise it writes fp32 partials (affine applied)
 //   linear_reduce (k-split only) wave per (row, 128 columns): partials in split order, Hadamard, * svh -> y
 struct LinArgs {
-    const _Float16* xh;
-    const float* xsum;
+    const _Float16* xh;                              // [S][m][k]
+    const float* xsum;                               // [S][m][k / 128]
+    const int32_t* sonb;                             // shard of each 128-column block (S > 1), else null
+    int S;
     const uint32_t* tr;
     const uint16_t* svh;
     void* out;
@@ -763,6 +768,9 @@ __global__ __launch_bounds__(256) void linear_had_kernel(const uint16_t* __restr
                                                          const uint16_t* __restrict__ suh, _Float16* xh, float* xsum) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kb = blockIdx.y, nblk = k / 128;
+    suh += (size_t)blockIdx.z * k;                               // shard s = blockIdx.z
+    xh += (size_t)blockIdx.z * m * k;
+    xsum += (size_t)blockIdx.z * m * nblk;
     const int r0 = blockIdx.x * 16 + wave;
     const float s0 = h2f(ldg(suh + kb * 128 + lane)), s1 = h2f(ldg(suh + kb * 128 + lane + 64));
     constexpr int RB = 4;
@@ -801,12 +809,14 @@ __device__ __forceinline__ void linear_store(const LinArgs& a, int row, int col,
     }
 }
 
-template <int K, int RGA>
+// NPS = 2 for several shards: the two 128-column halves of the block may read different shards' inputs, so both
+// are staged and waves 0, 1 (first half) read plane 0, waves 2, 3 plane 1.
+template <int K, int RGA, int NPS>
 __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_mfma_kernel(LinArgs a) {
-    __shared__ u32x4_t stage[2 * RGA * 64];            // [2 stages][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[2 * NPS * RGA * 64];      // [2 stages][planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
-    __shared__ float rsum[16 * RGA];
+    __shared__ float rsum[NPS][16 * RGA];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int blk, nb;
     xcd_map(a.ncb, blk, nb);
@@ -826,22 +836,34 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_m
         sd[h][0] = h2f(ldg(sv + 128 * hh + lane)) * kRsqrt128;
         sd[h][1] = h2f(ldg(sv + 128 * hh + lane + 64)) * kRsqrt128;
     }
-    if (threadIdx.x < 16 * RGA) {                      // the rows' sums over this split's 128-blocks
-        const int r = threadIdx.x;
-        rsum[r] = sum_ordered(a.xsum + (size_t)(r0 + (r < cnt ? r : cnt - 1)) * a.nblk + kb0, nkb);
+    // shard of each staged plane (plane p: the block's 128-column half p; clamped into [0, S))
+    int shard[NPS];
+#pragma unroll
+    for (int q = 0; q < NPS; ++q) {
+        int v = 0;
+        if (NPS > 1) {
+            v = a.sonb[2 * nb + (q < nhalf ? q : 0)];
+            v = v < 0 ? 0 : (v >= a.S ? a.S - 1 : v);
+        }
+        shard[q] = v;
+    }
+    if (threadIdx.x < NPS * 16 * RGA) {                // the rows' sums over this split's 128-blocks, per plane
+        const int q = threadIdx.x / (16 * RGA), r = threadIdx.x - q * 16 * RGA;
+        rsum[q][r] = sum_ordered(a.xsum + ((size_t)shard[q] * a.m + r0 + (r < cnt ? r : cnt - 1)) * a.nblk + kb0, nkb);
     }
     __syncthreads();
-    MfmaPipe<K, 1, RGA> L;
+    MfmaPipe<K, 1, RGA, NPS> L;
     L.nsteps = nkb * 4;
     L.lds = stage;
     L.lane = lane;
+    L.apl = NPS > 1 ? (wave >> 1) : 0;
     const uint32_t* trk = a.tr + (size_t)kb0 * 8 * tn * (8 * K);
     L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) {
         int ct = nb * 16 + 4 * wave + 2 * pair;
         ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
         return trk + (size_t)ct * (8 * K);
     });
-    L.setup_a(cnt, [&](int, int row) { return a.xh + (size_t)(r0 + row) * a.k + kb0 * 128; });
+    L.setup_a(cnt, [&](int q, int row) { return a.xh + ((size_t)shard[q] * a.m + r0 + row) * a.k + kb0 * 128; });
     f4_t acc[kMfT][RGA];
 #pragma unroll
     for (int t = 0; t < kMfT; ++t)
@@ -863,7 +885,7 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_m
         for (int j = 0; j < 8; ++j) {                 // (row, half) pairs of this wave
             const int ml = 4 * wave + (j >> 1), h = j & 1, m = 16 * rg + ml;
             if (m >= cnt || h >= nhalf) continue;
-            const float sx = kMul1C2 * rsum[m];
+            const float sx = kMul1C2 * rsum[NPS > 1 ? h : 0][m];
             float v0 = kMul1C1 * C[ml * 256 + 128 * h + lane] + sx, v1 = kMul1C1 * C[ml * 256 + 128 * h + lane + 64] + sx;
             const int col = nb * 256 + 128 * h + lane;
             if (single) {
@@ -995,24 +1017,30 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(LinArgs a) {
 
 typedef void (*lin_fn)(LinArgs);
 
-template <int RGA>
+template <int RGA, int NPS>
 static lin_fn pick_lin(int K) {
     switch (K) {
-        case 1: return linear_mfma_kernel<1, RGA>;
-        case 2: return linear_mfma_kernel<2, RGA>;
-        case 3: return linear_mfma_kernel<3, RGA>;
-        case 4: return linear_mfma_kernel<4, RGA>;
-        case 5: return linear_mfma_kernel<5, RGA>;
-        case 6: return linear_mfma_kernel<6, RGA>;
-        case 7: return linear_mfma_kernel<7, RGA>;
-        default: return linear_mfma_kernel<8, RGA>;
+        case 1: return linear_mfma_kernel<1, RGA, NPS>;
+        case 2: return linear_mfma_kernel<2, RGA, NPS>;
+        case 3: return linear_mfma_kernel<3, RGA, NPS>;
+        case 4: return linear_mfma_kernel<4, RGA, NPS>;
+        case 5: return linear_mfma_kernel<5, RGA, NPS>;
+        case 6: return linear_mfma_kernel<6, RGA, NPS>;
+        case 7: return linear_mfma_kernel<7, RGA, NPS>;
+        default: return linear_mfma_kernel<8, RGA, NPS>;
     }
+}
+
+template <int NPS>
+static lin_fn pick_lin_rga(int RGA, int K) {
+    return RGA == 4 ? pick_lin<4, NPS>(K) : RGA == 2 ? pick_lin<2, NPS>(K) : pick_lin<1, NPS>(K);
 }
 
 // Dense linear on MFMA (m > the GEMV's rows per pass). Row blocks of 16, 32 or 64 rows (by m); k-splits so that the
 // grid covers about the workgroups the device holds at once, each split at least two 128-blocks of k.
 int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K,
-                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, const uint16_t* svh, hipStream_t st) {
+                       void* C, int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb,
+                       const uint16_t* svh, hipStream_t st) {
     const int RGA = m <= 16 ? 1 : m <= 32 ? 2 : 4;
     const int R = 16 * RGA;
     const int nblk = (int)(k / 128);
@@ -1025,7 +1053,7 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     a.nblk = nblk;
     a.nrb = (int)((m + R - 1) / R);
     a.ncb = (int)((n + 255) / 256);
-    lin_fn fn = RGA == 4 ? pick_lin<4>(K) : RGA == 2 ? pick_lin<2>(K) : pick_lin<1>(K);
+    lin_fn fn = S > 1 ? pick_lin_rga<2>(RGA, K) : pick_lin_rga<1>(RGA, K);
     int resident = 0;
     int rc = resident_blocks((const void*)fn, 256, &resident);
     if (rc) return rc;
@@ -1036,23 +1064,26 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     P = P < 1 ? 1 : (P > pmax ? pmax : P);
     a.bps = (nblk + P - 1) / P;
     a.P = (nblk + a.bps - 1) / a.bps;
-    const size_t xh_b = carve_size((size_t)m * k, 2), xs_b = carve_size((size_t)m * nblk, 4);
+    const size_t xh_b = carve_size((size_t)S * m * k, 2), xs_b = carve_size((size_t)S * m * nblk, 4);
     const size_t part_b = a.P > 1 ? carve_size((size_t)a.P * m * n, 4) : 0;
     Workspace ws;
     rc = workspace(xh_b + xs_b + part_b, 0, &ws);
     if (rc) return rc;
     Carve cv{ws.scratch, ws.scratch_bytes};
-    _Float16* xh = cv.take<_Float16>((size_t)m * k);
-    float* xsum = cv.take<float>((size_t)m * nblk);
+    _Float16* xh = cv.take<_Float16>((size_t)S * m * k);
+    float* xsum = cv.take<float>((size_t)S * m * nblk);
     a.part = a.P > 1 ? cv.take<float>((size_t)a.P * m * n) : nullptr;
     a.xh = xh;
     a.xsum = xsum;
+    a.S = S;
+    a.sonb = S > 1 ? sonb : nullptr;
     a.tr = tr;
     a.svh = svh;
     a.out = C;
     a.out_ld = c_ld;
     a.f32 = f32 ? 1 : 0;
-    EXL3_LAUNCH("linear_had", linear_had_kernel, dim3((unsigned)((m + 15) / 16), (unsigned)nblk), dim3(256), 0, st, A,
+    EXL3_LAUNCH("linear_had", linear_had_kernel, dim3((unsigned)((m + 15) / 16), (unsigned)nblk, (unsigned)S), dim3(256),
+                0, st, A,
                 a_ld, (int)m, (int)k, suh, xh, xsum);
     const int64_t nx = ((int64_t)a.nrb * a.P + 7) / 8 * 8 * a.ncb;
     if (nx > 0x7FFFFFFF) return fail(EXL3_ERR_INVALID, "exl3_gemm: grid too large");

@@ -6,6 +6,9 @@ Interfaces mirror the reference boundary:
   * exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1, force_num_sms) (ext-op-inventory.md:498-557)
   * reconstruct / reconstruct_slice (ext-op-inventory.md:597-612), exl3_reconstruct (glm/xpu/csrc/exl3_ops.sycl:539-555)
   * had_r_128(input, output, pre_scale, post_scale, scale) (ext-op-inventory.md:576-595)
+  * linear(x, trellis, suh[S, k], svh, shard_of_nb, group_bounds, K, cb, small_m_max, slice_n): the fused
+    multi-projection linear of the XPU library (glm/xpu/csrc/exl3_ops.sycl:651-757, bound at :789-790); fuse_linears
+    builds its operands from several BC_LinearEXL3 that share the input
 Tensors live on the GPU; every op is asynchronous on the current stream and writes its output in place.
 """
 from __future__ import annotations
@@ -143,3 +146,72 @@ class BC_LinearEXL3:
             return y
         self.run(x.reshape(-1, x.shape[-1]), y.view(-1, out_features))
         return y
+
+
+def linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, shard_of_nb: torch.Tensor,
+           group_bounds, K: int, cb: int = CB_MUL1, small_m_max: int = 8, slice_n: int = 16384,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """exl3xpu_C::linear: y[..., g0:g1] = x @ W_s for the S projections (shards) whose trellises are concatenated
+    along the columns; suh fp16 [S, k] (one input sign vector per shard), svh fp16 [n], shard_of_nb int32 [n / 128]
+    (device), group_bounds the S + 1 column boundaries. Returns fp16 [..., n] (or writes `out`, fp16 / fp32).
+    small_m_max and slice_n tune the reference's own path choice and slicing; the library picks its paths itself."""
+    require_device(x, trellis, suh, svh, shard_of_nb, out)
+    Ki = _K_of(trellis, K)
+    if cb != CB_MUL1:
+        raise NotImplementedError(f"exl3mi: codebook {cb} not supported (mul1 = 2 only)")
+    k, n = trellis.shape[0] * 16, trellis.shape[1] * 16
+    if suh.dim() == 1:
+        suh = suh.view(1, -1)
+    S = suh.shape[0]
+    if suh.dtype != torch.float16 or suh.shape[1] != k or not suh.is_contiguous():
+        raise Exl3Error(f"linear: suh must be contiguous fp16 [S, {k}]")
+    if svh.dtype != torch.float16 or svh.numel() != n or not svh.is_contiguous():
+        raise Exl3Error(f"linear: svh must be contiguous fp16 [{n}]")
+    gb = [int(v) for v in group_bounds]
+    if len(gb) != S + 1 or gb[0] != 0 or gb[-1] != n or any(b % 128 for b in gb) or gb != sorted(gb):
+        raise Exl3Error(f"linear: group_bounds {gb} must be S + 1 = {S + 1} ascending multiples of 128 from 0 to {n}")
+    if S > 1 and (shard_of_nb is None or shard_of_nb.dtype != torch.int32 or shard_of_nb.numel() != n // 128 or
+                  not shard_of_nb.is_contiguous()):
+        raise Exl3Error(f"linear: shard_of_nb must be contiguous int32 [{n // 128}]")
+    if x.shape[-1] != k:
+        raise Exl3Error(f"linear: x must be [..., {k}]")
+    x2 = x.reshape(-1, k)
+    x2 = (x2 if x2.dtype == torch.float16 else x2.half()).contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (n,), dtype=torch.float16, device=x.device)
+    if out.dtype not in (torch.float16, torch.float32) or not out.is_contiguous() or out.numel() != M * n:
+        raise Exl3Error("linear: out must be contiguous fp16/fp32 [..., n]")
+    if M == 0:
+        return out
+    if not trellis.is_contiguous():
+        raise Exl3Error("linear: trellis must be contiguous")
+    check(lib().exl3_linear_sharded(ptr(x2), k, M, k, ptr(trellis), n, Ki, ptr(out), n,
+                                    EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, ptr(suh), S,
+                                    ptr(shard_of_nb) if S > 1 else None, ptr(svh), cb, stream_of(x2)), "linear")
+    return out
+
+
+def fuse_linears(linears):
+    """Operands of `linear` for BC_LinearEXL3 projections that share the input (same in_features and K): trellis
+    concatenated along the columns, suh stacked [S, k], svh concatenated, shard_of_nb and group_bounds (as the
+    reference's fused q|k|v and gate|up setup does, trellis-serve.patch:3705-3716). Returns
+    (trellis, suh, svh, shard_of_nb, group_bounds, K)."""
+    if not linears:
+        raise Exl3Error("fuse_linears: no projections")
+    k, K = linears[0].in_features, linears[0].Ki
+    for lin in linears:
+        if lin.in_features != k or lin.Ki != K:
+            raise Exl3Error("fuse_linears: projections must share in_features and K")
+        if lin.out_features % 128:
+            raise Exl3Error("fuse_linears: every projection's out_features must be a multiple of 128")
+    tr = torch.cat([lin.trellis for lin in linears], 1).contiguous()
+    suh = torch.stack([lin.suh.half() for lin in linears]).contiguous()
+    svh = torch.cat([lin.svh.half() for lin in linears]).contiguous()
+    bounds = [0]
+    for lin in linears:
+        bounds.append(bounds[-1] + lin.out_features)
+    sonb = torch.empty(bounds[-1] // 128, dtype=torch.int32)
+    for g in range(len(linears)):
+        sonb[bounds[g] // 128: bounds[g + 1] // 128] = g
+    return tr, suh, svh, sonb.to(tr.device), bounds, K

@@ -78,6 +78,18 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
               int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
               void* stream);
 
+/* Fused multi-projection linear: S projections that share the input x (e.g. q|k|v or gate|up), their trellises
+ * concatenated along the output columns (B = [k/16][n/16][16K] with n = the sum of the projections' widths, as
+ * torch.cat(trellises, 1)), per-projection input signs suh fp16 [S][k] (row s for shard s), output signs svh fp16 [n]
+ * (concatenated), and shard_of_nb int32 [n/128] (device) naming the shard of every 128-column block (values outside
+ * [0, S) are clamped). Column block j of C is x @ W_{shard_of_nb[j]} for that block. n_shards = 1 (shard_of_nb may be
+ * NULL) is exl3_gemm. Other arguments and paths as exl3_gemm.
+ * Replaces: exl3xpu_C::linear(x, trellis, suh[S, k], svh[n], shard_of_nb, group_bounds, K, cb, small_m_max, slice_n)
+ *           (glm/xpu/csrc/exl3_ops.sycl:651-757, bound at :789-790) and exl3_gemm_small with shard_of_nb (:258-321). */
+int exl3_linear_sharded(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K,
+                        void* C, int64_t c_ld, int c_dtype, const uint16_t* suh, int64_t n_shards,
+                        const int32_t* shard_of_nb, const uint16_t* svh, int cb, void* stream);
+
 /* Gated activation z = act(x, y) elementwise over n values, fp16 (dtype EXL3_F16) or fp32 (EXL3_F32) inputs, fp16
  * output (in place on y allowed). SiLU: z = min(silu(x), L) * clamp(y, -L, L) (L = act_limit, 0 disables);
  * GELU-tanh: z = gelu_tanh(x) * y. Computed in fp32, rounded once.

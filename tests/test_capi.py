@@ -53,6 +53,17 @@ def test_validation_errors(exl3):
     assert L.exl3_gemm(None, 256, 1, 256, fake, 256, 3, fake, 256, 0, fake, None, fake, 2, None) == 1
     # m == 0 is a no-op
     assert L.exl3_gemm(fake, 256, 0, 256, fake, 256, 3, fake, 256, 0, fake, None, fake, 2, None) == 0
+    # sharded linear: several shards need shard_of_nb; the shard count is bounded
+    assert L.exl3_linear_sharded(fake, 256, 1, 256, fake, 256, 3, fake, 256, 0, fake, 2, None, fake, 2, None) == 1
+    assert L.exl3_linear_sharded(fake, 256, 1, 256, fake, 256, 3, fake, 256, 0, fake, 0, None, fake, 2, None) == 1
+    assert L.exl3_linear_sharded(fake, 256, 0, 256, fake, 256, 3, fake, 256, 0, fake, 2, fake, fake, 2, None) == 0
+    # routers: scoring and flags are checked, sizes as the softmax router
+    assert L.exl3_route_topk(fake, 64, 1, 64, None, 4, 7, 1, ctypes.c_float(1.0), fake, fake, None) == 2
+    assert L.exl3_route_topk(fake, 64, 1, 64, None, 4, 1, 8, ctypes.c_float(1.0), fake, fake, None) == 1
+    assert L.exl3_route_topk(fake, 64, 1, 64, None, 40, 1, 1, ctypes.c_float(1.0), fake, fake, None) == 1
+    assert L.exl3_router_logits(fake, 200, 1, 200, fake, 64, 64, 0, 0, fake, 64, None) == 1
+    assert L.exl3_router_logits(fake, 256, 1, 256, fake, 60, 60, 0, 0, fake, 60, None) == 1
+    assert L.exl3_router_logits(fake, 256, 1, 256, fake, 64, 64, 2, 0, fake, 64, None) == 1
 
 
 def test_python_errors_match_reference(exl3):

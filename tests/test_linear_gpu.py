@@ -179,3 +179,26 @@ def test_gemm_mfma_strided_rows_and_determinism(exl3, oracle):
     y20 = torch.empty(20, n, dtype=torch.float32, device="cuda")
     run(20, y20)
     assert max_rel(y20.cpu().numpy(), ref[:20]) <= MAX_REL
+
+
+@pytest.mark.parametrize("M", [1, 4, 9, 40, 100])
+def test_linear_sharded_matches_per_shard_oracle(exl3, oracle, M):
+    """Fused multi-projection linear (the XPU library's linear with suh[S, k] and shard_of_nb): three projections
+    of widths 384 | 128 | 640 sharing the input, so 256-column blocks straddle shard boundaries; each column range
+    equals its own projection's oracle output."""
+    S_ = synth()
+    k, widths, K = 1024, (384, 128, 640), 3
+    shards = [S_.linear(k, n, K, 5000 + 10 * i) for i, n in enumerate(widths)]
+    lins = [exl3.BC_LinearEXL3(tr.cuda(), su.cuda(), sv.cuda(), K, None, False, True, None) for tr, su, sv in shards]
+    tr, suh, svh, sonb, bounds, Kf = exl3.fuse_linears(lins)
+    x = S_.activations(M, k, 5100 + M)
+    y = exl3.linear(x.cuda(), tr, suh, svh, sonb, bounds, Kf).float().cpu().numpy()
+    for i, (t, su, sv) in enumerate(shards):
+        ref = oracle.exl3_linear(x.numpy(), t.numpy(), su.numpy(), sv.numpy(), K, np.float16)
+        assert max_rel(y[:, bounds[i]:bounds[i + 1]], ref) <= MAX_REL, i
+    # fp32 output and the single-shard form agree with exl3_gemm
+    y32 = torch.empty(M, sum(widths), dtype=torch.float32, device="cuda")
+    exl3.linear(x.cuda(), tr, suh, svh, sonb, bounds, Kf, out=y32)
+    assert max_rel(y32.cpu().numpy(), y) <= MAX_REL
+    one = exl3.linear(x.cuda(), lins[2].trellis, lins[2].suh, lins[2].svh, None, [0, 640], K).float()
+    assert torch.equal(one, lins[2].run_alloc(x.cuda(), 640, False).float())
