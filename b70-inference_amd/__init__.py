@@ -9,3 +9,4 @@ from .linear import (BC_LinearEXL3, exl3_gemm, exl3_reconstruct, fuse_linears, h
 from .moe import (BC_GatedMLP, BlockSparseMLP, ExpertTables, MixedEXL3, gelu_mul, moe_align, moe_forward,  # noqa: F401
                   moe_forward_logits, route_softmax_topk, route_topk, router_logits, routing_ds3_nogroup,
                   silu_mul)
+from . import blob  # noqa: F401,E402

@@ -16,6 +16,8 @@ Sources restated (paths relative to the reference root):
   * routing                trellis-serve.patch:395-441 (softmax -> top-k -> renormalise, +1e-20); sigmoid + bias,
                            glm/xpu/glm_xpu/ops.py:177-193; sqrt-softplus, dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193
   * router logits          glm/xpu/glm_xpu/ops.py:183-184 (x @ gate[:, :E]); dsv_moe_glue.sycl:442-470 (x @ W^T)
+  * expert blob            glm/xpu/exl3xpu/moe_offload.py:68-94 (planar4, pack_expert); glm/xpu/pack_store.py:35-60
+                           (blob_perm); glm/xpu/csrc/exl3_moe.n128.sycl:56-68 (Geom byte offsets)
   * align / pair lists     glm/xpu/csrc/exl3_moe.n128.sycl:691-734
 
 Every floating-point reduction here runs in float64 unless a caller asks for float32 (`acc`), so the oracle is at
@@ -384,3 +386,33 @@ def align(ids: np.ndarray, w: np.ndarray, E: int, pad: int = 1):
                 act_cnt=cnt[act].astype(np.int32), n_act=np.int32(act.size), act_pstart=pstart[act].astype(np.int32),
                 pair_tok=(order // topk).astype(np.int32), pair_w=w.reshape(-1)[order].astype(np.float32),
                 pair_of=pair_of.astype(np.int32), count=cnt.astype(np.int32))
+
+
+# ------------------------------------------------------------------------------------------------ expert blob
+
+
+def planar4_words(tr: np.ndarray, K: int) -> np.ndarray:
+    """int16 trellis [rows, tiles, 16K] -> uint32 words in the reference's PLANAR4 order: a tile is G periods of D
+    words (D = K / gcd(K, 32), G = 8K / D); groups of 4 consecutive tiles are stored plane by plane, [D][4][G]
+    (moe_offload.py:68-78, pack_store.py:41-54). D = 1 (K = 2, 4, 8) leaves the words in tile order."""
+    rows, tiles, _ = tr.shape
+    D = K // math.gcd(K, 32)
+    G = 8 * K // D
+    w = np.ascontiguousarray(tr).view(np.uint32).reshape(rows, tiles // 4, 4, G, D)
+    return w.transpose(0, 1, 4, 2, 3).reshape(-1)
+
+
+def reference_blob(gate: dict, up: dict, down: dict, K: int) -> np.ndarray:
+    """The reference's expert blob bytes (pack_expert, moe_offload.py:81-94): planar4(gate|up trellis concatenated
+    along the columns), planar4(down), then gate.suh, up.suh, gate.svh, up.svh, down.suh, down.svh (fp16)."""
+    gu = np.concatenate([gate["trellis"], up["trellis"]], axis=1)
+    parts = [planar4_words(gu, K).view(np.uint8), planar4_words(down["trellis"], K).view(np.uint8)]
+    for v in (gate["suh"], up["suh"], gate["svh"], up["svh"], down["suh"], down["svh"]):
+        parts.append(np.ascontiguousarray(v, dtype=np.float16).view(np.uint8))
+    return np.concatenate(parts)
+
+
+def reference_geom_bytes(H: int, I: int, K: int) -> int:
+    """Geom::blob() (exl3_moe.n128.sycl:56-68): gate|up and down trellis words, then six fp16 vectors."""
+    W = 8 * K
+    return (H // 16) * (2 * I // 16) * W * 4 + (I // 16) * (H // 16) * W * 4 + 2 * (3 * H + 3 * I)

@@ -1,0 +1,118 @@
+"""Expert records and the record store (host side), the reference's expert blob unpacked (against the oracle's
+restatement of its packer), and (GPU) the arena-packed experts giving the same layer outputs as separately allocated
+ones."""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3_oracle as O
+
+blob = importlib.import_module("b70-inference_amd.blob")
+synth = importlib.import_module("b70-inference_amd.synth")
+
+
+def _expert(H, I, Kgu, Kd, seed):
+    g = synth.linear(H, I, Kgu, seed)
+    u = synth.linear(H, I, Kgu, seed + 1)
+    d = synth.linear(I, H, Kd, seed + 2)
+    return [{"trellis": t, "suh": su, "svh": sv} for t, su, sv in (g, u, d)]
+
+
+def test_reference_planar4_is_a_permutation_and_identity_for_even_k():
+    """The reference's own check (pack_store.py:58) and its K = 4 note (moe_offload.py:71-73)."""
+    for K in (2, 3, 4, 5, 6, 7, 8):
+        idx = np.arange(2 * 8 * 8 * K, dtype=np.uint32)
+        tr32 = idx.view(np.int16).reshape(2, 8, 16 * K)
+        w = O.planar4_words(tr32, K)
+        assert np.array_equal(np.sort(w), idx)
+        if K in (2, 4, 8):
+            assert np.array_equal(w, idx)
+        else:
+            assert not np.array_equal(w, idx)
+
+
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
+def test_unpack_reference_blob_round_trip(K):
+    H, I = 256, 128
+    gate, up, down = _expert(H, I, K, K, 700 + K)
+    b = O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in (gate, up, down)], K)
+    assert b.size == O.reference_geom_bytes(H, I, K)
+    g2, u2, d2 = blob.unpack_reference_blob(torch.from_numpy(b), H, I, K)
+    for a, r in ((gate, g2), (up, u2), (down, d2)):
+        for kind in ("trellis", "suh", "svh"):
+            assert torch.equal(a[kind], r[kind]), kind
+
+
+def test_record_pack_views_and_arena_layout():
+    H, I, Kgu, Kd = 256, 384, 2, 3
+    geom = blob.RecordGeom(H, I, Kgu, Kd)
+    assert geom.bytes % 4096 == 0
+    offs = sorted(v[0] for v in geom.sections.values())
+    assert offs[0] == 0 and all(o % 256 == 0 for o in offs)
+    experts = [_expert(H, I, Kgu, Kd, 800 + 10 * e) for e in range(3)]
+    arena = blob.ExpertArena(3, geom, device="cpu")
+    for e, ex in enumerate(experts):
+        arena.put(e, *ex)
+    for e, views in enumerate(arena.experts()):
+        for src, v in zip(experts[e], views):
+            assert torch.equal(src["trellis"], v.trellis)
+            assert torch.equal(src["suh"], v.suh) and torch.equal(src["svh"], v.svh)
+    tabs = arena.tables()
+    assert tabs.layout is not None                       # uniform strides: base + e * record bytes
+    assert list(tabs.layout)[9:] == [geom.bytes] * 9
+    assert (tabs.K_gate, tabs.K_up, tabs.K_down) == (Kgu, Kgu, Kd)
+    with pytest.raises(RuntimeError):
+        blob.pack_expert(experts[0][0], experts[0][1], experts[0][0], geom)    # down shape wrong
+
+
+def test_store_write_verify_load(tmp_path):
+    H, I = 256, 128
+    g1, g2 = blob.RecordGeom(H, I, 3), blob.RecordGeom(H, I, 2, 3)
+    l1 = [_expert(H, I, 3, 3, 900 + 10 * e) for e in range(4)]
+    l2 = [_expert(H, I, 2, 3, 950 + 10 * e) for e in range(2)]
+    path = str(tmp_path / "experts")
+    man = blob.write_store(path, [(g1, l1), (g2, l2)])
+    assert man["layers"][1]["offset"] == 4 * g1.bytes
+    assert blob.verify_store(path) == []
+    arena = blob.load_layer(path, 1, device="cpu")
+    views = arena.experts()
+    for e in range(2):
+        for src, v in zip(l2[e], views[e]):
+            assert torch.equal(src["trellis"], v.trellis)
+    # a flipped byte in layer 0, expert 2 is found, and loading that layer refuses
+    with open(path + ".bin", "r+b") as f:
+        f.seek(2 * g1.bytes + 1000)
+        c = f.read(1)
+        f.seek(2 * g1.bytes + 1000)
+        f.write(bytes([c[0] ^ 1]))
+    assert blob.verify_store(path) == [(0, 2)]
+    with pytest.raises(RuntimeError):
+        blob.load_layer(path, 0, device="cpu")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [3, 40])
+def test_arena_experts_same_outputs(exl3, M):
+    """Arena-packed experts (uniform-stride tables) and separately allocated copies give bit-identical layers."""
+    E, H, I = 6, 256, 256
+    geom = blob.RecordGeom(H, I, 3)
+    experts = [_expert(H, I, 3, 3, 1000 + 10 * e) for e in range(E)]
+    arena = blob.ExpertArena(E, geom, device="cuda")
+    for e, ex in enumerate(experts):
+        arena.put(e, *ex)
+    t_arena = arena.tables()
+    assert t_arena.layout is not None
+
+    def lin(p):
+        return exl3.BC_LinearEXL3(p["trellis"].cuda(), p["suh"].cuda(), p["svh"].cuda(), 3, None, False, True, None)
+
+    t_sep = exl3.ExpertTables([lin(x[0]) for x in experts], [lin(x[1]) for x in experts],
+                              [lin(x[2]) for x in experts])
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, H, generator=g).half().cuda()
+    logits = torch.randn(M, E, generator=g).cuda()
+    a = exl3.moe_forward_logits(x, logits, 2, t_arena)
+    b = exl3.moe_forward_logits(x, logits, 2, t_sep)
+    assert torch.equal(a, b)
