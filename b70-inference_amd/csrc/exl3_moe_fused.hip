@@ -815,7 +815,12 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.out = m.out;
     a.out_ld = m.out_ld;
     a.out_f32 = m.out_f32;
-    const int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
+    // rows per item: up to the batch size, but at most 2 when the routing is sparse (pairs <= E / 4: an expert rarely
+    // takes more than one row, and the 2-row variant needs fewer registers and less LDS than the 4- and 8-row ones)
+    int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
+    if (MR > 2 && (int64_t)m.M * m.slots * 4 <= m.E) MR = 2;
+    const int mr_env = env_int("EXL3MI_FUSED_MR", 0);
+    if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) MR = mr_env;
     const int kbf = MR <= 4 ? 8 : 4;
     fused_fn fn;
     switch (MR) {
