@@ -33,6 +33,7 @@ namespace exl3 {
 
 constexpr int kFusedMaxPairs = 128;
 constexpr int kFusedMaxRows = 8;
+constexpr int kFusedMinJobRows = 20;    // tile-rows of H per gate|up job, at least
 constexpr int kSpinMax = 1 << 20;       // polls of a down job's wait (each backs off up to ~512 cycles)
 constexpr int kCS = 32;                 // counter stride in ints (one 128-byte line per counter)
 #ifndef EXL3_FUSED_RING
@@ -834,14 +835,18 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     int mi = (a.np + active * (MR - 1)) / MR;
     a.max_items = mi < a.np ? mi : a.np;
     const int nbI = a.I / 128, nbH = a.H / 128;
-    // gate|up jobs: about one per workgroup the device holds at once (EXL3MI_FUSED_JOBS overrides); the grid adds one
+    // gate|up jobs: at most one per workgroup the device holds at once (EXL3MI_FUSED_JOBS overrides); the grid adds one
     // item's worth of workgroups for the last item's down jobs. Down jobs split I only as far as the staged blocks
     // need: an unsplit down job writes its rows directly, with no partial-sum round trip.
     int resident = 0;
     int rc = resident_blocks(reinterpret_cast<const void*>(fn), 256, &resident);
     if (rc) return rc;
     const int target = env_int("EXL3MI_FUSED_JOBS", resident);
-    a.P_gu = fused_splits(target / (a.max_items * nbI), a.H / 16, kbf);
+    // gate|up jobs of at least kFusedMinJobRows tile-rows: more, shorter jobs add partial sums to every epilogue and,
+    // past the resident grid, queue behind each other
+    const int by_rows = a.H / 16 / kFusedMinJobRows > 1 ? a.H / 16 / kFusedMinJobRows : 1;
+    const int by_grid = target / (a.max_items * nbI);
+    a.P_gu = fused_splits(env_int("EXL3MI_FUSED_PGU", by_grid < by_rows ? by_grid : by_rows), a.H / 16, kbf);
     a.GU = nbI * a.P_gu;
     a.P_d = fused_splits(1, a.I / 16, kbf);
     a.DN = nbH * a.P_d;
