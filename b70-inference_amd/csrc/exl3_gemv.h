@@ -12,6 +12,7 @@ namespace exl3 {
 
 constexpr int kGemvKBMax = 8;        // Hadamard blocks (128 k) per workgroup split
 constexpr int kGemvTargetWG = 1024;  // workgroups a GEMV launch aims for (256 CUs x 4); EXL3MI_TARGET_WG overrides
+constexpr int kGemvMaxSplits = 8;    // k-splits of a launch with up to 2 rows, at most (twice that for more rows)
 constexpr int kGemvMaxRows = 8;      // rows per GEMV pass
 #ifndef EXL3_LINEAR_RING
 #define EXL3_LINEAR_RING 3

@@ -232,10 +232,14 @@ static gemv_fn gemv_select(int K, int M, bool f32) {
     }
 }
 
-// Number of k-splits: enough workgroups to cover the chip, at most kGemvKBMax Hadamard blocks per split.
-static int gemv_splits(int strips, int nblk) {
+// Number of k-splits: enough workgroups to cover the chip, but at most kGemvMaxSplits (8 for up to 2 rows, 16 for
+// more: every split adds a partial row to the last workgroup's reduction, and more rows give each split more work to
+// hide it behind; measured over 1024² .. 21504 x 5376 at 1 and 4 rows) and at most kGemvKBMax blocks per split.
+static int gemv_splits(int strips, int nblk, int rows) {
     const int target = env_int("EXL3MI_TARGET_WG", kGemvTargetWG);
     int P = (target + strips - 1) / strips;
+    const int smax = env_int("EXL3MI_GEMV_MAX_SPLITS", rows <= 2 ? kGemvMaxSplits : 2 * kGemvMaxSplits);
+    if (P > smax) P = smax;
     int pmin = (nblk + kGemvKBMax - 1) / kGemvKBMax;
     if (P < pmin) P = pmin;
     if (P > nblk) P = nblk;
@@ -252,7 +256,7 @@ int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uin
                 int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh,
                 hipStream_t st) {
     const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
-    const int P = gemv_splits(strips, nblk);
+    const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
     const int Mmax = kGemvMaxRows;
     Workspace ws;
     int rc = workspace((size_t)strips * P * Mmax * 128 * sizeof(float), (size_t)strips, &ws);
