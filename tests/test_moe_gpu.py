@@ -121,6 +121,22 @@ def test_moe_per_projection_k(exl3, oracle, Kgu, Kd):
     assert max_rel(y, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("Kgu,Kd", [(2, 3), (3, 4), (1, 3), (6, 8), (4, 3)])
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_moe_mixed_bitrate_decode_paths(exl3, oracle, monkeypatch, Kgu, Kd, M):
+    """Gate/up and down at different bitrates on the fused decode layer (down one or two bits above gate/up) and on
+    the multi-kernel path (every other combination, or forced): both match the oracle, with the shared expert."""
+    tables, orc = make_experts(exl3, oracle, 7, 256, 384, Kgu, Kd, 1400 + 10 * Kgu + Kd)
+    ids, w = _ids_w(M, 3, 6, 1401 + M)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(1402 + M)).half()
+    ref = oracle.moe_layer(x.numpy(), orc[:6], ids.numpy(), w.numpy(), oracle.ACT_SILU, 0.0, orc[6])
+    y = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables, shared=6).cpu().numpy()
+    assert max_rel(y, ref) <= MAX_REL
+    monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    y2 = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables, shared=6).cpu().numpy()
+    assert max_rel(y2, ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("Ks,probs", [((1, 2), (0.38, 0.62)), ((1, 2, 3, 4, 5, 6, 7, 8), (0.125,) * 8)])
 def test_moe_per_tile_k(exl3, oracle, Ks, probs):
     tables, orc = make_experts(exl3, oracle, 5, 256, 384, 0, 0, 900, per_tile=(Ks, probs))
