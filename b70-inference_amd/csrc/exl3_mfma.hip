@@ -24,11 +24,41 @@
 namespace exl3 {
 
 // ------------------------------------------------------------------------------------------------ input transform
-// Workgroup (row block, 128-column block kb of H): every row's x block times suh_gate and suh_up, Hadamard, fp16
-// (the GEMM inputs xh) and their block sums (xsum). The block's token list and both sign vectors are loaded once;
-// each wave then takes 4 rows at a time with all their x loads in flight before the first transform.
+// Eight consecutive fp16 values: one 16-byte load when the address allows it (a wave-uniform choice), else eight.
+__device__ __forceinline__ h8_t load_h8(const uint16_t* p, bool vec) {
+    if (vec) return __builtin_bit_cast(h8_t, ldg(reinterpret_cast<const u32x4_t*>(p)));
+    h8_t v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_bit_cast(_Float16, ldg(p + j));
+    return v;
+}
+
+// B fragment (v_mfma_f32_16x16x32_f16 layout: lane L holds column n = L & 15, rows k = 8 (L >> 4) + j) of the 128-point
+// Hadamard matrix H[K][N] = (-1)^popcount(K & N) for K in 32 ks + [0, 32), N in 16 nb + [0, 16). popcount(K & N)
+// splits into popcount(k & n) (bits 0-3), bit 4 of k with bit 0 of nb, and bits 0-1 of ks with bits 1-2 of nb: the
+// fragment is F_{nb & 1} (lane-dependent, bit 4 of k = L >> 5) times the sign S(ks, nb), a compile-time constant.
+__device__ __forceinline__ h8_t had_fragment(int lane, int p) {
+    const int n = lane & 15, k0 = 8 * (lane >> 4);
+    h8_t f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int odd = (__builtin_popcount((unsigned)((k0 + j) & n)) + p * (lane >> 5)) & 1;
+        f[j] = odd ? (_Float16)-1.0f : (_Float16)1.0f;
+    }
+    return f;
+}
+__host__ __device__ constexpr bool had_sign_neg(int ks, int nb) {
+    return (((ks & 1) & ((nb >> 1) & 1)) ^ (((ks >> 1) & 1) & ((nb >> 2) & 1))) != 0;
+}
+
+// Workgroup (row block, 128-column block kb of H): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128),
+// fp16 (the GEMM inputs xh) and their block sums (xsum). Wave w takes rows 16 w .. 16 w + 15: A fragments are
+// fp16(x * suh) (packed fp16 multiplies, one rounding: the reference's fp16(x * suh)), the Hadamard is 8 output tiles
+// x 4 k-steps of v_mfma_f32_16x16x32_f16 against the two base fragments (fp32 accumulation of exact +-x products),
+// and the sums of the fp16-rounded outputs reduce over the 16 lanes of a row.
 __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     __shared__ int s_tok[kMfmaRows];
+    __shared__ __attribute__((aligned(16))) _Float16 s_out[4][16][136];    // per wave: 16 rows x 128 (+ pad)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int blk = blockIdx.x, kb = blockIdx.y;
     const ItemDesc* d = a.blocks + blk;
@@ -37,37 +67,68 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     const int p0 = d->p0;
     const int nblk = a.H / 128;
     if (threadIdx.x < cnt) s_tok[threadIdx.x] = a.pair_tok[p0 + threadIdx.x];
-    const uint16_t* sg = reinterpret_cast<const uint16_t*>(d->tab[1]) + kb * 128;
-    const uint16_t* su = reinterpret_cast<const uint16_t*>(d->tab[4]) + kb * 128;
-    const float g0 = h2f(ldg(sg + lane)), g1 = h2f(ldg(sg + lane + 64));
-    const float u0 = h2f(ldg(su + lane)), u1 = h2f(ldg(su + lane + 64));
     __syncthreads();
-    constexpr int RB = 4;
-    for (int r0 = wave; r0 < cnt; r0 += 4 * RB) {
-        float xa[RB], xb[RB];
+    const int r0 = 16 * wave;
+    if (r0 >= cnt) return;
+    const int m = lane & 15, g = lane >> 4;
+    const int row = r0 + m < cnt ? r0 + m : cnt - 1;          // rows past cnt repeat the last one (not stored)
+    const uint16_t* xr = a.x + (int64_t)s_tok[row] * a.x_ld + kb * 128 + 8 * g;
+    const bool vx = ((uintptr_t)a.x & 15) == 0 && (a.x_ld & 7) == 0;
+    h8_t xv[4];
 #pragma unroll
-        for (int k = 0; k < RB; ++k) {
-            const int row = r0 + 4 * k < cnt ? r0 + 4 * k : r0;   // unconditional load (repeats row r0, unused)
-            const uint16_t* x = a.x + (int64_t)s_tok[row] * a.x_ld + kb * 128;
-            xa[k] = h2f(ldg(x + lane));
-            xb[k] = h2f(ldg(x + lane + 64));
+    for (int ks = 0; ks < 4; ++ks) xv[ks] = load_h8(xr + 32 * ks, vx);
+    const h8_t F[2] = {had_fragment(lane, 0), had_fragment(lane, 1)};
+#pragma unroll
+    for (int proj = 0; proj < 2; ++proj) {
+        const uint16_t* sv = reinterpret_cast<const uint16_t*>(d->tab[proj ? 4 : 1]) + kb * 128 + 8 * g;
+        const bool vs = ((uintptr_t)sv & 15) == 0;
+        h8_t A[4], An[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            A[ks] = xv[ks] * load_h8(sv + 32 * ks, vs);
+            An[ks] = -A[ks];
         }
+        f4_t acc[8];
 #pragma unroll
-        for (int k = 0; k < RB; ++k) {
-            const int row = r0 + 4 * k;
-            if (row >= cnt) break;
+        for (int nb = 0; nb < 8; ++nb) {
+            acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int proj = 0; proj < 2; ++proj) {
-                float va = (float)(_Float16)(xa[k] * (proj ? u0 : g0));
-                float vb = (float)(_Float16)(xb[k] * (proj ? u1 : g1));
-                fwht128_wave(va, vb, lane);
-                const _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
-                _Float16* dst = a.xh + ((size_t)(p0 + row) * 2 + proj) * a.H + kb * 128;
-                dst[lane] = ha;
-                dst[lane + 64] = hb;
-                const float bs = wave_sum_f32((float)ha + (float)hb);
-                if (lane == 0) a.xsum[((size_t)(p0 + row) * 2 + proj) * nblk + kb] = bs;
+            for (int ks = 0; ks < 4; ++ks)
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(had_sign_neg(ks, nb) ? An[ks] : A[ks], F[nb & 1],
+                                                                 acc[nb], 0, 0, 0);
+        }
+        // lane holds rows 4 g + i (i < 4) of the wave's 16 at column 16 nb + m: through the wave's LDS tile to
+        // 16-byte row stores
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 h = (_Float16)(acc[nb][i] * kRsqrt128);
+                part[i] += (float)h;
+                s_out[wave][4 * g + i][16 * nb + m] = h;
             }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;          // row rr of 16, 16-byte chunk ch
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_out[wave][rr][8 * ch]);
+            if (r0 + rr < cnt)
+                *reinterpret_cast<u32x4_t*>(a.xh + ((size_t)(p0 + r0 + rr) * 2 + proj) * a.H + kb * 128 + 8 * ch) = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = part[i];
+            v += __shfl_xor(v, 1);
+            v += __shfl_xor(v, 2);
+            v += __shfl_xor(v, 4);
+            v += __shfl_xor(v, 8);
+            if (m == 0 && r0 + 4 * g + i < cnt) a.xsum[((size_t)(p0 + r0 + 4 * g + i) * 2 + proj) * nblk + kb] = v;
         }
     }
 }
