@@ -1105,7 +1105,7 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     const int RGA = m <= 16 ? 1 : m <= 32 ? 2 : 4;
     const int R = 16 * RGA;
     const int nblk = (int)(k / 128);
-    if (m > 0x7FFFFFFF / 64 || k > 0x7FFFFFFF || n > 0x7FFFFFFF)
+    if (m > 0x7FFFFFFF / 64 || k > 0x7FFFFFFF || n > 0x7FFFFFFF || nblk > 65535)
         return fail(EXL3_ERR_INVALID, "exl3_gemm: shape too large");
     LinArgs a;
     a.m = (int)m;
@@ -1134,6 +1134,7 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     _Float16* xh = cv.take<_Float16>((size_t)S * m * k);
     float* xsum = cv.take<float>((size_t)S * m * nblk);
     a.part = a.P > 1 ? cv.take<float>((size_t)a.P * m * n) : nullptr;
+    if (!xh || !xsum || (a.P > 1 && !a.part)) return fail(EXL3_ERR_INVALID, "exl3_gemm: workspace carve failed");
     a.xh = xh;
     a.xsum = xsum;
     a.S = S;
@@ -1143,9 +1144,8 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     a.out = C;
     a.out_ld = c_ld;
     a.f32 = f32 ? 1 : 0;
-    EXL3_LAUNCH("linear_had", linear_had_kernel, dim3((unsigned)((m + 15) / 16), (unsigned)nblk, (unsigned)S), dim3(256),
-                0, st, A,
-                a_ld, (int)m, (int)k, suh, xh, xsum);
+    const dim3 hgrid((unsigned)((m + 15) / 16), (unsigned)nblk, (unsigned)S);
+    EXL3_LAUNCH("linear_had", linear_had_kernel, hgrid, dim3(256), 0, st, A, a_ld, (int)m, (int)k, suh, xh, xsum);
     const int64_t nx = ((int64_t)a.nrb * a.P + 7) / 8 * 8 * a.ncb;
     if (nx > 0x7FFFFFFF) return fail(EXL3_ERR_INVALID, "exl3_gemm: grid too large");
     EXL3_LAUNCH("linear_mfma", fn, dim3((unsigned)nx), dim3(256), 0, st, a);
