@@ -51,6 +51,52 @@ __host__ __device__ constexpr bool had_sign_neg(int ks, int nb) {
     return (((ks & 1) & ((nb >> 1) & 1)) ^ (((ks >> 1) & 1) & ((nb >> 2) & 1))) != 0;
 }
 
+// fp16(H128(fp16(x * s)) / sqrt(128)) of one wave's 16 rows: xv holds the rows' x in A-fragment layout (lane L: row
+// L & 15, columns 32 ks + 8 (L >> 4) + j), sv points at s + 8 (L >> 4) (16-byte loads when vs). The results go to the
+// wave's LDS tile (16 x 128 fp16) and part[i] gets the sum of the fp16 results of row 4 (L >> 4) + i over this lane's
+// 8 columns (the caller reduces over the 16 lanes of a row).
+__device__ __forceinline__ void had16_rows(const h8_t (&xv)[4], const uint16_t* sv, bool vs, const h8_t (&F)[2],
+                                           int lane, _Float16 (*tile)[136], float (&part)[4]) {
+    const int m = lane & 15, g = lane >> 4;
+    h8_t A[4], An[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        A[ks] = xv[ks] * load_h8(sv + 32 * ks, vs);
+        An[ks] = -A[ks];
+    }
+    f4_t acc[8];
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) {
+        acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(had_sign_neg(ks, nb) ? An[ks] : A[ks], F[nb & 1],
+                                                             acc[nb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[i] = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const _Float16 h = (_Float16)(acc[nb][i] * kRsqrt128);
+            part[i] += (float)h;
+            tile[4 * g + i][16 * nb + m] = h;
+        }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sum of v over the 16 lanes of a row (lanes with equal L >> 4).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    return v;
+}
+
 // Workgroup (row block, 128-column block kb of H): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128),
 // fp16 (the GEMM inputs xh) and their block sums (xsum). Wave w takes rows 16 w .. 16 w + 15: A fragments are
 // fp16(x * suh) (packed fp16 multiplies, one rounding: the reference's fp16(x * suh)), the Hadamard is 8 output tiles
@@ -81,55 +127,23 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
 #pragma unroll
     for (int proj = 0; proj < 2; ++proj) {
         const uint16_t* sv = reinterpret_cast<const uint16_t*>(d->tab[proj ? 4 : 1]) + kb * 128 + 8 * g;
-        const bool vs = ((uintptr_t)sv & 15) == 0;
-        h8_t A[4], An[4];
+        float part[4];
+        had16_rows(xv, sv, ((uintptr_t)sv & 15) == 0, F, lane, s_out[wave], part);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            A[ks] = xv[ks] * load_h8(sv + 32 * ks, vs);
-            An[ks] = -A[ks];
-        }
-        f4_t acc[8];
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb) {
-            acc[nb] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(had_sign_neg(ks, nb) ? An[ks] : A[ks], F[nb & 1],
-                                                                 acc[nb], 0, 0, 0);
-        }
-        // lane holds rows 4 g + i (i < 4) of the wave's 16 at column 16 nb + m: through the wave's LDS tile to
-        // 16-byte row stores
-        float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int nb = 0; nb < 8; ++nb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const _Float16 h = (_Float16)(acc[nb][i] * kRsqrt128);
-                part[i] += (float)h;
-                s_out[wave][4 * g + i][16 * nb + m] = h;
-            }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;          // row rr of 16, 16-byte chunk ch
+        for (int c = 0; c < 4; ++c) {                   // 16-byte row stores from the tile
+            const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;
             const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_out[wave][rr][8 * ch]);
             if (r0 + rr < cnt)
                 *reinterpret_cast<u32x4_t*>(a.xh + ((size_t)(p0 + r0 + rr) * 2 + proj) * a.H + kb * 128 + 8 * ch) = v;
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float v = part[i];
-            v += __shfl_xor(v, 1);
-            v += __shfl_xor(v, 2);
-            v += __shfl_xor(v, 4);
-            v += __shfl_xor(v, 8);
+            const float v = row16_sum(part[i]);
             if (m == 0 && r0 + 4 * g + i < cnt) a.xsum[((size_t)(p0 + r0 + 4 * g + i) * 2 + proj) * nblk + kb] = v;
         }
+        __builtin_amdgcn_wave_barrier();                // the tile is rewritten by the next projection
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
@@ -805,6 +819,7 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix
 // straight into MFMA B fragments once per row block (up to 64 rows), as in the reference's large-M linear
 // (glm/xpu/csrc/exl3_ops.sycl:643-757), which reconstructs 16384-column fp16 slices and runs a GEMM instead.
 //   linear_had   xh[s][m][k] = fp16(H128(fp16(x * suh[s])) / sqrt(128)) and the 128-blocks' sums xsum[s][m][k / 128]
+//                (the Hadamard on MFMA, as in the MoE input transform; 16 rows per wave)
 //                for every shard s (a fused multi-projection linear: output column blocks of S projections that share
 //                the input, each with its own input signs suh[s]; shard_of_nb maps 128-column blocks to shards)
 //   linear_mfma  workgroup per (row block, k-split, 256-column block); a wave owns four tile columns. With one split
@@ -827,34 +842,35 @@ struct LinArgs {
 
 __global__ __launch_bounds__(256) void linear_had_kernel(const uint16_t* __restrict__ x, int64_t x_ld, int m, int k,
                                                          const uint16_t* __restrict__ suh, _Float16* xh, float* xsum) {
+    __shared__ __attribute__((aligned(16))) _Float16 s_out[4][16][136];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kb = blockIdx.y, nblk = k / 128;
     suh += (size_t)blockIdx.z * k;                               // shard s = blockIdx.z
     xh += (size_t)blockIdx.z * m * k;
     xsum += (size_t)blockIdx.z * m * nblk;
-    const int r0 = blockIdx.x * 16 + wave;
-    const float s0 = h2f(ldg(suh + kb * 128 + lane)), s1 = h2f(ldg(suh + kb * 128 + lane + 64));
-    constexpr int RB = 4;
-    float xa[RB], xb[RB];
+    const int r0 = blockIdx.x * 64 + 16 * wave;                  // this wave's 16 rows
+    if (r0 >= m) return;
+    const int mm = lane & 15, g = lane >> 4;
+    const int row = r0 + mm < m ? r0 + mm : m - 1;               // rows past m repeat the last one (not stored)
+    const uint16_t* xr = x + (int64_t)row * x_ld + kb * 128 + 8 * g;
+    const bool vx = ((uintptr_t)x & 15) == 0 && (x_ld & 7) == 0;
+    h8_t xv[4];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) {
-        const int row = r0 + 4 * j < m ? r0 + 4 * j : m - 1;     // unconditional loads (clamped, unused past m)
-        const uint16_t* xr = x + (int64_t)row * x_ld + kb * 128;
-        xa[j] = h2f(ldg(xr + lane));
-        xb[j] = h2f(ldg(xr + lane + 64));
+    for (int ks = 0; ks < 4; ++ks) xv[ks] = load_h8(xr + 32 * ks, vx);
+    const h8_t F[2] = {had_fragment(lane, 0), had_fragment(lane, 1)};
+    const uint16_t* sv = suh + kb * 128 + 8 * g;
+    float part[4];
+    had16_rows(xv, sv, ((uintptr_t)sv & 15) == 0, F, lane, s_out[wave], part);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_out[wave][rr][8 * ch]);
+        if (r0 + rr < m) *reinterpret_cast<u32x4_t*>(xh + (size_t)(r0 + rr) * k + kb * 128 + 8 * ch) = v;
     }
 #pragma unroll
-    for (int j = 0; j < RB; ++j) {
-        const int row = r0 + 4 * j;
-        if (row >= m) break;
-        float va = (float)(_Float16)(xa[j] * s0), vb = (float)(_Float16)(xb[j] * s1);
-        fwht128_wave(va, vb, lane);
-        const _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
-        _Float16* dst = xh + (size_t)row * k + kb * 128;
-        dst[lane] = ha;
-        dst[lane + 64] = hb;
-        const float bs = wave_sum_f32((float)ha + (float)hb);
-        if (lane == 0) xsum[(size_t)row * nblk + kb] = bs;
+    for (int i = 0; i < 4; ++i) {
+        const float v = row16_sum(part[i]);
+        if (mm == 0 && r0 + 4 * g + i < m) xsum[(size_t)(r0 + 4 * g + i) * nblk + kb] = v;
     }
 }
 
@@ -1144,7 +1160,7 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     a.out = C;
     a.out_ld = c_ld;
     a.f32 = f32 ? 1 : 0;
-    const dim3 hgrid((unsigned)((m + 15) / 16), (unsigned)nblk, (unsigned)S);
+    const dim3 hgrid((unsigned)((m + 63) / 64), (unsigned)nblk, (unsigned)S);
     EXL3_LAUNCH("linear_had", linear_had_kernel, hgrid, dim3(256), 0, st, A, a_ld, (int)m, (int)k, suh, xh, xsum);
     const int64_t nx = ((int64_t)a.nrb * a.P + 7) / 8 * 8 * a.ncb;
     if (nx > 0x7FFFFFFF) return fail(EXL3_ERR_INVALID, "exl3_gemm: grid too large");
