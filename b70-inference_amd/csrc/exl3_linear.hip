@@ -111,7 +111,25 @@ struct GemvArgs {
     int* cnt;
     int P;
     int nblk;
+    // multi-matrix mode (exl3_mgemm; trp == null otherwise): slot z = blockIdx.z runs matrix q = idx[z] (z without
+    // idx; with qmin >= 0 only q in [qmin, qmax), rebased by qmin; slots whose q falls outside [0, nmat) are skipped)
+    // on A batch z / a_div (x_bs = 0 broadcasts) into out + z * out_bs, with its own partials and counters
+    const int64_t* trp;
+    const int64_t* suhp;
+    const int64_t* svhp;
+    const int64_t* idx;
+    int nmat;
+    int a_div;
+    int64_t qmin, qmax;
+    int64_t x_bs, out_bs;
 };
+
+// Matrix of multi-matrix slot z (-1: skipped).
+__device__ __forceinline__ int64_t mgemm_matrix(const int64_t* idx, int z, int64_t qmin, int64_t qmax, int nmat) {
+    int64_t q = idx ? idx[z] : z;
+    if (qmin >= 0) q = (q >= qmin && q < qmax) ? q - qmin : -1;
+    return (q >= 0 && q < nmat) ? q : -1;
+}
 
 template <int K, int M, bool F32>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
@@ -120,11 +138,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     __shared__ float bsum[M][kGemvKBMax];
     __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int strip = blockIdx.x, p = blockIdx.y;
+    const int strip = blockIdx.x, p = blockIdx.y, z = blockIdx.z;
+    const uint32_t* tr = a.tr;
+    const uint16_t* suh_all = a.suh;
+    const uint16_t* svh = a.svh;
+    if (a.trp) {
+        const int64_t q = mgemm_matrix(a.idx, z, a.qmin, a.qmax, a.nmat);
+        if (q < 0) return;                                          // uniform: the whole workgroup leaves
+        tr = reinterpret_cast<const uint32_t*>(a.trp[q]);
+        suh_all = reinterpret_cast<const uint16_t*>(a.suhp[q]);
+        svh = reinterpret_cast<const uint16_t*>(a.svhp[q]);
+    }
+    const uint16_t* x = a.x + (int64_t)(z / a.a_div) * a.x_bs;
+    float* part = a.part + (size_t)z * gridDim.x * a.P * M * 128;
+    int* cnt = a.cnt + (size_t)z * gridDim.x;
     const int b0 = (int)((int64_t)p * a.nblk / a.P), b1 = (int)((int64_t)(p + 1) * a.nblk / a.P);
     const int kb = b1 - b0;
     const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
-    const uint32_t* sp = a.tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
+    const uint32_t* sp = tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
     StripRing<K, kLinearRing> ring;
     strip_prefetch<K, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, ring);   // weight loads in flight during phase 1
 
@@ -135,11 +166,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         shard = a.sonb[strip];
         shard = shard < 0 ? 0 : (shard >= a.S ? a.S - 1 : shard);
     }
-    const uint16_t* suh = a.suh + (size_t)shard * (a.nblk * 128);
+    const uint16_t* suh = suh_all + (size_t)shard * (a.nblk * 128);
     for (int i = wave; i < M * kb; i += 4) {
         const int m = i / kb, b = i - m * kb;
         const int k0 = (b0 + b) * 128;
-        float s = had_in_block(m < a.m ? a.x + (int64_t)m * a.x_ld + k0 : nullptr, suh + k0, &xs[m][b * 128], lane);
+        float s = had_in_block(m < a.m ? x + (int64_t)m * a.x_ld + k0 : nullptr, suh + k0, &xs[m][b * 128], lane);
         if (lane == 0) bsum[m][b] = s;
     }
     __syncthreads();
@@ -158,7 +189,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     const int cbase = 16 * (lane >> 3) + (lane & 7);
-    float* mypart = a.part + ((size_t)strip * a.P + p) * M * 128;
+    float* mypart = part + ((size_t)strip * a.P + p) * M * 128;
     if (wave == 0) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
@@ -171,30 +202,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
             }
         }
     }
-    if (!splitk_arrive(&a.cnt[strip], a.P, &s_last)) return;
+    if (!splitk_arrive(&cnt[strip], a.P, &s_last)) return;
     for (int m = wave; m < M && m < a.m; m += 4) {
         float va = 0.f, vb = 0.f;
 #pragma unroll 8
         for (int pp = 0; pp < a.P; ++pp) {
-            const float* q = a.part + (((size_t)strip * a.P + pp) * M + m) * 128;
+            const float* q = part + (((size_t)strip * a.P + pp) * M + m) * 128;
             va += splitk_load(q + lane);
             vb += splitk_load(q + lane + 64);
         }
         fwht128_wave(va, vb, lane);
         const int c0 = strip * 128 + lane, c1 = c0 + 64;
-        va *= kRsqrt128 * h2f(ldg(a.svh + c0));
-        vb *= kRsqrt128 * h2f(ldg(a.svh + c1));
+        va *= kRsqrt128 * h2f(ldg(svh + c0));
+        vb *= kRsqrt128 * h2f(ldg(svh + c1));
         if (F32) {
-            float* o = reinterpret_cast<float*>(a.out) + (int64_t)m * a.out_ld;
+            float* o = reinterpret_cast<float*>(a.out) + z * a.out_bs + (int64_t)m * a.out_ld;
             o[c0] = va;
             o[c1] = vb;
         } else {
-            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)m * a.out_ld;
+            uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + z * a.out_bs + (int64_t)m * a.out_ld;
             o[c0] = f2h(va);
             o[c1] = f2h(vb);
         }
     }
-    if (threadIdx.x == 0) a.cnt[strip] = 0;
+    if (threadIdx.x == 0) cnt[strip] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------ dispatch
@@ -252,37 +283,77 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
                        const uint16_t* svh, hipStream_t st);
 constexpr int kLinearMfmaMinRows = 9;
 
+// Launches over chunks of up to kGemvMaxRows rows of `ga` (x, out and m describe all rows; the workspace holds
+// slots x strips x P partial blocks and slots x strips counters).
+static int gemv_chunks(GemvArgs ga, int64_t m, int K, bool f32, int strips, int slots, hipStream_t st) {
+    const int Mmax = kGemvMaxRows;
+    for (int64_t m0 = 0; m0 < m; m0 += Mmax) {
+        const int mm = (int)((m - m0) < Mmax ? (m - m0) : Mmax);
+        GemvArgs c = ga;
+        c.x = ga.x + m0 * ga.x_ld;
+        c.m = mm;
+        c.out = f32 ? (void*)(reinterpret_cast<float*>(ga.out) + m0 * ga.out_ld)
+                    : (void*)(reinterpret_cast<uint16_t*>(ga.out) + m0 * ga.out_ld);
+        gemv_fn fn = gemv_select(K, mm, f32);
+        EXL3_LAUNCH("gemv", fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+    }
+    return EXL3_OK;
+}
+
 int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
                 int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh,
                 hipStream_t st) {
     const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
     const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
-    const int Mmax = kGemvMaxRows;
     Workspace ws;
-    int rc = workspace((size_t)strips * P * Mmax * 128 * sizeof(float), (size_t)strips, &ws);
+    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, &ws);
     if (rc) return rc;
-    for (int64_t m0 = 0; m0 < m; m0 += Mmax) {
-        const int mm = (int)((m - m0) < Mmax ? (m - m0) : Mmax);
-        GemvArgs ga;
-        ga.x = A + m0 * a_ld;
-        ga.x_ld = a_ld;
-        ga.m = mm;
-        ga.tr = tr;
-        ga.tn = tn;
-        ga.suh = suh;
-        ga.S = S;
-        ga.sonb = S > 1 ? sonb : nullptr;
-        ga.svh = svh;
-        ga.out = f32 ? (void*)(reinterpret_cast<float*>(C) + m0 * c_ld) : (void*)(reinterpret_cast<uint16_t*>(C) + m0 * c_ld);
-        ga.out_ld = c_ld;
-        ga.part = reinterpret_cast<float*>(ws.scratch);
-        ga.cnt = ws.counters;
-        ga.P = P;
-        ga.nblk = nblk;
-        gemv_fn fn = gemv_select(K, mm, f32);
-        EXL3_LAUNCH("gemv", fn, dim3(strips, P), dim3(256), 0, st, ga);
+    GemvArgs ga = {};
+    ga.x = A;
+    ga.x_ld = a_ld;
+    ga.tr = tr;
+    ga.tn = tn;
+    ga.suh = suh;
+    ga.S = S;
+    ga.sonb = S > 1 ? sonb : nullptr;
+    ga.svh = svh;
+    ga.out = C;
+    ga.out_ld = c_ld;
+    ga.part = reinterpret_cast<float*>(ws.scratch);
+    ga.cnt = ws.counters;
+    ga.P = P;
+    ga.nblk = nblk;
+    ga.a_div = 1;
+    return gemv_chunks(ga, m, K, f32, strips, 1, st);
+}
+
+// ------------------------------------------------------------------------------------------------ multi-matrix
+// Weighted slot sum of exl3_mgemm: C[t, e] = sum over the token's slots j in order of w[j] * y[j, e] (fp32; skipped
+// slots add nothing). Grid (ceil(m n / 256), tokens).
+template <bool F32>
+__global__ __launch_bounds__(256) void mgemm_sum_kernel(const float* __restrict__ y, int64_t mn,
+                                                        const int64_t* __restrict__ idx, int64_t qmin, int64_t qmax,
+                                                        int nmat, const uint16_t* __restrict__ w, int per_tok,
+                                                        void* __restrict__ out) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (e >= mn) return;
+    float v = 0.f;
+    for (int j0 = 0; j0 < per_tok; j0 += 8) {
+        float yv[8], wv[8];
+        bool ok[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {                 // every load of a group issued before the first add
+            const int jj = t * per_tok + (j0 + i < per_tok ? j0 + i : per_tok - 1);
+            ok[i] = j0 + i < per_tok && mgemm_matrix(idx, jj, qmin, qmax, nmat) >= 0;
+            yv[i] = y[(int64_t)jj * mn + e];
+            wv[i] = h2f(w[jj]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v += ok[i] ? wv[i] * yv[i] : 0.f;
     }
-    return EXL3_OK;
+    if (F32) reinterpret_cast<float*>(out)[(int64_t)t * mn + e] = v;
+    else reinterpret_cast<uint16_t*>(out)[(int64_t)t * mn + e] = f2h(v);
 }
 
 }  // namespace exl3
@@ -368,6 +439,84 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
               void* stream) {
     (void)A_had;
     return exl3_linear_sharded(A, a_ld, m, k, B, n, K, C, c_ld, c_dtype, suh, 1, nullptr, svh, cb, stream);
+}
+
+int exl3_mgemm(const uint16_t* A, int64_t a_batches, int64_t m, int64_t k, const int64_t* B_ptrs,
+               const int64_t* suh_ptrs, const int64_t* svh_ptrs, int64_t num_mats, int64_t n, int K, int cb,
+               const int64_t* indices, int64_t slots, const uint16_t* weights, int64_t num_tokens, int64_t min_index,
+               int64_t max_index, void* C, int c_dtype, void* stream) {
+    if (cb != 2) return fail(EXL3_ERR_UNSUPPORTED, "exl3_mgemm: codebook %d not supported (mul1 = 2 only)", cb);
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_mgemm: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(c_dtype == EXL3_F16 || c_dtype == EXL3_F32, "exl3_mgemm: C must be fp16 or fp32");
+    EXL3_CHECK_ARG(m >= 0 && k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0,
+                   "exl3_mgemm: k=%lld and n=%lld must be positive multiples of 128", (long long)k, (long long)n);
+    EXL3_CHECK_ARG(num_mats >= 1 && num_mats <= 0x7FFFFFFF, "exl3_mgemm: num_mats=%lld", (long long)num_mats);
+    EXL3_CHECK_ARG(slots >= 0 && slots <= 65535, "exl3_mgemm: slots=%lld not in 0..65535", (long long)slots);
+    EXL3_CHECK_ARG(indices || slots <= num_mats, "exl3_mgemm: without indices slot j uses matrix j (slots <= num_mats)");
+    const bool weighted = weights != nullptr;
+    EXL3_CHECK_ARG(!weighted || (num_tokens >= 1 && num_tokens <= 65535 && slots % num_tokens == 0),
+                   "exl3_mgemm: weighted sum needs 1 <= num_tokens <= 65535 dividing slots (%lld)", (long long)slots);
+    const int64_t per_tok = num_tokens >= 1 && slots % num_tokens == 0 ? slots / num_tokens : 0;
+    EXL3_CHECK_ARG(a_batches == 1 || a_batches == slots || (per_tok > 0 && a_batches == num_tokens),
+                   "exl3_mgemm: a_batches=%lld must be 1, slots (%lld) or num_tokens (%lld)", (long long)a_batches,
+                   (long long)slots, (long long)num_tokens);
+    EXL3_CHECK_ARG(min_index < 0 || max_index > min_index, "exl3_mgemm: max_index must exceed min_index");
+    EXL3_CHECK_ARG(n / 128 <= 65535, "exl3_mgemm: n too large");
+    EXL3_CHECK_ARG(k / 16 * (n / 16) * 8 * (int64_t)K < (1LL << 32),
+                   "exl3_mgemm: trellis of %lld x %lld at K=%d exceeds 2^32 words", (long long)k, (long long)n, K);
+    if (m == 0 || (slots == 0 && !weighted)) return EXL3_OK;
+    EXL3_CHECK_ARG(A && B_ptrs && suh_ptrs && svh_ptrs && C, "exl3_mgemm: null pointer");
+    const bool f32 = c_dtype == EXL3_F32;
+    hipStream_t st = (hipStream_t)stream;
+    const int strips = (int)(n / 128), nblk = (int)(k / 128);
+    const int P = gemv_splits(strips * (int)(slots > 0 ? slots : 1), nblk,
+                              m < kGemvMaxRows ? (int)m : kGemvMaxRows);
+    const size_t part_bytes = carve_size((size_t)slots * strips * P * kGemvMaxRows * 128, sizeof(float));
+    const size_t y_bytes = weighted ? carve_size((size_t)slots * m * n, sizeof(float)) : 0;
+    Workspace ws;
+    int rc = workspace(part_bytes + y_bytes, (size_t)(slots > 0 ? slots : 1) * strips, &ws);
+    if (rc) return rc;
+    Carve cv{ws.scratch, ws.scratch_bytes};
+    float* part = cv.take<float>((size_t)slots * strips * P * kGemvMaxRows * 128);
+    float* y = weighted ? cv.take<float>((size_t)slots * m * n) : nullptr;
+    if (!part || (weighted && !y)) return fail(EXL3_ERR_HIP, "exl3_mgemm: workspace carve failed");
+    if (slots > 0) {
+        GemvArgs ga = {};
+        ga.x = A;
+        ga.x_ld = k;
+        ga.tn = (int)(n / 16);
+        ga.S = 1;
+        ga.out = weighted ? (void*)y : C;
+        ga.out_ld = n;
+        ga.part = part;
+        ga.cnt = ws.counters;
+        ga.P = P;
+        ga.nblk = nblk;
+        ga.trp = B_ptrs;
+        ga.suhp = suh_ptrs;
+        ga.svhp = svh_ptrs;
+        ga.idx = indices;
+        ga.nmat = (int)num_mats;
+        ga.qmin = min_index;
+        ga.qmax = max_index;
+        ga.a_div = a_batches == 1 || a_batches == slots ? 1 : (int)per_tok;
+        ga.x_bs = a_batches == 1 ? 0 : m * k;
+        ga.out_bs = m * n;
+        rc = gemv_chunks(ga, m, K, weighted || f32, strips, (int)slots, st);
+        if (rc) return rc;
+    }
+    if (weighted) {
+        const int64_t mn = m * n;
+        EXL3_CHECK_ARG((mn + 255) / 256 <= 0x7FFFFFFF, "exl3_mgemm: m * n too large");
+        const dim3 grid((unsigned)((mn + 255) / 256), (unsigned)num_tokens);
+        if (f32)
+            EXL3_LAUNCH("mgemm_sum", mgemm_sum_kernel<true>, grid, dim3(256), 0, st, y, mn, indices, min_index,
+                        max_index, (int)num_mats, weights, (int)per_tok, C);
+        else
+            EXL3_LAUNCH("mgemm_sum", mgemm_sum_kernel<false>, grid, dim3(256), 0, st, y, mn, indices, min_index,
+                        max_index, (int)num_mats, weights, (int)per_tok, C);
+    }
+    return EXL3_OK;
 }
 
 }  // extern "C"

@@ -4,6 +4,8 @@ Interfaces mirror the reference boundary:
   * BC_LinearEXL3(trellis, suh, svh, K, bias, mcg, mul1, xh) with run(x, y) / run_alloc(x, out_features, output_fp32)
     (glm/xpu/glm_xpu/ops.py:34-88; ext-op-inventory.md:471-496)
   * exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1, force_num_sms) (ext-op-inventory.md:498-557)
+  * exl3_mgemm(A, B, C, suh, A_had, svh, indices, weights, K, force_shape_idx, mcg, mul1, min_index, max_index,
+    force_num_sms, num_tokens, ...) over int64 tables of device addresses (ext-op-inventory.md:664-685, 1104-1119)
   * reconstruct / reconstruct_slice (ext-op-inventory.md:597-612), exl3_reconstruct (glm/xpu/csrc/exl3_ops.sycl:539-555)
   * had_r_128(input, output, pre_scale, post_scale, scale) (ext-op-inventory.md:576-595)
   * linear(x, trellis, suh[S, k], svh, shard_of_nb, group_bounds, K, cb, small_m_max, slice_n): the fused
@@ -103,6 +105,75 @@ def exl3_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tens
     check(lib().exl3_gemm(ptr(A), k, m, k, ptr(B), n, K, ptr(C), n, dt, ptr(suh.contiguous()), ptr(A_had),
                           ptr(svh.contiguous()), cb, stream_of(A)), "exl3_gemm")
     return 0
+
+
+def exl3_mgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor, A_had, svh: torch.Tensor,
+               indices, weights, K, force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True,
+               min_index: int = -1, max_index: int = -1, force_num_sms: int = 0, num_tokens: int = 1,
+               size_n_list=None, c_ptrs=None, n_stride_list=None, had_src_list=None, num_had_src: int = 0) -> int:
+    """Multi-matrix EXL3 linear (exllamav3 ext exl3_mgemm). B, suh, svh: int64 device tensors holding one trellis /
+    suh / svh address per matrix (e.g. from `mgemm_tables`). A fp16 [a_batches, m, k] with a_batches 1 (broadcast),
+    the slot count or num_tokens. Slot j runs matrix indices[j] (indices int64, any shape, flattened; without indices
+    slot j runs matrix j); min_index >= 0 keeps only indices in [min_index, max_index), rebased. Negative (or out of
+    range) indices skip the slot. Without weights C [slots, m, n] receives each slot's result (skipped slots keep
+    their C); with weights ([slots], converted to fp16 as the reference stores them) C [num_tokens, m, n] receives each
+    token's weighted sum over its slots in slot order (fp32). A_had is accepted and not used (the input transform is
+    fused). The sliced mode (size_n_list, c_ptrs, n_stride_list, had_src_list) is not provided. Returns 0."""
+    if size_n_list is not None or c_ptrs is not None or n_stride_list is not None or had_src_list is not None \
+            or num_had_src:
+        raise NotImplementedError("exl3_mgemm: the sliced mode (size_n_list / c_ptrs / had_src_list) is not provided")
+    require_device(A, B, C, suh, svh, indices, weights)
+    cb = _cb(mcg, mul1)
+    Ki = int(K)
+    if float(K) != Ki:
+        raise Exl3Error(f"exl3_mgemm: K={K} must be a whole number of bits")
+    for name, t in (("B", B), ("suh", suh), ("svh", svh)):
+        if t.dtype != torch.int64 or t.numel() != B.numel():
+            raise Exl3Error(f"exl3_mgemm: {name} must be an int64 address table of {B.numel()} entries")
+    if A.dtype != torch.float16 or not A.is_contiguous() or A.dim() not in (2, 3):
+        raise Exl3Error("exl3_mgemm: A must be contiguous fp16 [a_batches, m, k] or [m, k]")
+    A3 = A if A.dim() == 3 else A.unsqueeze(0)
+    a_batches, m, k = A3.shape
+    if C.dtype not in (torch.float16, torch.float32) or not C.is_contiguous() or C.dim() != 3 or C.shape[1] != m:
+        raise Exl3Error(f"exl3_mgemm: C must be contiguous fp16/fp32 [batches, {m}, n]")
+    n = C.shape[2]
+    idx = None
+    if indices is not None:
+        idx = indices.reshape(-1).to(torch.int64).contiguous()
+        slots = idx.numel()
+    else:
+        slots = B.numel() if weights is not None else C.shape[0]
+    w = None
+    if weights is not None:
+        w = weights.reshape(-1).to(torch.float16).contiguous()
+        if w.numel() != slots:
+            raise Exl3Error(f"exl3_mgemm: weights must have one entry per slot ({slots})")
+        if C.shape[0] != num_tokens:
+            raise Exl3Error(f"exl3_mgemm: weighted C must be [num_tokens={num_tokens}, m, n]")
+    elif C.shape[0] != slots:
+        raise Exl3Error(f"exl3_mgemm: C must be [slots={slots}, m, n]")
+    dt = EXL3_F32 if C.dtype == torch.float32 else EXL3_F16
+    check(lib().exl3_mgemm(ptr(A3), a_batches, m, k, ptr(B.contiguous()), ptr(suh.contiguous()),
+                           ptr(svh.contiguous()), B.numel(), n, Ki, cb, ptr(idx), slots, ptr(w), num_tokens,
+                           min_index, max_index, ptr(C), dt, stream_of(A)), "exl3_mgemm")
+    return 0
+
+
+def mgemm_tables(linears, device=None):
+    """int64 address tables (trellis, suh, svh) of BC_LinearEXL3 objects of one shape and bitrate, for exl3_mgemm.
+    The tables hold raw addresses: the linears' tensors must outlive every call that uses them."""
+    if not linears:
+        raise Exl3Error("mgemm_tables: no linears")
+    shape, K = tuple(linears[0].trellis.shape), linears[0].Ki
+    for L in linears:
+        if tuple(L.trellis.shape) != shape or L.Ki != K:
+            raise Exl3Error("mgemm_tables: every matrix must have the same shape and K")
+        for t in (L.trellis, L.suh, L.svh):
+            if not t.is_contiguous():
+                raise Exl3Error("mgemm_tables: trellis, suh and svh must be contiguous")
+    dev = device if device is not None else linears[0].trellis.device
+    mk = lambda f: torch.tensor([f(L).data_ptr() for L in linears], dtype=torch.int64).to(dev)  # noqa: E731
+    return mk(lambda L: L.trellis), mk(lambda L: L.suh), mk(lambda L: L.svh)
 
 
 class BC_LinearEXL3:

@@ -90,6 +90,24 @@ int exl3_linear_sharded(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, c
                         void* C, int64_t c_ld, int c_dtype, const uint16_t* suh, int64_t n_shards,
                         const int32_t* shard_of_nb, const uint16_t* svh, int cb, void* stream);
 
+/* Multi-matrix EXL3 linear over `slots` slots. Matrix q (0 <= q < num_mats) is the trellis, suh and svh whose device
+ * addresses are B_ptrs[q], suh_ptrs[q], svh_ptrs[q] (int64 device tables; every matrix [k, n] at bitrate K, trellis
+ * 4-byte aligned). Slot j runs matrix q_j = indices[j] (int64 device array, or j when indices is NULL); with
+ * min_index >= 0 only q in [min_index, max_index) run, as q - min_index; slots whose q is negative or not below
+ * num_mats are skipped. Slot j reads A batch 0 (a_batches == 1), j (a_batches == slots) or j / (slots / num_tokens)
+ * (a_batches == num_tokens) of A fp16 [a_batches, m, k] (contiguous) and computes Y_j = exl3_gemm(A_batch, q_j), [m, n].
+ * Without weights: C[j] = Y_j, C [slots, m, n] (fp16 or fp32, contiguous); skipped slots leave C[j] unchanged.
+ * With weights (fp16 [slots], device): C[t] = sum over token t's slots j = t * (slots / num_tokens) + i in order of
+ * weights[j] * Y_j (fp32 sum, one rounding for fp16 C; skipped slots add nothing), C [num_tokens, m, n]. Rows are
+ * processed 8 at a time by the decode GEMV (the op serves decode batches). cb must be 2 (mul1).
+ * Replaces: exllamav3 ext exl3_mgemm(A, B, C, suh, A_had, svh, indices, weights, K, force_shape_idx, mcg, mul1,
+ *           min_index, max_index, force_num_sms, num_tokens, ...) (ext-op-inventory.md:664-685, 1104-1119); the
+ *           sliced mode (size_n_list, c_ptrs, n_stride_list, had_src_list) is not provided. */
+int exl3_mgemm(const uint16_t* A, int64_t a_batches, int64_t m, int64_t k, const int64_t* B_ptrs,
+               const int64_t* suh_ptrs, const int64_t* svh_ptrs, int64_t num_mats, int64_t n, int K, int cb,
+               const int64_t* indices, int64_t slots, const uint16_t* weights, int64_t num_tokens, int64_t min_index,
+               int64_t max_index, void* C, int c_dtype, void* stream);
+
 /* Gated activation z = act(x, y) elementwise over n values, fp16 (dtype EXL3_F16) or fp32 (EXL3_F32) inputs, fp16
  * output (in place on y allowed). SiLU: z = min(silu(x), L) * clamp(y, -L, L) (L = act_limit, 0 disables);
  * GELU-tanh: z = gelu_tanh(x) * y. Computed in fp32, rounded once.

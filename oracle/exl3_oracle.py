@@ -10,6 +10,7 @@ Sources restated (paths relative to the reference root):
   * reconstruct            glm/xpu/csrc/exl3_ops.sycl:539-555; ext-op-inventory.md:597-612, 758-760
   * had_r_128              ext-op-inventory.md:576-595; glm/xpu/glm_xpu/ops.py:118-142
   * linear                 ext-op-inventory.md:512-535, 707-712, 762-773
+  * multi-matrix linear    ext-op-inventory.md:664-685 (exl3_mgemm: slots, indices, min/max filter, weighted sum)
   * expert math / MoE      ext-op-inventory.md:923-942; glm/xpu/csrc/exl3_moe.n128.sycl:253-271, 370-379, 405-408;
                            dsv41/xpu/dsv_xpu/moe.py:967-994
   * activations            ext-op-inventory.md:944-956 (SiLU, act_limit clamp); GELU-tanh = torch gelu(approximate='tanh')
@@ -203,6 +204,58 @@ def exl3_linear(x: np.ndarray, trellis: np.ndarray, suh: np.ndarray, svh: np.nda
         W = reconstruct(trellis, K)
     y = had_out(linear_acc(xh, W, acc), svh, out_dtype)
     return y.reshape(x.shape[:-1] + (y.shape[-1],))
+
+
+def mgemm_matrix(indices, j: int, nmat: int, min_index: int = -1, max_index: int = -1) -> int:
+    """Matrix of slot j of exl3_mgemm: indices[j] (j without indices), filtered to [min_index, max_index) and rebased
+    when min_index >= 0; -1 (slot skipped) for a negative or out-of-range result (inventory:677-682)."""
+    q = int(indices[j]) if indices is not None else j
+    if min_index >= 0:
+        q = q - min_index if min_index <= q < max_index else -1
+    return q if 0 <= q < nmat else -1
+
+
+def mgemm(A: np.ndarray, mats, K: int, indices=None, weights=None, num_tokens: int = 1, min_index: int = -1,
+          max_index: int = -1, slots: int | None = None, out_dtype=np.float32, C=None):
+    """exllamav3 exl3_mgemm (inventory:664-685). A [a_batches, m, k]; mats = [(trellis, suh, svh)]; slot j runs
+    matrix mgemm_matrix(j) on A batch 0 / j / j // (slots // num_tokens) (a_batches 1 / slots / num_tokens).
+    Without weights returns C [slots, m, n] (skipped slots keep C's rows: C given, else zeros); with weights
+    C[t] = sum over token t's slots in order of weights[j] * Y_j, in float64 then out_dtype."""
+    A = np.asarray(A)
+    a_batches = A.shape[0]
+    if slots is None:
+        slots = len(indices) if indices is not None else len(mats)
+    per_tok = slots // num_tokens if num_tokens else 0
+    n = mats[0][0].shape[1] * 16
+
+    def a_of(j):
+        if a_batches == 1:
+            return A[0]
+        return A[j] if a_batches == slots else A[j // per_tok]
+
+    ys = []
+    for j in range(slots):
+        q = mgemm_matrix(indices, j, len(mats), min_index, max_index)
+        if q < 0:
+            ys.append(None)
+            continue
+        tr, suh, svh = mats[q]
+        y = exl3_linear(a_of(j), tr, suh, svh, K, np.float64 if weights is not None else out_dtype)
+        ys.append(y)
+    if weights is None:
+        out = np.array(C, copy=True) if C is not None else np.zeros((slots, A.shape[1], n), out_dtype)
+        for j, y in enumerate(ys):
+            if y is not None:
+                out[j] = y
+        return out
+    w = np.asarray(weights, dtype=np.float16).astype(np.float64)
+    out = np.zeros((num_tokens, A.shape[1], n), np.float64)
+    for t in range(num_tokens):
+        for i in range(per_tok):
+            j = t * per_tok + i
+            if ys[j] is not None:
+                out[t] += w[j] * ys[j]
+    return out.astype(out_dtype)
 
 
 def dense_weight(trellis: np.ndarray, suh: np.ndarray, svh: np.ndarray, K: int) -> np.ndarray:

@@ -220,6 +220,37 @@ def test_linear_tiny_bruteforce(bf):
     assert np.abs(y - ref).max() / np.abs(ref).max() < 2e-3
 
 
+def test_mgemm_slots_filter_and_weighted_sum():
+    """exl3_mgemm restatement pinned by independent forms: each slot equals x @ dense_weight of its matrix (closed
+    form), the [min, max) filter equals a manual remap of the indices, and the weighted token sum equals the weighted
+    sum of the dense products."""
+    mats = [_lin(128, 256, 2, 30 + q) for q in range(4)]
+    dense = [O.dense_weight(tr, suh, svh, 2) for tr, suh, svh in mats]
+    rng = np.random.default_rng(31)
+    A = rng.normal(size=(6, 2, 128)).astype(np.float16)           # a_batches = slots = 6
+    idx = np.array([2, -1, 0, 3, 7, 1])                           # 7 is out of range: skipped like -1
+    C0 = np.full((6, 2, 256), 5.0, np.float32)
+    y = O.mgemm(A, mats, 2, idx, C=C0)
+    for j, q in enumerate(idx):
+        if 0 <= q < 4:
+            ref = A[j].astype(np.float64) @ dense[q]
+            assert np.abs(y[j] - ref).max() / np.abs(ref).max() < 2e-3, j
+        else:
+            assert (y[j] == 5.0).all(), j
+    # filter [1, 3): indices 2 -> 1, 1 -> 0, others skipped
+    yf = O.mgemm(A, mats, 2, idx, min_index=1, max_index=3, C=C0)
+    remap = np.array([1, -1, -1, -1, -1, 0])
+    assert np.array_equal(yf, O.mgemm(A, mats, 2, remap, C=C0))
+    # weighted, 2 tokens x 3 slots, A per token
+    At = A[:2]
+    w = np.array([0.5, 1.25, -2.0, 0.75, 3.0, -0.5], np.float16)
+    yw = O.mgemm(At, mats, 2, idx, w, num_tokens=2, out_dtype=np.float64)
+    for t in range(2):
+        ref = sum(float(w[j]) * (At[t].astype(np.float64) @ dense[idx[j]])
+                  for j in range(3 * t, 3 * t + 3) if 0 <= idx[j] < 4)
+        assert np.abs(yw[t] - ref).max() / np.abs(ref).max() < 2e-3, t
+
+
 # ------------------------------------------------------------------------------------------------ routing / align
 
 def test_route_softmax_topk():
