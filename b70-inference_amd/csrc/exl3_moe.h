@@ -48,6 +48,9 @@ struct RouteArgs {
     int out_f32, H;
 };
 
+constexpr int kFusedRouteMaxE = 512;    // logits per row that the fused layer's in-layer routing handles (8 per lane)
+constexpr int kFusedRouteMaxRows = 2;   // tokens up to which the routed entry point ranks inside the fused layer
+
 struct MoeArgs {
     const uint16_t* x;
     int64_t x_ld;
@@ -59,6 +62,14 @@ struct MoeArgs {
     int uniform;                       // tables[i][e] == tb[i] + e * ts[i] for every entry (host-known layout)
     int64_t tb[9], ts[9];
     int Kg, Kd;                        // gate/up K, down K (0 = per-tile)
+    // routing from logits inside the fused layer (null: ids / tw hold the routing): softmax over logits (+ rbias)
+    // -> top-k -> renormalised, picks written to ids_out / tw_out
+    const float* logits;
+    int64_t lg_ld;
+    int n_logits;
+    const float* rbias;
+    int32_t* ids_out;
+    float* tw_out;
     int act;
     float limit;
     int shared;

@@ -975,6 +975,20 @@ int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t 
             a.ts[i] = table_layout[9 + i];
         }
     }
+    // Batches of up to kFusedRouteMaxRows tokens on the fused layer rank the logits inside it: every workgroup ranks
+    // every token itself, which costs less than the router launch (C3: 1 token 24.1 us against 25.0, 2 tokens 29.1
+    // against 29.9) until the rankings of more tokens in every workgroup outweigh it (4 tokens: 40.1 against 38.6).
+    // Otherwise the router kernel runs first.
+    if (M <= kFusedRouteMaxRows && moe_fused_ok(a) && n_logits <= kFusedRouteMaxE &&
+        env_int("EXL3MI_ROUTER_KERNEL", 0) == 0) {
+        a.logits = logits;
+        a.lg_ld = logits_ld;
+        a.n_logits = (int)n_logits;
+        a.rbias = bias;
+        a.ids_out = ids_out;
+        a.tw_out = w_out;
+        return moe_run(a, (hipStream_t)stream);
+    }
     if ((rc = exl3_route_softmax_topk(logits, logits_ld, M, n_logits, bias, topk, ids_out, w_out, stream))) return rc;
     return moe_run(a, (hipStream_t)stream);
 }

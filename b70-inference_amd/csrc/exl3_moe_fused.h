@@ -71,6 +71,14 @@ struct FusedArgs {
     void* out;
     int64_t out_ld;
     int out_f32;
+    // in-layer routing (logits non-null): every workgroup ranks the logits itself (the picks stay in LDS) and
+    // workgroup 0 writes them to ids_out / tw_out
+    const float* logits;
+    int64_t lg_ld;
+    int n_logits;
+    const float* rbias;
+    int32_t* ids_out;
+    float* tw_out;
 };
 
 __device__ __forceinline__ int atomic_add_agent(int* p, int v) {
@@ -92,6 +100,8 @@ struct FusedShared {
     float ksum[2][MR];                  // per projection and row: sum of the transformed x over the job's k range
     _Float16 su[2][KBF * 128];          // gate / up input sign vectors of the staged blocks
     int ge[kFusedMaxPairs];             // the pairs' experts (grouping sweep of wave 0)
+    int rid[kFusedMaxPairs];            // in-layer routing: expert of pick (token, j) at token * topk + j
+    float rw[kFusedMaxPairs];           //   and its weight
     int64_t tab[9];                     // the item's (trellis, suh, svh) addresses for gate, up, down
     int64_t km[6];                      // the item's (kmap, woff) addresses when K is per tile
     uint64_t valid[2];                  // valid pairs
@@ -134,17 +144,39 @@ struct Item {
 
 // Expert of pair p, -1 for none (p >= np, a negative id, the absent shared expert). The id load is unconditional
 // (clamped index) so that both of a lane's loads are in flight together.
-__device__ __forceinline__ int pair_expert(const FusedArgs& a, int p) {
+// With in-layer routing the picks come from LDS (rid / rw), else from the ids / tw arrays.
+__device__ __forceinline__ int pair_expert(const FusedArgs& a, int p, const int* rid) {
     const int pc = p < a.np ? p : a.np - 1;
     const int tok = pc / a.slots, j = pc - tok * a.slots;
-    const int v = a.topk > 0 ? ldg(a.ids + tok * a.topk + (j < a.topk ? j : a.topk - 1)) : 0;
+    const int q = tok * a.topk + (j < a.topk ? j : a.topk - 1);
+    const int v = a.topk <= 0 ? 0 : a.logits ? rid[q] : ldg(a.ids + q);
     const int e = j < a.topk ? v : a.shared;
     return p < a.np && e < a.E ? e : -1;
 }
 
-__device__ __forceinline__ float pair_weight(const FusedArgs& a, int p) {
+__device__ __forceinline__ float pair_weight(const FusedArgs& a, int p, const float* rw) {
     const int tok = p / a.slots, j = p - tok * a.slots;
-    return j < a.topk ? ldg(a.tw + tok * a.topk + j) : 1.0f;
+    const int q = tok * a.topk + j;
+    return j < a.topk ? (a.logits ? rw[q] : ldg(a.tw + q)) : 1.0f;
+}
+
+// In-layer routing: wave w ranks the logits of tokens w, w + 4 (softmax over logits + bias, top-k, renormalised:
+// exl3_route_softmax_topk's route_row) into rid / rw; workgroup 0 also writes the picks out.
+__device__ __forceinline__ void route_in_layer(const FusedArgs& a, int wave, int lane, int* rid, float* rw) {
+    for (int t = wave; t < a.M; t += 4) {
+        int id;
+        float w;
+        route_row<kFusedRouteMaxE / 64, EXL3_SCORE_SOFTMAX>(a.logits + (int64_t)t * a.lg_ld, a.rbias, a.n_logits,
+                                                           a.topk, lane, true, true, 1.0f, id, w);
+        if (lane < a.topk) {
+            rid[t * a.topk + lane] = id;
+            rw[t * a.topk + lane] = w;
+            if (blockIdx.x == 0) {
+                a.ids_out[t * a.topk + lane] = id;
+                a.tw_out[t * a.topk + lane] = w;
+            }
+        }
+    }
 }
 
 __device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
@@ -160,11 +192,11 @@ __device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n
 // Groups the pairs (one wave; `ge` is a 128-int LDS array written and read by this wave only: LDS keeps a wave's
 // accesses in order).
 template <int MR>
-__device__ __forceinline__ void group_pairs(const FusedArgs& a, int lane, Groups& g, int* ge) {
+__device__ __forceinline__ void group_pairs(const FusedArgs& a, int lane, Groups& g, int* ge, const int* rid) {
     const int np = a.np;
     const int l1 = lane + 64;
-    g.e0 = pair_expert(a, lane);
-    g.e1 = pair_expert(a, l1);
+    g.e0 = pair_expert(a, lane, rid);
+    g.e1 = pair_expert(a, l1, rid);
     ge[lane] = g.e0;
     ge[l1] = g.e1;
     int bf0 = 0, bf1 = 0;
@@ -520,7 +552,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     const float sd0 = h2f(ldg(svd + lane)), sd1 = h2f(ldg(svd + lane + 64));
     float wrow[RW];
 #pragma unroll
-    for (int j = 0; j < RW; ++j) wrow[j] = pair_weight(a, s.rows[wave + 4 * j < MR ? wave + 4 * j : 0]);
+    for (int j = 0; j < RW; ++j) wrow[j] = pair_weight(a, s.rows[wave + 4 * j < MR ? wave + 4 * j : 0], s.rw);
 
     // wait for the down input this job reads, then count the job as a consumer (the last consumer clears the counter
     // for the next call). Direct mode: every gate|up split of the item (nbI * P_gu arrivals on the item counter).
@@ -715,10 +747,14 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = blockIdx.x;
     const int gi = g / a.GU, gr0 = g - gi * a.GU;
+    if (a.logits) {
+        route_in_layer(a, wave, lane, s.rid, s.rw);
+        __syncthreads();
+    }
     // wave 0 groups the pairs and describes the gate|up job's item; the others wait at the barrier
     Groups gr;
     if (wave == 0) {
-        group_pairs<MR>(a, lane, gr, s.ge);
+        group_pairs<MR>(a, lane, gr, s.ge, s.rid);
         if (lane == 0) {
             s.valid[0] = gr.v0;
             s.valid[1] = gr.v1;

@@ -71,6 +71,14 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.np = m.M * m.slots;
     a.ids = m.ids;
     a.tw = m.tw;
+    if (m.logits) {
+        a.logits = m.logits;
+        a.lg_ld = m.lg_ld;
+        a.n_logits = m.n_logits;
+        a.rbias = m.rbias;
+        a.ids_out = m.ids_out;
+        a.tw_out = m.tw_out;
+    }
     a.tables = m.tables;
     a.kmaps = m.kmaps;
     a.act = m.act;
