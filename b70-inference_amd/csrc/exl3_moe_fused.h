@@ -2,7 +2,8 @@
 //
 // For decode batches (at most 8 tokens, at most kFusedMaxPairs (token, slot) pairs) the multi-kernel path is a chain
 // of short latency-bound launches. Here every workgroup:
-//   1. reads the routing ids (pair l in lanes l and l + 64 of wave 0) and groups the pairs by expert in
+//   1. reads the routing ids (or, given router logits, ranks them itself: every wave one token, the picks in LDS) and
+//      groups the pairs (pair l in lanes l and l + 64 of wave 0) by expert in
 //      registers, once: a pair's index among its expert's pairs in flat order comes from an LDS sweep, items are
 //      chunks of up to MR such pairs (the reference's per-expert row groups, glm/xpu/csrc/exl3_moe.n128.sycl:691-734)
 //      numbered by a ballot over their first pairs, and an item's expert and rows follow from ballots. No align

@@ -139,8 +139,10 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
                      int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
                      int64_t out_ld, int out_dtype, void* stream);
 
-/* The routed MoE layer from router logits: exl3_route_softmax_topk followed by exl3_moe_forward, as one call (the
- * routing launch, then the layer's launches on the same stream). logits fp32 [M, n_logits] (row stride logits_ld),
+/* The routed MoE layer from router logits: exl3_route_softmax_topk followed by exl3_moe_forward, as one call, with
+ * the same results bit for bit. Up to 2 tokens with n_logits <= 512 on the fused decode layer, the layer ranks the
+ * logits itself (one launch); otherwise the routing launch runs first on the same stream. logits fp32 [M, n_logits]
+ * (row stride logits_ld),
  * bias fp32 [n_logits] or NULL; the routed experts are table entries 0 .. n_logits - 1 (n_logits <= E; the shared
  * expert, if any, is another entry). ids_out int32 [M, topk] and w_out fp32 [M, topk] receive the routing.
  * topk <= 32, n_logits <= 8192. table_layout: NULL, or a HOST array of 18 int64 (base[9], stride[9]) with
