@@ -127,9 +127,12 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.DN = nbH * a.P_d;
     // unsplit down jobs compute their whole input from the partials (each column block of I is then rebuilt by the
     // item's nbH down jobs instead of once by a gate|up epilogue, saving that stage's round trips); with many
-    // gate|up splits the partial loads cost more than the stage saves
-    a.direct = a.P_d == 1 && a.P_gu <= 8 && nbH <= 64 && env_int("EXL3MI_FUSED_EPILOGUE", 0) == 0;
+    // gate|up splits the partial loads cost more than the stage saves, and once the gate|up jobs fill more than half
+    // of the device the rebuilt inputs' ALU work costs more than the round trip (C3 at 4 tokens: 37.5 against 38.2 us
+    // with the epilogue stage; 1 and 2 tokens 0.3 - 0.5 us faster without it)
     const int64_t jgu = (int64_t)a.max_items * a.GU, grid = jgu + a.GU;
+    a.direct = a.P_d == 1 && a.P_gu <= 8 && nbH <= 64 && 2 * jgu <= resident &&
+               env_int("EXL3MI_FUSED_EPILOGUE", 0) == 0;
     EXL3_CHECK_ARG(grid < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
     a.J_gu = (int)jgu;
 
