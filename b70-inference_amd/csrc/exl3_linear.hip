@@ -469,7 +469,8 @@ int exl3_mgemm(const uint16_t* A, int64_t a_batches, int64_t m, int64_t k, const
     const bool f32 = c_dtype == EXL3_F32;
     hipStream_t st = (hipStream_t)stream;
     const int strips = (int)(n / 128), nblk = (int)(k / 128);
-    const int P = gemv_splits(strips * (int)(slots > 0 ? slots : 1), nblk,
+    const int64_t units = (int64_t)strips * (slots > 0 ? slots : 1);          // strips of every slot
+    const int P = gemv_splits(units < (1 << 30) ? (int)units : (1 << 30), nblk,
                               m < kGemvMaxRows ? (int)m : kGemvMaxRows);
     const size_t part_bytes = carve_size((size_t)slots * strips * P * kGemvMaxRows * 128, sizeof(float));
     const size_t y_bytes = weighted ? carve_size((size_t)slots * m * n, sizeof(float)) : 0;
