@@ -27,7 +27,7 @@ def synth():
     return importlib.import_module("b70-inference_amd.synth")
 
 
-@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("m", [1, 3, 12])
 @pytest.mark.parametrize("cdt", [torch.float16, torch.float32])
 def test_mgemm_slots_broadcast(exl3, oracle, synth, K, m, cdt):
