@@ -20,9 +20,36 @@
 namespace exl3 {
 
 // ================================================================================================ align
-// Exclusive scan of n ints in LDS by a 1024-thread workgroup (each thread a contiguous run). Returns the total.
+// Exclusive scan of n ints in LDS by a 1024-thread workgroup. Returns the total. Up to one value per thread: shuffle
+// scans within the waves, then over the wave totals (three barriers); more: each thread scans a contiguous run.
 __device__ int block_scan_exclusive(int* a, int n, int* tmp /* [1024] */) {
     const int t = threadIdx.x, T = blockDim.x;
+    if (n <= T) {
+        const int lane = t & 63, wv = t >> 6, nw = T >> 6;
+        const int v = t < n ? a[t] : 0;
+        int x = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(x, d);
+            if (lane >= d) x += y;
+        }
+        if (lane == 63) tmp[wv] = x;
+        __syncthreads();
+        if (t < 64) {
+            int w = t < nw ? tmp[t] : 0;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(w, d);
+                if (t >= d) w += y;
+            }
+            tmp[64 + t] = w;
+        }
+        __syncthreads();
+        if (t < n) a[t] = (wv > 0 ? tmp[64 + wv - 1] : 0) + x - v;
+        const int total = tmp[64 + nw - 1];
+        __syncthreads();
+        return total;
+    }
     const int per = (n + T - 1) / T;
     const int lo = t * per, hi = min(n, lo + per);
     int s = 0;
