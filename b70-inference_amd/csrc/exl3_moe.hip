@@ -581,6 +581,33 @@ __global__ __launch_bounds__(64) void route_kernel(const float* __restrict__ log
 
 typedef void (*route_fn)(const float*, int64_t, int, const float*, int, int, float, int32_t*, float*);
 
+// route_kernel with the picks ranked by s * mul + b + max(res, -1e30) (route_row's ADJ form).
+template <int V, int SC>
+__global__ __launch_bounds__(64) void route_adj_kernel(const float* __restrict__ logits, int64_t ld, int E,
+                                                       const float* __restrict__ bias, const float* __restrict__ mul,
+                                                       const float* __restrict__ res, int k, int flags, float scaling,
+                                                       int32_t* __restrict__ ids, float* __restrict__ w) {
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    int id;
+    float wt;
+    route_row<V, SC, true>(logits + row * ld, bias, E, k, lane, true, (flags & EXL3_ROUTE_RENORM) != 0, scaling, id,
+                           wt, mul, res);
+    if (lane < k) {
+        ids[row * k + lane] = id;
+        w[row * k + lane] = wt;
+    }
+}
+
+typedef void (*route_adj_fn)(const float*, int64_t, int, const float*, const float*, const float*, int, int, float,
+                             int32_t*, float*);
+
+template <int SC>
+static route_adj_fn route_adj_pick(int64_t E) {
+    return E <= 64 ? route_adj_kernel<1, SC> : E <= 128 ? route_adj_kernel<2, SC> : E <= 256 ? route_adj_kernel<4, SC>
+         : E <= 512 ? route_adj_kernel<8, SC> : E <= 1024 ? route_adj_kernel<16, SC> : route_adj_kernel<32, SC>;
+}
+
 template <int SC>
 static route_fn route_pick(int64_t E) {
     return E <= 64 ? route_kernel<1, SC> : E <= 128 ? route_kernel<2, SC> : E <= 256 ? route_kernel<4, SC>
@@ -1076,6 +1103,25 @@ int exl3_route_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const
                   : route_pick<EXL3_SCORE_SQRT_SOFTPLUS>(E);
     EXL3_LAUNCH("route_topk", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
                 (int)k, flags, scaling, ids, w);
+    return EXL3_OK;
+}
+
+int exl3_route_adjusted(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, const float* mul,
+                        const float* res, int64_t k, int score, int flags, float scaling, int32_t* ids, float* w,
+                        void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && E > 0 && E <= 2048 && k > 0 && k <= 32 && k <= E && ld >= E,
+                   "exl3_route_adjusted: bad sizes (M %lld, E %lld, k %lld, ld %lld)", (long long)M, (long long)E,
+                   (long long)k, (long long)ld);
+    if (score != EXL3_SCORE_SIGMOID && score != EXL3_SCORE_SQRT_SOFTPLUS)
+        return fail(EXL3_ERR_UNSUPPORTED, "exl3_route_adjusted: scoring %d (sigmoid or sqrt-softplus only)", score);
+    EXL3_CHECK_ARG((flags & ~EXL3_ROUTE_RENORM) == 0, "exl3_route_adjusted: bad flags %d", flags);
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(logits && ids && w, "exl3_route_adjusted: null pointer");
+    EXL3_CHECK_ARG(M <= 0x7FFFFFFF, "exl3_route_adjusted: too many rows");
+    route_adj_fn kern = score == EXL3_SCORE_SIGMOID ? route_adj_pick<EXL3_SCORE_SIGMOID>(E)
+                                                    : route_adj_pick<EXL3_SCORE_SQRT_SOFTPLUS>(E);
+    EXL3_LAUNCH("route_adjusted", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
+                mul, res, (int)k, flags, scaling, ids, w);
     return EXL3_OK;
 }
 

@@ -71,9 +71,15 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
 // registers; picked and padding entries hold key 0, NaN keys 1 (below every number, still pickable, as a stable
 // descending sort places them last). Each round is one DPP wave max, a ballot of the lanes holding it, and a DPP wave
 // min of their lowest indices only when several lanes tie. Lane j < k returns pick j in (id, w).
-template <int V, int SC>
+//
+// ADJ (sigmoid and sqrt-softplus only): the picks rank by s * mul + b + max(res, -1e30) instead (mul, res per entry,
+// either may be null: the reference dsv router's residency terms, dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193), each
+// operation rounded separately; the weights still come from s.
+template <int V, int SC, bool ADJ = false>
 __device__ __forceinline__ void route_row(const float* __restrict__ z, const float* __restrict__ bias, int E, int k,
-                                          int lane, bool bias_both, bool renorm, float scaling, int& id, float& w) {
+                                          int lane, bool bias_both, bool renorm, float scaling, int& id, float& w,
+                                          const float* __restrict__ mul = nullptr,
+                                          const float* __restrict__ res = nullptr) {
     // every load issued before any is used (clamped indices, no per-element branch): one memory round trip
     float f[V], b[V];
 #pragma unroll
@@ -86,6 +92,15 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
         for (int v = 0; v < V; ++v) {
             const int i = lane + 64 * v;
             b[v] = ldg(bias + (i < E ? i : E - 1));
+        }
+    }
+    float mv[V], rv[V];
+    if (ADJ) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int i = lane + 64 * v < E ? lane + 64 * v : E - 1;
+            mv[v] = mul ? ldg(mul + i) : 1.f;
+            rv[v] = res ? ldg(res + i) : 0.f;
         }
     }
     float g[V];                          // weight source per entry
@@ -105,6 +120,11 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
             }
             g[v] = s;
             r = bias ? s + b[v] : (SC == EXL3_SCORE_SIGMOID ? f[v] : s);
+        }
+        if (ADJ && SC != EXL3_SCORE_SOFTMAX) {
+            r = __fmul_rn(g[v], mv[v]);
+            if (bias) r = __fadd_rn(r, b[v]);
+            if (res) r = __fadd_rn(r, fmaxf(rv[v], -1e30f));
         }
         const int i = lane + 64 * v;
         key[v] = i < E ? (r != r ? 1u : float_key(r)) : 0u;

@@ -255,6 +255,43 @@ def route_topk(logits: torch.Tensor, k: int, bias: torch.Tensor | None = None, s
     return ids, w
 
 
+def route_adjusted(logits: torch.Tensor, k: int, bias: torch.Tensor | None = None, mul: torch.Tensor | None = None,
+                   res: torch.Tensor | None = None, score: str = "sqrt_softplus", renorm: bool = True,
+                   scaling: float = 1.0):
+    """Top-k with the reference dsv router's residency terms (exl3_route_adjusted): rank by s * mul + bias +
+    max(res, -1e30) (mul, res fp32 [E] or None), weights from s (sigmoid or sqrt_softplus of the logit) as route_topk.
+    Returns (ids int32 [M, k], w fp32 [M, k])."""
+    require_device(logits, bias, mul, res)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise Exl3Error("route_adjusted: logits must be fp32 [M, E] with contiguous rows")
+    if score not in ("sigmoid", "sqrt_softplus"):
+        raise NotImplementedError(f"route_adjusted: scoring {score!r} (sigmoid or sqrt_softplus)")
+    M, E = logits.shape
+    for name, t in (("bias", bias), ("mul", mul), ("res", res)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != E or not t.is_contiguous()):
+            raise Exl3Error(f"route_adjusted: {name} must be fp32 [E]")
+    ids = torch.empty(M, k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=logits.device)
+    check(lib().exl3_route_adjusted(ptr(logits), logits.stride(0), M, E, ptr(bias), ptr(mul), ptr(res), k,
+                                    SCORES[score], ROUTE_RENORM if renorm else 0, float(scaling), ptr(ids), ptr(w),
+                                    stream_of(logits)), "route_adjusted")
+    return ids, w
+
+
+def moe_route(logits: torch.Tensor, bias: torch.Tensor, res, ids: torch.Tensor, w: torch.Tensor, want,
+              scaling: float) -> None:
+    """dsv_moe::moe_route(logits, bias, res, ids, w, want, scaling) (dsv41/xpu/csrc/dsv_moe_glue.sycl:426-439, bound at
+    :621-622): s = sqrt(softplus(logit)); ids (in place, int64 or int32) = top-k of s + bias + res; w = s of the picks
+    renormalised (+1e-20) * scaling; want (optional, in place) = the plain top-k of s + bias."""
+    k = ids.shape[-1]
+    pi, pw = route_adjusted(logits, k, bias, None, res, "sqrt_softplus", True, scaling)
+    ids.copy_(pi)
+    w.copy_(pw)
+    if want is not None:
+        wi, _ = route_topk(logits, k, bias, "sqrt_softplus", True, scaling)
+        want.copy_(wi)
+
+
 def router_logits(x: torch.Tensor, weight: torch.Tensor, E: int | None = None, layout: str = "he",
                   round_fp16: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
     """Router logits fp32 [M, E] = x @ W on the router GEMV (exl3_router_logits). layout "he": weight fp16 [H, >= E]

@@ -184,6 +184,18 @@ int exl3_route_softmax_topk(const float* logits, int64_t ld, int64_t M, int64_t 
 int exl3_route_topk(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, int64_t k, int score,
                     int flags, float scaling, int32_t* ids, float* w, void* stream);
 
+/* Top-k routing with the reference dsv router's residency terms: the picks rank by s * mul[e] + bias[e] +
+ * max(res[e], -1e30) (s = sigmoid or sqrt-softplus of the logit, each operation rounded separately; mul, res fp32 [E]
+ * or NULL: a per-expert selection multiplier and an additive 0 / -margin / -inf residency bias, so that experts
+ * already in memory are preferred), exact ties to the lower index; the weights come from s as in exl3_route_topk
+ * (flags: EXL3_ROUTE_RENORM). E <= 2048. The plain picks (the reference's `want`) are exl3_route_topk with the same
+ * bias.
+ * Replaces: dsv_moe::moe_route(logits, bias, res, ids, w, want, scaling) and the mul term of route_fused
+ *           (dsv41/xpu/csrc/dsv_moe_glue.sycl:155-193, 426-439, bound at :621-622). */
+int exl3_route_adjusted(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, const float* mul,
+                        const float* res, int64_t k, int score, int flags, float scaling, int32_t* ids, float* w,
+                        void* stream);
+
 /* Router logits from hidden states: logits[m, e] = sum_h x[m, h] * W(h, e) in fp32 (fixed summation order), x fp16
  * [M, H] (row stride x_ld), logits fp32 [M, E] (row stride logits_ld), rounded to fp16 precision when round_fp16 != 0
  * (what a matmul of two fp16 tensors returns). w_layout EXL3_ROUTER_W_HE: W fp16 [H, E] (row stride w_ld >= E,

@@ -379,7 +379,8 @@ SCORES = ("softmax", "sigmoid", "sqrt_softplus")
 
 
 def route_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None, score: str = "softmax",
-               renorm: bool = True, scaling: float = 1.0, bias_select_only: bool = False):
+               renorm: bool = True, scaling: float = 1.0, bias_select_only: bool = False,
+               mul: np.ndarray | None = None, res: np.ndarray | None = None):
     """Top-k routing with a scoring function; ranking values in float32 (as the kernel ranks), weights in float64.
       softmax        rank by f + b; weights from softmax(f + b), or softmax(f) when the bias only selects
                      (trellis-serve.patch:395-441, its `cold` term)
@@ -387,6 +388,8 @@ def route_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None, score
       sqrt_softplus  s = sqrt(softplus(f)), softplus(f) = f above 20; rank by s + b; weights from s
                      (dsv41/xpu/csrc/dsv_moe_glue.sycl:163-193)
     A pick's weight is v * scaling / (sum of picked v + 1e-20) with renorm, v * scaling without.
+    mul / res (sigmoid and sqrt_softplus, the dsv router's residency terms, dsv41/xpu/csrc/dsv_moe_glue.sycl:163-175):
+    rank by s * mul + b + max(res, -1e30) instead, each float32 operation rounded on its own.
     Returns ids int32 [M, k] (descending rank, exact ties to the lower index) and w float32 [M, k]."""
     if score not in SCORES:
         raise ValueError(score)
@@ -407,6 +410,12 @@ def route_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None, score
             s32 = np.sqrt(sp32).astype(np.float32)
             v = np.sqrt(np.where(f64 > 20, f64, np.log1p(np.exp(np.minimum(f64, 20)))))
         r = (s32 + b) if b is not None else (f if score == "sigmoid" else s32)
+        if mul is not None or res is not None:
+            r = s32 * (np.float32(1) if mul is None else mul.astype(np.float32)[None, :])
+            if b is not None:
+                r = r + b
+            if res is not None:
+                r = r + np.maximum(res.astype(np.float32), np.float32(-1e30))[None, :]
     ids = topk_lowest_index(r, k)
     pv = np.take_along_axis(v, ids, -1)
     w = pv * scaling / (pv.sum(-1, keepdims=True) + 1e-20) if renorm else pv * scaling

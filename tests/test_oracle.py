@@ -306,6 +306,29 @@ def test_route_topk_scorings_against_torch(score, with_bias):
     assert np.abs(w_raw - (pv * scaling).numpy()).max() <= 1e-6 * float(pv.max()) * scaling
 
 
+@pytest.mark.parametrize("score", ["sigmoid", "sqrt_softplus"])
+def test_route_topk_residency_terms(score):
+    """mul / res ranking (the dsv router's residency terms) pinned by properties: without them it is the plain router;
+    a uniform positive mul without bias keeps the plain order; -inf residency never picks an expert while k others
+    remain, and equals dropping those experts from the plain ranking; weights always come from the unmodified score."""
+    rng = np.random.default_rng(41)
+    lg = rng.normal(size=(6, 40)).astype(np.float32) * 2
+    b = (rng.normal(size=40) * 0.3).astype(np.float32)
+    ids0, w0 = O.route_topk(lg, 6, b, score)
+    ids1, w1 = O.route_topk(lg, 6, b, score, mul=None, res=np.zeros(40, np.float32))
+    assert np.array_equal(ids0, ids1) and np.array_equal(w0, w1)
+    ids2, _ = O.route_topk(lg, 6, None, score, mul=np.full(40, 2.0, np.float32))
+    ids3, _ = O.route_topk(lg, 6, None, "sqrt_softplus" if score == "sqrt_softplus" else score)
+    if score == "sqrt_softplus":
+        assert np.array_equal(ids2, ids3)
+    res = np.where(np.arange(40) % 3 == 0, -np.inf, 0.0).astype(np.float32)
+    ids4, w4 = O.route_topk(lg, 6, b, score, res=res)
+    assert not np.isin(ids4, np.arange(0, 40, 3)).any()
+    keep = np.arange(40)[np.arange(40) % 3 != 0]
+    idk, wk = O.route_topk(lg[:, keep], 6, b[keep], score)
+    assert np.array_equal(ids4, keep[idk]) and np.allclose(w4, wk, rtol=1e-6)
+
+
 def test_route_topk_softmax_bias_both_is_route_softmax_topk():
     rng = np.random.default_rng(5)
     logits = rng.standard_normal((7, 200)).astype(np.float32)

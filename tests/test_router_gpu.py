@@ -61,6 +61,45 @@ def test_route_topk_ties_and_small_rows(exl3, oracle):
         assert np.abs(w.cpu().numpy() - rw).max() <= 1e-6
 
 
+@pytest.mark.parametrize("score", ["sigmoid", "sqrt_softplus"])
+@pytest.mark.parametrize("E,k", [(64, 1), (160, 6), (256, 8), (1000, 8)])
+@pytest.mark.parametrize("terms", ["mul", "res", "both"])
+def test_route_adjusted_matches_oracle(exl3, oracle, score, E, k, terms):
+    """Residency-adjusted ranking s * mul + bias + max(res, -1e30): picks identical to the oracle, weights from s."""
+    M = 9
+    logits, bias = _logits(M, E, 300 + E + k)
+    g = torch.Generator().manual_seed(400 + E)
+    mul = (0.5 + 1.5 * torch.rand(E, generator=g)) if terms in ("mul", "both") else None
+    res = None
+    if terms in ("res", "both"):
+        u = torch.rand(E, generator=g)
+        res = torch.where(u < 0.2, torch.tensor(float("-inf")), torch.where(u < 0.5, torch.tensor(-0.75),
+                                                                             torch.tensor(0.0)))
+    for scaling in (1.0, 2.5):
+        ids, w = exl3.route_adjusted(logits.cuda(), k, bias.cuda(), None if mul is None else mul.cuda(),
+                                     None if res is None else res.cuda(), score, True, scaling)
+        rid, rw = oracle.route_topk(logits.numpy(), k, bias.numpy(), score, True, scaling,
+                                    mul=None if mul is None else mul.numpy(), res=None if res is None else res.numpy())
+        assert np.array_equal(ids.cpu().numpy(), rid), scaling
+        assert np.abs(w.cpu().numpy() - rw).max() <= 1e-5 * max(1.0, float(np.abs(rw).max()))
+
+
+def test_moe_route_in_place(exl3, oracle):
+    """The reference op's signature: int64 ids / want written in place, want = the plain sqrt-softplus top-k."""
+    M, E, k = 5, 256, 8
+    logits, bias = _logits(M, E, 77)
+    res = torch.zeros(E)
+    res[::4] = -1.0
+    ids = torch.empty(M, k, dtype=torch.int64, device="cuda")
+    w = torch.empty(M, k, dtype=torch.float32, device="cuda")
+    want = torch.empty(M, k, dtype=torch.int64, device="cuda")
+    exl3.moe_route(logits.cuda(), bias.cuda(), res.cuda(), ids, w, want, 2.0)
+    rid, rw = oracle.route_topk(logits.numpy(), k, bias.numpy(), "sqrt_softplus", True, 2.0, res=res.numpy())
+    pid, _ = oracle.route_topk(logits.numpy(), k, bias.numpy(), "sqrt_softplus", True, 2.0)
+    assert np.array_equal(ids.cpu().numpy(), rid) and np.array_equal(want.cpu().numpy(), pid)
+    assert np.abs(w.cpu().numpy() - rw).max() <= 1e-5 * 2.0
+
+
 @pytest.mark.parametrize("layout", ["he", "eh"])
 @pytest.mark.parametrize("H,E", [(128, 72), (2048, 512), (5120, 160), (7168, 256)])
 @pytest.mark.parametrize("M", [1, 3, 4, 9, 33])
