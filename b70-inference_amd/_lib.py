@@ -34,6 +34,7 @@ SIGNATURES = {
                    _i32, _vp],
     "exl3_act_mul": [_vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp],
     "exl3_route_adjusted": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp, _vp, _vp],
+    "exl3_route_block": [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _f32, _f32, _vp, _vp, _vp],
     "exl3_moe_forward": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _f32,
                          _i64, _vp, _i64, _i32, _vp],
     "exl3_moe_forward_logits": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i32,

@@ -599,6 +599,58 @@ __global__ __launch_bounds__(64) void route_adj_kernel(const float* __restrict__
     }
 }
 
+// Verify blocks of S rows, one wave per block, rows in order (sqrt-softplus): an expert that an earlier row of the
+// block picked ranks by s * mul * (1 + boost) + b instead of s * mul + b (each operation rounded separately), so the
+// block reads fewer distinct experts; the weights stay the plain s, renormalised (+1e-20) and scaled (the reference's
+// RouteBlock, dsv41/xpu/csrc/dsv_moe_glue.sycl:194-240).
+template <int V>
+__global__ __launch_bounds__(64) void route_block_kernel(const float* __restrict__ logits, int64_t ld, int E,
+                                                         const float* __restrict__ bias, const float* __restrict__ mul,
+                                                         int k, int S, float boost, float scaling,
+                                                         int32_t* __restrict__ ids, float* __restrict__ w) {
+    const int lane = threadIdx.x;
+    bool chosen[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) chosen[v] = false;
+    const float up = 1.0f + boost;
+    for (int si = 0; si < S; ++si) {
+        const int64_t row = (int64_t)blockIdx.x * S + si;
+        float f[V], b[V], m[V], g[V];
+        uint32_t key[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int i = lane + 64 * v < E ? lane + 64 * v : E - 1;
+            f[v] = ldg(logits + row * ld + i);
+            b[v] = bias ? ldg(bias + i) : 0.f;
+            m[v] = mul ? ldg(mul + i) : 1.f;
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const float sv = sqrtf(f[v] > 20.f ? f[v] : log1pf(expf(f[v])));
+            g[v] = sv;
+            float r = __fmul_rn(__fmul_rn(sv, m[v]), chosen[v] ? up : 1.0f);
+            if (bias) r = __fadd_rn(r, b[v]);
+            key[v] = lane + 64 * v < E ? (r != r ? 1u : float_key(r)) : 0u;
+        }
+        int id;
+        float wt;
+        route_select<V, EXL3_SCORE_SQRT_SOFTPLUS>(key, g, 0.f, 1.f, k, lane, true, scaling, id, wt);
+        if (lane < k) {
+            ids[row * k + lane] = id;
+            w[row * k + lane] = wt;
+        }
+        for (int j = 0; j < k; ++j) {                 // the row's picks join the block's chosen experts
+            const int pid = __builtin_amdgcn_readlane(id, j);
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                if (pid >= 0 && pid == lane + 64 * v) chosen[v] = true;
+        }
+    }
+}
+
+typedef void (*route_block_fn)(const float*, int64_t, int, const float*, const float*, int, int, float, float,
+                               int32_t*, float*);
+
 typedef void (*route_adj_fn)(const float*, int64_t, int, const float*, const float*, const float*, int, int, float,
                              int32_t*, float*);
 
@@ -1122,6 +1174,26 @@ int exl3_route_adjusted(const float* logits, int64_t ld, int64_t M, int64_t E, c
                                                     : route_adj_pick<EXL3_SCORE_SQRT_SOFTPLUS>(E);
     EXL3_LAUNCH("route_adjusted", kern, dim3((unsigned)M), dim3(64), 0, (hipStream_t)stream, logits, ld, (int)E, bias,
                 mul, res, (int)k, flags, scaling, ids, w);
+    return EXL3_OK;
+}
+
+int exl3_route_block(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, const float* mul,
+                     int64_t k, int64_t rows_per_block, float block_boost, float scaling, int32_t* ids, float* w,
+                     void* stream) {
+    EXL3_CHECK_ARG(M >= 0 && E > 0 && E <= 2048 && k > 0 && k <= 32 && k <= E && ld >= E,
+                   "exl3_route_block: bad sizes (M %lld, E %lld, k %lld, ld %lld)", (long long)M, (long long)E,
+                   (long long)k, (long long)ld);
+    EXL3_CHECK_ARG(rows_per_block >= 1 && M % rows_per_block == 0 && rows_per_block <= 65536,
+                   "exl3_route_block: %lld rows do not split into blocks of %lld", (long long)M,
+                   (long long)rows_per_block);
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(logits && ids && w, "exl3_route_block: null pointer");
+    EXL3_CHECK_ARG(M / rows_per_block <= 0x7FFFFFFF, "exl3_route_block: too many blocks");
+    route_block_fn kern = E <= 64 ? route_block_kernel<1> : E <= 128 ? route_block_kernel<2>
+                        : E <= 256 ? route_block_kernel<4> : E <= 512 ? route_block_kernel<8>
+                        : E <= 1024 ? route_block_kernel<16> : route_block_kernel<32>;
+    EXL3_LAUNCH("route_block", kern, dim3((unsigned)(M / rows_per_block)), dim3(64), 0, (hipStream_t)stream, logits,
+                ld, (int)E, bias, mul, (int)k, (int)rows_per_block, block_boost, scaling, ids, w);
     return EXL3_OK;
 }
 

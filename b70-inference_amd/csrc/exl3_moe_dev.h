@@ -59,6 +59,10 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
     if (lane == 0) a.cnt_tok[(size_t)t * (a.H / 128) + nb] = 0;
 }
 
+template <int V, int SC>
+__device__ __forceinline__ void route_select(uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
+                                             int lane, bool renorm, float scaling, int& id, float& w);
+
 // Top-k routing of one row by one wave. Scoring SC (EXL3_SCORE_*), per entry with logit f and bias b (0 without one):
 //   softmax (trellis-serve.patch:395-441): rank by f + b; weight source g = f + b (bias_both) or f (selection-only
 //            bias, the reference's `cold` term); p = exp(g - max g) / sum exp(g - max g) over the row
@@ -145,6 +149,14 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
         sum = wave_sum_f32(se);
     }
 
+    route_select<V, SC>(key, g, mx, sum, k, lane, renorm, scaling, id, w);
+}
+
+// The k rounds of route_row over prepared order keys (0: not pickable) and weight sources: lane j < k returns pick j
+// in (id, w); mx / sum are the softmax maximum and denominator (SC softmax only).
+template <int V, int SC>
+__device__ __forceinline__ void route_select(uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
+                                             int lane, bool renorm, float scaling, int& id, float& w) {
     float gv = 0.f;
     id = -1;
     for (int j = 0; j < k; ++j) {

@@ -292,6 +292,62 @@ def moe_route(logits: torch.Tensor, bias: torch.Tensor, res, ids: torch.Tensor, 
         want.copy_(wi)
 
 
+def route_block(logits: torch.Tensor, k: int, bias: torch.Tensor | None = None, mul: torch.Tensor | None = None,
+                rows_per_block: int = 1, block_boost: float = 0.0, scaling: float = 1.0):
+    """Verify-block routing (exl3_route_block, sqrt_softplus): rows in blocks of rows_per_block, in order; an expert an
+    earlier row of the block picked ranks by s * mul * (1 + block_boost) + bias, the others by s * mul + bias; weights
+    from s, renormalised and scaled. Returns (ids int32 [M, k], w fp32 [M, k])."""
+    require_device(logits, bias, mul)
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise Exl3Error("route_block: logits must be fp32 [M, E] with contiguous rows")
+    M, E = logits.shape
+    for name, t in (("bias", bias), ("mul", mul)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != E or not t.is_contiguous()):
+            raise Exl3Error(f"route_block: {name} must be fp32 [E]")
+    ids = torch.empty(M, k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(M, k, dtype=torch.float32, device=logits.device)
+    check(lib().exl3_route_block(ptr(logits), logits.stride(0), M, E, ptr(bias), ptr(mul), k, int(rows_per_block),
+                                 float(block_boost), float(scaling), ptr(ids), ptr(w), stream_of(logits)),
+          "route_block")
+    return ids, w
+
+
+def route_fused(x, w0, w1, bias0, bias1, res0, ids0, w0o, want0, ids1, w1o, logits, scaling0, scaling1, mul0=None,
+                mul1=None, rows_per_block: int = 1, block_boost: float = 0.0) -> None:
+    """dsv_moe::route_fused (dsv41/xpu/csrc/dsv_moe_glue.sycl:476-520, bound at :622-624): the router logits of this
+    layer's gate w0 fp16 [E0, H] and optionally the next layer's w1 [E1, H] into logits (fp32, R rows of E0 + E1, in
+    place), then sqrt-softplus picks written in place: ids0 / w0o ranked by s * mul0 + bias0 + res0 (the verify-block
+    boost instead when rows_per_block > 1, block_boost > 0 and no res0), want0 (optional) the plain top-k of
+    s + bias0, and ids1 / w1o the next layer's picks by s * mul1 + bias1."""
+    R = x.shape[0]
+    E0 = w0.shape[0]
+    E1 = 0 if w1 is None else w1.shape[0]
+    k = ids0.shape[-1]
+    if logits.numel() < R * (E0 + E1) or not logits.is_contiguous():
+        raise Exl3Error("route_fused: logits must hold R * (E0 + E1) contiguous fp32 values")
+    lv = logits.reshape(-1)[: R * (E0 + E1)].view(R, E0 + E1)
+    router_logits(x, w0, E0, "eh", False, out=lv[:, :E0])
+    if E1:
+        router_logits(x, w1, E1, "eh", False, out=lv[:, E0:])
+    S = int(rows_per_block)
+    blk = S > 1 and block_boost > 0.0 and R % S == 0
+
+    def rt(lg, bias, res, mul, sc, ids_out, w_out, want_out):
+        if blk and res is None:
+            pi, pw = route_block(lg, k, bias, mul, S, block_boost, sc)
+        else:
+            pi, pw = route_adjusted(lg, k, bias, mul, res, "sqrt_softplus", True, sc)
+        ids_out.copy_(pi)
+        w_out.copy_(pw)
+        if want_out is not None:
+            wi, _ = route_topk(lg, k, bias, "sqrt_softplus", True, sc)
+            want_out.copy_(wi)
+
+    rt(lv[:, :E0], bias0, res0, mul0, scaling0, ids0, w0o, want0)
+    if E1:
+        rt(lv[:, E0:], bias1, None, mul1, scaling1, ids1, w1o, None)
+
+
 def router_logits(x: torch.Tensor, weight: torch.Tensor, E: int | None = None, layout: str = "he",
                   round_fp16: bool = False, out: torch.Tensor | None = None) -> torch.Tensor:
     """Router logits fp32 [M, E] = x @ W on the router GEMV (exl3_router_logits). layout "he": weight fp16 [H, >= E]

@@ -196,6 +196,15 @@ int exl3_route_adjusted(const float* logits, int64_t ld, int64_t M, int64_t E, c
                         const float* res, int64_t k, int score, int flags, float scaling, int32_t* ids, float* w,
                         void* stream);
 
+/* Verify-block routing (sqrt-softplus): rows in blocks of rows_per_block (M a multiple), each block's rows in order; an
+ * expert that an earlier row of the block picked ranks by s * mul[e] * (1 + block_boost) + bias[e], the others by
+ * s * mul[e] + bias[e] (mul, bias fp32 [E] or NULL; each operation rounded separately), exact ties to the lower
+ * index; weights s renormalised (+1e-20) * scaling. E <= 2048, k <= 32.
+ * Replaces: the block mode of dsv_moe::route_fused (RouteBlock, dsv41/xpu/csrc/dsv_moe_glue.sycl:194-240, 495-507). */
+int exl3_route_block(const float* logits, int64_t ld, int64_t M, int64_t E, const float* bias, const float* mul,
+                     int64_t k, int64_t rows_per_block, float block_boost, float scaling, int32_t* ids, float* w,
+                     void* stream);
+
 /* Router logits from hidden states: logits[m, e] = sum_h x[m, h] * W(h, e) in fp32 (fixed summation order), x fp16
  * [M, H] (row stride x_ld), logits fp32 [M, E] (row stride logits_ld), rounded to fp16 precision when round_fp16 != 0
  * (what a matmul of two fp16 tensors returns). w_layout EXL3_ROUTER_W_HE: W fp16 [H, E] (row stride w_ld >= E,

@@ -422,6 +422,35 @@ def route_topk(logits: np.ndarray, k: int, bias: np.ndarray | None = None, score
     return ids.astype(np.int32), w.astype(np.float32)
 
 
+def route_block(logits: np.ndarray, k: int, bias: np.ndarray | None = None, mul: np.ndarray | None = None,
+                rows_per_block: int = 1, boost: float = 0.0, scaling: float = 1.0):
+    """Verify-block routing (dsv41/xpu/csrc/dsv_moe_glue.sycl:194-240): sqrt-softplus s; rows of a block in order, an
+    expert picked by an earlier row of the block ranks by s * mul * (1 + boost) + b, the others by s * mul + b (float32
+    operations rounded one by one); weights from s (float64), renormalised (+1e-20) and scaled."""
+    f = logits.astype(np.float32)
+    M, E = f.shape
+    sp32 = np.where(f > 20, f, np.log1p(np.exp(np.minimum(f, 20)))).astype(np.float32)
+    s32 = np.sqrt(sp32).astype(np.float32)
+    f64 = f.astype(np.float64)
+    v = np.sqrt(np.where(f64 > 20, f64, np.log1p(np.exp(np.minimum(f64, 20)))))
+    m32 = np.ones(E, np.float32) if mul is None else mul.astype(np.float32)
+    up = np.float32(1) + np.float32(boost)
+    ids = np.zeros((M, k), np.int32)
+    w = np.zeros((M, k), np.float32)
+    for b0 in range(0, M, rows_per_block):
+        chosen = np.zeros(E, bool)
+        for r in range(b0, b0 + rows_per_block):
+            key = (s32[r] * m32).astype(np.float32) * np.where(chosen, up, np.float32(1)).astype(np.float32)
+            if bias is not None:
+                key = key + bias.astype(np.float32)
+            order = topk_lowest_index(key.astype(np.float32)[None, :], k)[0]
+            pv = v[r, order]
+            ids[r] = order
+            w[r] = pv * scaling / (pv.sum() + 1e-20)
+            chosen[order] = True
+    return ids, w
+
+
 def router_logits(x: np.ndarray, W: np.ndarray, layout: str = "he", round_fp16: bool = False) -> np.ndarray:
     """logits[m, e] = sum_h x[m, h] W(h, e) in float64, returned as float32, or rounded to fp16 precision (the result of
     a matmul of two fp16 tensors, glm/xpu/glm_xpu/ops.py:183-184). layout "he": W [H, E] (gate_tensor); "eh": W [E, H]

@@ -329,6 +329,29 @@ def test_route_topk_residency_terms(score):
     assert np.array_equal(ids4, keep[idk]) and np.allclose(w4, wk, rtol=1e-6)
 
 
+def test_route_block_properties():
+    """Verify-block routing pinned by properties: no boost (or blocks of one row) is the plain sqrt-softplus router row
+    by row; a boost large enough makes every later row of a block take the first row's experts; the weights always
+    come from the plain score of the picks."""
+    rng = np.random.default_rng(43)
+    lg = rng.normal(size=(8, 64)).astype(np.float32) * 2
+    b = (rng.normal(size=64) * 0.2).astype(np.float32)
+    mul = (1 + rng.random(64)).astype(np.float32)
+    pi, pw = O.route_topk(lg, 5, b, "sqrt_softplus", mul=mul)
+    for S, boost in ((4, 0.0), (1, 3.0)):
+        bi, bw = O.route_block(lg, 5, b, mul, S, boost)
+        assert np.array_equal(bi, pi) and np.allclose(bw, pw, rtol=1e-6)
+    bi, bw = O.route_block(lg, 5, b, None, 4, 1e4)
+    for blk in range(2):
+        first = set(bi[4 * blk].tolist())
+        assert all(set(bi[4 * blk + r].tolist()) == first for r in range(4))
+    pi0, pw0 = O.route_topk(lg, 5, None, "sqrt_softplus")
+    v = np.sqrt(np.log1p(np.exp(lg.astype(np.float64))))
+    for r in range(8):
+        pv = v[r, bi[r]]
+        assert np.allclose(bw[r], pv / (pv.sum() + 1e-20), rtol=1e-6)
+
+
 def test_route_topk_softmax_bias_both_is_route_softmax_topk():
     rng = np.random.default_rng(5)
     logits = rng.standard_normal((7, 200)).astype(np.float32)

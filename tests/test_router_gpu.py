@@ -100,6 +100,63 @@ def test_moe_route_in_place(exl3, oracle):
     assert np.abs(w.cpu().numpy() - rw).max() <= 1e-5 * 2.0
 
 
+@pytest.mark.parametrize("E,k,S,boost", [(64, 4, 2, 0.5), (256, 8, 4, 0.25), (1000, 6, 3, 1.0), (256, 8, 4, 0.0)])
+@pytest.mark.parametrize("with_mul", [False, True])
+def test_route_block_matches_oracle(exl3, oracle, E, k, S, boost, with_mul):
+    """Verify-block routing: rows of a block in order, earlier rows' experts boosted; picks identical to the oracle."""
+    M = 4 * S
+    logits, bias = _logits(M, E, 500 + E + S)
+    mul = (0.5 + torch.rand(E, generator=torch.Generator().manual_seed(E))) if with_mul else None
+    ids, w = exl3.route_block(logits.cuda(), k, bias.cuda(), None if mul is None else mul.cuda(), S, boost, 1.5)
+    rid, rw = oracle.route_block(logits.numpy(), k, bias.numpy(), None if mul is None else mul.numpy(), S, boost, 1.5)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.abs(w.cpu().numpy() - rw).max() <= 1e-5 * 1.5
+
+
+@pytest.mark.parametrize("S,boost,with_res", [(1, 0.0, True), (2, 0.5, False), (2, 0.5, True)])
+def test_route_fused_two_layers(exl3, oracle, S, boost, with_res):
+    """route_fused with the reference op's signature: logits of this layer's and the next layer's gates in one buffer,
+    this layer's picks (residency or block boost), the plain picks, and the next layer's picks."""
+    g = torch.Generator().manual_seed(600 + S)
+    R, H, E0, E1, k = 4, 512, 256, 160, 8
+    x = torch.randn(R, H, generator=g).half()
+    w0 = (torch.randn(E0, H, generator=g) / H ** 0.5).half()
+    w1 = (torch.randn(E1, H, generator=g) / H ** 0.5).half()
+    b0, b1 = torch.randn(E0, generator=g) * 0.1, torch.randn(E1, generator=g) * 0.1
+    m0, m1 = 1 + torch.rand(E0, generator=g), 1 + torch.rand(E1, generator=g)
+    res = torch.where(torch.rand(E0, generator=g) < 0.3, torch.tensor(-0.5), torch.tensor(0.0)) if with_res else None
+    dev = lambda t: None if t is None else t.cuda()  # noqa: E731
+    ids0 = torch.empty(R, k, dtype=torch.int64, device="cuda")
+    want0 = torch.empty(R, k, dtype=torch.int64, device="cuda")
+    ids1 = torch.empty(R, k, dtype=torch.int64, device="cuda")
+    w0o = torch.empty(R, k, device="cuda")
+    w1o = torch.empty(R, k, device="cuda")
+    logits = torch.empty(R * (E0 + E1), device="cuda")
+    exl3.route_fused(x.cuda(), w0.cuda(), w1.cuda(), b0.cuda(), b1.cuda(), dev(res), ids0, w0o, want0, ids1, w1o,
+                     logits, 1.5, 2.0, m0.cuda(), m1.cuda(), S, boost)
+    lg = logits.view(R, E0 + E1).cpu().numpy()
+    ref0 = oracle.router_logits(x.numpy(), w0.numpy(), "eh")
+    ref1 = oracle.router_logits(x.numpy(), w1.numpy(), "eh")
+    assert np.abs(lg[:, :E0] - ref0).max() <= 1e-5 * np.abs(ref0).max()
+    assert np.abs(lg[:, E0:] - ref1).max() <= 1e-5 * np.abs(ref1).max()
+    # picks from the GPU's own logits (a logit one ulp from the oracle's could reorder a near-tie)
+    l0, l1 = lg[:, :E0].copy(), lg[:, E0:].copy()
+    if S > 1 and boost > 0 and res is None:
+        rid0, rw0 = oracle.route_block(l0, k, b0.numpy(), m0.numpy(), S, boost, 1.5)
+        rid1, rw1 = oracle.route_block(l1, k, b1.numpy(), m1.numpy(), S, boost, 2.0)
+    else:
+        rid0, rw0 = oracle.route_topk(l0, k, b0.numpy(), "sqrt_softplus", True, 1.5, mul=m0.numpy(),
+                                      res=None if res is None else res.numpy())
+        if S > 1 and boost > 0:
+            rid1, rw1 = oracle.route_block(l1, k, b1.numpy(), m1.numpy(), S, boost, 2.0)
+        else:
+            rid1, rw1 = oracle.route_topk(l1, k, b1.numpy(), "sqrt_softplus", True, 2.0, mul=m1.numpy())
+    pid, _ = oracle.route_topk(l0, k, b0.numpy(), "sqrt_softplus", True, 1.5)
+    assert np.array_equal(ids0.cpu().numpy(), rid0) and np.array_equal(want0.cpu().numpy(), pid)
+    assert np.array_equal(ids1.cpu().numpy(), rid1)
+    assert np.abs(w0o.cpu().numpy() - rw0).max() <= 1e-5 * 1.5 and np.abs(w1o.cpu().numpy() - rw1).max() <= 2e-5
+
+
 @pytest.mark.parametrize("layout", ["he", "eh"])
 @pytest.mark.parametrize("H,E", [(128, 72), (2048, 512), (5120, 160), (7168, 256)])
 @pytest.mark.parametrize("M", [1, 3, 4, 9, 33])
