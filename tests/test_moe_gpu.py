@@ -182,6 +182,23 @@ def test_moe_forward_logits_in_layer_routing_exact(exl3, oracle, E, k, H, I, bia
     assert torch.equal(out, exl3.moe_forward(x, rid, rw, tables))
 
 
+@pytest.mark.parametrize("M", [1, 2])
+def test_moe_forward_logits_in_layer_fp16_and_router_kernel_switch(exl3, small, M, monkeypatch):
+    """fp16 outputs of the in-layer routing path, and the same call with the router kernel forced
+    (EXL3MI_ROUTER_KERNEL=1): bit-identical rows and picks either way."""
+    tables, _ = small
+    g = torch.Generator().manual_seed(2300 + M)
+    x = torch.randn(M, 256, generator=g).half().cuda()
+    logits = torch.randn(M, 11, generator=g).cuda()
+    a, ia, wa = exl3.moe_forward_logits(x, logits, 3, tables, shared=11, out_dtype=torch.float16, return_routing=True)
+    rid, rw = exl3.route_softmax_topk(logits, 3)
+    ref = exl3.moe_forward(x, rid, rw, tables, shared=11, out_dtype=torch.float16)
+    assert torch.equal(a, ref) and torch.equal(ia, rid) and torch.equal(wa, rw)
+    monkeypatch.setenv("EXL3MI_ROUTER_KERNEL", "1")
+    b, ib, wb = exl3.moe_forward_logits(x, logits, 3, tables, shared=11, out_dtype=torch.float16, return_routing=True)
+    assert torch.equal(a, b) and torch.equal(ia, ib) and torch.equal(wa, wb)
+
+
 @pytest.mark.parametrize("M", [1, 4, 12])
 def test_moe_packed_tables_same_rows(exl3, small, M):
     """ExpertTables.packed (uniform strides: the decode kernels compute expert addresses instead of loading them)
