@@ -1,6 +1,6 @@
 // Fused small-batch MoE layer on gfx950: gate|up, activation, down and combine in ONE launch.
 //
-// For decode batches (at most 8 tokens, at most kFusedMaxPairs (token, slot) pairs) the multi-kernel path is a chain
+// For decode batches (at most 16 tokens, at most kFusedMaxPairs (token, slot) pairs) the multi-kernel path is a chain
 // of short latency-bound launches. Here every workgroup:
 //   1. reads the routing ids (or, given router logits, ranks them itself: every wave one token, the picks in LDS) and
 //      groups the pairs (pair l in lanes l and l + 64 of wave 0) by expert in
@@ -35,7 +35,7 @@
 namespace exl3 {
 
 constexpr int kFusedMaxPairs = 128;
-constexpr int kFusedMaxRows = 8;
+constexpr int kFusedMaxRows = 16;     // tokens (items still hold at most 8 rows)
 constexpr int kFusedMinJobRows = 20;    // tile-rows of H per gate|up job, at least
 constexpr int kSpinMax = 1 << 20;       // polls of a down job's wait (each backs off up to ~512 cycles)
 constexpr int kCS = 32;                 // counter stride in ints (one 128-byte line per counter)

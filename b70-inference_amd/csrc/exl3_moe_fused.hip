@@ -43,7 +43,7 @@ static int fused_splits(int want, int T, int kbf) {
 }
 
 // Eligible: gate, up and down share one K (or all per-tile), or down has one or two bits more than gate/up; at most
-// 8 tokens and kFusedMaxPairs pairs; x rows 16-byte aligned.
+// kFusedMaxRows tokens and kFusedMaxPairs pairs; x rows 16-byte aligned.
 bool moe_fused_ok(const MoeArgs& a) {
     return (a.Kg == a.Kd || pick_fused_mixed(a.Kg, a.Kd, 1) != nullptr) && a.M <= kFusedMaxRows &&
            (int64_t)a.M * a.slots <= kFusedMaxPairs &&

@@ -78,6 +78,22 @@ def test_moe_fused_and_multi_kernel_paths(exl3, oracle, small, monkeypatch, M):
     assert max_rel(y2, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("M,k,E,Kg,Kd", [(12, 10, 64, 3, 3), (16, 8, 40, 2, 2), (10, 12, 200, 2, 3), (16, 7, 16, 4, 4)])
+def test_moe_fused_up_to_16_tokens(exl3, oracle, monkeypatch, M, k, E, Kg, Kd):
+    """9 to 16 tokens within 128 pairs take the one-launch layer (items of up to 8 rows, or 2 under sparse routing);
+    against the oracle and against the grouped multi-launch path (EXL3MI_NO_FUSED=1, MFMA above 8 rows)."""
+    tables, orc = make_experts(exl3, oracle, E, 256, 256, Kg, Kd, 2400 + E + M)
+    ids, w = _ids_w(M, k, E, 2401 + M, dup=True, inactive=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2402 + M)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert np.array_equal(y, y1)
+    monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    y2, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y2, ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("I,M", [(2048, 1), (2560, 2), (2560, 4)])
 def test_moe_fused_split_down_blocks(exl3, oracle, I, M):
     """Wide intermediate (I = 2048: two k splits of the down projection; I = 2560: three, whose staged ranges share
