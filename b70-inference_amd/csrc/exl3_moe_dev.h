@@ -60,7 +60,7 @@ __device__ __forceinline__ void combine_token(const MoeArgs& a, int t, int nb, i
 }
 
 template <int V, int SC>
-__device__ __forceinline__ void route_select(uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
+__device__ __forceinline__ void route_select(const uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
                                              int lane, bool renorm, float scaling, int& id, float& w);
 
 // Top-k routing of one row by one wave. Scoring SC (EXL3_SCORE_*), per entry with logit f and bias b (0 without one):
@@ -152,43 +152,62 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
     route_select<V, SC>(key, g, mx, sum, k, lane, renorm, scaling, id, w);
 }
 
+// A lane's two best keys not yet picked, ascending v so that equal keys keep their lowest index first: (k1, v1, g1)
+// then (k2, v2, g2); key 0 means none. A lane's picks come in descending (key, ascending v) order, so the keys not yet
+// picked are those ordered after its last pick (kl, vl); vl < 0: nothing picked yet.
+template <int V>
+__device__ __forceinline__ void lane_top2(const uint32_t (&key)[V], const float (&g)[V], uint32_t kl, int vl,
+                                          uint32_t& k1, int& v1, float& g1, uint32_t& k2, int& v2, float& g2) {
+    k1 = k2 = 0u;
+    v1 = v2 = 0;
+    g1 = g2 = 0.f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const bool left = vl < 0 || key[v] < kl || (key[v] == kl && v > vl);
+        const uint32_t kv = left ? key[v] : 0u;
+        if (kv > k1) {
+            k2 = k1; v2 = v1; g2 = g1;
+            k1 = kv; v1 = v; g1 = g[v];
+        } else if (kv > k2) {
+            k2 = kv; v2 = v; g2 = g[v];
+        }
+    }
+}
+
 // The k rounds of route_row over prepared order keys (0: not pickable) and weight sources: lane j < k returns pick j
-// in (id, w); mx / sum are the softmax maximum and denominator (SC softmax only).
+// in (id, w); mx / sum are the softmax maximum and denominator (SC softmax only). Each round takes the wave maximum of
+// the lanes' best remaining keys (ties: the lowest index) from a per-lane cache of two; a lane rescans its keys only
+// when a pick empties its cache, so a round costs a wave reduction rather than a scan of every key.
 template <int V, int SC>
-__device__ __forceinline__ void route_select(uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
+__device__ __forceinline__ void route_select(const uint32_t (&key)[V], const float (&g)[V], float mx, float sum, int k,
                                              int lane, bool renorm, float scaling, int& id, float& w) {
     float gv = 0.f;
     id = -1;
+    uint32_t kl = 0u, k1, k2;
+    int vl = -1, v1, v2;
+    float g1, g2;
+    lane_top2<V>(key, g, kl, vl, k1, v1, g1, k2, v2, g2);
     for (int j = 0; j < k; ++j) {
-        uint32_t best = 0u;
-        int bv = 0;
-        float gb = 0.f;
-#pragma unroll
-        for (int v = 0; v < V; ++v)
-            if (key[v] > best) {          // ascending v: a lane keeps its lowest index among equal keys
-                best = key[v];
-                bv = v;
-                gb = g[v];
-            }
-        const uint32_t kmax = wave_max_u32(best);
+        const uint32_t kmax = wave_max_u32(k1);
         if (kmax == 0u) break;            // fewer than k entries (k <= E is checked on the host)
-        const uint64_t mask = __ballot(best == kmax);
-        const int mine = lane + 64 * bv;
-        int widx;
-        if (__popcll(mask) == 1) widx = __builtin_amdgcn_readlane(mine, __ffsll((unsigned long long)mask) - 1);
-        else widx = (int)wave_min_u32(best == kmax ? (uint32_t)mine : 0xFFFFFFFFu);
-        // the winner's lane holds it as its own best (bv = widx >> 6): its weight source comes from there
-        const float gw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gb), widx & 63));
-        if (lane == (widx & 63)) {
-            const int vv = widx >> 6;
-#pragma unroll
-            for (int v = 0; v < V; ++v)
-                if (v == vv) key[v] = 0u;
+        const uint64_t mask = __ballot(k1 == kmax);
+        int wl;
+        if (__popcll(mask) == 1) wl = __ffsll((unsigned long long)mask) - 1;
+        else wl = (int)(wave_min_u32(k1 == kmax ? (uint32_t)(lane + 64 * v1) : 0xFFFFFFFFu) & 63u);
+        const int widx = wl + 64 * __builtin_amdgcn_readlane(v1, wl);
+        const float gw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g1), wl));
+        const bool empty = __builtin_amdgcn_readlane((int)k2, wl) == 0;
+        if (lane == wl) {
+            kl = k1;
+            vl = v1;
+            k1 = k2; v1 = v2; g1 = g2;
+            k2 = 0u;
         }
         if (lane == j) {
             id = widx;
             gv = gw;
         }
+        if (empty) lane_top2<V>(key, g, kl, vl, k1, v1, g1, k2, v2, g2);   // uniform: the winner's cache is empty
     }
     const float p = id >= 0 ? (SC == EXL3_SCORE_SOFTMAX ? expf(gv - mx) / sum : gv) : 0.f;
     const float s = wave_sum_f32(p);
