@@ -41,6 +41,29 @@ def test_route_topk_matches_oracle(exl3, oracle, score, E, k, bias_mode):
         assert np.abs(w.cpu().numpy() - rw).max() <= 1e-5 * max(1.0, float(np.abs(rw).max())), (renorm, scaling)
 
 
+@pytest.mark.parametrize("E,k", [(512, 10), (1000, 32), (4096, 32), (8192, 24)])
+def test_route_topk_picks_crowded_in_few_lanes(exl3, oracle, E, k):
+    """The top picks sit in one or two wave lanes (indices l + 64 v), with exact ties inside a lane and across
+    lanes: a lane is picked many times in a row, so its cache of best keys empties and refills repeatedly."""
+    g = torch.Generator().manual_seed(E + k)
+    logits = torch.randn(4, E, generator=g)
+    V = (E + 63) // 64
+    lane_a = torch.arange(5, E, 64)[: V]                     # lane 5, every value slot
+    lane_b = torch.arange(40, E, 64)[: V]
+    logits[0, lane_a] = 10.0 + torch.arange(len(lane_a)).float() % 3          # ties inside the lane
+    logits[1, lane_a] = 9.0
+    logits[1, lane_b] = 9.0                                                    # ties across two lanes
+    logits[2, lane_b] = 8.0 - torch.arange(len(lane_b)).float() * 0.25
+    logits[2, lane_a[: k // 2]] = 8.0                                          # ties with lane b's best
+    logits[3, lane_a] = float("-inf")
+    logits[3, lane_b[:3]] = float("-inf")
+    for score in ("softmax", "sigmoid"):
+        ids, w = exl3.route_topk(logits.cuda(), k, None, score)
+        rid, rw = oracle.route_topk(logits.numpy(), k, None, score)
+        assert np.array_equal(ids.cpu().numpy(), rid), score
+        assert np.abs(w.cpu().numpy() - rw).max() <= 1e-6, score
+
+
 def test_route_softmax_topk_unchanged_by_generalisation(exl3):
     """exl3_route_softmax_topk is route_topk(softmax, bias ranks and weights, renormalised): bit-identical results."""
     logits, bias = _logits(20, 512, 7)
