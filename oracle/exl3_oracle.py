@@ -21,6 +21,15 @@ Sources restated (paths relative to the reference root):
                            (blob_perm); glm/xpu/csrc/exl3_moe.n128.sycl:56-68 (Geom byte offsets)
   * align / pair lists     glm/xpu/csrc/exl3_moe.n128.sycl:691-734
 
+How each function is pinned (tests/test_oracle.py, tests/test_blob.py): codebook against six textual statements
+over all 65536 states; windows / reconstruct against the brute-force C ring decoder (oracle/trellis_bruteforce.c)
+for K = 1..8; permutation by three statements and bijectivity; Hadamard by orthogonality, basis rows and the dense
++-1 matmul; linear and MoE by the dense-weight form built the other way round; activations against
+torch.nn.functional gelu(approximate='tanh') / silu in float64 (with the clamp form); routing by hand-built ties and
+invariants; PLANAR4 against an element-by-element loop of the reference's stated index map. No function is
+"parity unpinned"; what stays unpinned is the un-vendored exllamav3 / trellis-serve code at the boundary (their
+testlib and packer), for which the agreeing statements above stand in.
+
 Every floating-point reduction here runs in float64 unless a caller asks for float32 (`acc`), so the oracle is at
 least as accurate as the fp32-accumulated reference. Rounding points that the reference fixes (fp16 x*suh, fp16
 transformed activations, fp16 gate/up/act) are reproduced exactly.

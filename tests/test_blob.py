@@ -2,6 +2,7 @@
 restatement of its packer), and (GPU) the arena-packed experts giving the same layer outputs as separately allocated
 ones."""
 import importlib
+import math
 
 import numpy as np
 import pytest
@@ -31,6 +32,40 @@ def test_reference_planar4_is_a_permutation_and_identity_for_even_k():
             assert np.array_equal(w, idx)
         else:
             assert not np.array_equal(w, idx)
+
+
+def _planar4_by_loops(words, K):
+    """PLANAR4 as the reference's kernel comment states it (exl3_moe.n128.sycl:8-11): within every k-row the tiles
+    are grouped by 4 along n, and word (tile t, period g, plane i) of a group, at [t][D g + i] in tile order, is
+    stored at [i][t][g]. words: uint32 [rows, tiles, 8K] in tile order. Built element by element."""
+    rows, tiles, W = words.shape
+    D = K // math.gcd(K, 32)
+    G = W // D
+    out = np.empty(words.size, dtype=np.uint32)
+    pos = 0
+    for r in range(rows):
+        for grp in range(tiles // 4):
+            for i in range(D):
+                for t in range(4):
+                    for g in range(G):
+                        out[pos] = words[r, 4 * grp + t, D * g + i]
+                        pos += 1
+    return out
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_planar4_matches_the_loop_built_index_map(K):
+    """The oracle's reshape/transpose statement of PLANAR4 equals the element loop for every K (a transposed
+    [tile][plane] order or swapped period/plane index fails: odd K has D = K planes of 8 periods)."""
+    rows, tiles = 3, 8
+    idx = np.arange(rows * tiles * 8 * K, dtype=np.uint32)
+    tr = idx.view(np.int16).reshape(rows, tiles, 16 * K)
+    assert np.array_equal(O.planar4_words(tr, K), _planar4_by_loops(idx.reshape(rows, tiles, 8 * K), K))
+    if K == 3:
+        # spot values: group 0 of row 0 starts with plane 0 of tiles 0..3 (words 0, 3, 6, ... of tile 0)
+        w = O.planar4_words(tr, K)
+        assert list(w[:9]) == [0, 3, 6, 9, 12, 15, 18, 21, 24]
+        assert w[8] == 24 and w[8 * 4] == 1 and w[8 * 4 * 3 - 1] == 4 * 24 - 1
 
 
 @pytest.mark.parametrize("K", [2, 3, 4, 5, 6])
@@ -95,7 +130,8 @@ def test_store_write_verify_load(tmp_path):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M", [3, 40])
 def test_arena_experts_same_outputs(exl3, M):
-    """Arena-packed experts (uniform-stride tables) and separately allocated copies give bit-identical layers."""
+    """Arena-packed experts (uniform-stride tables) and separately allocated copies give bit-identical layers, within
+    the tolerance of the oracle's layer."""
     E, H, I = 6, 256, 256
     geom = blob.RecordGeom(H, I, 3)
     experts = [_expert(H, I, 3, 3, 1000 + 10 * e) for e in range(E)]
@@ -116,3 +152,10 @@ def test_arena_experts_same_outputs(exl3, M):
     a = exl3.moe_forward_logits(x, logits, 2, t_arena)
     b = exl3.moe_forward_logits(x, logits, 2, t_sep)
     assert torch.equal(a, b)
+    # and the arena layer against the oracle's layer on the same experts and routing
+    rid, rw = O.route_softmax_topk(logits.cpu().numpy(), 2)
+    orc = [tuple(O.Proj(p["suh"].numpy(), p["svh"].numpy(), trellis=p["trellis"].numpy(), K=3) for p in ex)
+           for ex in experts]
+    ref = O.moe_layer(x.cpu().numpy(), orc, rid, rw, O.ACT_SILU)
+    err = float(np.abs(a.cpu().numpy() - ref).max() / np.abs(ref).max())
+    assert err <= 2e-3, err

@@ -445,17 +445,35 @@ def test_moe_layer_structure():
     assert np.allclose(O.moe_layer(x, ex, ids_m, w, O.ACT_SILU), O.moe_layer(x, ex, ids, w_m, O.ACT_SILU), atol=1e-6)
 
 
-def test_gelu_tanh_and_silu_closed_forms():
-    g = np.array([-3.0, -0.5, 0.0, 0.7, 2.0])
-    u = np.array([1.0, 2.0, 3.0, -1.0, 0.5])
-    silu = g / (1 + np.exp(-g)) * u
-    assert np.allclose(O.act_mul(g, u, O.ACT_SILU), silu)
-    clamp = np.minimum(g / (1 + np.exp(-g)), 1.0) * np.clip(u, -1.0, 1.0)
-    assert np.allclose(O.act_mul(g, u, O.ACT_SILU, 1.0), clamp)
-    # GELU-tanh at known points: gelu(0) = 0, gelu(x) -> x for large x, odd-symmetry gelu(x) - gelu(-x) = x
-    ge = O.act_mul(g, np.ones_like(g), O.ACT_GELU_TANH)
-    assert ge[2] == 0.0
-    assert np.allclose(O.act_mul(np.array([10.0]), np.ones(1), O.ACT_GELU_TANH), 10.0)
-    xs = np.linspace(-4, 4, 17)
-    gx = O.act_mul(xs, np.ones_like(xs), O.ACT_GELU_TANH)
-    assert np.allclose(gx - gx[::-1], xs, atol=1e-12)
+def _act_points():
+    """A dense grid over [-20, 20], the fp16 extremes (largest finite, smallest normal and subnormal) of both signs,
+    and N(0, 3) samples: float64."""
+    fp16 = np.array([65504.0, 6.103515625e-05, 5.960464477539063e-08, 1e-3, 0.5, 8.0, 11.0])
+    rng = np.random.default_rng(7)
+    return np.concatenate([np.linspace(-20.0, 20.0, 40001), fp16, -fp16, [0.0], rng.normal(0, 3, 5000)])
+
+
+def test_act_mul_matches_torch_gelu_tanh_and_silu():
+    """GELU-tanh and SiLU (with and without the act_limit clamp) against torch.nn.functional in float64 (the SiLU
+    clamp form of ext-op-inventory.md:944-956: min(silu(g), L) * clamp(u, -L, L)). torch is an independent
+    statement of both functions (gelu(approximate='tanh'), silu)."""
+    import torch
+    import torch.nn.functional as F
+    g = _act_points()
+    u = np.random.default_rng(8).normal(0, 2, g.size)
+    tg, tu = torch.from_numpy(g), torch.from_numpy(u)
+    ref_gelu = (F.gelu(tg, approximate="tanh") * tu).numpy()
+    ref_silu = (F.silu(tg) * tu).numpy()
+    for L in (1.0, 10.0):
+        ref_clamp = (torch.clamp(F.silu(tg), max=L) * torch.clamp(tu, -L, L)).numpy()
+        np.testing.assert_allclose(O.act_mul(g, u, O.ACT_SILU, L), ref_clamp, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(O.act_mul(g, u, O.ACT_GELU_TANH), ref_gelu, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(O.act_mul(g, u, O.ACT_SILU), ref_silu, rtol=1e-12, atol=1e-14)
+    # the check separates the plausible mistakes: exact-erf GELU, the cubic coefficient off by 10x, SiLU with the
+    # clamp applied before the activation (sglang's swiglu_clamped), all differ by far more than the tolerance
+    erf = (F.gelu(tg) * tu).numpy()
+    c = math.sqrt(2.0 / math.pi)
+    bad_coef = 0.5 * g * (1.0 + np.tanh(c * (g + 0.44715 * g ** 3))) * u
+    pre_clamp = (F.silu(torch.clamp(tg, max=1.0)) * torch.clamp(tu, -1.0, 1.0)).numpy()
+    for wrong, good in ((erf, ref_gelu), (bad_coef, ref_gelu), (pre_clamp, O.act_mul(g, u, O.ACT_SILU, 1.0))):
+        assert np.abs(wrong - good).max() > 1e-5
