@@ -24,6 +24,8 @@ SIGNATURES = {
     "exl3_last_error": [],
     "exl3_abi_version": [],
     "exl3_reserve_workspace": [_i64, _i64],
+    "exl3_device_status": [_vp],
+    "exl3_release_workspace": [],
     "exl3_profile_enable": [_i32],
     "exl3_profile_read": [ctypes.c_char_p, _i64],
     "exl3_reconstruct": [_vp, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64, _vp],
@@ -101,6 +103,24 @@ def profile_read() -> dict:
         name, cnt, avg = line.rsplit(" ", 2)
         out[name] = (int(cnt), float(avg))
     return out
+
+
+def device_status() -> int:
+    """The current device's status word: non-zero after a fused MoE layer launch gave up waiting (read on the host,
+    no synchronisation; the next library call on the device reports and clears it)."""
+    v = ctypes.c_int(0)
+    check(lib().exl3_device_status(ctypes.byref(v)), "exl3_device_status")
+    return v.value
+
+
+def reserve_workspace(nbytes: int, ncounters: int = 0):
+    """Pre-size this device's workspace (e.g. before HIP graph capture; growth is refused while capturing)."""
+    check(lib().exl3_reserve_workspace(int(nbytes), int(ncounters)), "exl3_reserve_workspace")
+
+
+def release_workspace():
+    """Free outgrown workspace buffers (synchronises; no graph captured before may be replayed afterwards)."""
+    check(lib().exl3_release_workspace(), "exl3_release_workspace")
 
 
 def require_device(*ts):

@@ -306,7 +306,7 @@ int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uin
     const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
     const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
     Workspace ws;
-    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, &ws);
+    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, st, &ws);
     if (rc) return rc;
     GemvArgs ga = {};
     ga.x = A;
@@ -475,7 +475,7 @@ int exl3_mgemm(const uint16_t* A, int64_t a_batches, int64_t m, int64_t k, const
     const size_t part_bytes = carve_size((size_t)slots * strips * P * kGemvMaxRows * 128, sizeof(float));
     const size_t y_bytes = weighted ? carve_size((size_t)slots * m * n, sizeof(float)) : 0;
     Workspace ws;
-    int rc = workspace(part_bytes + y_bytes, (size_t)(slots > 0 ? slots : 1) * strips, &ws);
+    int rc = workspace(part_bytes + y_bytes, (size_t)(slots > 0 ? slots : 1) * strips, st, &ws);
     if (rc) return rc;
     Carve cv{ws.scratch, ws.scratch_bytes};
     float* part = cv.take<float>((size_t)slots * strips * P * kGemvMaxRows * 128);

@@ -1144,7 +1144,7 @@ int launch_linear_mfma(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, co
     const size_t xh_b = carve_size((size_t)S * m * k, 2), xs_b = carve_size((size_t)S * m * nblk, 4);
     const size_t part_b = a.P > 1 ? carve_size((size_t)a.P * m * n, 4) : 0;
     Workspace ws;
-    rc = workspace(xh_b + xs_b + part_b, 0, &ws);
+    rc = workspace(xh_b + xs_b + part_b, 0, st, &ws);
     if (rc) return rc;
     Carve cv{ws.scratch, ws.scratch_bytes};
     _Float16* xh = cv.take<_Float16>((size_t)S * m * k);

@@ -907,7 +907,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
                    carve_size(npairs * a.I, 2) + carve_size(npairs * a.H, 4) +
                    carve_size(n_gu * a.P_gu * 2 * MR * 128, 4) + carve_size(n_d * a.P_d * MR * 128, 4);
     const size_t n_tok = (size_t)a.M * nbH;
-    int rc = workspace(bytes, n_gu + n_d + n_tok, &ws);
+    int rc = workspace(bytes, n_gu + n_d + n_tok, st, &ws);
     if (rc) return rc;
     Carve c{ws.scratch, ws.scratch_bytes};
     a.n_items = c.take<int>(1);

@@ -21,7 +21,9 @@
 // each XCD (ids round-robin over the XCDs), and every workgroup finishes its gate|up job before it can wait, so the
 // lowest waiting workgroup always has its inputs coming: no co-residency is assumed. The grid is sized to what the
 // device holds at once, so in practice every workgroup is resident from the start. The wait is also bounded: a
-// timeout sets an error word instead of hanging. Cross-workgroup data (partials, down inputs, y) moves with
+// timeout sets the device's host-mapped status word instead of hanging (the job then runs on incomplete inputs and
+// the counters may be left non-zero; the next library call on the device finds the word on the host, zeroes the
+// counters and fails with EXL3_ERR_HIP). Cross-workgroup data (partials, down inputs, y) moves with
 // agent-scope stores and loads that write through the XCD-local L2, published by counters after the stores have
 // drained (the split-K handoff). Every counter sits on its own 128-byte line.
 #pragma once
@@ -37,7 +39,6 @@ namespace exl3 {
 constexpr int kFusedMaxPairs = 128;
 constexpr int kFusedMaxRows = 16;     // tokens (items still hold at most 8 rows)
 constexpr int kFusedMinJobRows = 20;    // tile-rows of H per gate|up job, at least
-constexpr int kSpinMax = 1 << 20;       // polls of a down job's wait (each backs off up to ~512 cycles)
 constexpr int kCS = 32;                 // counter stride in ints (one 128-byte line per counter)
 #ifndef EXL3_FUSED_RING
 #define EXL3_FUSED_RING 4
@@ -62,7 +63,8 @@ struct FusedArgs {
     int* cnt_d;                         // [max_items * nbH] * kCS
     int* cnt_tok;                       // [M * nbH] * kCS
     int* cnt_item;                      // [max_items] * kCS
-    int* err;                           // set when a wait times out
+    int* status;                        // host-mapped status word, set when a wait gives up (report_timeout)
+    int spin_max;                       // polls of a down job's wait before it gives up (each backs off <= ~512 cycles)
     int P_gu, P_d;                      // k-splits (in tile-rows) of H for gate|up and of I for down
     int direct;                         // down jobs build their inputs from the gate|up partials (no epilogue stage)
     int uniform;                        // expert e's table entry i is tb[i] + e * ts[i] (no table loads)
@@ -566,8 +568,8 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         const int need = a.direct ? nbI * a.P_gu : a.P_gu + 1;
         int n = 0, back = 1;
         while (__ballot(mine && atomic_load_agent(c) < need)) {
-            if (++n > kSpinMax) {
-                if (lane0 == 0) atomic_store_agent(a.err, 1);
+            if (++n > a.spin_max) {
+                if (lane0 == 0) report_timeout(a.status);
                 break;
             }
             for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(2);

@@ -140,9 +140,9 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     const size_t pd = a.P_d > 1 ? mx * nbH * a.P_d * MR * 128 : 1;
     const size_t bytes = carve_size(mx * MR * a.I, 4) + carve_size(np * a.H, 4) +
                          carve_size(mx * nbI * a.P_gu * 2 * MR * 128, 4) + carve_size(pd, 4);
-    const size_t n_cnt = (mx * nbI + mx * nbH + (size_t)a.M * nbH + mx + 1) * kCS;
+    const size_t n_cnt = (mx * nbI + mx * nbH + (size_t)a.M * nbH + mx) * kCS;
     Workspace ws;
-    rc = workspace(bytes, n_cnt, &ws);
+    rc = workspace(bytes, n_cnt, st, &ws);
     if (rc) return rc;
     Carve c{ws.scratch, ws.scratch_bytes};
     a.abuf = c.take<float>(mx * MR * a.I);
@@ -155,7 +155,8 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     a.cnt_d = a.cnt_gu + mx * nbI * kCS;
     a.cnt_tok = a.cnt_d + mx * nbH * kCS;
     a.cnt_item = a.cnt_tok + (size_t)a.M * nbH * kCS;
-    a.err = a.cnt_item + mx * kCS;
+    a.status = ws.status;
+    a.spin_max = spin_limit();
     EXL3_LAUNCH("moe_fused", fn, dim3((unsigned)grid), dim3(256), 0, st, a);
     return EXL3_OK;
 }

@@ -26,6 +26,7 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_ws_mu;
 Workspace g_ws[kMaxDevices];
+int* g_status_host[kMaxDevices];   // host view of each device's status word (Workspace::status is its device address)
 }  // namespace
 
 namespace {
@@ -76,38 +77,104 @@ int resident_blocks(const void* fn, int threads, int* out) {
     return EXL3_OK;
 }
 
-int workspace(size_t bytes, size_t ncounters, Workspace* out) {
+namespace {
+std::vector<void*> g_retired[kMaxDevices];   // outgrown workspace buffers, freed by exl3_release_workspace
+
+__global__ void zero_ints_kernel(int* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+int zero_ints(int* p, size_t n, hipStream_t st) {
+    if (!p || !n) return EXL3_OK;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, st, p, n);
+    EXL3_CHECK_HIP(hipGetLastError());
+    return EXL3_OK;
+}
+
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+}  // namespace
+
+int workspace(size_t bytes, size_t ncounters, hipStream_t st, Workspace* out) {
     int dev = 0;
     EXL3_CHECK_HIP(hipGetDevice(&dev));
     if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_ws_mu);
     Workspace& w = g_ws[dev];
+    if (!w.status) {
+        if (capturing(st))
+            return fail(EXL3_ERR_INVALID, "workspace: first use of device %d under stream capture; call "
+                                          "exl3_reserve_workspace before capturing", dev);
+        int* h = nullptr;
+        EXL3_CHECK_HIP(hipHostMalloc(reinterpret_cast<void**>(&h), 64, hipHostMallocMapped | hipHostMallocCoherent));
+        *h = 0;
+        int* d = nullptr;
+        EXL3_CHECK_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&d), h, 0));
+        g_status_host[dev] = h;
+        w.status = d;
+    }
+    if (*reinterpret_cast<volatile int*>(g_status_host[dev]) != 0) {
+        const int rc = zero_ints(w.counters, w.ncounters, st);
+        *reinterpret_cast<volatile int*>(g_status_host[dev]) = 0;
+        if (rc) return rc;
+        return fail(EXL3_ERR_HIP, "a fused MoE layer launch on device %d gave up waiting for its gate|up inputs (its "
+                                  "outputs are incomplete, and so may be those of calls queued behind it); the "
+                                  "counters have been reset, later calls run normally", dev);
+    }
     if (bytes > w.scratch_bytes) {
+        if (capturing(st))
+            return fail(EXL3_ERR_INVALID, "workspace: %zu bytes of scratch needed under stream capture, %zu reserved; "
+                                          "call exl3_reserve_workspace before capturing", bytes, w.scratch_bytes);
         size_t nb = bytes + bytes / 4;
         nb = (nb + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
         char* p = nullptr;
-        EXL3_CHECK_HIP(hipDeviceSynchronize());
-        if (w.scratch) EXL3_CHECK_HIP(hipFree(w.scratch));
-        w.scratch = nullptr;
-        w.scratch_bytes = 0;
         EXL3_CHECK_HIP(hipMalloc(&p, nb));
+        if (w.scratch) g_retired[dev].push_back(w.scratch);
         w.scratch = p;
         w.scratch_bytes = nb;
     }
     if (ncounters > w.ncounters) {
+        if (capturing(st))
+            return fail(EXL3_ERR_INVALID, "workspace: %zu counters needed under stream capture, %zu reserved; call "
+                                          "exl3_reserve_workspace before capturing", ncounters, w.ncounters);
         size_t nc = ncounters < 65536 ? 65536 : ncounters * 2;
         int* c = nullptr;
-        EXL3_CHECK_HIP(hipDeviceSynchronize());
-        if (w.counters) EXL3_CHECK_HIP(hipFree(w.counters));
-        w.counters = nullptr;
-        w.ncounters = 0;
         EXL3_CHECK_HIP(hipMalloc(&c, nc * sizeof(int)));
-        EXL3_CHECK_HIP(hipMemset(c, 0, nc * sizeof(int)));
-        EXL3_CHECK_HIP(hipDeviceSynchronize());
+        const int rc = zero_ints(c, nc, st);
+        if (rc) {
+            (void)hipFree(c);
+            return rc;
+        }
+        if (w.counters) g_retired[dev].push_back(w.counters);
         w.counters = c;
         w.ncounters = nc;
     }
     *out = w;
+    return EXL3_OK;
+}
+
+int spin_limit() { return env_int("EXL3MI_SPIN_LIMIT", 1 << 20); }
+
+int device_status(int* out) {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    *out = g_status_host[dev] ? *reinterpret_cast<volatile int*>(g_status_host[dev]) : 0;
+    return EXL3_OK;
+}
+
+int release_workspace() {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
+    EXL3_CHECK_HIP(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (void* p : g_retired[dev]) EXL3_CHECK_HIP(hipFree(p));
+    g_retired[dev].clear();
     return EXL3_OK;
 }
 
@@ -203,7 +270,17 @@ int exl3_abi_version(void) { return EXL3_ABI_VERSION; }
 int exl3_reserve_workspace(int64_t bytes, int64_t ncounters) {
     if (bytes < 0 || ncounters < 0) return exl3::fail(EXL3_ERR_INVALID, "negative workspace size");
     exl3::Workspace w;
-    return exl3::workspace((size_t)bytes, (size_t)ncounters, &w);
+    const int rc = exl3::workspace((size_t)bytes, (size_t)ncounters, nullptr, &w);
+    if (rc) return rc;
+    EXL3_CHECK_HIP(hipDeviceSynchronize());   // counters zeroed for every stream
+    return EXL3_OK;
 }
+
+int exl3_device_status(int* status) {
+    if (!status) return exl3::fail(EXL3_ERR_INVALID, "exl3_device_status: null output");
+    return exl3::device_status(status);
+}
+
+int exl3_release_workspace(void) { return exl3::release_workspace(); }
 
 }  // extern "C"

@@ -23,16 +23,34 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
     } while (0)
 
 // Device workspace of the current device. `bytes` of plain scratch (256-byte aligned) and `ncounters` int32 arrival
-// counters that are zero between calls (kernels that use a counter reset it before they exit). Grows on demand;
-// growing synchronises the device. Calls that share a device must be ordered on one stream (as the reference's
-// library-owned scratch, glm/xpu/csrc/exl3_ops.sycl:202-207).
+// counters that are zero between calls (kernels that use a counter reset it before they exit), plus `status`, the
+// device address of a host-mapped word that a kernel sets (system-scope store) when one of its bounded waits gives
+// up. Calls that share a device must be ordered on one stream (as the reference's library-owned scratch,
+// glm/xpu/csrc/exl3_ops.sycl:202-207).
+// Growing allocates new buffers and keeps the old ones alive (kernels already queued and captured graphs still point
+// at them) until exl3_release_workspace; it never synchronises, the new counters are zeroed by a fill kernel on
+// `stream`, and it is refused while `stream` is being captured (exl3_reserve_workspace beforehand).
+// Before anything else it checks the status word (a host read, no synchronisation): when a wait has timed out it
+// zeroes the counters on `stream`, clears the word and fails with EXL3_ERR_HIP.
 struct Workspace {
     char* scratch = nullptr;
     size_t scratch_bytes = 0;
     int* counters = nullptr;
     size_t ncounters = 0;
+    int* status = nullptr;
 };
-int workspace(size_t bytes, size_t ncounters, Workspace* out);
+int workspace(size_t bytes, size_t ncounters, hipStream_t stream, Workspace* out);
+
+// Wait bound of the kernels' cross-workgroup waits (polls): EXL3MI_SPIN_LIMIT, default 2^20. A small value makes a
+// wait give up early (failure-path tests); every kernel still exits.
+int spin_limit();
+int device_status(int* out);
+int release_workspace();
+
+// Marks the status word (device code; `status` from Workspace).
+__device__ __forceinline__ void report_timeout(int* status) {
+    __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 
 // Two library-owned side streams (default priority) and three events of the current device, created on first use:
 // a launch sequence forks onto them with events and joins back, which also works under stream capture.

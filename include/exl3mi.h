@@ -1,9 +1,10 @@
 /* exl3mi: EXL3 trellis-quantized linear and grouped-MoE kernels for AMD Instinct MI355X (gfx950).
  *
  * Plain C ABI: device pointers, sizes, a hipStream_t passed as void*. Every entry point is asynchronous on `stream`
- * (NULL = the default stream), never synchronises the host, and returns an exl3_status. The caller owns every input
- * and output buffer; outputs are written in place. Library-owned scratch is cached per device (grown on demand; see
- * exl3_reserve_workspace). Calls on one device must be ordered on one stream.
+ * (NULL = the default stream), never synchronises the host (the workspace calls below say where they do), and
+ * returns an exl3_status. The caller owns every input and output buffer; outputs are written in place.
+ * Library-owned scratch is cached per device (grown on demand; see exl3_reserve_workspace). Calls on one device must
+ * be ordered on one stream: they share that device's workspace, and two calls that overlap in time race on it.
  *
  * Data formats (identical to exllamav3 / the reference, ext-op-inventory.md:698-777):
  *   trellis  int16 [k/16][n/16][16*K], K = bits per weight (1..8), one 16x16 tile = 8*K little-endian uint32 words
@@ -40,8 +41,22 @@ const char* exl3_last_error(void);
 int exl3_abi_version(void);
 
 /* Pre-size this device's workspace (bytes of scratch, number of arrival counters) so later calls do not allocate,
- * e.g. before HIP graph capture. No reference counterpart (the reference grows its scratch inside the op). */
+ * e.g. before HIP graph capture (a call that would grow the workspace while its stream is being captured fails with
+ * EXL3_ERR_INVALID). Synchronises the device. Growing (here or inside a call) keeps the outgrown buffers alive, since
+ * queued kernels and captured graphs may still use them, until exl3_release_workspace.
+ * No reference counterpart (the reference grows its scratch inside the op, glm/xpu/csrc/exl3_ops.sycl:202-207). */
 int exl3_reserve_workspace(int64_t bytes, int64_t ncounters);
+
+/* Free the outgrown workspace buffers of the current device. Synchronises the device; graphs captured while those
+ * buffers were current must not be replayed afterwards. No reference counterpart. */
+int exl3_release_workspace(void);
+
+/* The current device's status word: 0, or 1 after a fused MoE layer launch gave up one of its bounded
+ * cross-workgroup waits (its outputs, and possibly those of launches queued behind it, are then incomplete). Read on
+ * the host without synchronising; the next library call on the device that uses the workspace zeroes the library's
+ * arrival counters on its stream, clears the word and returns EXL3_ERR_HIP. No reference counterpart (the
+ * reference's kernels do not wait across work-groups). */
+int exl3_device_status(int* status);
 
 /* Kernel timing: while enabled (on != 0), every kernel the library launches is bracketed by a HIP event pair on its
  * stream; with on = R > 1 each launch runs R times inside its pair (the kernels are idempotent) to amortise the event
