@@ -31,6 +31,7 @@ SIGNATURES = {
     "exl3_reconstruct": [_vp, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64, _vp],
     "exl3_had_r_128": [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _f32, _vp],
     "exl3_gemm": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp],
+    "exl3_gemm_noalloc": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp],
     "exl3_linear_sharded": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _vp, _i32, _vp],
     "exl3_mgemm": [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _i64, _i64, _i64, _vp,
                    _i32, _vp],

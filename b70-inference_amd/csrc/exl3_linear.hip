@@ -4,6 +4,8 @@
 // XPU library's exl3_reconstruct / exl3_gemm_small (glm/xpu/csrc/exl3_ops.sycl:258-321, 539-555).
 #include "exl3_device.h"
 #include "exl3_gemv.h"
+
+#include <mutex>
 #include "exl3_runtime.h"
 
 namespace exl3 {
@@ -285,7 +287,10 @@ constexpr int kLinearMfmaMinRows = 9;
 
 // Launches over chunks of up to kGemvMaxRows rows of `ga` (x, out and m describe all rows; the workspace holds
 // slots x strips x P partial blocks and slots x strips counters).
-static int gemv_chunks(GemvArgs ga, int64_t m, int K, bool f32, int strips, int slots, hipStream_t st) {
+// With `profiled` false the launches bypass the opt-in event profiler (which creates events), so that the
+// allocation-free entry point never allocates.
+static int gemv_chunks(GemvArgs ga, int64_t m, int K, bool f32, int strips, int slots, hipStream_t st,
+                       bool profiled = true) {
     const int Mmax = kGemvMaxRows;
     for (int64_t m0 = 0; m0 < m; m0 += Mmax) {
         const int mm = (int)((m - m0) < Mmax ? (m - m0) : Mmax);
@@ -295,36 +300,84 @@ static int gemv_chunks(GemvArgs ga, int64_t m, int K, bool f32, int strips, int 
         c.out = f32 ? (void*)(reinterpret_cast<float*>(ga.out) + m0 * ga.out_ld)
                     : (void*)(reinterpret_cast<uint16_t*>(ga.out) + m0 * ga.out_ld);
         gemv_fn fn = gemv_select(K, mm, f32);
-        EXL3_LAUNCH("gemv", fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+        if (profiled) {
+            EXL3_LAUNCH("gemv", fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+        } else {
+            hipLaunchKernelGGL(fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+            EXL3_CHECK_HIP(hipGetLastError());
+        }
     }
     return EXL3_OK;
 }
 
-int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
-                int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh,
-                hipStream_t st) {
-    const int strips = (int)(n / 128), nblk = (int)(k / 128), tn = (int)(n / 16);
-    const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
-    Workspace ws;
-    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, st, &ws);
-    if (rc) return rc;
+// Arguments of a dense decode GEMV over all of x's rows, partials and counters left to the caller.
+static GemvArgs gemv_args(const uint16_t* A, int64_t a_ld, int64_t k, const uint32_t* tr, int64_t n, void* C,
+                          int64_t c_ld, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh, int P) {
     GemvArgs ga = {};
     ga.x = A;
     ga.x_ld = a_ld;
     ga.tr = tr;
-    ga.tn = tn;
+    ga.tn = (int)(n / 16);
     ga.suh = suh;
     ga.S = S;
     ga.sonb = S > 1 ? sonb : nullptr;
     ga.svh = svh;
     ga.out = C;
     ga.out_ld = c_ld;
+    ga.P = P;
+    ga.nblk = (int)(k / 128);
+    ga.a_div = 1;
+    return ga;
+}
+
+int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uint32_t* tr, int64_t n, int K, void* C,
+                int64_t c_ld, bool f32, const uint16_t* suh, int S, const int32_t* sonb, const uint16_t* svh,
+                hipStream_t st) {
+    const int strips = (int)(n / 128), nblk = (int)(k / 128);
+    const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
+    Workspace ws;
+    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, st, &ws);
+    if (rc) return rc;
+    GemvArgs ga = gemv_args(A, a_ld, k, tr, n, C, c_ld, suh, S, sonb, svh, P);
     ga.part = reinterpret_cast<float*>(ws.scratch);
     ga.cnt = ws.counters;
-    ga.P = P;
-    ga.nblk = nblk;
-    ga.a_div = 1;
     return gemv_chunks(ga, m, K, f32, strips, 1, st);
+}
+
+// ------------------------------------------------------------------------------------------------ allocation-free
+// The decode GEMV of exl3_gemm with its split-K partials and arrival counters in a fixed device array instead of the
+// library workspace, for callers that cannot allocate (code under HIP graph capture, serving loops). The array lives
+// as long as the process, one copy per device; every call on a device shares it (calls that overlap race).
+constexpr size_t kNoAllocPartBytes = 16u << 20;              // split-K partials: strips x P x 8 rows x 128 fp32
+constexpr size_t kNoAllocCounters = 16384;                   // arrival counters: one per 128-column strip
+static __device__ __align__(256) char scratch[kNoAllocPartBytes + kNoAllocCounters * sizeof(int)];
+
+namespace {
+std::mutex g_scratch_mu;
+char* g_scratch_dev[64];                                      // device address of `scratch`, per device
+
+__global__ void zero_counters_kernel(int* c, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) c[i] = 0;
+}
+}  // namespace
+
+// Device address of this device's `scratch` (looked up once per device with that device current); the first call
+// on a device also clears the counters on `st` (the kernels leave them at zero after every call).
+static int noalloc_scratch(hipStream_t st, char** out) {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        char* p = nullptr;
+        EXL3_CHECK_HIP(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)));
+        hipLaunchKernelGGL(zero_counters_kernel, dim3(64), dim3(256), 0, st,
+                           reinterpret_cast<int*>(p + kNoAllocPartBytes), (int)kNoAllocCounters);
+        EXL3_CHECK_HIP(hipGetLastError());
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return EXL3_OK;
 }
 
 // ------------------------------------------------------------------------------------------------ multi-matrix
@@ -439,6 +492,41 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
               void* stream) {
     (void)A_had;
     return exl3_linear_sharded(A, a_ld, m, k, B, n, K, C, c_ld, c_dtype, suh, 1, nullptr, svh, cb, stream);
+}
+
+int exl3_gemm_noalloc(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K,
+                      void* C, int64_t c_ld, int c_dtype, const uint16_t* suh, const uint16_t* svh, int cb,
+                      void* stream) {
+    if (cb != 2) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm_noalloc: codebook %d not supported (mul1 = 2 only)", cb);
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_gemm_noalloc: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(c_dtype == EXL3_F16 || c_dtype == EXL3_F32, "exl3_gemm_noalloc: C must be fp16 or fp32");
+    EXL3_CHECK_ARG(m >= 0 && m <= kGemvMaxRows, "exl3_gemm_noalloc: m=%lld rows, at most %d", (long long)m,
+                   kGemvMaxRows);
+    EXL3_CHECK_ARG(k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0,
+                   "exl3_gemm_noalloc: k=%lld and n=%lld must be positive multiples of 128", (long long)k,
+                   (long long)n);
+    EXL3_CHECK_ARG(a_ld >= k && c_ld >= n, "exl3_gemm_noalloc: row strides must cover k / n");
+    if (m == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(A && B && C && suh && svh, "exl3_gemm_noalloc: null pointer");
+    EXL3_CHECK_ARG(aligned(B, 4), "exl3_gemm_noalloc: trellis must be 4-byte aligned");
+    EXL3_CHECK_ARG(k / 16 * (n / 16) * 8 * (int64_t)K < (1LL << 32),
+                   "exl3_gemm_noalloc: trellis of %lld x %lld at K=%d exceeds 2^32 words", (long long)k,
+                   (long long)n, K);
+    const int64_t strips = n / 128;
+    EXL3_CHECK_ARG(strips <= (int64_t)kNoAllocCounters, "exl3_gemm_noalloc: n=%lld exceeds the %zu columns of the "
+                   "fixed scratch", (long long)n, kNoAllocCounters * 128);
+    const int P = gemv_splits((int)strips, (int)(k / 128), (int)m);
+    const size_t part = (size_t)strips * P * kGemvMaxRows * 128 * sizeof(float);
+    EXL3_CHECK_ARG(part <= kNoAllocPartBytes, "exl3_gemm_noalloc: %zu bytes of split-K partials needed, the fixed "
+                   "scratch holds %zu", part, kNoAllocPartBytes);
+    hipStream_t st = (hipStream_t)stream;
+    char* sc = nullptr;
+    const int rc = noalloc_scratch(st, &sc);
+    if (rc) return rc;
+    GemvArgs ga = gemv_args(A, a_ld, k, reinterpret_cast<const uint32_t*>(B), n, C, c_ld, suh, 1, nullptr, svh, P);
+    ga.part = reinterpret_cast<float*>(sc);
+    ga.cnt = reinterpret_cast<int*>(sc + kNoAllocPartBytes);
+    return gemv_chunks(ga, m, K, c_dtype == EXL3_F32, (int)strips, 1, st, false);
 }
 
 int exl3_mgemm(const uint16_t* A, int64_t a_batches, int64_t m, int64_t k, const int64_t* B_ptrs,

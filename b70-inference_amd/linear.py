@@ -107,6 +107,24 @@ def exl3_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tens
     return 0
 
 
+def exl3_gemm_noalloc(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor) -> None:
+    """exl3_gemm for up to 8 rows with no allocation in the library (its scratch is a fixed per-device array); same
+    results as exl3_gemm bit for bit. Calls on one device must not overlap in time."""
+    require_device(A, B, C, suh, svh)
+    K = _K_of(B)
+    k, n = B.shape[0] * 16, B.shape[1] * 16
+    if A.dtype != torch.float16 or A.shape[-1] != k or not A.is_contiguous():
+        raise Exl3Error(f"exl3_gemm_noalloc: A must be contiguous fp16 [..., {k}]")
+    if C.shape[-1] != n or C.dtype not in (torch.float16, torch.float32) or not C.is_contiguous():
+        raise Exl3Error(f"exl3_gemm_noalloc: C must be contiguous fp16/fp32 [..., {n}]")
+    m = A.numel() // k
+    if C.numel() // n != m:
+        raise Exl3Error("exl3_gemm_noalloc: A and C row counts differ")
+    dt = EXL3_F32 if C.dtype == torch.float32 else EXL3_F16
+    check(lib().exl3_gemm_noalloc(ptr(A), k, m, k, ptr(B.contiguous()), n, K, ptr(C), n, dt, ptr(suh.contiguous()),
+                                  ptr(svh.contiguous()), CB_MUL1, stream_of(A)), "exl3_gemm_noalloc")
+
+
 def exl3_mgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor, A_had, svh: torch.Tensor,
                indices, weights, K, force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True,
                min_index: int = -1, max_index: int = -1, force_num_sms: int = 0, num_tokens: int = 1,

@@ -93,6 +93,17 @@ int exl3_gemm(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16
               int64_t c_ld, int c_dtype, const uint16_t* suh, uint16_t* A_had, const uint16_t* svh, int cb,
               void* stream);
 
+/* exl3_gemm for up to 8 rows (the decode GEMV, same kernels and results bit for bit) without the library workspace:
+ * its split-K partials and arrival counters live in a fixed device array (16 MiB + 64 KiB per device, held until the
+ * process ends), so the call never allocates, e.g. under HIP graph capture or in a serving loop that must not
+ * allocate. Limits: m <= 8, n <= 2 097 152 columns, and strips (n / 128) x k-splits x 8 x 128 x 4 bytes of partials
+ * <= 16 MiB (k-splits <= 16; e.g. n = 21504 at any k fits); larger shapes return EXL3_ERR_INVALID. Every call on a
+ * device shares that device's array: calls that overlap in time (two streams, two threads) race. A_had is dropped.
+ * No counterpart in the reference: an entry point for callers that cannot allocate. */
+int exl3_gemm_noalloc(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const int16_t* B, int64_t n, int K,
+                      void* C, int64_t c_ld, int c_dtype, const uint16_t* suh, const uint16_t* svh, int cb,
+                      void* stream);
+
 /* Fused multi-projection linear: S projections that share the input x (e.g. q|k|v or gate|up), their trellises
  * concatenated along the output columns (B = [k/16][n/16][16K] with n = the sum of the projections' widths, as
  * torch.cat(trellises, 1)), per-projection input signs suh fp16 [S][k] (row s for shard s), output signs svh fp16 [n]
