@@ -127,6 +127,90 @@ def reconstruct(trellis: np.ndarray, K: int, n0: int = 0, n_slice: int | None = 
     return tiles.transpose(0, 2, 1, 3).reshape(tk * 16, n_slice)
 
 
+# Fast C statement of the same decode (oracle/trellis_fast.c, built into oracle/_build/libexl3_oracle.so), pinned bit
+# for bit against reconstruct / reconstruct_mixed and the brute-force decoder; Proj uses it for large matrices.
+_FAST = None
+
+
+def _fast_lib():
+    global _FAST
+    if _FAST is None:
+        import ctypes
+        import os
+        import subprocess
+        here = os.path.dirname(os.path.abspath(__file__))
+        path = os.path.join(here, "_build", "libexl3_oracle.so")
+        if not os.path.exists(path):
+            subprocess.run(["make", "-C", here], check=True, capture_output=True)
+        L = ctypes.CDLL(path)
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.exl3_fast_reconstruct.argtypes = [vp, i64, i64, i32, i64, i64, vp, i32]
+        L.exl3_fast_reconstruct_mixed.argtypes = [vp, vp, vp, i64, i64, vp, i32]
+        L.exl3_fast_matmul.argtypes = [vp, i64, i64, i32, vp, i64, vp, i32]
+        L.exl3_fast_matmul_mixed.argtypes = [vp, vp, vp, i64, i64, vp, i64, vp, i32]
+        _FAST = L
+    return _FAST
+
+
+def _threads() -> int:
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def reconstruct_fast(trellis: np.ndarray, K: int, n0: int = 0, n_slice: int | None = None) -> np.ndarray:
+    """reconstruct() through the C decoder, multithreaded."""
+    tr = np.ascontiguousarray(trellis, dtype=np.int16)
+    tk, tn, w = tr.shape
+    assert w == 16 * K
+    if n_slice is None:
+        n_slice = tn * 16 - n0
+    assert n0 % 16 == 0 and n_slice % 16 == 0 and n0 + n_slice <= tn * 16
+    out = np.empty((tk * 16, n_slice), dtype=np.uint16)
+    rc = _fast_lib().exl3_fast_reconstruct(tr.ctypes.data, tk, tn, K, n0 // 16, n_slice // 16, out.ctypes.data,
+                                           _threads())
+    assert rc == 0
+    return out.view(np.float16)
+
+
+def reconstruct_mixed_fast(words: np.ndarray, kmap: np.ndarray, woff: np.ndarray, k: int, n: int) -> np.ndarray:
+    """reconstruct_mixed() through the C decoder, multithreaded."""
+    w = np.ascontiguousarray(words).view(np.uint32)
+    km = np.ascontiguousarray(kmap, dtype=np.uint8).reshape(-1)
+    wo = np.ascontiguousarray(woff, dtype=np.int64).reshape(-1)
+    tk, tn = k // 16, n // 16
+    assert km.size == tk * tn and wo.size == tk * tn + 1 and int(wo[-1]) <= w.size
+    out = np.empty((k, n), dtype=np.uint16)
+    rc = _fast_lib().exl3_fast_reconstruct_mixed(w.ctypes.data, km.ctypes.data, wo.ctypes.data, tk, tn,
+                                                 out.ctypes.data, _threads())
+    assert rc == 0
+    return out.view(np.float16)
+
+
+def matmul_fast(xh: np.ndarray, trellis=None, K=None, words=None, kmap=None, woff=None) -> np.ndarray:
+    """xh @ W_hat in float64 (= linear_acc(xh, reconstruct(...))) through the C decoder, without materialising W_hat:
+    uniform K (`trellis`, `K`) or per-tile K (`words`, `kmap`, `woff`). xh [m, k] -> float64 [m, n]."""
+    x = np.ascontiguousarray(xh, dtype=np.float64)
+    m = x.shape[0]
+    if trellis is not None:
+        tr = np.ascontiguousarray(trellis, dtype=np.int16)
+        tk, tn, w = tr.shape
+        assert w == 16 * K and x.shape[1] == tk * 16
+        y = np.empty((m, tn * 16), dtype=np.float64)
+        assert _fast_lib().exl3_fast_matmul(tr.ctypes.data, tk, tn, K, x.ctypes.data, m, y.ctypes.data,
+                                            _threads()) == 0
+        return y
+    wd = np.ascontiguousarray(words).view(np.uint32)
+    km = np.ascontiguousarray(kmap, dtype=np.uint8).reshape(-1)
+    wo = np.ascontiguousarray(woff, dtype=np.int64).reshape(-1)
+    tk = x.shape[1] // 16
+    tn = km.size // tk
+    assert km.size == tk * tn and wo.size == tk * tn + 1 and int(wo[-1]) <= wd.size
+    y = np.empty((m, tn * 16), dtype=np.float64)
+    assert _fast_lib().exl3_fast_matmul_mixed(wd.ctypes.data, km.ctypes.data, wo.ctypes.data, tk, tn, x.ctypes.data,
+                                              m, y.ctypes.data, _threads()) == 0
+    return y
+
+
 def reconstruct_mixed(words: np.ndarray, kmap: np.ndarray, woff: np.ndarray, k: int, n: int) -> np.ndarray:
     """Per-tile K: tile i (row-major over [k/16, n/16]) is stored at words[woff[i] : woff[i] + 8 kmap[i]]."""
     tk, tn = k // 16, n // 16
@@ -315,11 +399,15 @@ class Proj:
         self._W = None
 
     def W(self) -> np.ndarray:
+        """W_hat fp16 [k, n]: the NumPy statement for small matrices, the (pinned, identical) C decoder from 2^20
+        weights on."""
         if self._W is None:
+            fast = self.k * self.n >= (1 << 20)
             if self.trellis is not None:
-                self._W = reconstruct(self.trellis, self.K)
+                self._W = (reconstruct_fast if fast else reconstruct)(self.trellis, self.K)
             else:
-                self._W = reconstruct_mixed(self.words, self.kmap, self.woff, self.k, self.n)
+                self._W = (reconstruct_mixed_fast if fast else reconstruct_mixed)(self.words, self.kmap, self.woff,
+                                                                                  self.k, self.n)
         return self._W
 
     def drop(self):
@@ -327,6 +415,13 @@ class Proj:
 
     def __call__(self, x, out_dtype, acc=np.float64):
         xh = had_in(x.reshape(-1, self.k), self.suh)
+        if acc == np.float64 and self._W is None and self.k * self.n >= (1 << 20):
+            # large matrices in float64: decode and multiply in C (same sums, W_hat never materialised)
+            if self.trellis is not None:
+                y = matmul_fast(xh, trellis=self.trellis, K=self.K)
+            else:
+                y = matmul_fast(xh, words=self.words, kmap=self.kmap, woff=self.woff)
+            return had_out(y, self.svh, out_dtype)
         return had_out(linear_acc(xh, self.W(), acc), self.svh, out_dtype)
 
 

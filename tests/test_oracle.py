@@ -118,6 +118,48 @@ def test_decode_vs_bruteforce(bf, K):
     assert np.array_equal(O.reconstruct(tr, K).view(np.uint16), bf_reconstruct(bf, tr))
 
 
+@pytest.mark.parametrize("K", range(1, 9))
+def test_fast_decoder_matches_numpy_and_bruteforce(bf, K):
+    """The C decoder used for full-size parity cases (oracle/trellis_fast.c) is bit-identical to the NumPy statement
+    and the bit-by-bit decoder, whole matrices and column slices."""
+    rng = np.random.default_rng(200 + K)
+    tr = rng.integers(-32768, 32768, size=(5, 24, 16 * K), dtype=np.int16)
+    ref = O.reconstruct(tr, K)
+    assert np.array_equal(O.reconstruct_fast(tr, K).view(np.uint16), ref.view(np.uint16))
+    assert np.array_equal(ref.view(np.uint16), bf_reconstruct(bf, tr))
+    assert np.array_equal(O.reconstruct_fast(tr, K, 128, 128).view(np.uint16), ref[:, 128:256].view(np.uint16))
+
+
+def test_fast_mixed_decoder_matches_numpy():
+    rng = np.random.default_rng(5)
+    k, n = 96, 160
+    tk, tn = k // 16, n // 16
+    kmap = rng.integers(1, 9, tk * tn).astype(np.uint8)
+    woff = np.concatenate([[0], np.cumsum(kmap.astype(np.int64) * 8)])
+    words = rng.integers(0, 2 ** 32, int(woff[-1]), dtype=np.uint64).astype(np.uint32)
+    a = O.reconstruct_mixed(words, kmap, woff, k, n)
+    b = O.reconstruct_mixed_fast(words, kmap, woff, k, n)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 8])
+def test_fast_matmul_matches_dense_product(K):
+    """x @ W_hat through the C decoder (used by Proj for large matrices) equals the float64 product with the NumPy
+    reconstruction, uniform and per-tile K, for 1 and 19 rows (the C loop takes rows 16 at a time)."""
+    rng = np.random.default_rng(300 + K)
+    k, n = 128, 96
+    tr = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16)
+    kmap = rng.integers(1, 9, (k // 16) * (n // 16)).astype(np.uint8)
+    woff = np.concatenate([[0], np.cumsum(kmap.astype(np.int64) * 8)])
+    words = rng.integers(0, 2 ** 32, int(woff[-1]), dtype=np.uint64).astype(np.uint32)
+    for m in (1, 19):
+        x = rng.normal(0, 1, (m, k))
+        ref = x @ O.reconstruct(tr, K).astype(np.float64)
+        np.testing.assert_allclose(O.matmul_fast(x, trellis=tr, K=K), ref, rtol=1e-12, atol=1e-12)
+        refm = x @ O.reconstruct_mixed(words, kmap, woff, k, n).astype(np.float64)
+        np.testing.assert_allclose(O.matmul_fast(x, words=words, kmap=kmap, woff=woff), refm, rtol=1e-12, atol=1e-12)
+
+
 def test_window_special_cases(bf):
     # K = 8: windows are byte aligned; K = 1: 15 of 16 bits of early windows come from the ring's end
     for K in (1, 8, 16 // 2, 3):
