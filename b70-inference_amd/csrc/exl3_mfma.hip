@@ -544,37 +544,50 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mfm
 
 // ------------------------------------------------------------------------------------------------ per-tile K
 // Per-tile bitrate (K = 0: tile i of a projection holds 8 kmap[i] words at woff[i]). MFMA 16x16x16 per tile-row, so
-// the 64 lanes of a wave always share one tile and branch uniformly on its K. Fragment layout: B[k][n] lane L holds
-// n = L & 15, k = 4 (L >> 4) + j, j < 4, i.e. tile rows 4g .. 4g + 3 (g = L >> 4) of column n = chunk positions
-// u0 + {0, 1, 8, 9}, u0 = 4 (n >> 3) + 2 (g >> 1) + 16 (g & 1); A[m][k] lane L holds m = L & 15, same k.
+// the 64 lanes of a wave always share one tile and its K is wave-uniform. Fragment layout: B[k][n] lane L holds
+// n = L & 15, k = 4 (L >> 4) + j, j < 4; A[m][k] lane L holds m = L & 15, same k; D[m][n] n = L & 15,
+// m = 4 (L >> 4) + i (the tile rows behind the k slots are permuted, see decode4p).
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 constexpr int kMixKMax = 8;
 constexpr int kMixTS = 8 * kMixKMax + 4;                    // LDS words per staged tile (w(-1), 8K words, w(0), pad)
 
-// Lane's four h values of a staged tile of bitrate K (1 .. 8, any lane value): slot[1 + w] = ring word w for
-// w = -1 .. 8K. Positions u0, u0 + 1 and u0 + 8, u0 + 9 of chunk q, u0 = 4 h + 2 (g >> 1) + 16 (g & 1), form two window
-// pairs. A pair whose first window starts at ring bit `start` reads words floor((start - 1) / 32) and the next one,
-// funnel-shifted by 32 - (start - 32 floor((start - 1) / 32)); its windows then sit at bits 0 and K from the top. With
-// t = start + 31 (> 0): the slot index is t >> 5 and the shift 31 - (t & 31), the low bits of ~t. cA = 32 q + u0 + 1.
-__device__ __forceinline__ h4_t decode4_rt(const uint32_t* slot, int K, uint32_t cA) {
-    const uint32_t tA = cA * (uint32_t)K + 15u;                // start = (32 q + u0 + 1) K - 16
-    const uint32_t tB = tA + 8u * (uint32_t)K;                 // positions u0 + 8, u0 + 9
-    const uint32_t s1 = 16u - (uint32_t)K;
-    const uint32_t* pa = slot + (tA >> 5);
-    const uint32_t* pb = slot + (tB >> 5);
-    const uint32_t na = __builtin_amdgcn_alignbit(pa[0], pa[1], ~tA);
-    const uint32_t nb = __builtin_amdgcn_alignbit(pb[0], pb[1], ~tB);
-    const uint32_t p0 = __builtin_bit_cast(uint32_t, mul1_pair_raw(na >> 16, na >> s1));
-    const uint32_t p1 = __builtin_bit_cast(uint32_t, mul1_pair_raw(nb >> 16, nb >> s1));
+// k-permuted fragments. An MFMA sums over k, so B and A may list a tile-row's 16 k in any common order. In the order
+// used here lane L's four k slots are tile rows 2g, 2g + 1, 2g + 8, 2g + 9 (g = L >> 4) of column n = L & 15: the
+// positions t0 .. t0 + 3, t0 = 32 (n & 7) + 4 (n >> 3) + 8 g, four consecutive windows (row 8 ((t >> 1) & 1) +
+// 2 ((t >> 3) & 3) + (t & 1), column (t >> 5) + 8 ((t >> 2) & 1)). Their bits [(t0 + 1) K - 16, (t0 + 4) K) fit one
+// funnel-shifted word for K <= 5: window b sits at bit 16 - b K of it.
+// Staged slot: slot[0] = ring word 8K - 1, slot[1 + w] = ring word w. A funnel whose first bit is ring bit `start`
+// (>= -16) reads slot words (start + 31) >> 5 and the next one, shifted by 31 - ((start + 31) & 31).
+__device__ __forceinline__ h4_t decode4p(uint32_t F, int K) {
+    const uint32_t w0 = F >> 16;
+    const uint32_t w1 = __builtin_amdgcn_ubfe(F, 16 - K, 16);
+    const uint32_t w2 = __builtin_amdgcn_ubfe(F, 16 - 2 * K, 16);
+    const uint32_t w3 = __builtin_amdgcn_ubfe(F, 16 - 3 * K, 16);
     typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-    const u2_t v = {p0, p1};
+    const u2_t v = {__builtin_bit_cast(uint32_t, mul1_pair_raw(w0, w1)),
+                    __builtin_bit_cast(uint32_t, mul1_pair_raw(w2, w3))};
+    return __builtin_bit_cast(h4_t, v);
+}
+
+// Any K (1 .. 8): the funnel origin from the lane's t0 + 1 at run time, and a second funnel for windows 2 and 3.
+__device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_t t0p1) {
+    const uint32_t ta = t0p1 * (uint32_t)K + 15u, tb = ta + 2u * (uint32_t)K;     // start + 31 of windows 0 and 2
+    const uint32_t* pa = slot + (ta >> 5);
+    const uint32_t* pb = slot + (tb >> 5);
+    const uint32_t Fa = __builtin_amdgcn_alignbit(pa[0], pa[1], ~ta);
+    const uint32_t Fb = __builtin_amdgcn_alignbit(pb[0], pb[1], ~tb);
+    typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+    const u2_t v = {__builtin_bit_cast(uint32_t, mul1_pair_raw(Fa >> 16, __builtin_amdgcn_ubfe(Fa, 16 - K, 16))),
+                    __builtin_bit_cast(uint32_t, mul1_pair_raw(Fb >> 16, __builtin_amdgcn_ubfe(Fb, 16 - K, 16)))};
     return __builtin_bit_cast(h4_t, v);
 }
 
 // One wave, kMfT tile columns (column pair t >> 1: gate|up projection, or down columns c0 + 2 (t >> 1)), RGA row
 // groups, 32 k per step = two tile-rows. Per step the wave's 8 tiles (slot 2t + tile-row half) are fetched by 8 lanes
 // each with two clamped 16-byte loads (any K <= 8, every address inside the tile), after their (kmap, woff) one step
-// earlier; staged in LDS like MfmaPipe with the tile's K beside it, then decoded per tile-row with that K. Rings of 4
+// earlier; staged in LDS like MfmaPipe, then decoded per tile-row with that tile's K (read from the loading lanes
+// with readlane: wave-uniform) into k-permuted fragments (decode4p): branch-free, the lane's funnel origins for K = 1
+// and K = 2 precomputed and selected per tile; a step holding a tile of K > 2 takes the run-time form. Rings of 4
 // (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4 steps ahead) make the loop a 4-step unroll;
 // the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A as in MfmaPipe.
 template <int NP, int RGA>
@@ -589,8 +602,10 @@ struct MfmaPipeMix {
     int col[2];                                              // per column pair: its first tile column
     int tn, nsteps;
     uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
-    int* kt;                                                 // the wave's staged K per slot [8]
-    uint32_t cA;                                             // 32 q + u0 + 1 of the lane's fragment positions
+    uint32_t t0p1;                                           // t0 + 1 of the lane's k-permuted positions
+    const uint32_t* org1;                                    // the lane's funnel word in slot 0 at K = 1, K = 2
+    const uint32_t* org2;
+    uint32_t sh1, sh2;                                       // and the funnel shifts
     const _Float16* asrc[CPT];
     int adst[CPT];
     u32x4_t* lds;
@@ -626,30 +641,63 @@ struct MfmaPipeMix {
             t[1 + a1 + j] = D[1][j];
         }
         if (a1 + 4 == 8 * K) t[0] = D[1][3];                 // w(8K - 1) in front (a1 = 8K - 4 for K <= 4)
-        if (i == 0) {
-            t[8 * K + 1] = D[0][0];                          // w(0) behind
-            kt[sl] = K;
-        }
+        if (i == 0) t[8 * K + 1] = D[0][0];                  // w(0) behind
     }
-    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA]) const {
+    // A fragments of tile-row half sr in the k-permuted order: k 2g, 2g + 1 from chunk 2 sr, 2g + 8, 2g + 9 from
+    // chunk 2 sr + 1 (4 bytes at 4g in each unit)
+    __device__ __forceinline__ void load_af(int stage, int sr, h4_t (&af)[NP][RGA]) const {
+        const int g = lane >> 4;
 #pragma unroll
-        for (int sr = 0; sr < 2; ++sr) {
-            h4_t af[NP][RGA];
-            const int ch = 2 * sr + ((lane >> 4) >> 1), hf = (lane >> 4) & 1;
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
-            for (int p = 0; p < NP; ++p)
+            for (int rg = 0; rg < RGA; ++rg) {
+                const u32x4_t* base = lds + stage * UNITS + p * RGA * 64;
+                const int row = 16 * rg + (lane & 15);
+                typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+                const u2_t v = {reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr))[g],
+                                reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr + 1))[g]};
+                af[p][rg] = __builtin_bit_cast(h4_t, v);
+            }
+    }
+    // Kk: the lane's loaded (K, woff) of this step; the K of slot sl is that of lane 8 sl
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], int Kk) const {
+        int ks[8];
+        int kmax = 0;
 #pragma unroll
-                for (int rg = 0; rg < RGA; ++rg) {
-                    const u32x4_t* u = lds + stage * UNITS + p * RGA * 64 + a_unit(16 * rg + (lane & 15), ch);
-                    af[p][rg] = *(reinterpret_cast<const h4_t*>(u) + hf);
+        for (int sl = 0; sl < 8; ++sl) {
+            ks[sl] = __builtin_amdgcn_readlane(Kk, 8 * sl);
+            kmax = ks[sl] > kmax ? ks[sl] : kmax;
+        }
+        if (kmax <= 2) {
+#pragma unroll
+            for (int sr = 0; sr < 2; ++sr) {
+                h4_t af[NP][RGA];
+                load_af(stage, sr, af);
+#pragma unroll
+                for (int t = 0; t < kMfT; ++t) {
+                    const int sl = 2 * t + sr;
+                    const bool k1 = ks[sl] == 1;
+                    const uint32_t* o = k1 ? org1 : org2;
+                    const uint32_t F = __builtin_amdgcn_alignbit(o[sl * kMixTS], o[sl * kMixTS + 1], k1 ? sh1 : sh2);
+                    const h4_t bf = decode4p(F, ks[sl]);
+#pragma unroll
+                    for (int rg = 0; rg < RGA; ++rg)
+                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
                 }
+            }
+        } else {
 #pragma unroll
-            for (int t = 0; t < kMfT; ++t) {
-                const int sl = 2 * t + sr;
-                const h4_t bf = decode4_rt(wl + sl * kMixTS, kt[sl], cA);
+            for (int sr = 0; sr < 2; ++sr) {
+                h4_t af[NP][RGA];
+                load_af(stage, sr, af);
 #pragma unroll
-                for (int rg = 0; rg < RGA; ++rg)
-                    acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
+                for (int t = 0; t < kMfT; ++t) {
+                    const int sl = 2 * t + sr;
+                    const h4_t bf = decode4p_rt(wl + sl * kMixTS, ks[sl], t0p1);
+#pragma unroll
+                    for (int rg = 0; rg < RGA; ++rg)
+                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
+                }
             }
         }
     }
@@ -671,7 +719,7 @@ struct MfmaPipeMix {
         load_meta(M[(R + DW) % 4], s + DW);
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
         stage_w(W[R], M[R]);
-        compute(R % 2, acc);
+        compute(R % 2, acc, M[R][0]);
         store_a(RA[(R + 1) % 4], (R + 1) % 2);
         __syncthreads();
     }
@@ -704,14 +752,19 @@ struct MfmaPipeMix {
             asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
             adst[j] = p * RGA * 64 + a_unit(row, ch);
         }
-        const int q = lane & 7, h = (lane >> 3) & 1, g = lane >> 4;
-        cA = (uint32_t)(32 * q + 4 * h + 2 * (g >> 1) + 16 * (g & 1) + 1);
+        const int n = lane & 15, g = lane >> 4;
+        t0p1 = (uint32_t)(32 * (n & 7) + 4 * (n >> 3) + 8 * g + 1);
+        const uint32_t ta1 = t0p1 + 15u, ta2 = 2u * t0p1 + 15u;           // start + 31 at K = 1, 2
+        org1 = wl + (ta1 >> 5);
+        org2 = wl + (ta2 >> 5);
+        sh1 = ~ta1;
+        sh2 = ~ta2;
     }
 };
 
 template <int RGA>
 __device__ __forceinline__ void gateup_mix_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
-                                                uint32_t* wlds, int* kts, float* C, float* rsum) {
+                                                uint32_t* wlds, float* C, float* rsum) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
     MfmaPipeMix<2, RGA> L;
@@ -720,7 +773,6 @@ __device__ __forceinline__ void gateup_mix_body(const MoeArgs& a, const ItemDesc
     L.lds = stage;
     L.lane = lane;
     L.wl = wlds + wave * 8 * kMixTS;
-    L.kt = kts + wave * 8;
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
         L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[3 * pr]);
@@ -740,7 +792,7 @@ __device__ __forceinline__ void gateup_mix_body(const MoeArgs& a, const ItemDesc
 
 template <int RGA>
 __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
-                                              uint32_t* wlds, int* kts, float* C, float* rsum, int* s_comb) {
+                                              uint32_t* wlds, float* C, float* rsum, int* s_comb) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
     const int tn = a.H / 16;
@@ -750,7 +802,6 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
     L.lds = stage;
     L.lane = lane;
     L.wl = wlds + wave * 8 * kMixTS;
-    L.kt = kts + wave * 8;
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
         L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[6]);
@@ -774,7 +825,6 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_m
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * 2 * RGA * 64];
     __shared__ uint32_t wlds[4 * 8 * kMixTS];
-    __shared__ int kts[4 * 8];
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
     const int nbI = a.I / 128;
@@ -789,7 +839,7 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_m
         rsum[i] = m < cnt ? sum_ordered(a.xsum + ((size_t)(d->p0 + m) * 2 + p) * nblk, nblk) : 0.f;
     }
     __syncthreads();
-    gateup_mix_body<RGA>(a, d, nb, cnt, stage, wlds, kts, C, rsum);
+    gateup_mix_body<RGA>(a, d, nb, cnt, stage, wlds, C, rsum);
 }
 
 template <int RGA>
@@ -797,7 +847,6 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * RGA * 64];
     __shared__ uint32_t wlds[4 * 8 * kMixTS];
-    __shared__ int kts[4 * 8];
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
     __shared__ int s_comb[2 * 64];
@@ -811,7 +860,7 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix
     for (int m = threadIdx.x; m < 64; m += 256)
         rsum[m] = m < cnt ? sum_ordered(a.asum + (size_t)(d->p0 + m) * nbI, nbI) : 0.f;
     __syncthreads();
-    down_mix_body<RGA>(a, d, nb, cnt, stage, wlds, kts, C, rsum, s_comb);
+    down_mix_body<RGA>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
 }
 
 // ------------------------------------------------------------------------------------------------ dense linear

@@ -1,19 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the EXL3 quantized-linear + MoE-expert hot path on one MI355X.
 
-One step = one layer call of the headline workload (C3 below) on 4 decode tokens: softmax/top-10 routing from fp32
-logits and the grouped MoE layer (gate|up + activation, down, combine) in one library call (moe_forward_logits). Timed as HIP-graph replay of exactly
---steps steps (warmup steps run eagerly first); every step uses a fresh routing and cycles through layer copies so the
-expert weights come from HBM, not the 256 MB Infinity Cache. Prints one JSON line.
+Headline: the largest layer, C5 below. One step = one layer call: 4 decode rows and a 256-row prefill chunk routed
+top-8 over 256 experts (+ 1 shared expert), per-tile 1/2-bit weights (1.62 bpw), in one library call
+(moe_forward). Timed as a HIP-graph replay of exactly --steps steps (--warmup steps run eagerly first); steps cycle
+through fresh routings. value = microseconds per token (lower is better). Prints one JSON line.
 
-Workloads (seeded synthetic EXL3 tensors generated on the device; parity is tested separately against the oracle):
-  C1  dense linear 4096 -> 4096, K=4, 1 token
+Workloads (seeded synthetic EXL3 tensors generated on the device; parity is tested against the oracle separately):
+  C1  dense linear 4096 -> 4096, K=4, 1 token (128 weight copies cycled: beyond the 256 MB Infinity Cache)
   C2  dense MLP 5376 <-> 21504, K=4, GELU-tanh gate, 1 / 2 / 4 tokens
-  C3  MoE decode layer H=2048, 512 experts of I=512, K=3, top-10 softmax, SiLU, 1 / 2 / 4 tokens   (headline)
+  C3  MoE decode layer H=2048, 512 experts of I=512, K=3, top-10 softmax, SiLU, 1 / 2 / 4 tokens
   C4  MoE prefill layer H=5120, 160 experts of I=1536, gate/up K=2 + down K=3, top-8 softmax over logits + Zipf(1.1)
       expert bias, 512 tokens
   C5  MoE layer H=7168, 256 experts of I=2048 + 1 shared, per-tile K in {1, 2} (38/62), top-8, 4 decode + 256
-      prefill rows in one call
+      prefill rows in one call                                                                       (headline)
+
+Every config reports: time per layer and per token; algorithmic bytes and FLOP per layer and the HBM / fp16-MFMA
+fractions they imply; the library's kernels per step with their event-timed durations; a roofline block for its
+dominant kernel (the kernel with the most time per step: its algorithmic bytes or FLOP per launch over its average
+launch duration, HIP events on the launch stream); and the CPU baseline (the oracle on this host, bounded sample).
 """
 from __future__ import annotations
 
@@ -22,6 +27,8 @@ import importlib
 import json
 import math
 import os
+import statistics
+import subprocess
 import sys
 import time
 
@@ -33,6 +40,8 @@ sys.path.insert(0, ROOT)
 METRIC = "EXL3 MoE layer µs/token + achieved HBM GB/s (% of peak), 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+VALU_PEAK_LANE_OPS = 256 * 64 * 2.4e9           # 256 CUs x 4 SIMDs x 16 lanes per clock x 2.4 GHz
+MFMA_ROWS = 64                                  # the library's MFMA row block (kMfmaRows) and its row classes
 
 exl3 = importlib.import_module("b70-inference_amd")
 
@@ -46,12 +55,14 @@ def dev_gen(seed):
     return torch.Generator(device="cuda").manual_seed(int(seed))
 
 
+def _signs(n, g, scale=1.0):
+    return ((torch.randint(0, 2, (n,), device="cuda", generator=g).float() * 2 - 1) * scale).half()
+
+
 def dev_linear(k, n, K, g):
     tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, device="cuda", generator=g)
-    suh = (torch.randint(0, 2, (k,), device="cuda", generator=g).float() * 2 - 1).half()
-    svh = ((torch.randint(0, 2, (n,), device="cuda", generator=g).float() * 2 - 1) *
-           float(torch.tensor(1.0 / math.sqrt(k)).half())).half()
-    return exl3.BC_LinearEXL3(tr, suh, svh, K, None, False, True, None)
+    return exl3.BC_LinearEXL3(tr, _signs(k, g), _signs(n, g, float(torch.tensor(1.0 / math.sqrt(k)).half())), K, None,
+                              False, True, None)
 
 
 def dev_mixed(k, n, g, Ks=(1, 2), probs=(0.38, 0.62)):
@@ -64,12 +75,10 @@ def dev_mixed(k, n, g, Ks=(1, 2), probs=(0.38, 0.62)):
         acc += p
     woff = torch.zeros(tk * tn + 1, dtype=torch.int64, device="cuda")
     woff[1:] = torch.cumsum(kmap.to(torch.int64) * 8, 0)
-    total = int(woff[-1])
-    words = torch.randint(-(2 ** 31), 2 ** 31, (total,), dtype=torch.int64, device="cuda", generator=g).to(torch.int32)
-    suh = (torch.randint(0, 2, (k,), device="cuda", generator=g).float() * 2 - 1).half()
-    svh = ((torch.randint(0, 2, (n,), device="cuda", generator=g).float() * 2 - 1) *
-           float(torch.tensor(1.0 / math.sqrt(k)).half())).half()
-    return exl3.MixedEXL3(words, kmap, woff.to(torch.int32), suh, svh)
+    words = torch.randint(-(2 ** 31), 2 ** 31, (int(woff[-1]),), dtype=torch.int64, device="cuda",
+                          generator=g).to(torch.int32)
+    return exl3.MixedEXL3(words, kmap, woff.to(torch.int32), _signs(k, g),
+                          _signs(n, g, float(torch.tensor(1.0 / math.sqrt(k)).half())))
 
 
 def dev_packed(E, k, n, K, g):
@@ -95,40 +104,40 @@ def dev_experts(E, H, I, Kgu, Kd, seed, mixed=False):
     return exl3.ExpertTables(gates, ups, downs)
 
 
-def proj_bytes(p):
-    b = p.trellis.numel() * p.trellis.element_size() + 2 * (p.in_features + p.out_features)
+def weight_bytes(p):
+    """Algorithmic bytes of one projection: its trellis words (per-tile K: 32 K bytes per tile, no maps) and its two
+    fp16 sign vectors."""
     if isinstance(p, exl3.MixedEXL3):
-        b += p.kmap.numel() + 4 * p.woff.numel()
-    return b
+        tw = int(p.woff[-1]) * 4
+    else:
+        tw = p.trellis.numel() * p.trellis.element_size()
+    return tw + 2 * (p.in_features + p.out_features)
 
 
 # ------------------------------------------------------------------------------------------------ timing
-def graph_time(fns, reps=1, wall=False):
-    """Capture fns (in order) into one HIP graph, replay `reps` times; returns (us per fn call, wall seconds)."""
+def graph_time(fns):
+    """Capture fns (in order) into one HIP graph and replay it once (after an untimed replay): us per fn call."""
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for f in fns:
             f()
     torch.cuda.synchronize()
-    g.replay()                      # untimed replay: first-touch costs out of the timed region
+    g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
     e0.record()
-    for _ in range(reps):
-        g.replay()
+    g.replay()
     e1.record()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    return e0.elapsed_time(e1) * 1e3 / (reps * len(fns)), t1 - t0
+    return e0.elapsed_time(e1) * 1e3 / len(fns)
 
 
-def kernel_profile(fns, repeat=1):
-    """Eager run of fns with the library's event profiler (a HIP event pair around each launch on its own stream):
-    {kernel: (launches, avg us)}. repeat > 1 re-runs each launch between its events (weights then partly cached)."""
+def kernel_profile(fns):
+    """Eager run of fns with the library's event profiler (a HIP event pair recorded with each dispatch on its own
+    stream): {kernel: (launches, avg us)}."""
     torch.cuda.synchronize()
-    exl3._lib.profile_enable(True, repeat=repeat)
+    exl3._lib.profile_enable(True)
     for f in fns:
         f()
     torch.cuda.synchronize()
@@ -137,108 +146,266 @@ def kernel_profile(fns, repeat=1):
     return prof
 
 
-# ------------------------------------------------------------------------------------------------ workloads
-class MoEWorkload:
-    """Routed MoE layer over `copies` layer copies, with `nrout` precomputed routings (fp32 logits on the device)."""
+def cpu_info():
+    cores = len(os.sched_getaffinity(0))
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return cores, model
 
-    def __init__(self, name, layers, M, topk, nrout, seed, act, shared=False, bias=None):
-        self.name, self.layers, self.M, self.topk = name, layers, M, topk
+
+def cpu_time(fn, runs=3):
+    """One warm-up call, then the median of `runs` timed calls (seconds)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+# ------------------------------------------------------------------------------------------------ workloads
+class Dense:
+    """C1: one EXL3 linear k -> n over `copies` weight copies."""
+
+    def __init__(self, k, n, K, M, copies, seed):
+        g = dev_gen(seed)
+        self.k, self.n, self.K, self.M = k, n, K, M
+        self.lins = [dev_linear(k, n, K, g) for _ in range(copies)]
+        self.x = torch.randn(M, k, device="cuda", generator=g).half()
+        self.y = torch.empty(M, n, dtype=torch.float16, device="cuda")
+
+    def step_fn(self, j):
+        lin = self.lins[j % len(self.lins)]
+        return lambda: exl3.exl3_gemm(self.x, lin.trellis, self.y, lin.suh, None, lin.svh)
+
+    def bytes_per_step(self, j):
+        return self.k * self.n * self.K / 8 + 2 * self.k + 2 * self.n + 2 * self.M * self.k + 2 * self.M * self.n
+
+    def flops_per_step(self, j):
+        return 2.0 * self.M * self.k * self.n
+
+    def weights_per_step(self, j):
+        return self.k * self.n
+
+    def kernel_work(self, name, j):
+        return (self.bytes_per_step(j), self.flops_per_step(j)) if name == "gemv" else None
+
+    def cpu(self, O, np):
+        lin = self.lins[0]
+        tr, su, sv = lin.trellis.cpu().numpy(), lin.suh.cpu().numpy(), lin.svh.cpu().numpy()
+        x = self.x.cpu().numpy()
+        return cpu_time(lambda: O.Proj(su, sv, trellis=tr, K=self.K)(x, np.float16)), self.M, "one layer call"
+
+
+class Mlp:
+    """C2: dense gated MLP H <-> I (the fused decode layer with one always-on expert)."""
+
+    def __init__(self, H, I, K, M, copies, seed):
+        g = dev_gen(seed)
+        self.H, self.I, self.K, self.M = H, I, K, M
+        self.mlps = []
+        for _ in range(copies):
+            gt, up, dn = dev_linear(H, I, K, g), dev_linear(H, I, K, g), dev_linear(I, H, K, g)
+            self.mlps.append(exl3.BC_GatedMLP(None, None, None, None, None, None, None, K, False, True, False, True,
+                                              False, gt, up, dn, 0.0))
+        self.x = torch.randn(M, H, device="cuda", generator=g).half()
+        self.d = torch.empty(M, H, dtype=torch.float32, device="cuda")
+
+    def step_fn(self, j):
+        m = self.mlps[j % len(self.mlps)]
+        return lambda: m.run_bszN(self.x, self.d)
+
+    def bytes_per_step(self, j):
+        return 3 * self.H * self.I * self.K / 8 + 2 * 3 * (self.H + self.I) + 2 * self.M * self.H + 4 * self.M * self.H
+
+    def flops_per_step(self, j):
+        return 6.0 * self.M * self.H * self.I
+
+    def weights_per_step(self, j):
+        return 3 * self.H * self.I
+
+    def kernel_work(self, name, j):
+        return (self.bytes_per_step(j), self.flops_per_step(j)) if name == "moe_fused" else None
+
+    def cpu(self, O, np):
+        m = self.mlps[0]
+        ps = [O.Proj(p.suh.cpu().numpy(), p.svh.cpu().numpy(), trellis=p.trellis.cpu().numpy(), K=self.K)
+              for p in (m.tables.projs[0][0], m.tables.projs[1][0], m.tables.projs[2][0])]
+        x = self.x.cpu().numpy()
+        return cpu_time(lambda: O.gated_mlp(x, *ps, O.ACT_GELU_TANH)), self.M, "one layer call"
+
+
+def mfma_blocks(rows):
+    """Row blocks of one expert with `rows` rows in the MFMA path: up to MFMA_ROWS rows each -> class index
+    (0: <= 16 rows, 1: <= 32, 2: <= 64) per block."""
+    out = []
+    for q in range(0, rows, MFMA_ROWS):
+        c = min(MFMA_ROWS, rows - q)
+        out.append((0 if c <= 16 else 1 if c <= 32 else 2, c))
+    return out
+
+
+class MoE:
+    """C3 / C4 / C5: a routed MoE layer over `copies` layer copies and `nrout` precomputed routings."""
+
+    def __init__(self, layers, M, topk, nrout, seed, act, shared=False, bias=None, logits_api=False):
+        self.layers, self.M, self.topk = layers, M, topk
         t = layers[0]
-        self.H, self.I, self.E = t.H, t.I, t.E - (1 if shared else 0)
+        self.H, self.I = t.H, t.I
+        self.E = t.E - (1 if shared else 0)
         self.shared = self.E if shared else -1
-        self.act = act
-        self.bias = bias
+        self.act, self.bias, self.logits_api = act, bias, logits_api
         g = dev_gen(seed)
         self.x = [torch.randn(M, self.H, device="cuda", generator=g).half() for _ in range(nrout)]
         self.logits = [torch.randn(M, self.E, device="cuda", generator=g) for _ in range(nrout)]
-        self.i = 0
-        # host copy of every routing (for byte / flop accounting)
-        self.ids = []
-        for lg in self.logits:
-            ids, _ = exl3.route_softmax_topk(lg, topk, bias)
-            self.ids.append(ids.cpu())
-        self.exp_bytes = [proj_bytes(t.projs[0][e]) + proj_bytes(t.projs[1][e]) + proj_bytes(t.projs[2][e])
-                          for e in range(t.E)]
-        self.gu_bytes = proj_bytes(t.projs[0][0]) + proj_bytes(t.projs[1][0]) + 2 * self.I
+        self.routing = [exl3.route_softmax_topk(lg, topk, bias) for lg in self.logits]
+        self.ids = [ids.cpu() for ids, _ in self.routing]
+        self.exp_bytes = [[weight_bytes(t.projs[q][e]) for q in range(3)] for e in range(t.E)]
+        self.out = torch.empty(M, self.H, dtype=torch.float32, device="cuda")
 
     def step_fn(self, j):
         lay = self.layers[j % len(self.layers)]
         r = j % len(self.logits)
         x, lg = self.x[r], self.logits[r]
+        if self.logits_api:
+            return lambda: exl3.moe_forward_logits(x, lg, self.topk, lay, self.act, 0.0, self.shared, bias=self.bias,
+                                                   out=self.out)
+        ids, w = self.routing[r]
+        return lambda: exl3.moe_forward(x, ids, w, lay, self.act, 0.0, self.shared, out=self.out)
 
-        def f():
-            exl3.moe_forward_logits(x, lg, self.topk, lay, self.act, 0.0, self.shared, bias=self.bias)
-        return f
-
-    def experts_used(self, j):
+    def rows_per_expert(self, j):
         ids = self.ids[j % len(self.ids)]
-        used = [int(e) for e in torch.unique(ids[ids >= 0])]
-        return used + ([self.shared] if self.shared >= 0 else [])
-
-    def unique(self, j):
-        return len(self.experts_used(j))
+        v = ids[ids >= 0]
+        cnt = torch.bincount(v.to(torch.int64), minlength=self.E + (1 if self.shared >= 0 else 0)).tolist()
+        if self.shared >= 0:
+            cnt[self.shared] = self.M
+        return {e: c for e, c in enumerate(cnt) if c > 0}
 
     def bytes_per_step(self, j):
-        """Algorithmic HBM bytes: the weights of every expert touched once, activations in and out."""
-        return sum(self.exp_bytes[e] for e in self.experts_used(j)) + 2 * self.M * self.H + 4 * self.M * self.H
+        """Algorithmic HBM bytes: the weights of every expert touched, once, x in and fp32 rows out."""
+        return sum(sum(self.exp_bytes[e]) for e in self.rows_per_expert(j)) + 2 * self.M * self.H + 4 * self.M * self.H
 
     def flops_per_step(self, j):
-        ids = self.ids[j % len(self.ids)]
-        pairs = int((ids >= 0).sum()) + (self.M if self.shared >= 0 else 0)
-        return 6.0 * pairs * self.H * self.I
+        return 6.0 * sum(self.rows_per_expert(j).values()) * self.H * self.I
+
+    def weights_per_step(self, j):
+        return 3 * len(self.rows_per_expert(j)) * self.H * self.I
+
+    def unique(self, j):
+        return len(self.rows_per_expert(j))
+
+    def kernel_work(self, name, j):
+        """(algorithmic bytes, FLOP) of one launch of kernel `name` in step j, or None when not modelled."""
+        rpe = self.rows_per_expert(j)
+        if name == "moe_fused":
+            return self.bytes_per_step(j), self.flops_per_step(j)
+        for proj, tag in ((0, "gateup"), (2, "down")):
+            if name.startswith(f"moe_{tag}_mfma_r"):
+                cl = {"1": 0, "2": 1, "4": 2}[name[-1]]
+                experts = {e: sum(c for k, c in mfma_blocks(r) if k == cl) for e, r in rpe.items()}
+                experts = {e: r for e, r in experts.items() if r > 0}
+                rows = sum(experts.values())
+                if proj == 0:      # gate + up weights, xh rows in (two fp16 planes), fp16 down inputs out
+                    b = sum(self.exp_bytes[e][0] + self.exp_bytes[e][1] for e in experts) + 4 * rows * self.H + \
+                        2 * rows * self.I
+                    f = 4.0 * rows * self.H * self.I
+                else:              # down weights, fp16 inputs in, fp32 rows out
+                    b = sum(self.exp_bytes[e][2] for e in experts) + 2 * rows * self.I + 4 * rows * self.H
+                    f = 2.0 * rows * self.H * self.I
+                return b, f
+        return None
+
+    def cpu(self, O, np, rows=None):
+        """The oracle on rows `rows` of routing 0 (default: all), layer copy 0."""
+        import numpy as np_
+        lay = self.layers[0]
+        x = self.x[0].cpu().numpy()
+        ids, w = O.route_softmax_topk(self.logits[0].cpu().numpy(), self.topk,
+                                      None if self.bias is None else self.bias.cpu().numpy())
+        sel = np_.arange(self.M) if rows is None else np_.asarray(rows)
+        used = sorted(set(int(e) for e in np_.unique(ids[sel])) | ({self.shared} if self.shared >= 0 else set()))
+
+        def oproj(p):
+            if isinstance(p, exl3.MixedEXL3):
+                return O.Proj(p.suh.cpu().numpy(), p.svh.cpu().numpy(), words=p.words.cpu().numpy().view(np_.uint32),
+                              kmap=p.kmap.cpu().numpy(), woff=p.woff.cpu().numpy().astype(np_.int64))
+            return O.Proj(p.suh.cpu().numpy(), p.svh.cpu().numpy(), trellis=p.trellis.cpu().numpy(), K=p.Ki)
+
+        experts = {e: tuple(oproj(lay.projs[q][e]) for q in range(3)) for e in used}
+        ex_list = [experts.get(e) for e in range(self.E)]
+        sh = experts.get(self.shared) if self.shared >= 0 else None
+        act = O.ACT_SILU
+
+        def run():
+            # routing is part of the layer call, as on the GPU
+            r_ids, r_w = O.route_softmax_topk(self.logits[0].cpu().numpy()[sel], self.topk,
+                                              None if self.bias is None else self.bias.cpu().numpy())
+            O.moe_layer(x[sel], ex_list, r_ids, r_w, act, 0.0, sh)
+        return cpu_time(run), len(sel), f"{len(sel)} of the {self.M} rows of one layer call"
 
 
-def run_moe(wl, steps, label):
+def measure(name, wl, steps, cpu=True):
+    """Graph-replayed time per step over `steps` steps, the kernel breakdown, the dominant kernel's roofline and the
+    CPU baseline of one workload."""
     fns = [wl.step_fn(j) for j in range(steps)]
     for f in fns[: min(steps, 4)]:
         f()
-    us, _ = graph_time(fns)
+    us = graph_time(fns)
+    nprof = min(steps, 16)
+    prof = kernel_profile([wl.step_fn(j) for j in range(nprof)])
     byts = sum(wl.bytes_per_step(j) for j in range(steps)) / steps
     flops = sum(wl.flops_per_step(j) for j in range(steps)) / steps
+    wts = sum(wl.weights_per_step(j) for j in range(steps)) / steps
     gbs = byts / us / 1e3
     r = {"us_per_layer": round(us, 3), "us_per_token": round(us / wl.M, 3), "tokens": wl.M,
-         "gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-         "tflops": round(flops / us / 1e6, 2), "mfma_frac": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
-         "bytes_per_layer": int(byts), "unique_experts": round(sum(wl.unique(j) for j in range(steps)) / steps, 2)}
-    log(label, r)
-    return r
-
-
-def run_dense(k, n, K, M, copies, steps, seed, label):
-    g = dev_gen(seed)
-    lins = [dev_linear(k, n, K, g) for _ in range(copies)]
-    x = torch.randn(M, k, device="cuda", generator=g).half()
-    y = torch.empty(M, n, dtype=torch.float16, device="cuda")
-    fns = [(lambda l=lins[j % copies]: exl3.exl3_gemm(x, l.trellis, y, l.suh, None, l.svh)) for j in range(steps)]
-    for f in fns[:4]:
-        f()
-    us, _ = graph_time(fns)
-    byts = k * n * K / 8 + 2 * k + 2 * n + 2 * M * k + 2 * M * n
-    gbs = byts / us / 1e3
-    r = {"us_per_layer": round(us, 3), "us_per_token": round(us / M, 3), "tokens": M, "gbps": round(gbs, 1),
-         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": int(byts), "weight_copies": copies}
-    log(label, r)
-    return r
-
-
-def run_mlp(H, I, K, M, copies, steps, seed, label):
-    g = dev_gen(seed)
-    mlps = []
-    for _ in range(copies):
-        gt, up, dn = dev_linear(H, I, K, g), dev_linear(H, I, K, g), dev_linear(I, H, K, g)
-        mlps.append(exl3.BC_GatedMLP(None, None, None, None, None, None, None, K, False, True, False, True, False,
-                                     gt, up, dn, 0.0))
-    x = torch.randn(M, H, device="cuda", generator=g).half()
-    d = torch.empty(M, H, dtype=torch.float32, device="cuda")
-    fns = [(lambda m=mlps[j % copies]: m.run_bszN(x, d)) for j in range(steps)]
-    for f in fns[:4]:
-        f()
-    us, _ = graph_time(fns)
-    byts = 3 * (H * I * K / 8) + 2 * (2 * (H + I) + 2 * (I + H)) + 2 * M * H + 4 * M * H
-    gbs = byts / us / 1e3
-    r = {"us_per_layer": round(us, 3), "us_per_token": round(us / M, 3), "tokens": M, "gbps": round(gbs, 1),
-         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_layer": int(byts), "weight_copies": copies}
-    log(label, r)
+         "bytes_per_layer": int(byts), "gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+         "flop_per_layer": int(flops), "tflops": round(flops / us / 1e6, 2),
+         "mfma_frac": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
+         "weights_decoded_per_s": float(f"{wts / us * 1e6:.4g}"),
+         "kernels": {k: {"launches_per_step": round(n / nprof, 2), "avg_us": round(t, 3)} for k, (n, t) in prof.items()}}
+    if isinstance(wl, MoE):
+        r["unique_experts"] = round(sum(wl.unique(j) for j in range(steps)) / steps, 2)
+    # dominant kernel: most time per step
+    dom = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])[0] if prof else None
+    work = [wl.kernel_work(dom, j) for j in range(nprof)] if dom else []
+    if work and all(w is not None for w in work):
+        k_n, k_us = prof[dom]
+        per_launch = k_n / nprof
+        kb = sum(w[0] for w in work) / nprof / per_launch
+        kf = sum(w[1] for w in work) / nprof / per_launch
+        bound = getattr(wl, "bound", "hbm")
+        if bound == "mfma":
+            ach = kf / k_us / 1e6
+            roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4)}
+        else:
+            ach = kb / k_us / 1e3
+            roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4)}
+        roof.update({"kernel": dom, "kernel_us": round(k_us, 3), "launches_per_step": round(per_launch, 2),
+                     "bytes_per_launch": int(kb), "flop_per_launch": int(kf),
+                     "hbm_frac": round(kb / k_us / 1e3 / HBM_PEAK_GBS, 4),
+                     "mfma_frac": round(kf / k_us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)})
+        r["roofline"] = roof
+    log(name, {k: v for k, v in r.items() if k != "kernels"})
+    log(name, "kernels", r["kernels"])
+    if cpu:
+        import numpy as np
+        O = importlib.import_module("oracle.exl3_oracle")
+        rows = getattr(wl, "cpu_rows", None)
+        t, ntok, what = wl.cpu(O, np, rows) if rows is not None else wl.cpu(O, np)
+        cores, _ = cpu_info()
+        r["cpu_baseline"] = {"value": round(t * 1e6 / ntok, 1), "unit": "us/token", "cores": min(16, cores),
+                             "kind": "port", "sample": f"{what}, oracle (decode + float64 products in C, OpenMP), "
+                                                       f"1 warm-up + median of 3"}
+        log(name, "cpu", r["cpu_baseline"])
     return r
 
 
@@ -248,11 +415,10 @@ def zipf_bias(E, s, seed):
     return (-s * torch.log(rank + 1)).cuda()
 
 
-def recorded_traffic(kname):
-    """HBM bytes per launch of the headline kernel from its committed rocprofv3 counter summary (FETCH_SIZE and
-    WRITE_SIZE per dispatch, each scaled by what the counter reads for a plain copy of known size); None without
-    one. The counters need a profiler run of their own, so the figure is the recorded one, not a live one."""
-    path = os.path.join(ROOT, "profiles", f"{kname}_c3_m4_hbm_traffic.md")
+def recorded_traffic(kname, workload):
+    """HBM bytes per launch of a kernel from its committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by what the counter reads for a plain copy of known size); None without one."""
+    path = os.path.join(ROOT, "profiles", f"{kname}_{workload}_hbm_traffic.md")
     try:
         with open(path) as f:
             for line in f:
@@ -263,48 +429,45 @@ def recorded_traffic(kname):
     return None
 
 
-# ------------------------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(wl, seconds=12.0):
-    """The oracle (NumPy, fp32 accumulation) on a bounded sample of the headline workload: whole layer calls on the
-    host cores until ~`seconds` have passed (at least one)."""
-    import numpy as np
-    O = importlib.import_module("oracle.exl3_oracle")
-    lay = wl.layers[0]
+# ------------------------------------------------------------------------------------------------ configs
+def build(name):
+    if name == "c1":
+        return Dense(4096, 4096, 4, 1, 128, 1000), 256
+    if name.startswith("c2_m"):
+        m = int(name[4:])
+        return Mlp(5376, 21504, 4, m, 6, 2000 + m), 48
+    if name.startswith("c3_m"):
+        m = int(name[4:])
+        layers = [dev_experts(512, 2048, 512, 3, 3, 3000 + 97 * c) for c in range(4)]
+        return MoE(layers, m, 10, 64, 40 + m, "silu", logits_api=True), 64
+    if name == "c4":
+        layers = [dev_experts(160, 5120, 1536, 2, 3, 4000 + c) for c in range(2)]
+        wl = MoE(layers, 512, 8, 4, 41, "silu", bias=zipf_bias(160, 1.1, 4100))
+        wl.bound, wl.cpu_rows = "mfma", list(range(64))
+        return wl, 4
+    if name == "c5":
+        wl = c5_workload()
+        return wl, 4
+    raise ValueError(name)
 
-    def oproj(p):
-        return O.Proj(p.suh.cpu().numpy(), p.svh.cpu().numpy(), trellis=p.trellis.cpu().numpy(), K=p.Ki)
 
-    t_tot, calls = 0.0, 0
-    j = 0
-    while t_tot < seconds and calls < 64:
-        r = j % len(wl.logits)
-        ids, w = O.route_softmax_topk(wl.logits[r].cpu().numpy(), wl.topk)
-        used = np.unique(ids)
-        experts = {int(e): tuple(oproj(lay.projs[q][int(e)]) for q in range(3)) for e in used}
-        x = wl.x[r].cpu().numpy()
-        t0 = time.perf_counter()
-        O.moe_layer(x, experts, ids, w, O.ACT_SILU, 0.0, None, acc=np.float32)
-        t_tot += time.perf_counter() - t0
-        calls += 1
-        j += 1
-    us_tok = t_tot * 1e6 / (calls * wl.M)
-    return {"value": round(us_tok, 1), "unit": "us/token", "cores": len(os.sched_getaffinity(0)), "kind": "port",
-            "sample": f"{calls} layer calls of the headline workload ({wl.M} tokens each, routing + expert decode + "
-                      f"fp32-accumulated matmuls) by the NumPy oracle; BLAS may use every listed core, the trellis "
-                      f"decode runs on one"}
+def c5_workload(nrout=4):
+    wl = MoE([dev_experts(257, 7168, 2048, 0, 0, 5000, mixed=True)], 260, 8, nrout, 51, "silu", shared=True)
+    wl.cpu_rows = list(range(4)) + list(range(4, 260, 21))     # the 4 decode rows and 12 prefill rows
+    return wl
 
 
 # ------------------------------------------------------------------------------------------------ main
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="all", help="comma list of c1..c5 to report next to the headline, or none")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--configs", default="all", help="comma list of c1, c2, c3, c4, c5 to report, or none")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB each (the HBM counter calibration) and exit")
+    ap.add_argument("--only", default=None, help="run just this one workload eagerly (--steps calls; profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (every expert resident on one MI355X); "
@@ -323,14 +486,19 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "copies": 3}), flush=True)
         return
+    if args.only:
+        wl, _ = build(args.only)
+        for j in range(args.steps):
+            wl.step_fn(j)()
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "calls": args.steps}), flush=True)
+        return
     torch.manual_seed(0)
     K, W = args.steps, args.warmup
     log("device", torch.cuda.get_device_name(0))
 
-    # ---- headline: C3 MoE decode layer, 4 tokens per step
-    H, I, E, M = 2048, 512, 512, 4
-    layers = [dev_experts(E, H, I, 3, 3, 3000 + 97 * c) for c in range(4)]
-    wl = MoEWorkload("c3", layers, M, 10, 64, 31, "silu")
+    # ---- headline: C5, 260 rows per step
+    wl = c5_workload()
     fns = [wl.step_fn(j) for j in range(K)]
     for j in range(W):
         wl.step_fn(j)()
@@ -344,64 +512,45 @@ def main():
     g.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    del g
     ms_step = wall * 1e3 / K
+    us_tok = ms_step * 1e3 / wl.M
     byts = sum(wl.bytes_per_step(j) for j in range(K)) / K
-    us_tok = ms_step * 1e3 / M
+    c5 = measure("c5", wl, min(K, 16), cpu=not args.no_cpu_baseline)
+    roofline = dict(c5.get("roofline", {}))
+    if roofline:
+        roofline["traffic"] = recorded_traffic(roofline["kernel"], "c5")
+    roofline["layer_gbps"] = round(byts / (ms_step * 1e3) / 1e3, 1)
+    cpu = c5.pop("cpu_baseline", None)
+    cores, model = cpu_info()
+    if cpu:
+        cpu["model"] = model
+    del wl, fns
+    torch.cuda.empty_cache()
 
-    # dominant kernel, timed live with HIP events on the stream it is launched on: the one-launch fused layer kernel
-    # (every touched expert's gate, up and down weights, x in, combined rows out) where the layer takes it, else the
-    # gate|up GEMV kernel (gate and up weights of every touched expert, x in, activations out)
-    nprof = 64
-    prof = kernel_profile([wl.step_fn(j) for j in range(nprof)])
-    if "moe_fused" in prof:
-        kname = "moe_fused"
-        k_bytes = sum(wl.bytes_per_step(j) for j in range(nprof)) / nprof
-    else:
-        kname = "moe_gateup"
-        k_bytes = sum(wl.unique(j) * wl.gu_bytes + 2 * M * H + 2 * M * 10 * I for j in range(nprof)) / nprof
-    k_n, k_us = prof.get(kname, (0, float("nan")))
-    traffic = recorded_traffic(kname)
-    achieved = k_bytes / k_us / 1e3
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
-                "kernel_us": round(k_us, 3), "launches": k_n, "bytes_per_launch": int(k_bytes),
-                "layer_gbps": round(byts / (ms_step * 1e3) / 1e3, 1)}
-    log("kernel profile", prof)
-
-    configs = {}
+    configs = {"c5": c5}
     want = [c.strip() for c in args.configs.split(",")] if args.configs not in ("all", "none") else \
-        (["c1", "c2", "c3", "c4", "c5"] if args.configs == "all" else [])
-    if "c3" in want:
-        for m in (1, 2, 4):
-            configs[f"c3_m{m}"] = run_moe(MoEWorkload("c3", layers, m, 10, 64, 40 + m, "silu"), 64, f"c3 M={m}")
-    if "c1" in want:
-        configs["c1"] = run_dense(4096, 4096, 4, 1, 128, 256, 1000, "c1")
-    if "c2" in want:
-        for m in (1, 2, 4):
-            configs[f"c2_m{m}"] = run_mlp(5376, 21504, 4, m, 6, 48, 2000 + m, f"c2 M={m}")
-    if "c4" in want:
-        l4 = [dev_experts(160, 5120, 1536, 2, 3, 4000 + c) for c in range(2)]
-        wl4 = MoEWorkload("c4", l4, 512, 8, 4, 41, "silu", bias=zipf_bias(160, 1.1, 4100))
-        configs["c4"] = run_moe(wl4, 4, "c4")
-        del l4, wl4
-    if "c5" in want:
-        l5 = [dev_experts(257, 7168, 2048, 0, 0, 5000, mixed=True)]
-        wl5 = MoEWorkload("c5", l5, 260, 8, 2, 51, "silu", shared=True)
-        configs["c5"] = run_moe(wl5, 2, "c5")
-        del l5, wl5
+        (["c1", "c2", "c3", "c4"] if args.configs == "all" else [])
+    names = [n for c in want for n in ((c,) if c in ("c1", "c4") else (f"{c}_m1", f"{c}_m2", f"{c}_m4"))
+             if c != "c5"]
+    for n in names:
+        w, steps = build(n)
+        configs[n] = measure(n, w, steps, cpu=not args.no_cpu_baseline)
+        del w
+        torch.cuda.empty_cache()
     torch.cuda.synchronize()
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(wl, args.cpu_seconds)
     out = {
         "metric": METRIC, "value": round(us_tok, 3), "unit": "us/token", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(ms_step, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16", "data": "synthetic",
-        "config": {"workload": "C3 fine-grained MoE decode layer: H=2048, 512 experts (gate/up 2048->512, down "
-                               "512->2048), 3.0 bpw EXL3, softmax top-10 routing from fp32 logits, SiLU, 4 tokens "
-                               "per step, fresh routing every step, 4 layer copies (2.4 GB) cycled",
-                   "hidden": H, "intermediate": I, "experts": E, "topk": 10, "bits": 3, "tokens_per_step": M,
-                   "timing": "HIP graph replay of all steps, wall clock", "layer_gbps": roofline["layer_gbps"],
-                   "layer_hbm_frac": round(roofline["layer_gbps"] / HBM_PEAK_GBS, 4)},
+        "config": {"workload": "MoE layer H=7168, 256 routed experts of I=2048 + 1 shared expert, per-tile 1/2-bit "
+                               "EXL3 weights (38/62, 1.62 bpw), softmax top-8, SiLU; 260 rows per step (4 decode + "
+                               "256 prefill) in one call, fresh routing every step",
+                   "hidden": 7168, "intermediate": 2048, "experts": 256, "shared_experts": 1, "topk": 8,
+                   "bits": 1.62, "rows_per_step": 260, "timing": "HIP graph replay of all steps, wall clock",
+                   "layer_gbps": roofline["layer_gbps"],
+                   "layer_hbm_frac": round(roofline["layer_gbps"] / HBM_PEAK_GBS, 4), "host_cpu": model},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "configs": configs,
