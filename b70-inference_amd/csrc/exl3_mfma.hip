@@ -603,9 +603,9 @@ struct MfmaPipeMix {
     int tn, nsteps;
     uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
     uint32_t t0p1;                                           // t0 + 1 of the lane's k-permuted positions
-    const uint32_t* org1;                                    // the lane's funnel word in slot 0 at K = 1, K = 2
-    const uint32_t* org2;
-    uint32_t sh1, sh2;                                       // and the funnel shifts
+    int org1, dorg;                                          // the lane's funnel word in slot 0 at K = 1, and the
+    int sh1, dsh;                                            // step to K = 2; the funnel shifts likewise (origin and
+                                                             // shift at K in {1, 2}: x1 + (K - 1) dx, one mad each)
     const _Float16* asrc[CPT];
     int adst[CPT];
     u32x4_t* lds;
@@ -676,9 +676,9 @@ struct MfmaPipeMix {
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const bool k1 = ks[sl] == 1;
-                    const uint32_t* o = k1 ? org1 : org2;
-                    const uint32_t F = __builtin_amdgcn_alignbit(o[sl * kMixTS], o[sl * kMixTS + 1], k1 ? sh1 : sh2);
+                    const uint32_t* o = wl + (org1 + (ks[sl] - 1) * dorg);
+                    const uint32_t F = __builtin_amdgcn_alignbit(o[sl * kMixTS], o[sl * kMixTS + 1],
+                                                                 (uint32_t)(sh1 + (ks[sl] - 1) * dsh));
                     const h4_t bf = decode4p(F, ks[sl]);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
@@ -755,10 +755,10 @@ struct MfmaPipeMix {
         const int n = lane & 15, g = lane >> 4;
         t0p1 = (uint32_t)(32 * (n & 7) + 4 * (n >> 3) + 8 * g + 1);
         const uint32_t ta1 = t0p1 + 15u, ta2 = 2u * t0p1 + 15u;           // start + 31 at K = 1, 2
-        org1 = wl + (ta1 >> 5);
-        org2 = wl + (ta2 >> 5);
-        sh1 = ~ta1;
-        sh2 = ~ta2;
+        org1 = (int)(ta1 >> 5);
+        dorg = (int)(ta2 >> 5) - org1;
+        sh1 = (int)(~ta1 & 31u);
+        dsh = (int)(~ta2 & 31u) - sh1;
     }
 };
 
