@@ -29,6 +29,7 @@ SIGNATURES = {
     "exl3_profile_enable": [_i32],
     "exl3_profile_read": [ctypes.c_char_p, _i64],
     "exl3_reconstruct": [_vp, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64, _vp],
+    "exl3_reconstruct_had_slice": [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i64, _i64, _vp, _i64, _vp],
     "exl3_had_r_128": [_vp, _i64, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _f32, _vp],
     "exl3_gemm": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _i32, _vp],
     "exl3_gemm_noalloc": [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp],

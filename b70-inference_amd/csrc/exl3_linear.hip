@@ -42,6 +42,53 @@ __global__ __launch_bounds__(64) void reconstruct_kernel(const uint32_t* __restr
     }
 }
 
+// ================================================================================================ reconstruct_had
+// Original-basis weight slice W = diag(suh) Hblk W_hat Hblk diag(svh) (Hblk = blockdiag(H128 / sqrt(128))): one
+// workgroup per 128 x 128 block. The block's 8 tile-row strips are decoded into LDS (fp32), every column gets the
+// 128-point transform (one wave per column), then every row (one wave per row), which also applies
+// suh[row] * svh[col] / 128 and rounds once to fp16. All of it in fp32: within one fp16 rounding of the exact weight.
+template <int K>
+__global__ __launch_bounds__(256) void reconstruct_had_kernel(const uint32_t* __restrict__ tr, int tn, int n0_tiles,
+                                                              const uint16_t* __restrict__ suh,
+                                                              const uint16_t* __restrict__ svh,
+                                                              uint16_t* __restrict__ out, int64_t out_ld) {
+    __shared__ float M[128][129];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = blockIdx.x, kb = blockIdx.y;
+    const int cbase = 16 * (lane >> 3) + (lane & 7);
+    for (int s = wave; s < 8; s += 4) {                         // tile-row strips of the block
+        const uint32_t* p = tr + ((size_t)(8 * kb + s) * tn + n0_tiles + (size_t)nb * 8) * (8 * K);
+        uint32_t R[K + 1];
+        load_chunk<K>(p, lane, R);
+        chunk_prev<K>(lane, R);
+        h2_t w[16];
+        decode_chunk<K>(R, w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int r = 16 * s + pos_row(2 * j), c = cbase + 8 * pos_half(2 * j);
+            M[r][c] = (float)w[j][0];
+            M[r + 1][c] = (float)w[j][1];
+        }
+    }
+    __syncthreads();
+    for (int c = wave; c < 128; c += 4) {                       // Hblk W_hat: transform every column
+        float a = M[lane][c], b = M[lane + 64][c];
+        fwht128_wave(a, b, lane);
+        M[lane][c] = a;
+        M[lane + 64][c] = b;
+    }
+    __syncthreads();
+    const float s0 = h2f(ldg(svh + nb * 128 + lane)), s1 = h2f(ldg(svh + nb * 128 + lane + 64));
+    for (int r = wave; r < 128; r += 4) {                       // (..) Hblk: transform every row, then the signs
+        float a = M[r][lane], b = M[r][lane + 64];
+        fwht128_wave(a, b, lane);
+        const float su = h2f(ldg(suh + kb * 128 + r)) * (1.0f / 128.0f);
+        uint16_t* o = out + (size_t)(kb * 128 + r) * out_ld + nb * 128;
+        o[lane] = f2h(a * su * s0);
+        o[lane + 64] = f2h(b * su * s1);
+    }
+}
+
 // ================================================================================================ had_r_128
 template <bool F16>
 __global__ __launch_bounds__(64) void had_kernel(const void* __restrict__ in, int64_t in_ld, void* __restrict__ out,
@@ -439,6 +486,35 @@ int exl3_reconstruct(const int16_t* trellis, int64_t k, int64_t n_total, int K, 
                                reconstruct_kernel<4>, reconstruct_kernel<5>, reconstruct_kernel<6>,
                                reconstruct_kernel<7>, reconstruct_kernel<8>};
     EXL3_LAUNCH("reconstruct", fns[K - 1], grid, dim3(64), 0, st, tr, tn, n0t, out, out_ld);
+    return EXL3_OK;
+}
+
+int exl3_reconstruct_had_slice(const int16_t* trellis, int64_t k, int64_t n_total, int K, int cb, const uint16_t* suh,
+                               const uint16_t* svh, int64_t n_offset, int64_t n_slice, uint16_t* out, int64_t out_ld,
+                               void* stream) {
+    if (cb != 2)
+        return fail(EXL3_ERR_UNSUPPORTED, "exl3_reconstruct_had_slice: codebook %d not supported (mul1 = 2 only)", cb);
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_reconstruct_had_slice: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(trellis && suh && svh && out, "exl3_reconstruct_had_slice: null pointer");
+    EXL3_CHECK_ARG(k > 0 && k % 128 == 0 && n_total % 128 == 0,
+                   "exl3_reconstruct_had_slice: k=%lld and n=%lld must be multiples of 128", (long long)k,
+                   (long long)n_total);
+    EXL3_CHECK_ARG(n_offset % 128 == 0 && n_slice % 128 == 0 && n_offset >= 0 && n_slice >= 0 &&
+                       n_offset + n_slice <= n_total,
+                   "exl3_reconstruct_had_slice: slice [%lld, +%lld) of %lld must be 128-aligned and in range",
+                   (long long)n_offset, (long long)n_slice, (long long)n_total);
+    EXL3_CHECK_ARG(out_ld >= n_slice, "exl3_reconstruct_had_slice: output row stride below the slice width");
+    EXL3_CHECK_ARG(aligned(trellis, 4), "exl3_reconstruct_had_slice: trellis must be 4-byte aligned");
+    EXL3_CHECK_ARG(k / 128 <= 65535 && n_slice / 128 <= 65535, "exl3_reconstruct_had_slice: shape too large");
+    if (n_slice == 0) return EXL3_OK;
+    hipStream_t st = (hipStream_t)stream;
+    typedef void (*rfn)(const uint32_t*, int, int, const uint16_t*, const uint16_t*, uint16_t*, int64_t);
+    static const rfn fns[8] = {reconstruct_had_kernel<1>, reconstruct_had_kernel<2>, reconstruct_had_kernel<3>,
+                               reconstruct_had_kernel<4>, reconstruct_had_kernel<5>, reconstruct_had_kernel<6>,
+                               reconstruct_had_kernel<7>, reconstruct_had_kernel<8>};
+    EXL3_LAUNCH("reconstruct_had", fns[K - 1], dim3((unsigned)(n_slice / 128), (unsigned)(k / 128)), dim3(256), 0, st,
+                reinterpret_cast<const uint32_t*>(trellis), (int)(n_total / 16), (int)(n_offset / 16), suh, svh, out,
+                out_ld);
     return EXL3_OK;
 }
 

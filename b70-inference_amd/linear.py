@@ -65,6 +65,29 @@ def reconstruct_slice(unpacked: torch.Tensor, packed: torch.Tensor, K, mcg: bool
     exl3_reconstruct(packed, unpacked, n_offset, _K_of(packed, K), _cb(mcg, mul1))
 
 
+def reconstruct_had_slice(unpacked: torch.Tensor, packed: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K,
+                          mcg: bool, mul1: bool, n_offset: int) -> None:
+    """exllamav3 ext reconstruct_had_slice(unpacked, packed, suh, svh, K, mcg, mul1, n_offset): unpacked fp16
+    [k, n_slice] = the original-basis weight diag(suh) Hblk W_hat Hblk diag(svh) for columns n_offset .. + n_slice,
+    with svh the slice's signs (the caller passes svh[n_offset:], as the reference does). x @ unpacked is the
+    linear's output for those columns."""
+    require_device(unpacked, packed, suh, svh)
+    cb = _cb(mcg, mul1)
+    K = _K_of(packed, K)
+    if unpacked.dtype != torch.float16 or unpacked.dim() != 2 or unpacked.stride(1) != 1:
+        raise Exl3Error("reconstruct_had_slice: unpacked must be a 2D fp16 tensor with unit column stride")
+    if not packed.is_contiguous():
+        raise Exl3Error("reconstruct_had_slice: trellis must be contiguous")
+    k, n_slice = packed.shape[0] * 16, unpacked.shape[1]
+    if unpacked.shape[0] != k or suh.numel() != k or svh.numel() < n_slice:
+        raise Exl3Error("reconstruct_had_slice: unpacked [k, n_slice], suh [k] and svh [>= n_slice] expected")
+    if suh.dtype != torch.float16 or svh.dtype != torch.float16:
+        raise Exl3Error("reconstruct_had_slice: suh / svh must be fp16")
+    check(lib().exl3_reconstruct_had_slice(ptr(packed), k, packed.shape[1] * 16, K, cb, ptr(suh.contiguous()),
+                                           ptr(svh.contiguous()), int(n_offset), n_slice, ptr(unpacked),
+                                           unpacked.stride(0), stream_of(unpacked)), "reconstruct_had_slice")
+
+
 def had_r_128(input: torch.Tensor, output: torch.Tensor, pre_scale, post_scale, scale: float) -> None:
     """Blockwise H128 * scale / sqrt(128) with optional fp16 pre/post scales (pre wins), written into output."""
     require_device(input, output, pre_scale, post_scale)

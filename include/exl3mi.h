@@ -73,6 +73,17 @@ int exl3_profile_read(char* out, int64_t cap);
 int exl3_reconstruct(const int16_t* trellis, int64_t k, int64_t n_total, int K, int cb, int64_t n_offset,
                      int64_t n_slice, uint16_t* out, int64_t out_ld, void* stream);
 
+/* Original-basis weight slice: out[r, c] = W[r, n_offset + c] with W = diag(suh) Hblk W_hat Hblk diag(svh_full),
+ * where svh points at the slice's output signs (svh_full + n_offset, as the reference passes svh[n_start:]) and suh
+ * covers all k rows; fp16 out (row stride out_ld), computed in fp32 and rounded once (within one fp16 rounding of the
+ * exact weight; the reference's fp16 butterflies are less precise, so results are not bit-identical with it).
+ * y = x @ out is the linear's output for those columns. k, n_total, n_offset and n_slice multiples of 128.
+ * Replaces: exllamav3 ext reconstruct_had_slice(unpacked, packed, suh, svh, K, mcg, mul1, n_offset)
+ *           (ext-op-inventory.md:614-627; the fused large-M prefill, ext-op-inventory.md:437-446). */
+int exl3_reconstruct_had_slice(const int16_t* trellis, int64_t k, int64_t n_total, int K, int cb, const uint16_t* suh,
+                               const uint16_t* svh, int64_t n_offset, int64_t n_slice, uint16_t* out, int64_t out_ld,
+                               void* stream);
+
 /* Blockwise 128-point Hadamard: out[r, blk] = (H128 @ (in[r, blk] (* pre))) * scale / sqrt(128) (* post).
  * in/out [rows, cols] with row strides in_ld/out_ld, both of `dtype`; cols % 128 == 0; in-place allowed.
  * pre/post fp16 [cols] or NULL; if both are given only pre is applied. fp16 path rounds x*pre, the scaled sum and

@@ -53,6 +53,30 @@ def test_reconstruct_full_c1(exl3, oracle):
     assert np.array_equal(w.cpu().numpy().view(np.uint16), oracle.reconstruct(tr.numpy(), 4).view(np.uint16))
 
 
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 8])
+def test_reconstruct_had_slice_matches_dense_weight(exl3, oracle, K):
+    """Original-basis weight slices (reconstruct_had_slice, the reference's svh[n_offset:] convention) within one fp16
+    ulp of the oracle's float64 diag(suh) Hblk W_hat Hblk diag(svh); columns past the slice untouched; x @ W equals
+    the linear's output within the tolerance."""
+    k, n = 384, 640
+    tr, suh, svh = synth().linear(k, n, K, 1100 + K)
+    ref = oracle.dense_weight(tr.numpy(), suh.numpy(), svh.numpy(), K)
+    full = None
+    for n_off, n_sl in ((0, n), (256, 256), (512, 128)):
+        buf = torch.full((k, n_sl + 64), float("nan"), dtype=torch.float16, device="cuda")
+        exl3.reconstruct_had_slice(buf[:, :n_sl], tr.cuda(), suh.cuda(), svh[n_off:].cuda(), K, False, True, n_off)
+        got = buf.cpu().numpy()
+        r = ref[:, n_off:n_off + n_sl]
+        ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float64)
+        assert (np.abs(got[:, :n_sl].astype(np.float64) - r) <= ulp).all()
+        assert np.isnan(got[:, n_sl:]).all()
+        if n_off == 0:
+            full = got[:, :n_sl].astype(np.float64)
+    x = synth().activations(3, k, 1200 + K)
+    y = oracle.exl3_linear(x.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), K, np.float32)
+    assert max_rel(x.numpy().astype(np.float64) @ full, y) <= MAX_REL
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_had_r_128(exl3, oracle, dtype):
     g = torch.Generator().manual_seed(3)
