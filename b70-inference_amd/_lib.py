@@ -41,6 +41,9 @@ SIGNATURES = {
     "exl3_route_block": [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _f32, _f32, _vp, _vp, _vp],
     "exl3_moe_forward": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _f32,
                          _i64, _vp, _i64, _i32, _vp],
+    "exl3_moe_forward_blobs": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _f32, _vp, _i64,
+                               _i32, _vp],
+    "exl3_blob_unplanarize": [_vp, _i64, _i64, _i64, _i32, _vp],
     "exl3_moe_forward_logits": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i32,
                                 _i32, _i32, _f32, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "exl3_moe_align": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp],

@@ -316,7 +316,7 @@ __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDes
                                                  uint32_t* wlds, float* C, float* rsum) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
-    const int tn = a.I / 16;
+    const int tn = a.gu_tn;
     const uint32_t* trp[2] = {reinterpret_cast<const uint32_t*>(d->tab[0]),
                               reinterpret_cast<const uint32_t*>(d->tab[3])};
     const int ct0 = nb * 8 + 2 * wave;

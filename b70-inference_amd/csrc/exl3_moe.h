@@ -62,6 +62,9 @@ struct MoeArgs {
     int uniform;                       // tables[i][e] == tb[i] + e * ts[i] for every entry (host-known layout)
     int64_t tb[9], ts[9];
     int Kg, Kd;                        // gate/up K, down K (0 = per-tile)
+    int gu_tn;                         // tiles per tile-row of the gate and up trellises (uniform K): I / 16, or
+                                       // 2 I / 16 for the reference's expert blob (gate and up tiles of a tile-row
+                                       // side by side, up at gate + I / 16 tiles)
     // routing from logits inside the fused layer (null: ids / tw hold the routing): softmax over logits (+ rbias)
     // -> top-k -> renormalised, picks written to ids_out / tw_out
     const float* logits;

@@ -372,7 +372,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(d->tab[3 * proj]);
     const int tn = a.I / 16;
     constexpr int KL = K > 0 ? K : 1;
-    const size_t rs = (size_t)tn * (8 * KL);
+    const size_t rs = (size_t)a.gu_tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
     StripRing<KL, 3> ring;
     if (K > 0) strip_prefetch<KL, 3>(sp, rs, half, kb * 8, 2, lane, ring);
@@ -981,6 +981,62 @@ static int check_K(int K, const char* what) {
 
 }  // namespace exl3
 
+namespace exl3 {
+
+// ------------------------------------------------------------------------------------------------ expert blobs
+// The reference's expert blob (glm/xpu/csrc/exl3_moe.n128.sycl:3-11, Geom at :56-68; packed by pack_expert,
+// glm/xpu/exl3xpu/moe_offload.py:81-94): gate|up trellis words [H/16][2I/16][8K] (per tile-row the I/16 gate tiles,
+// then the I/16 up tiles), down trellis [I/16][H/16][8K], then fp16 suh_g[H] suh_u[H] svh_g[I] svh_u[I] suh_d[I]
+// svh_d[H]. Tables [9][E] (trellis, suh, svh per projection) from one blob address per expert.
+__global__ void blob_tables_kernel(const int64_t* __restrict__ ptrs, int E, int64_t gu_bytes, int64_t d_bytes,
+                                   int64_t H, int64_t I, int K, int64_t* __restrict__ tab) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int64_t b = ptrs[e], sg = b + gu_bytes + d_bytes;
+    tab[0 * (int64_t)E + e] = b;                                   // gate trellis
+    tab[1 * (int64_t)E + e] = sg;                                  // suh_g
+    tab[2 * (int64_t)E + e] = sg + 4 * H;                          // svh_g
+    tab[3 * (int64_t)E + e] = b + (I / 16) * 8 * K * 4;            // up trellis: I/16 tiles into every tile-row
+    tab[4 * (int64_t)E + e] = sg + 2 * H;                          // suh_u
+    tab[5 * (int64_t)E + e] = sg + 4 * H + 2 * I;                  // svh_u
+    tab[6 * (int64_t)E + e] = b + gu_bytes;                        // down trellis
+    tab[7 * (int64_t)E + e] = sg + 4 * H + 4 * I;                  // suh_d
+    tab[8 * (int64_t)E + e] = sg + 4 * H + 6 * I;                  // svh_d
+}
+
+// In-place PLANAR4 -> tile order for odd K (D = K planes of G = 8 periods): within every group of 4 consecutive
+// tiles of a tile-row, word (tile t, period g, plane i) sits at 32 i + 8 t + g; in tile order it is word K g + i of
+// tile t, at 8K t + K g + i (glm/xpu/exl3xpu/moe_offload.py:68-78, glm/xpu/pack_store.py:41-54). Workgroup per
+// (expert, tile-row of gate|up then of down); the row's groups pass through LDS one at a time.
+__global__ __launch_bounds__(256) void blob_unplanarize_kernel(const int64_t* __restrict__ ptrs, int64_t gu_bytes,
+                                                               int H, int I, int K) {
+    __shared__ uint32_t g[4 * 8 * 8];
+    const int e = blockIdx.x, row = blockIdx.y;
+    const int rows_gu = H / 16;
+    uint32_t* base = reinterpret_cast<uint32_t*>(ptrs[e]);
+    int tiles;
+    if (row < rows_gu) {
+        tiles = 2 * I / 16;
+        base += (size_t)row * tiles * 8 * K;
+    } else {
+        tiles = H / 16;
+        base = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(base) + gu_bytes) + (size_t)(row - rows_gu) * tiles * 8 * K;
+    }
+    const int W = 32 * K;                                         // words per group of 4 tiles
+    for (int grp = 0; grp < tiles / 4; ++grp) {
+        uint32_t* gp = base + (size_t)grp * W;
+        for (int j = threadIdx.x; j < W; j += 256) g[j] = gp[j];
+        __syncthreads();
+        for (int n = threadIdx.x; n < W; n += 256) {                // natural word n = 8K t + K gg + i
+            const int t = n / (8 * K), r = n - t * 8 * K, gg = r / K, i = r - gg * K;
+            gp[n] = g[32 * i + 8 * t + gg];
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace exl3
+
 using namespace exl3;
 
 // Argument checks and MoeArgs shared by the two layer entry points (ids / weights may still be unset).
@@ -1017,6 +1073,7 @@ static int moe_setup(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.kmaps = kmaps;
     a.Kg = K_gate;
     a.Kd = K_down;
+    a.gu_tn = (int)(I / 16);
     a.act = act;
     a.limit = act_limit;
     a.shared = (int)shared;
@@ -1056,6 +1113,48 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     a.ids = topk_ids;
     a.tw = topk_w;
     return moe_run(a, (hipStream_t)stream);
+}
+
+int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
+                           const float* topk_w, int64_t topk, int64_t E, const int64_t* ptrs, int K, int act,
+                           float act_limit, void* out, int64_t out_ld, int out_dtype, void* stream) {
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward_blobs: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(E > 0 && E <= kMoeMaxExperts && H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
+                   "exl3_moe_forward_blobs: E=%lld, H=%lld, I=%lld out of range", (long long)E, (long long)H,
+                   (long long)I);
+    EXL3_CHECK_ARG(H / 16 * (2 * I / 16) * 8 * K < (1LL << 32), "exl3_moe_forward_blobs: blob trellis exceeds 2^32 words");
+    if (M == 0) return EXL3_OK;
+    EXL3_CHECK_ARG(ptrs && topk_ids && topk_w, "exl3_moe_forward_blobs: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    void* tb = nullptr;
+    int rc = aux_buffer((size_t)9 * E * sizeof(int64_t), st, &tb);
+    if (rc) return rc;
+    int64_t* tables = reinterpret_cast<int64_t*>(tb);
+    const int64_t gu_bytes = H / 16 * (2 * I / 16) * 8 * K * 4, d_bytes = I / 16 * (H / 16) * 8 * K * 4;
+    EXL3_LAUNCH("blob_tables", blob_tables_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, st, ptrs, (int)E,
+                gu_bytes, d_bytes, H, I, K, tables);
+    MoeArgs a;
+    rc = moe_setup(x, x_ld, M, H, I, topk, E, tables, nullptr, K, K, K, act, act_limit, -1, out, out_ld, out_dtype, a);
+    if (rc) return rc;
+    a.gu_tn = (int)(2 * I / 16);
+    a.ids = topk_ids;
+    a.tw = topk_w;
+    return moe_run(a, st);
+}
+
+int exl3_blob_unplanarize(const int64_t* ptrs, int64_t E, int64_t H, int64_t I, int K, void* stream) {
+    if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_blob_unplanarize: K=%d not in 1..8", K);
+    if (K == 6)
+        return fail(EXL3_ERR_UNSUPPORTED, "exl3_blob_unplanarize: the reference defines PLANAR4 for K = 2, 3, 4, 5, 7, 8");
+    EXL3_CHECK_ARG(E > 0 && E <= 65535 && H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0 && H / 16 + I / 16 <= 65535,
+                   "exl3_blob_unplanarize: E=%lld, H=%lld, I=%lld out of range", (long long)E, (long long)H,
+                   (long long)I);
+    if (K % 2 == 0) return EXL3_OK;                                // D = K / gcd(K, 32) = 1: already in tile order
+    EXL3_CHECK_ARG(ptrs, "exl3_blob_unplanarize: null pointer");
+    const int64_t gu_bytes = H / 16 * (2 * I / 16) * 8 * K * 4;
+    EXL3_LAUNCH("blob_unplanarize", blob_unplanarize_kernel, dim3((unsigned)E, (unsigned)(H / 16 + I / 16)), dim3(256),
+                0, (hipStream_t)stream, ptrs, gu_bytes, (int)H, (int)I, K);
+    return EXL3_OK;
 }
 
 int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const float* logits,

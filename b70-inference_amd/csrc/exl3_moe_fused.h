@@ -70,6 +70,7 @@ struct FusedArgs {
     int uniform;                        // expert e's table entry i is tb[i] + e * ts[i] (no table loads)
     int64_t tb[9], ts[9];
     int GU, DN;                         // gate|up jobs (I / 128 * P_gu) and down jobs (H / 128 * P_d) per item
+    int gu_tn;                          // tiles per tile-row of the gate and up trellises (MoeArgs::gu_tn)
     int J_gu, max_items;
     void* out;
     int64_t out_ld;
@@ -405,7 +406,7 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
     const int proj = wave >> 1, half = wave & 1;
     const uint32_t* tr = reinterpret_cast<const uint32_t*>(proj ? s.tab[3] : s.tab[0]);
     const int tn = a.I / 16;
-    const size_t rs = (size_t)tn * (8 * KL);
+    const size_t rs = (size_t)a.gu_tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
 

@@ -61,6 +61,7 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     }
     a.x = m.x;
     a.x_ld = m.x_ld;
+    a.gu_tn = m.gu_tn;
     a.M = m.M;
     a.H = m.H;
     a.I = m.I;

@@ -158,6 +158,31 @@ int workspace(size_t bytes, size_t ncounters, hipStream_t st, Workspace* out) {
 
 int spin_limit() { return env_int("EXL3MI_SPIN_LIMIT", 1 << 20); }
 
+namespace {
+char* g_auxbuf[kMaxDevices];
+size_t g_auxbuf_bytes[kMaxDevices];
+}  // namespace
+
+int aux_buffer(size_t bytes, hipStream_t st, void** out) {
+    int dev = 0;
+    EXL3_CHECK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(EXL3_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (bytes > g_auxbuf_bytes[dev]) {
+        if (capturing(st))
+            return fail(EXL3_ERR_INVALID, "aux buffer: %zu bytes needed under stream capture, %zu held; run the call "
+                                          "once before capturing", bytes, g_auxbuf_bytes[dev]);
+        const size_t nb = ((bytes + bytes / 4) + 4095) & ~(size_t)4095;
+        char* p = nullptr;
+        EXL3_CHECK_HIP(hipMalloc(&p, nb));
+        if (g_auxbuf[dev]) g_retired[dev].push_back(g_auxbuf[dev]);
+        g_auxbuf[dev] = p;
+        g_auxbuf_bytes[dev] = nb;
+    }
+    *out = g_auxbuf[dev];
+    return EXL3_OK;
+}
+
 int device_status(int* out) {
     int dev = 0;
     EXL3_CHECK_HIP(hipGetDevice(&dev));

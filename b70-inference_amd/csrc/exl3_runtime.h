@@ -44,6 +44,10 @@ int workspace(size_t bytes, size_t ncounters, hipStream_t stream, Workspace* out
 // Wait bound of the kernels' cross-workgroup waits (polls): EXL3MI_SPIN_LIMIT, default 2^20. A small value makes a
 // wait give up early (failure-path tests); every kernel still exits.
 int spin_limit();
+
+// A second per-device buffer for data a call builds before it runs on the workspace (e.g. expert tables); same
+// growth rules as the workspace (retired, never freed under queued work; refused under capture).
+int aux_buffer(size_t bytes, hipStream_t stream, void** out);
 int device_status(int* out);
 int release_workspace();
 

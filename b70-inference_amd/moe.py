@@ -165,6 +165,46 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, t
     return out
 
 
+def moe_forward_blobs(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, ptrs: torch.Tensor, I: int, K: int,
+                      n_experts: int, act=ACT_SILU, act_limit: float = 0.0, out: torch.Tensor | None = None,
+                      out_dtype=None) -> torch.Tensor:
+    """exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) -> [M, H] (x's dtype unless out_dtype):
+    the routed layer over one expert blob per expert (ptrs: int64 device addresses, the reference's Geom layout in
+    tile order; odd-K blobs pass through blob_unplanarize once first)."""
+    require_device(x, topk_ids, topk_w, ptrs)
+    if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1:
+        raise Exl3Error("moe_forward_blobs: x must be fp16 [M, H] with contiguous rows")
+    if topk_ids.dtype != torch.int32 or topk_w.dtype != torch.float32 or topk_ids.shape != topk_w.shape:
+        raise Exl3Error("moe_forward_blobs: topk_ids int32 and topk_w fp32 [M, k] expected")
+    if ptrs.dtype != torch.int64 or ptrs.numel() < n_experts:
+        raise Exl3Error("moe_forward_blobs: ptrs must be int64 [n_experts]")
+    M, H = x.shape
+    topk_ids, topk_w, ptrs = topk_ids.contiguous(), topk_w.contiguous(), ptrs.contiguous()
+    if out is None:
+        out = torch.empty(M, H, dtype=out_dtype or x.dtype, device=x.device)
+    if out.dtype not in (torch.float16, torch.float32) or out.stride(1) != 1 or tuple(out.shape) != (M, H):
+        raise Exl3Error("moe_forward_blobs: out must be fp16/fp32 [M, H] with contiguous rows")
+    a = ACTS.get(act)
+    if a is None:
+        raise NotImplementedError(f"moe_forward_blobs: activation {act!r}")
+    check(lib().exl3_moe_forward_blobs(ptr(x), x.stride(0), M, H, int(I), ptr(topk_ids), ptr(topk_w),
+                                       topk_ids.shape[1] if topk_ids.dim() == 2 else 0, int(n_experts), ptr(ptrs),
+                                       int(K), a, float(act_limit), ptr(out), out.stride(0),
+                                       EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, stream_of(x)),
+          "moe_forward_blobs")
+    return out
+
+
+def blob_unplanarize(ptrs: torch.Tensor, H: int, I: int, K: int) -> None:
+    """Put odd-K reference expert blobs (PLANAR4 word order) into tile order in place, once, before
+    moe_forward_blobs; even K needs nothing."""
+    require_device(ptrs)
+    if ptrs.dtype != torch.int64:
+        raise Exl3Error("blob_unplanarize: ptrs must be int64")
+    check(lib().exl3_blob_unplanarize(ptr(ptrs.contiguous()), ptrs.numel(), int(H), int(I), int(K), stream_of(ptrs)),
+          "blob_unplanarize")
+
+
 def moe_forward_logits(x: torch.Tensor, logits: torch.Tensor, k: int, tables: ExpertTables, act=ACT_SILU,
                        act_limit: float = 0.0, shared: int = -1, bias: torch.Tensor | None = None,
                        out: torch.Tensor | None = None, out_dtype=torch.float32, return_routing: bool = False):

@@ -167,14 +167,38 @@ int exl3_act_mul(const void* x, const void* y, uint16_t* z, int64_t n, int dtype
  * x fp16 [M, H] (row stride x_ld); topk_ids int32 [M, topk] in [0, E) (negative = inactive slot); topk_w fp32
  * [M, topk]; out fp32 or fp16 [M, H] (row stride out_ld). H % 128 == 0, I % 128 == 0.
  * act: EXL3_ACT_SILU (a = min(silu(g), L) * clamp(u, -L, L), L = act_limit, 0 = no clamp) or EXL3_ACT_GELU_TANH.
- * Experts with up to 8 rows use the decode GEMV kernels; experts with more rows use the fp16 MFMA grouped GEMM.
- * Replaces: exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) (glm/xpu/csrc/exl3_moe.n128.sycl:
- *           1380-1439, bound at :1681-1682), BC_BlockSparseMLP.run_bszN and exl3_moe + exl3_moe_gather
- *           (ext-op-inventory.md:1036-1102), dsv_moe::moe_gemv with per-item K (dsv41/xpu/csrc/dsv_moe.sycl:157-170). */
+ * Batches of at most 16 tokens and 128 (token, slot) pairs run as one fused launch; larger batches on 8 tokens or
+ * fewer use the decode GEMV kernels, and larger ones the fp16 MFMA grouped GEMM.
+ * Replaces: BC_BlockSparseMLP.run_bszN and exl3_moe + exl3_moe_gather over the nine pointer tables
+ *           (ext-op-inventory.md:1036-1102), dsv_moe::moe_gemv with per-item K (dsv41/xpu/csrc/dsv_moe.sycl:157-170).
+ *           The reference's blob-pointer op is exl3_moe_forward_blobs below. */
 int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
                      const float* topk_w, int64_t topk, int64_t E, const int64_t* tables, const int64_t* kmaps,
                      int K_gate, int K_up, int K_down, int act, float act_limit, int64_t shared, void* out,
                      int64_t out_ld, int out_dtype, void* stream);
+
+/* The routed MoE layer over the reference's expert blobs: ptrs (device int64 [E]) holds one blob address per expert,
+ * each blob laid out as the reference's Geom (glm/xpu/csrc/exl3_moe.n128.sycl:3-11, 56-68; packed by pack_expert,
+ * glm/xpu/exl3xpu/moe_offload.py:81-94): gate|up trellis uint32 [H/16][2I/16][8K] (per tile-row the I/16 gate tiles,
+ * then the I/16 up tiles), down trellis [I/16][H/16][8K], then fp16 suh_g[H] suh_u[H] svh_g[I] svh_u[I] suh_d[I]
+ * svh_d[H]; blobs 16-byte aligned, every routed expert's pointer valid. The words must be in tile order: so they are
+ * for even K (PLANAR4 is the identity there), odd-K blobs are converted once by exl3_blob_unplanarize. One K for all
+ * projections; no shared expert (the reference adds it outside the op). Other arguments, paths and results as
+ * exl3_moe_forward with the same weights.
+ * Replaces: exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) (glm/xpu/csrc/exl3_moe.n128.sycl:
+ *           1380-1439, bound at :1681-1682). */
+int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
+                           const float* topk_w, int64_t topk, int64_t E, const int64_t* ptrs, int K, int act,
+                           float act_limit, void* out, int64_t out_ld, int out_dtype, void* stream);
+
+/* One-time conversion of the reference's expert blobs to tile order, in place: for odd K (3, 5, 7) the trellis words
+ * of every group of 4 tiles of a tile-row are stored plane by plane (PLANAR4, glm/xpu/exl3xpu/moe_offload.py:68-78,
+ * glm/xpu/pack_store.py:41-54) and are put back into tile order; even K is already in tile order (no work). K = 6 is
+ * not a PLANAR4 bitrate of the reference. Blobs and sizes as exl3_moe_forward_blobs. After it the blobs serve
+ * exl3_moe_forward_blobs (and no longer the reference's kernels).
+ * No reference counterpart: the reference's kernels read PLANAR4 directly (Xe register regions cannot stride by K);
+ * the gfx950 kernels load K words per lane from tile order. */
+int exl3_blob_unplanarize(const int64_t* ptrs, int64_t E, int64_t H, int64_t I, int K, void* stream);
 
 /* The routed MoE layer from router logits: exl3_route_softmax_topk followed by exl3_moe_forward, as one call, with
  * the same results bit for bit. Up to 2 tokens with n_logits <= 512 on the fused decode layer, the layer ranks the

@@ -159,3 +159,39 @@ def test_arena_experts_same_outputs(exl3, M):
     ref = O.moe_layer(x.cpu().numpy(), orc, rid, rw, O.ACT_SILU)
     err = float(np.abs(a.cpu().numpy() - ref).max() / np.abs(ref).max())
     assert err <= 2e-3, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [2, 3, 4])
+@pytest.mark.parametrize("M", [3, 40])
+def test_moe_forward_blobs_on_reference_blobs(exl3, K, M):
+    """The reference's blob-pointer op: experts packed as the reference packs them (pack_expert / planar4, restated in
+    the oracle), one device blob per expert, odd K put into tile order once; the layer equals exl3_moe_forward on
+    separately allocated tensors bit for bit (fused decode at 3 rows, MFMA at 40) and the oracle's layer."""
+    E, H, I = 6, 256, 256
+    experts = [_expert(H, I, K, K, 1200 + 10 * e) for e in range(E)]
+    blobs = [torch.from_numpy(O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in ex], K)).cuda()
+             for ex in experts]
+    ptrs = torch.tensor([b.data_ptr() for b in blobs], dtype=torch.int64, device="cuda")
+    exl3.blob_unplanarize(ptrs, H, I, K)
+    g = torch.Generator().manual_seed(1300 + 10 * M + K)
+    x = torch.randn(M, H, generator=g).half()
+    logits = torch.randn(M, E, generator=g)
+    rid, rw = O.route_softmax_topk(logits.numpy(), 2)
+    ids = torch.from_numpy(rid.astype(np.int32)).cuda()
+    w = torch.from_numpy(rw.astype(np.float32)).cuda()
+    y = exl3.moe_forward_blobs(x.cuda(), ids, w, ptrs, I, K, E, out_dtype=torch.float32)
+
+    def lin(p):
+        return exl3.BC_LinearEXL3(p["trellis"].cuda(), p["suh"].cuda(), p["svh"].cuda(), K, None, False, True, None)
+
+    t_sep = exl3.ExpertTables([lin(ex[0]) for ex in experts], [lin(ex[1]) for ex in experts],
+                              [lin(ex[2]) for ex in experts])
+    assert torch.equal(y, exl3.moe_forward(x.cuda(), ids, w, t_sep))
+    orc = [tuple(O.Proj(p["suh"].numpy(), p["svh"].numpy(), trellis=p["trellis"].numpy(), K=K) for p in ex)
+           for ex in experts]
+    ref = O.moe_layer(x.numpy(), orc, rid, rw, O.ACT_SILU)
+    assert np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max() <= 2e-3
+    # the reference op returns x's dtype
+    y16 = exl3.moe_forward_blobs(x.cuda(), ids, w, ptrs, I, K, E)
+    assert y16.dtype == torch.float16 and np.abs(y16.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= 2e-3
