@@ -136,7 +136,9 @@ int exl3_linear_sharded(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, c
  * Without weights: C[j] = Y_j, C [slots, m, n] (fp16 or fp32, contiguous); skipped slots leave C[j] unchanged.
  * With weights (fp16 [slots], device): C[t] = sum over token t's slots j = t * (slots / num_tokens) + i in order of
  * weights[j] * Y_j (fp32 sum, one rounding for fp16 C; skipped slots add nothing), C [num_tokens, m, n]. Rows are
- * processed 8 at a time by the decode GEMV (the op serves decode batches). cb must be 2 (mul1).
+ * processed 8 at a time by the decode GEMV (the op serves decode batches). cb must be 2 (mul1). Differences from the
+ * reference op: for fp16 C it adds each slot's fp16 result with __hadd (ext-op-inventory.md:682), this sums in
+ * fp32 and rounds once (a few fp16 ulps apart at most); it returns the shape index it ran, this returns a status.
  * Replaces: exllamav3 ext exl3_mgemm(A, B, C, suh, A_had, svh, indices, weights, K, force_shape_idx, mcg, mul1,
  *           min_index, max_index, force_num_sms, num_tokens, ...) (ext-op-inventory.md:664-685, 1104-1119); the
  *           sliced mode (size_n_list, c_ptrs, n_stride_list, had_src_list) is not provided. */

@@ -37,6 +37,8 @@ def small(exl3, oracle):
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 9])
 def test_moe_small_silu(exl3, oracle, small, M):
+    """Decode batches (the one-launch fused layer at all of these sizes; the multi-kernel path is covered by
+    test_moe_fused_and_multi_kernel_paths), an expert shared by two tokens."""
     tables, orc = small
     ids, w = _ids_w(M, 4, 12, 600 + M, dup=True)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(M)).half()
@@ -371,10 +373,10 @@ def _skewed_ids(M, k, E, seed, hot=(0, 1, 2)):
     return ids, (w / w.sum(1, keepdim=True)).float()
 
 
-@pytest.mark.parametrize("M", [12, 80])
+@pytest.mark.parametrize("M", [24, 80])
 def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
-    """M > 8: experts with more than 8 rows go through the MFMA grouped GEMM (80 tokens: the hot experts cross the
-    64-row block boundary), the rest through the GEMV kernels, in one call."""
+    """More than 16 tokens: every expert's rows go through the MFMA grouped GEMM in blocks of up to 64 rows, hot and
+    cold experts in one call (80 tokens: the hot experts cross the 64-row block boundary)."""
     tables, orc = small
     ids, w = _skewed_ids(M, 4, 12, 1500 + M)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(16)).half()
