@@ -158,6 +158,18 @@ __device__ __forceinline__ void xcd_map(int nbc, int& blk, int& nb) {
 // ------------------------------------------------------------------------------------------------ pipelined K loop
 constexpr int kMfT = 4;                              // tile columns per wave
 
+// Workgroups per CU the uniform-K grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row groups)
+#ifndef EXL3_MFMA_OCC1
+#define EXL3_MFMA_OCC1 4
+#endif
+#ifndef EXL3_MFMA_OCC2
+#define EXL3_MFMA_OCC2 3
+#endif
+#ifndef EXL3_MFMA_OCC4
+#define EXL3_MFMA_OCC4 2
+#endif
+#define EXL3_MFMA_OCC(RGA) ((RGA) == 1 ? EXL3_MFMA_OCC1 : (RGA) == 2 ? EXL3_MFMA_OCC2 : EXL3_MFMA_OCC4)
+
 // 16-byte unit of (row, chunk) in one staged A plane (16 * RGA rows x four 16-byte chunks = 32 k); the chunk is
 // swizzled by row so that the 16 rows of a fragment read hit distinct banks.
 __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
@@ -404,7 +416,7 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
 // One instance per row class (RGA row groups of 16): workgroup (list index, column block); indices past the class's
 // block count exit at once.
 template <int K, int RGA>
-__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_mfma_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void gateup_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * 2 * RGA * 64];        // [2 stages][2 planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
@@ -522,7 +534,7 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 }
 
 template <int K, int RGA>
-__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mfma_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void down_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * RGA * 64];            // [2 stages][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
@@ -599,7 +611,7 @@ struct MfmaPipeMix {
     const uint32_t* words[2];                                // per column pair: the projection's words
     const uint8_t* kmap[2];
     const int32_t* woff[2];
-    int col[2];                                              // per column pair: its first tile column
+    int col[2];                                              // per column pair: its first tile column (even)
     int tn, nsteps;
     uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
     uint32_t t0p1;                                           // t0 + 1 of the lane's k-permuted positions
@@ -616,6 +628,21 @@ struct MfmaPipeMix {
         const int sl = lane >> 3, t = sl >> 1, hr = sl & 1;
         const int ss = s < nsteps ? s : nsteps - 1;
         return (2 * ss + hr) * tn + ((t >> 1) ? col[1] : col[0]) + (t & 1);
+    }
+    // Scalar loads of the 8 tile bitrates of step s (kmap bytes, 4-byte aligned base): for tile-row half sr and
+    // column pair pr the dword holding the pair's two adjacent bytes (the column is even and tn a multiple of 8, so
+    // both sit in one dword) -> KS[2 sr + pr]
+    __device__ __forceinline__ void load_ks(uint32_t (&KS)[4], int s) const {
+        const int ss = s < nsteps ? s : nsteps - 1;
+#pragma unroll
+        for (int sr = 0; sr < 2; ++sr)
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                const int idx = __builtin_amdgcn_readfirstlane((2 * ss + sr) * tn + col[pr]);
+                const auto* p = reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(
+                    reinterpret_cast<uintptr_t>(kmap[pr]) + (uint32_t)(idx & ~3));
+                KS[2 * sr + pr] = *p >> (8 * (idx & 3));     // byte of tile col[pr] at bits 0-7, col[pr] + 1 at 8-15
+            }
     }
     __device__ __forceinline__ void load_meta(int (&M)[2], int s) const {
         const int pr = (lane >> 4) >> 1, tile = tile_of(s);
@@ -659,16 +686,17 @@ struct MfmaPipeMix {
                 af[p][rg] = __builtin_bit_cast(h4_t, v);
             }
     }
-    // Kk: the lane's loaded (K, woff) of this step; the K of slot sl is that of lane 8 sl
-    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], int Kk) const {
+    // KS: the step's tile bitrates from load_ks; slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1)
+    // of tile-row half sr
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], const uint32_t (&KS)[4]) const {
         int ks[8];
-        int kmax = 0;
 #pragma unroll
         for (int sl = 0; sl < 8; ++sl) {
-            ks[sl] = __builtin_amdgcn_readlane(Kk, 8 * sl);
-            kmax = ks[sl] > kmax ? ks[sl] : kmax;
+            const int t = sl >> 1, sr = sl & 1;
+            ks[sl] = (int)((KS[2 * sr + (t >> 1)] >> (8 * (t & 1))) & 0xFFu);
         }
-        if (kmax <= 2) {
+        // every K of the step in {1, 2} (K >= 1 always): no bit above bit 1 in the two bytes of any KS word
+        if ((((KS[0] | KS[1] | KS[2] | KS[3]) & 0xFCFCu)) == 0) {
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
                 h4_t af[NP][RGA];
@@ -713,22 +741,26 @@ struct MfmaPipeMix {
     }
     // step s, R = s mod 4
     template <int R>
-    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
-                                         f4_t (&acc)[kMfT][RGA]) const {
+    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], uint32_t (&KS)[4][4],
+                                         u32x4_t (&RA)[4][CPT], f4_t (&acc)[kMfT][RGA]) const {
         load_a(RA[R], s + 4);
         load_meta(M[(R + DW) % 4], s + DW);
+        load_ks(KS[(R + 2) % 4], s + 2);
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
         stage_w(W[R], M[R]);
-        compute(R % 2, acc, M[R][0]);
+        compute(R % 2, acc, KS[R]);
         store_a(RA[(R + 1) % 4], (R + 1) % 2);
         __syncthreads();
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         u32x4_t W[4][2];
         int M[4][2];
+        uint32_t KS[4][4];
         u32x4_t RA[4][CPT];
 #pragma unroll
         for (int i = 0; i < DW; ++i) load_meta(M[i], i);
+        load_ks(KS[0], 0);
+        load_ks(KS[1], 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             load_a(RA[i], i);
@@ -737,10 +769,10 @@ struct MfmaPipeMix {
         store_a(RA[0], 0);
         __syncthreads();
         for (int s = 0; s < nsteps; s += 4) {
-            step<0>(s, W, M, RA, acc);
-            step<1>(s + 1, W, M, RA, acc);
-            step<2>(s + 2, W, M, RA, acc);
-            step<3>(s + 3, W, M, RA, acc);
+            step<0>(s, W, M, KS, RA, acc);
+            step<1>(s + 1, W, M, KS, RA, acc);
+            step<2>(s + 2, W, M, KS, RA, acc);
+            step<3>(s + 3, W, M, KS, RA, acc);
         }
     }
     template <typename F>

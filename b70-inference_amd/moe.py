@@ -46,6 +46,8 @@ class MixedEXL3:
             raise Exl3Error("MixedEXL3: woff must be the running sum of 8 * kmap starting at 0")
         if words.numel() * words.element_size() < 4 * int(wo[-1]) or words.data_ptr() % 16:
             raise Exl3Error("MixedEXL3: words must hold woff[-1] uint32 words and be 16-byte aligned")
+        if kmap.data_ptr() % 4 or not kmap.is_contiguous():
+            raise Exl3Error("MixedEXL3: kmap must be contiguous and 4-byte aligned (the kernels read it by dwords)")
         self.K = 0
         self.trellis = words
 
