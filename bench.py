@@ -23,6 +23,7 @@ launch duration, HIP events on the launch stream); and the CPU baseline (the ora
 from __future__ import annotations
 
 import argparse
+import glob
 import importlib
 import json
 import math
@@ -197,6 +198,9 @@ class Dense:
     def kernel_work(self, name, j):
         return (self.bytes_per_step(j), self.flops_per_step(j)) if name == "gemv" else None
 
+    def kernel_weights(self, name, j):
+        return self.k * self.n if name == "gemv" else None
+
     def cpu(self, O, np):
         lin = self.lins[0]
         tr, su, sv = lin.trellis.cpu().numpy(), lin.suh.cpu().numpy(), lin.svh.cpu().numpy()
@@ -233,6 +237,9 @@ class Mlp:
 
     def kernel_work(self, name, j):
         return (self.bytes_per_step(j), self.flops_per_step(j)) if name == "moe_fused" else None
+
+    def kernel_weights(self, name, j):
+        return 3 * self.H * self.I if name == "moe_fused" else None
 
     def cpu(self, O, np):
         m = self.mlps[0]
@@ -322,6 +329,18 @@ class MoE:
                 return b, f
         return None
 
+    def kernel_weights(self, name, j):
+        """Weights one launch of kernel `name` decodes in step j (a row block decodes its expert's projection once),
+        or None when not modelled."""
+        rpe = self.rows_per_expert(j)
+        if name == "moe_fused":
+            return 3 * len(rpe) * self.H * self.I
+        for per, tag in ((2, "gateup"), (1, "down")):
+            if name.startswith(f"moe_{tag}_mfma_r"):
+                cl = {"1": 0, "2": 1, "4": 2}[name[-1]]
+                return per * self.H * self.I * sum(1 for r in rpe.values() for k, _ in mfma_blocks(r) if k == cl)
+        return None
+
     def cpu(self, O, np, rows=None):
         """The oracle on rows `rows` of routing 0 (default: all), layer copy 0."""
         import numpy as np_
@@ -393,6 +412,14 @@ def measure(name, wl, steps, cpu=True):
                      "bytes_per_launch": int(kb), "flop_per_launch": int(kf),
                      "hbm_frac": round(kb / k_us / 1e3 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(kf / k_us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)})
+        roof["traffic"] = recorded_traffic(dom, name)
+        dw = [wl.kernel_weights(dom, j) for j in range(nprof)]
+        vpw = recorded_valu(dom, name)
+        if vpw is not None and all(w is not None for w in dw):
+            wps = sum(dw) / nprof / per_launch / (k_us * 1e-6)
+            roof["decode_alu"] = {"valu_lane_ops_per_weight": vpw, "weights_per_s": float(f"{wps:.4g}"),
+                                  "achieved": float(f"{wps * vpw:.4g}"), "peak": VALU_PEAK_LANE_OPS,
+                                  "unit": "VALU lane-ops/s", "frac": round(wps * vpw / VALU_PEAK_LANE_OPS, 4)}
         r["roofline"] = roof
     log(name, {k: v for k, v in r.items() if k != "kernels"})
     log(name, "kernels", r["kernels"])
@@ -415,18 +442,28 @@ def zipf_bias(E, s, seed):
     return (-s * torch.log(rank + 1)).cuda()
 
 
-def recorded_traffic(kname, workload):
-    """HBM bytes per launch of a kernel from its committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE per
-    dispatch, each scaled by what the counter reads for a plain copy of known size); None without one."""
-    path = os.path.join(ROOT, "profiles", f"{kname}_{workload}_hbm_traffic.md")
-    try:
+def recorded_figure(kind, key, kname, workload):
+    """A per-kernel figure `key[kname]: value` from the committed rocprofv3 summaries of a workload
+    (profiles/*_<workload>_<kind>.md); None without one."""
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"*_{workload}_{kind}.md"))):
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(float(line.split(":", 1)[1]))
-    except OSError:
-        pass
+                if line.startswith(f"{key}[{kname}]:"):
+                    return float(line.split(":", 1)[1].split()[0])
     return None
+
+
+def recorded_valu(kname, workload):
+    """VALU lane-operations per decoded weight of a kernel (64 x SQ_INSTS_VALU over the weights its launches decode)
+    from its committed counter summary; None without one."""
+    return recorded_figure("counters", "valu_lane_ops_per_weight", kname, workload)
+
+
+def recorded_traffic(kname, workload):
+    """HBM bytes per launch of a kernel from its committed counter summary (FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by what the counter reads for a plain copy of known size); None without one."""
+    v = recorded_figure("hbm_traffic", "traffic_bytes_per_launch", kname, workload)
+    return None if v is None else int(v)
 
 
 # ------------------------------------------------------------------------------------------------ configs
@@ -491,7 +528,16 @@ def main():
         for j in range(args.steps):
             wl.step_fn(j)()
         torch.cuda.synchronize()
-        print(json.dumps({"only": args.only, "calls": args.steps}), flush=True)
+        names = ["gemv", "moe_fused"] + [f"moe_{t}_mfma_r{c}" for t in ("gateup", "down") for c in (1, 2, 4)]
+        dec, work = {}, {}
+        for n in names:
+            w = [wl.kernel_weights(n, j) for j in range(args.steps)]
+            if all(v is not None for v in w) and sum(w) > 0:
+                dec[n] = sum(w) / args.steps
+                kw = [wl.kernel_work(n, j) for j in range(args.steps)]
+                work[n] = [sum(b for b, _ in kw) / args.steps, sum(f for _, f in kw) / args.steps]
+        print(json.dumps({"only": args.only, "calls": args.steps, "decoded_weights_per_call": dec,
+                          "algorithmic_bytes_flop_per_call": work}), flush=True)
         return
     torch.manual_seed(0)
     K, W = args.steps, args.warmup
