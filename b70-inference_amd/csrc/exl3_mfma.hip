@@ -169,6 +169,10 @@ constexpr int kMfT = 4;                              // tile columns per wave
 #define EXL3_MFMA_OCC4 2
 #endif
 #define EXL3_MFMA_OCC(RGA) ((RGA) == 1 ? EXL3_MFMA_OCC1 : (RGA) == 2 ? EXL3_MFMA_OCC2 : EXL3_MFMA_OCC4)
+#ifndef EXL3_MIX_OCC1
+#define EXL3_MIX_OCC1 4
+#endif
+#define EXL3_MIX_OCC(RGA) ((RGA) == 1 ? EXL3_MIX_OCC1 : (RGA) == 2 ? 3 : 2)
 
 // 16-byte unit of (row, chunk) in one staged A plane (16 * RGA rows x four 16-byte chunks = 32 k); the chunk is
 // swizzled by row so that the 16 rows of a fragment read hit distinct banks.
@@ -561,15 +565,17 @@ __global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void down_mfma_kernel(MoeA
 // m = 4 (L >> 4) + i (the tile rows behind the k slots are permuted, see decode4p).
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 constexpr int kMixKMax = 8;
-constexpr int kMixTS = 8 * kMixKMax + 4;                    // LDS words per staged tile (w(-1), 8K words, w(0), pad)
+constexpr int kMixTS = 8 * kMixKMax + 4;                    // LDS words per staged tile: 3 pad, w(8K - 1), 64 words
 
 // k-permuted fragments. An MFMA sums over k, so B and A may list a tile-row's 16 k in any common order. In the order
 // used here lane L's four k slots are tile rows 2g, 2g + 1, 2g + 8, 2g + 9 (g = L >> 4) of column n = L & 15: the
 // positions t0 .. t0 + 3, t0 = 32 (n & 7) + 4 (n >> 3) + 8 g, four consecutive windows (row 8 ((t >> 1) & 1) +
 // 2 ((t >> 3) & 3) + (t & 1), column (t >> 5) + 8 ((t >> 2) & 1)). Their bits [(t0 + 1) K - 16, (t0 + 4) K) fit one
 // funnel-shifted word for K <= 5: window b sits at bit 16 - b K of it.
-// Staged slot: slot[0] = ring word 8K - 1, slot[1 + w] = ring word w. A funnel whose first bit is ring bit `start`
-// (>= -16) reads slot words (start + 31) >> 5 and the next one, shifted by 31 - ((start + 31) & 31).
+// Seen from 3 words into a staged slot (v = slot + 3): v[0] = ring word 8K - 1, v[1 + w] = ring word w. A funnel whose
+// first bit is ring bit `start` (>= -16) reads v[(start + 31) >> 5] and the next word, shifted by
+// 31 - ((start + 31) & 31). The windows of positions t <= 255 end inside the ring, so a funnel's second word may lie
+// past it (any value: none of its bits is used).
 __device__ __forceinline__ h4_t decode4p(uint32_t F, int K) {
     const uint32_t w0 = F >> 16;
     const uint32_t w1 = __builtin_amdgcn_ubfe(F, 16 - K, 16);
@@ -582,7 +588,7 @@ __device__ __forceinline__ h4_t decode4p(uint32_t F, int K) {
 }
 
 // Any K (1 .. 8): the funnel origin from the lane's t0 + 1 at run time, and a second funnel for windows 2 and 3.
-__device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_t t0p1) {
+__device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_t t0p1) {   // slot: v above
     const uint32_t ta = t0p1 * (uint32_t)K + 15u, tb = ta + 2u * (uint32_t)K;     // start + 31 of windows 0 and 2
     const uint32_t* pa = slot + (ta >> 5);
     const uint32_t* pb = slot + (tb >> 5);
@@ -596,12 +602,23 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 
 // One wave, kMfT tile columns (column pair t >> 1: gate|up projection, or down columns c0 + 2 (t >> 1)), RGA row
 // groups, 32 k per step = two tile-rows. Per step the wave's 8 tiles (slot 2t + tile-row half) are fetched by 8 lanes
-// each with two clamped 16-byte loads (any K <= 8, every address inside the tile), after their (kmap, woff) one step
-// earlier; staged in LDS like MfmaPipe, then decoded per tile-row with that tile's K (read from the loading lanes
-// with readlane: wave-uniform) into k-permuted fragments (decode4p): branch-free, the lane's funnel origins for K = 1
-// and K = 2 precomputed and selected per tile; a step holding a tile of K > 2 takes the run-time form. Rings of 4
-// (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4 steps ahead) make the loop a 4-step unroll;
-// the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A as in MfmaPipe.
+// each (lane i of a tile: words min(4i, 8K - 4) and min(32 + 4i, 8K - 4), two 16-byte loads, every address inside
+// the tile) after their (kmap, woff) one step earlier, and staged in a wave-private LDS slot per tile at lane-fixed
+// positions: ring word w at slot[4 + w] (lanes past the tile's end leave copies of its last words behind it), the
+// last word w(8K - 1) again at slot[3] (written by lane 7, whose second load always ends the tile), so that a funnel
+// starting before the ring reads it. The step's 8 bitrates come by scalar loads two steps ahead: a step whose tiles
+// are all K <= 2 stages compactly (slot stride kMixTSF, the first load only) and decodes with per-lane funnel origins
+// and shifts precomputed for K = 1 and 2 (one select each per tile); other steps stage at stride kMixTS and decode
+// with the tile's K at run time. Rings of 4 (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4
+// steps ahead) make the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple
+// of 4. A as in MfmaPipe.
+constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
+
+typedef __attribute__((address_space(3))) const uint32_t* lds_cu32_t;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 template <int NP, int RGA>
 struct MfmaPipeMix {
     static constexpr int DW = 3;
@@ -614,21 +631,18 @@ struct MfmaPipeMix {
     int col[2];                                              // per column pair: its first tile column (even)
     int tn, nsteps;
     uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
+    const uint8_t* kp;                                       // this lane's tile entries at step 0 (its slot's tile)
+    const int32_t* wp;
+    const uint32_t* wb;                                      // its column pair's words
     uint32_t t0p1;                                           // t0 + 1 of the lane's k-permuted positions
-    int org1, dorg;                                          // the lane's funnel word in slot 0 at K = 1, and the
-    int sh1, dsh;                                            // step to K = 2; the funnel shifts likewise (origin and
-                                                             // shift at K in {1, 2}: x1 + (K - 1) dx, one mad each)
+    uint32_t fa1, fa2;                                       // fast path: LDS byte address of the lane's funnel
+    uint32_t sh1, sh2;                                       // word in compact slot 0 at K = 1 and 2, and the
+                                                             // funnel shifts
     const _Float16* asrc[CPT];
     int adst[CPT];
     u32x4_t* lds;
     int lane;
 
-    // this lane's tile of step s: slot lane >> 3 = 2 t + hr, tile (2 s + hr, column of t)
-    __device__ __forceinline__ int tile_of(int s) const {
-        const int sl = lane >> 3, t = sl >> 1, hr = sl & 1;
-        const int ss = s < nsteps ? s : nsteps - 1;
-        return (2 * ss + hr) * tn + ((t >> 1) ? col[1] : col[0]) + (t & 1);
-    }
     // Scalar loads of the 8 tile bitrates of step s (kmap bytes, 4-byte aligned base): for tile-row half sr and
     // column pair pr the dword holding the pair's two adjacent bytes (the column is even and tn a multiple of 8, so
     // both sit in one dword) -> KS[2 sr + pr]
@@ -644,31 +658,35 @@ struct MfmaPipeMix {
                 KS[2 * sr + pr] = *p >> (8 * (idx & 3));     // byte of tile col[pr] at bits 0-7, col[pr] + 1 at 8-15
             }
     }
+    // every K of the step in {1, 2}: K - 1 (no borrow: K >= 1) has no bit above bit 0 in the two bytes of each word
+    __device__ __forceinline__ static bool fast_step(const uint32_t (&KS)[4]) {
+        return (((KS[0] - 0x101u) | (KS[1] - 0x101u) | (KS[2] - 0x101u) | (KS[3] - 0x101u)) & 0xFEFEu) == 0;
+    }
     __device__ __forceinline__ void load_meta(int (&M)[2], int s) const {
-        const int pr = (lane >> 4) >> 1, tile = tile_of(s);
-        M[0] = ldg((pr ? kmap[1] : kmap[0]) + tile);
-        M[1] = ldg((pr ? woff[1] : woff[0]) + tile);
+        const int off = (s < nsteps ? s : nsteps - 1) * 2 * tn;
+        M[0] = ldg(kp + off);
+        M[1] = ldg(wp + off);
         __builtin_amdgcn_sched_barrier(0);
     }
     __device__ __forceinline__ void load_w(u32x4_t (&D)[2], const int (&M)[2]) const {
-        const int pr = (lane >> 4) >> 1, i = lane & 7, last = 8 * M[0] - 4;
-        const uint32_t* t = (pr ? words[1] : words[0]) + M[1];
-        const int a0 = 4 * i < last ? 4 * i : last, a1 = 32 + 4 * i < last ? 32 + 4 * i : last;
-        D[0] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (a0 > 0 ? a0 : 0)));
-        D[1] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (a1 > 0 ? a1 : 0)));
+        const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 4u * (uint32_t)(lane & 7);
+        const uint32_t* t = wb + M[1];
+        D[0] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (i4 < e ? i4 : e)));
+        D[1] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (i4 + 32u < e ? i4 + 32u : e)));
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ void stage_w(const u32x4_t (&D)[2], const int (&M)[2]) const {
-        const int sl = lane >> 3, i = lane & 7, K = M[0], last = 8 * K - 4;
-        uint32_t* t = wl + sl * kMixTS;
-        const int a0 = 4 * i < last ? 4 * i : last, a1 = 32 + 4 * i < last ? 32 + 4 * i : last;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            t[1 + a0 + j] = D[0][j];
-            t[1 + a1 + j] = D[1][j];
+    __device__ __forceinline__ void stage_w(const u32x4_t (&D)[2], bool fast) const {
+        const int sl = lane >> 3, i = lane & 7;
+        if (fast) {
+            uint32_t* t = wl + sl * kMixTSF;
+            if (i < 4) *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D[0];
+            if (i == 7) t[3] = D[1][3];
+        } else {
+            uint32_t* t = wl + sl * kMixTS;
+            *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D[0];
+            *reinterpret_cast<u32x4_t*>(t + 36 + 4 * i) = D[1];
+            if (i == 7) t[3] = D[1][3];
         }
-        if (a1 + 4 == 8 * K) t[0] = D[1][3];                 // w(8K - 1) in front (a1 = 8K - 4 for K <= 4)
-        if (i == 0) t[8 * K + 1] = D[0][0];                  // w(0) behind
     }
     // A fragments of tile-row half sr in the k-permuted order: k 2g, 2g + 1 from chunk 2 sr, 2g + 8, 2g + 9 from
     // chunk 2 sr + 1 (4 bytes at 4g in each unit)
@@ -688,25 +706,31 @@ struct MfmaPipeMix {
     }
     // KS: the step's tile bitrates from load_ks; slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1)
     // of tile-row half sr
-    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], const uint32_t (&KS)[4]) const {
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], const uint32_t (&KS)[4],
+                                            bool fast) const {
         int ks[8];
 #pragma unroll
         for (int sl = 0; sl < 8; ++sl) {
             const int t = sl >> 1, sr = sl & 1;
             ks[sl] = (int)((KS[2 * sr + (t >> 1)] >> (8 * (t & 1))) & 0xFFu);
         }
-        // every K of the step in {1, 2} (K >= 1 always): no bit above bit 1 in the two bytes of any KS word
-        if ((((KS[0] | KS[1] | KS[2] | KS[3]) & 0xFCFCu)) == 0) {
+        if (fast) {
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
                 h4_t af[NP][RGA];
                 load_af(stage, sr, af);
+                uint32_t wlo[kMfT], whi[kMfT];                   // the tiles' funnel words, all reads issued first
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const uint32_t* o = wl + (org1 + (ks[sl] - 1) * dorg);
-                    const uint32_t F = __builtin_amdgcn_alignbit(o[sl * kMixTS], o[sl * kMixTS + 1],
-                                                                 (uint32_t)(sh1 + (ks[sl] - 1) * dsh));
+                    const lds_cu32_t o = (lds_cu32_t)(ks[sl] == 2 ? fa2 : fa1);   // wave-uniform select
+                    whi[t] = o[sl * kMixTSF];
+                    wlo[t] = o[sl * kMixTSF + 1];
+                }
+#pragma unroll
+                for (int t = 0; t < kMfT; ++t) {
+                    const int sl = 2 * t + sr;
+                    const uint32_t F = __builtin_amdgcn_alignbit(whi[t], wlo[t], ks[sl] == 2 ? sh2 : sh1);
                     const h4_t bf = decode4p(F, ks[sl]);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
@@ -721,7 +745,7 @@ struct MfmaPipeMix {
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const h4_t bf = decode4p_rt(wl + sl * kMixTS, ks[sl], t0p1);
+                    const h4_t bf = decode4p_rt(wl + sl * kMixTS + 3, ks[sl], t0p1);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
                         acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
@@ -747,8 +771,9 @@ struct MfmaPipeMix {
         load_meta(M[(R + DW) % 4], s + DW);
         load_ks(KS[(R + 2) % 4], s + 2);
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
-        stage_w(W[R], M[R]);
-        compute(R % 2, acc, KS[R]);
+        const bool fast = fast_step(KS[R]);
+        stage_w(W[R], fast);
+        compute(R % 2, acc, KS[R], fast);
         store_a(RA[(R + 1) % 4], (R + 1) % 2);
         __syncthreads();
     }
@@ -775,6 +800,8 @@ struct MfmaPipeMix {
             step<3>(s + 3, W, M, KS, RA, acc);
         }
     }
+    // After words / kmap / woff / col / tn / wl / lane are set: the lane's tile entries and fast-path origins, and
+    // the A staging of `cnt` rows (rowptr(plane, row) -> that row's first element)
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
 #pragma unroll
@@ -784,13 +811,18 @@ struct MfmaPipeMix {
             asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
             adst[j] = p * RGA * 64 + a_unit(row, ch);
         }
+        const int sl = lane >> 3, t = sl >> 1, hr = sl & 1, pr = t >> 1;
+        const int tile = hr * tn + (pr ? col[1] : col[0]) + (t & 1);
+        kp = (pr ? kmap[1] : kmap[0]) + tile;
+        wp = (pr ? woff[1] : woff[0]) + tile;
+        wb = pr ? words[1] : words[0];
         const int n = lane & 15, g = lane >> 4;
         t0p1 = (uint32_t)(32 * (n & 7) + 4 * (n >> 3) + 8 * g + 1);
         const uint32_t ta1 = t0p1 + 15u, ta2 = 2u * t0p1 + 15u;           // start + 31 at K = 1, 2
-        org1 = (int)(ta1 >> 5);
-        dorg = (int)(ta2 >> 5) - org1;
-        sh1 = (int)(~ta1 & 31u);
-        dsh = (int)(~ta2 & 31u) - sh1;
+        fa1 = lds_addr(wl) + 4u * (3u + (ta1 >> 5));
+        fa2 = lds_addr(wl) + 4u * (3u + (ta2 >> 5));
+        sh1 = ~ta1 & 31u;
+        sh2 = ~ta2 & 31u;
     }
 };
 
@@ -853,10 +885,10 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
 }
 
 template <int RGA>
-__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_mix_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * 2 * RGA * 64];
-    __shared__ uint32_t wlds[4 * 8 * kMixTS];
+    __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
     const int nbI = a.I / 128;
@@ -875,10 +907,10 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void gateup_m
 }
 
 template <int RGA>
-__global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void down_mix_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[2 * RGA * 64];
-    __shared__ uint32_t wlds[4 * 8 * kMixTS];
+    __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
     __shared__ int s_comb[2 * 64];

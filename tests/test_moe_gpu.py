@@ -417,6 +417,16 @@ def test_moe_prefill_per_tile_k_all_bitrates(exl3, oracle):
         assert max_rel(y, ref) <= MAX_REL
 
 
+def test_moe_prefill_per_tile_k_1_2_3(exl3, oracle):
+    """Per-tile K in {1, 2, 3} on the MFMA path: most 8-tile steps hold only K <= 3 with some K = 3, which must take
+    the run-time decode (the fast path's funnel origins hold for K = 1 and 2 only)."""
+    tables, orc = make_experts(exl3, oracle, 6, 256, 256, 0, 0, 1760, per_tile=((1, 2, 3), (0.3, 0.4, 0.3)))
+    ids, w = _skewed_ids(60, 3, 6, 1761)
+    x = torch.randn(60, 256, generator=torch.Generator().manual_seed(1762)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
 def test_moe_prefill_deterministic_and_token_permutation(exl3, small):
     """Row results do not depend on which other rows share a block: permuting the tokens permutes the output rows
     bit for bit, and two calls agree exactly."""
