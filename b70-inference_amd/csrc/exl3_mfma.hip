@@ -9,8 +9,8 @@
 //               affine is applied as c1 * acc + c2 * rowsum(A) in the epilogue), then the fused activation / down-input
 //               epilogue (Hadamard * svh, act, * suh_d, Hadamard) per 16-row group
 //   down        workgroup per (block, 256-column block of H), full I, epilogue Hadamard * svh_d * w, then the combine
-// The A rows of the active row groups are staged through a two-stage LDS ring (loaded into registers two steps
-// ahead), weight words three steps ahead; one barrier per step. Workgroup ids are laid out so that the column blocks
+// The A rows of the active row groups are staged through a four-stage LDS ring (loaded into registers four steps
+// ahead, stored two steps ahead), weight words three steps ahead; one barrier every second step. Workgroup ids are laid out so that the column blocks
 // of one row block run on one XCD (shared L2 for its A rows).
 // Semantics: the reference's GateUpDpasKernel / DownDpasKernel / moe_prefill (glm/xpu/csrc/exl3_moe.n128.sycl:
 // 472-689, 868-916) and exllamav3's exl3_moe (ext-op-inventory.md:1060-1093).
@@ -187,8 +187,9 @@ __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ 
 //            lane's fragment window (first word -1 .. 8K - 1, at most 8K + 2 past) is contiguous: no wrap logic, and
 //            per-lane scattered loads (64-bit addresses per lane into the texture unit) become LDS reads.
 //   A:       staged per step by the whole workgroup: loaded into register slot s % 4 four steps ahead, stored to LDS
-//            stage s % 2 one step ahead; memory-counter waits complete in issue order, so each step issues its A load
-//            before its weight load.
+//            stage s % 4 two steps ahead, with a barrier after the even steps only (a stage is rewritten two steps
+//            after its last read, with a barrier in between, and read at least one barrier after its write); memory-
+//            counter waits complete in issue order, so each step issues its A load before its weight load.
 template <int K, int NP, int RGA, int NPS = NP>
 struct MfmaPipe {
     static constexpr int NW = FragCfg<K>::NW;
@@ -254,12 +255,12 @@ struct MfmaPipe {
     template <int R>
     __device__ __forceinline__ void step(int s, uint32_t (&W)[DW][K], u32x4_t (&RA)[4][CPT],
                                          f4_t (&acc)[kMfT][RGA]) const {
-        load_a(RA[R], s + 4);                            // slot R held A(s), stored to LDS one step ago
+        load_a(RA[R], s + 4);                            // slot R held A(s), stored to LDS two steps ago
         load_w(W[(R + DW - 1) % DW], s + DW - 1);
         stage_w(W[R % DW]);
-        compute(R % 2, acc);
-        store_a(RA[(R + 1) % 4], (R + 1) % 2);
-        __syncthreads();
+        compute(R, acc);
+        store_a(RA[(R + 2) % 4], (R + 2) % 4);
+        if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
         const int ss = (s < nsteps ? s : nsteps - 1) * 32;
@@ -280,6 +281,7 @@ struct MfmaPipe {
             if (i < DW - 1) load_w(W[i], i);
         }
         store_a(RA[0], 0);
+        store_a(RA[1], 1);
         __syncthreads();
         int s = 0;
         for (; s + 4 <= nsteps; s += 4) {
@@ -422,7 +424,7 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void gateup_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[2 * 2 * RGA * 64];        // [2 stages][2 planes][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * 2 * RGA * 64];        // [4 stages][2 planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
@@ -540,7 +542,7 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void down_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[2 * RGA * 64];            // [2 stages][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * RGA * 64];            // [4 stages][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
@@ -773,9 +775,9 @@ struct MfmaPipeMix {
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
         const bool fast = fast_step(KS[R]);
         stage_w(W[R], fast);
-        compute(R % 2, acc, KS[R], fast);
-        store_a(RA[(R + 1) % 4], (R + 1) % 2);
-        __syncthreads();
+        compute(R, acc, KS[R], fast);
+        store_a(RA[(R + 2) % 4], (R + 2) % 4);
+        if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         u32x4_t W[4][2];
@@ -792,6 +794,7 @@ struct MfmaPipeMix {
             if (i < DW - 1) load_w(W[i], M[i]);
         }
         store_a(RA[0], 0);
+        store_a(RA[1], 1);
         __syncthreads();
         for (int s = 0; s < nsteps; s += 4) {
             step<0>(s, W, M, KS, RA, acc);
@@ -887,7 +890,7 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[2 * 2 * RGA * 64];
+    __shared__ u32x4_t stage[4 * 2 * RGA * 64];
     __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
@@ -909,7 +912,7 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[2 * RGA * 64];
+    __shared__ u32x4_t stage[4 * RGA * 64];
     __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
@@ -1003,7 +1006,7 @@ __device__ __forceinline__ void linear_store(const LinArgs& a, int row, int col,
 // are staged and waves 0, 1 (first half) read plane 0, waves 2, 3 plane 1.
 template <int K, int RGA, int NPS>
 __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_mfma_kernel(LinArgs a) {
-    __shared__ u32x4_t stage[2 * NPS * RGA * 64];      // [2 stages][planes][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * NPS * RGA * 64];      // [4 stages][planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
     __shared__ float rsum[NPS][16 * RGA];
