@@ -2,8 +2,9 @@
 //
 // A workgroup of 4 waves works on one 128-column strip of one projection over a k range made of whole Hadamard
 // blocks (128 k = 8 tile-rows). The transformed activations of that range sit in LDS; each wave streams every 4th
-// tile-row of the strip, decodes its 32 positions per lane in registers and accumulates sum_k a_k * h_k with
-// v_dot2_f32_f16 (h = 1024 + bytesum, the codebook affine is applied once per output: c1 * acc + c2 * sum_k a_k).
+// tile-row of the strip, decodes its 32 positions per lane in registers and accumulates sum_k a_k * h_k on the matrix
+// cores (4x4x4 MFMA blocks; h = 1024 + bytesum, the codebook affine is applied once per output: c1 * acc +
+// c2 * sum_k a_k).
 #pragma once
 
 #include "exl3_device.h"
@@ -23,15 +24,102 @@ constexpr int kLinearRing = EXL3_LINEAR_RING;   // register ring depth of the de
 // where `sp` points at tile-row 0 of the strip, tile-rows are `rs` words apart, and lane l owns columns
 // 16(l >> 3) + (l & 7) + 8h. Three register buffers in a ring: loads run two tile-rows ahead of the decode and every
 // buffer is consumed in place, so a decode only waits for its own load.
-template <int K, int M>
-__device__ __forceinline__ void strip_tile_row(const uint32_t (&D)[K], int lane, const _Float16* xr, int xs_ld,
-                                               float (&acc)[M][2]) {
+//
+// The products run on the matrix cores (EXL3_GEMV_MFMA, the default): v_mfma_f32_4x4x4_16b_f16 is 16 independent
+// 4x4x4 products, block b = lanes 4b .. 4b + 3, D[lane 4b + j][i] = sum_k A[lane 4b + i][k] B[lane 4b + j][k]. A lane
+// gives as A its own column's four decoded k of one row quad (two of its packed pairs: rows r, r + 1 and r + 2, r + 3
+// of one column half, the same rows in every lane) and as B token (lane & 3)'s activations at those rows, so
+// D[lane 4b + j][i] accumulates token j's product for lane 4b + i's column: eight 4x4x4 MFMAs per tile-row for up to
+// four tokens (sixteen for up to eight) instead of 16 v_dot2 per token, and the VALU keeps only the decode. The
+// accumulators are moved to the per-lane layout once, after the strip (quad broadcasts).
+#ifndef EXL3_GEMV_MFMA
+#define EXL3_GEMV_MFMA 1
+#endif
+#ifndef EXL3_GEMV_MFMA_MIN_ROWS
+#define EXL3_GEMV_MFMA_MIN_ROWS 2
+#endif
+// one-row GEMVs keep v_dot2 (16 per tile-row): there the MFMA form was 2-4 % slower (C1, one-token C2 and C3), from
+// two rows on it wins (two-row C2 -7 %, four-row -11 %)
+template <int M>
+constexpr bool gemv_mfma() { return EXL3_GEMV_MFMA && M >= EXL3_GEMV_MFMA_MIN_ROWS; }
+typedef _Float16 gh4_t __attribute__((ext_vector_type(4)));
+typedef float gf4_t __attribute__((ext_vector_type(4)));
+
+template <int M>
+struct GemvAcc {
+    static constexpr int NG = (M + 3) / 4;                // token groups of 4
+    gf4_t d[NG][2];                                       // [token group][column half]
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) d[g][0] = d[g][1] = gf4_t{0.f, 0.f, 0.f, 0.f};
+    }
+};
+
+// decoded pairs of one tile-row: w[j] = rows (pos_row(2j), pos_row(2j) + 1) of column half pos_half(2j)
+template <int K>
+__device__ __forceinline__ void strip_tile_decode(const uint32_t (&D)[K], int lane, h2_t (&w)[16]) {
     uint32_t R[K + 1];
 #pragma unroll
     for (int i = 0; i < K; ++i) R[1 + i] = D[i];
     chunk_prev<K>(lane, R);
-    h2_t w[16];
     decode_chunk_raw<K>(R, w);
+}
+
+// Row quad q (rows 4q .. 4q + 3) of column half h is pairs (kQuadPair[q] + 2h, kQuadPair[q] + 2h + 4).
+template <int M>
+__device__ __forceinline__ void tile_row_mfma(const h2_t (&w)[16], int lane, const _Float16* xr, int xs_ld,
+                                              GemvAcc<M>& acc) {
+    constexpr int NG = GemvAcc<M>::NG;
+    constexpr int kQuadPair[4] = {0, 8, 1, 9};
+    gh4_t b[NG][4];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int tok = min(4 * g + (lane & 3), M - 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[g][q] = *reinterpret_cast<const gh4_t*>(xr + tok * xs_ld + 4 * q);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j1 = kQuadPair[q] + 2 * h, j2 = j1 + 4;
+            const gh4_t a = {w[j1][0], w[j1][1], w[j2][0], w[j2][1]};
+#pragma unroll
+            for (int g = 0; g < NG; ++g) acc.d[g][h] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b[g][q], acc.d[g][h], 0, 0, 0);
+        }
+}
+
+// value of lane (lane & ~3) + q (DPP quad_perm [q, q, q, q]; q a compile-time constant after unrolling)
+__device__ __forceinline__ float quad_bcast(float v, int q) {
+    const int u = __builtin_bit_cast(int, v);
+    switch (q) {
+        case 0: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0x00, 0xF, 0xF, false));
+        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0x55, 0xF, 0xF, false));
+        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0xAA, 0xF, 0xF, false));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, u, 0xFF, 0xF, 0xF, false));
+    }
+}
+
+// out[m][h] += token m's sum for this lane's column: element (lane & 3) of lane (lane & ~3) + (m & 3) of d[m / 4][h]
+template <int M>
+__device__ __forceinline__ void gemv_acc_to_lanes(const GemvAcc<M>& acc, int lane, float (&out)[M][2]) {
+    const int e = lane & 3;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = quad_bcast(acc.d[m >> 2][h][i], m & 3);
+            out[m][h] += e == 0 ? v[0] : e == 1 ? v[1] : e == 2 ? v[2] : v[3];
+        }
+}
+
+template <int K, int M>
+__device__ __forceinline__ void strip_tile_row(const uint32_t (&D)[K], int lane, const _Float16* xr, int xs_ld,
+                                               float (&acc)[M][2]) {
+    h2_t w[16];
+    strip_tile_decode<K>(D, lane, w);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int r = pos_row(2 * j), h = pos_half(2 * j);
@@ -82,17 +170,30 @@ __device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, 
     const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
     const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
     const uint32_t rstep = (uint32_t)(rs * step);
+    GemvAcc<M> ma;
+    if constexpr (gemv_mfma<M>()) ma.zero();
+    auto tile_row = [&](int r, int i) {
+        const _Float16* xr = xs + (lt0 + i * step) * 16;
+        if constexpr (gemv_mfma<M>()) {
+            h2_t w[16];
+            strip_tile_decode<K>(ring.D[r], lane, w);
+            tile_row_mfma<M>(w, lane, xr, xs_ld, ma);
+        } else {
+            strip_tile_row<K, M>(ring.D[r], lane, xr, xs_ld, acc);
+        }
+    };
     int i = 0;
     for (; i + R <= n; i += R) {                         // branch-free body: loads stay R - 1 tile-rows ahead
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             strip_load<K>(ring.D[(r + R - 1) % R], base, rstep, i + r + R - 1, n);
-            strip_tile_row<K, M>(ring.D[r], lane, xs + (lt0 + (i + r) * step) * 16, xs_ld, acc);
+            tile_row(r, i + r);
         }
     }
 #pragma unroll
     for (int r = 0; r < R - 1; ++r)
-        if (i + r < n) strip_tile_row<K, M>(ring.D[r], lane, xs + (lt0 + (i + r) * step) * 16, xs_ld, acc);
+        if (i + r < n) tile_row(r, i + r);
+    if constexpr (gemv_mfma<M>()) gemv_acc_to_lanes<M>(ma, lane, acc);
 }
 
 template <int K, int M>
@@ -116,28 +217,55 @@ __device__ __forceinline__ void mixed_tile_row(const uint32_t* __restrict__ tw, 
     strip_tile_row<K, M>(D, lane, xr, xs_ld, acc);
 }
 
+template <int K>
+__device__ __forceinline__ void mixed_tile_decode(const uint32_t* __restrict__ tw, int lane, h2_t (&w)[16]) {
+    uint32_t D[K];
+    const uint32_t* q = tw + (lane & 7) * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) D[i] = ldg_nt(q + i);
+    strip_tile_decode<K>(D, lane, w);
+}
+
 template <int M>
 __device__ __forceinline__ void strip_gemv_mixed(const uint32_t* __restrict__ words, const uint8_t* __restrict__ kmap,
                                                  const int32_t* __restrict__ woff, int tn, int tile_n0, int tr0,
                                                  int lt0, int nt, int step, int lane, const _Float16* xs, int xs_ld,
                                                  float (&acc)[M][2]) {
+    GemvAcc<M> ma;
+    if constexpr (gemv_mfma<M>()) ma.zero();
     for (int lt = lt0; lt < nt; lt += step) {
         const int tile = (tr0 + lt) * tn + tile_n0 + (lane >> 3);
         const int Kt = ldg(kmap + tile);
         const uint32_t* tw = words + ldg(woff + tile);
         const _Float16* xr = xs + lt * 16;
-        switch (Kt) {
-            case 1: mixed_tile_row<1, M>(tw, lane, xr, xs_ld, acc); break;
-            case 2: mixed_tile_row<2, M>(tw, lane, xr, xs_ld, acc); break;
-            case 3: mixed_tile_row<3, M>(tw, lane, xr, xs_ld, acc); break;
-            case 4: mixed_tile_row<4, M>(tw, lane, xr, xs_ld, acc); break;
-            case 5: mixed_tile_row<5, M>(tw, lane, xr, xs_ld, acc); break;
-            case 6: mixed_tile_row<6, M>(tw, lane, xr, xs_ld, acc); break;
-            case 7: mixed_tile_row<7, M>(tw, lane, xr, xs_ld, acc); break;
-            case 8: mixed_tile_row<8, M>(tw, lane, xr, xs_ld, acc); break;
-            default: break;
+        if constexpr (gemv_mfma<M>()) {
+            h2_t w[16];                                  // decoded per lane (the 8 lanes of a tile share a case);
+            switch (Kt) {                                // the MFMAs run after the lanes reconverge
+                case 1: mixed_tile_decode<1>(tw, lane, w); break;
+                case 2: mixed_tile_decode<2>(tw, lane, w); break;
+                case 3: mixed_tile_decode<3>(tw, lane, w); break;
+                case 4: mixed_tile_decode<4>(tw, lane, w); break;
+                case 5: mixed_tile_decode<5>(tw, lane, w); break;
+                case 6: mixed_tile_decode<6>(tw, lane, w); break;
+                case 7: mixed_tile_decode<7>(tw, lane, w); break;
+                default: mixed_tile_decode<8>(tw, lane, w); break;
+            }
+            tile_row_mfma<M>(w, lane, xr, xs_ld, ma);
+        } else {
+            switch (Kt) {
+                case 1: mixed_tile_row<1, M>(tw, lane, xr, xs_ld, acc); break;
+                case 2: mixed_tile_row<2, M>(tw, lane, xr, xs_ld, acc); break;
+                case 3: mixed_tile_row<3, M>(tw, lane, xr, xs_ld, acc); break;
+                case 4: mixed_tile_row<4, M>(tw, lane, xr, xs_ld, acc); break;
+                case 5: mixed_tile_row<5, M>(tw, lane, xr, xs_ld, acc); break;
+                case 6: mixed_tile_row<6, M>(tw, lane, xr, xs_ld, acc); break;
+                case 7: mixed_tile_row<7, M>(tw, lane, xr, xs_ld, acc); break;
+                case 8: mixed_tile_row<8, M>(tw, lane, xr, xs_ld, acc); break;
+                default: break;
+            }
         }
     }
+    if constexpr (gemv_mfma<M>()) gemv_acc_to_lanes<M>(ma, lane, acc);
 }
 
 // ------------------------------------------------------------------------------------------------ split-K handoff
