@@ -1153,27 +1153,22 @@ static int fork3(hipStream_t st, F launch) {
     return EXL3_OK;
 }
 
-int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st) {
+// The grouped GEMM of one layer call: the input transform, then per row class gate|up followed by down on that class's
+// stream (a class's down blocks read only the down inputs its own gate|up blocks wrote; tokens whose slots span
+// classes are combined by the last slot to finish), so one class's down pass overlaps the others' gate|up.
+int launch_moe_mfma(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
     EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
-    const dim3 grid(nxb * (a.I / 128));
+    const dim3 grid_gu(nxb * (a.I / 128)), grid_dn(nxb * ((a.H / 128 + 1) / 2));
     return fork3(st, [&](int rga, hipStream_t s) -> int {
-        mfma_fn fn = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)
+        mfma_fn gu = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)
                                : (rga == 4 ? pick_gu<4>(a.Kg) : rga == 2 ? pick_gu<2>(a.Kg) : pick_gu<1>(a.Kg));
-        const char* nm = rga == 4 ? "moe_gateup_mfma_r4" : rga == 2 ? "moe_gateup_mfma_r2" : "moe_gateup_mfma_r1";
-        EXL3_LAUNCH(nm, fn, grid, dim3(256), 0, s, a);
-        return EXL3_OK;
-    });
-}
-
-int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st) {
-    const int nxb = (a.max_blocks + 7) / 8 * 8;
-    const dim3 grid(nxb * ((a.H / 128 + 1) / 2));
-    return fork3(st, [&](int rga, hipStream_t s) -> int {
-        mfma_fn fn = a.Kd == 0 ? (rga == 4 ? down_mix_kernel<4> : rga == 2 ? down_mix_kernel<2> : down_mix_kernel<1>)
+        mfma_fn dn = a.Kd == 0 ? (rga == 4 ? down_mix_kernel<4> : rga == 2 ? down_mix_kernel<2> : down_mix_kernel<1>)
                                : (rga == 4 ? pick_dn<4>(a.Kd) : rga == 2 ? pick_dn<2>(a.Kd) : pick_dn<1>(a.Kd));
-        const char* nm = rga == 4 ? "moe_down_mfma_r4" : rga == 2 ? "moe_down_mfma_r2" : "moe_down_mfma_r1";
-        EXL3_LAUNCH(nm, fn, grid, dim3(256), 0, s, a);
+        EXL3_LAUNCH(rga == 4 ? "moe_gateup_mfma_r4" : rga == 2 ? "moe_gateup_mfma_r2" : "moe_gateup_mfma_r1", gu,
+                    grid_gu, dim3(256), 0, s, a);
+        EXL3_LAUNCH(rga == 4 ? "moe_down_mfma_r4" : rga == 2 ? "moe_down_mfma_r2" : "moe_down_mfma_r1", dn, grid_dn,
+                    dim3(256), 0, s, a);
         return EXL3_OK;
     });
 }

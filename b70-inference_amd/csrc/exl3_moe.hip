@@ -879,8 +879,7 @@ static moe_fn down_select(int K, int MR) {
     }
 }
 
-int launch_moe_mfma_gateup(const MoeArgs& a, hipStream_t st);   // exl3_mfma.hip
-int launch_moe_mfma_down(const MoeArgs& a, hipStream_t st);
+int launch_moe_mfma(const MoeArgs& a, hipStream_t st);          // exl3_mfma.hip
 bool moe_fused_ok(const MoeArgs& a);                            // exl3_moe_fused.hip
 int moe_fused_path(const MoeArgs& a, hipStream_t st);
 
@@ -965,10 +964,9 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.H = a.H;
     rc = launch_align(r, st);
     if (rc) return rc;
-    if (use_mfma && (rc = launch_moe_mfma_gateup(a, st))) return rc;
+    if (use_mfma && (rc = launch_moe_mfma(a, st))) return rc;
     if (max_items > 0)
         EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
-    if (use_mfma && (rc = launch_moe_mfma_down(a, st))) return rc;
     if (max_items > 0)
         EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
     return EXL3_OK;
