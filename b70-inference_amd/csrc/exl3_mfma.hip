@@ -589,6 +589,18 @@ __device__ __forceinline__ h4_t decode4p(uint32_t F, int K) {
     return __builtin_bit_cast(h4_t, v);
 }
 
+// K = 2 (k2) or 1: decode4p with the window offsets as constants picked by a wave-uniform flag.
+__device__ __forceinline__ h4_t decode4p12(uint32_t F, bool k2) {
+    const uint32_t w0 = F >> 16;
+    const uint32_t w1 = __builtin_amdgcn_ubfe(F, k2 ? 14 : 15, 16);
+    const uint32_t w2 = __builtin_amdgcn_ubfe(F, k2 ? 12 : 14, 16);
+    const uint32_t w3 = __builtin_amdgcn_ubfe(F, k2 ? 10 : 13, 16);
+    typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+    const u2_t v = {__builtin_bit_cast(uint32_t, mul1_pair_raw(w0, w1)),
+                    __builtin_bit_cast(uint32_t, mul1_pair_raw(w2, w3))};
+    return __builtin_bit_cast(h4_t, v);
+}
+
 // Any K (1 .. 8): the funnel origin from the lane's t0 + 1 at run time, and a second funnel for windows 2 and 3.
 __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_t t0p1) {   // slot: v above
     const uint32_t ta = t0p1 * (uint32_t)K + 15u, tb = ta + 2u * (uint32_t)K;     // start + 31 of windows 0 and 2
@@ -608,8 +620,8 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 // the tile) after their (kmap, woff) one step earlier, and staged in a wave-private LDS slot per tile at lane-fixed
 // positions: ring word w at slot[4 + w] (lanes past the tile's end leave copies of its last words behind it), the
 // last word w(8K - 1) again at slot[3] (written by lane 7, whose second load always ends the tile), so that a funnel
-// starting before the ring reads it. The step's 8 bitrates come by scalar loads two steps ahead: a step whose tiles
-// are all K <= 2 stages compactly (slot stride kMixTSF, the first load only) and decodes with per-lane funnel origins
+// starting before the ring reads it. The step's 8 bitrates come from its lanes' kmap bytes (wave ballots): a step
+// whose tiles are all K <= 2 stages compactly (slot stride kMixTSF, the first load only) and decodes with per-lane funnel origins
 // and shifts precomputed for K = 1 and 2 (one select each per tile); other steps stage at stride kMixTS and decode
 // with the tile's K at run time. Rings of 4 (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4
 // steps ahead) make the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple
@@ -645,25 +657,10 @@ struct MfmaPipeMix {
     u32x4_t* lds;
     int lane;
 
-    // Scalar loads of the 8 tile bitrates of step s (kmap bytes, 4-byte aligned base): for tile-row half sr and
-    // column pair pr the dword holding the pair's two adjacent bytes (the column is even and tn a multiple of 8, so
-    // both sit in one dword) -> KS[2 sr + pr]
-    __device__ __forceinline__ void load_ks(uint32_t (&KS)[4], int s) const {
-        const int ss = s < nsteps ? s : nsteps - 1;
-#pragma unroll
-        for (int sr = 0; sr < 2; ++sr)
-#pragma unroll
-            for (int pr = 0; pr < 2; ++pr) {
-                const int idx = __builtin_amdgcn_readfirstlane((2 * ss + sr) * tn + col[pr]);
-                const auto* p = reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(
-                    reinterpret_cast<uintptr_t>(kmap[pr]) + (uint32_t)(idx & ~3));
-                KS[2 * sr + pr] = *p >> (8 * (idx & 3));     // byte of tile col[pr] at bits 0-7, col[pr] + 1 at 8-15
-            }
-    }
-    // every K of the step in {1, 2}: K - 1 (no borrow: K >= 1) has no bit above bit 0 in the two bytes of each word
-    __device__ __forceinline__ static bool fast_step(const uint32_t (&KS)[4]) {
-        return (((KS[0] - 0x101u) | (KS[1] - 0x101u) | (KS[2] - 0x101u) | (KS[3] - 0x101u)) & 0xFEFEu) == 0;
-    }
+    // The step's tile bitrates come from the kmap bytes its lanes loaded (lane 8 sl + i holds slot sl's K), as two
+    // wave ballots: `big` (some K > 2: the run-time decode, which reads each K with v_readlane) and `two` (bit 8 sl:
+    // slot sl has K = 2, else 1 on the fast path). Scalar loads of the kmap are avoided on purpose: they share the
+    // LDS wait counter and may return out of order, so every LDS wait after one would wait for it too.
     __device__ __forceinline__ void load_meta(int (&M)[2], int s) const {
         const int off = (s < nsteps ? s : nsteps - 1) * 2 * tn;
         M[0] = ldg(kp + off);
@@ -706,16 +703,8 @@ struct MfmaPipeMix {
                 af[p][rg] = __builtin_bit_cast(h4_t, v);
             }
     }
-    // KS: the step's tile bitrates from load_ks; slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1)
-    // of tile-row half sr
-    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], const uint32_t (&KS)[4],
-                                            bool fast) const {
-        int ks[8];
-#pragma unroll
-        for (int sl = 0; sl < 8; ++sl) {
-            const int t = sl >> 1, sr = sl & 1;
-            ks[sl] = (int)((KS[2 * sr + (t >> 1)] >> (8 * (t & 1))) & 0xFFu);
-        }
+    // slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1) of tile-row half sr; m0 = this lane's K
+    __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], int m0, uint64_t two, bool fast) const {
         if (fast) {
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
@@ -725,15 +714,17 @@ struct MfmaPipeMix {
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const lds_cu32_t o = (lds_cu32_t)(ks[sl] == 2 ? fa2 : fa1);   // wave-uniform select
+                    const bool k2 = (two >> (8 * sl)) & 1;       // wave-uniform select
+                    const lds_cu32_t o = (lds_cu32_t)(k2 ? fa2 : fa1);
                     whi[t] = o[sl * kMixTSF];
                     wlo[t] = o[sl * kMixTSF + 1];
                 }
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const uint32_t F = __builtin_amdgcn_alignbit(whi[t], wlo[t], ks[sl] == 2 ? sh2 : sh1);
-                    const h4_t bf = decode4p(F, ks[sl]);
+                    const bool k2 = (two >> (8 * sl)) & 1;
+                    const uint32_t F = __builtin_amdgcn_alignbit(whi[t], wlo[t], k2 ? sh2 : sh1);
+                    const h4_t bf = decode4p12(F, k2);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
                         acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
@@ -747,7 +738,7 @@ struct MfmaPipeMix {
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
                     const int sl = 2 * t + sr;
-                    const h4_t bf = decode4p_rt(wl + sl * kMixTS + 3, ks[sl], t0p1);
+                    const h4_t bf = decode4p_rt(wl + sl * kMixTS + 3, __builtin_amdgcn_readlane(m0, 8 * sl), t0p1);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
                         acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
@@ -767,27 +758,25 @@ struct MfmaPipeMix {
     }
     // step s, R = s mod 4
     template <int R>
-    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], uint32_t (&KS)[4][4],
-                                         u32x4_t (&RA)[4][CPT], f4_t (&acc)[kMfT][RGA]) const {
+    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
+                                         f4_t (&acc)[kMfT][RGA]) const {
         load_a(RA[R], s + 4);
         load_meta(M[(R + DW) % 4], s + DW);
-        load_ks(KS[(R + 2) % 4], s + 2);
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
-        const bool fast = fast_step(KS[R]);
+        const int m0 = M[R][0];
+        const uint64_t two = __builtin_amdgcn_ballot_w64(m0 == 2);
+        const bool fast = __builtin_amdgcn_ballot_w64(m0 > 2) == 0;
         stage_w(W[R], fast);
-        compute(R, acc, KS[R], fast);
+        compute(R, acc, m0, two, fast);
         store_a(RA[(R + 2) % 4], (R + 2) % 4);
         if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         u32x4_t W[4][2];
         int M[4][2];
-        uint32_t KS[4][4];
         u32x4_t RA[4][CPT];
 #pragma unroll
         for (int i = 0; i < DW; ++i) load_meta(M[i], i);
-        load_ks(KS[0], 0);
-        load_ks(KS[1], 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             load_a(RA[i], i);
@@ -797,10 +786,10 @@ struct MfmaPipeMix {
         store_a(RA[1], 1);
         __syncthreads();
         for (int s = 0; s < nsteps; s += 4) {
-            step<0>(s, W, M, KS, RA, acc);
-            step<1>(s + 1, W, M, KS, RA, acc);
-            step<2>(s + 2, W, M, KS, RA, acc);
-            step<3>(s + 3, W, M, KS, RA, acc);
+            step<0>(s, W, M, RA, acc);
+            step<1>(s + 1, W, M, RA, acc);
+            step<2>(s + 2, W, M, RA, acc);
+            step<3>(s + 3, W, M, RA, acc);
         }
     }
     // After words / kmap / woff / col / tn / wl / lane are set: the lane's tile entries and fast-path origins, and
