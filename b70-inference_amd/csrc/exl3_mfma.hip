@@ -616,14 +616,14 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 
 // One wave, kMfT tile columns (column pair t >> 1: gate|up projection, or down columns c0 + 2 (t >> 1)), RGA row
 // groups, 32 k per step = two tile-rows. Per step the wave's 8 tiles (slot 2t + tile-row half) are fetched by 8 lanes
-// each (lane i of a tile: words min(4i, 8K - 4) and min(32 + 4i, 8K - 4), two 16-byte loads, every address inside
-// the tile) after their (kmap, woff) one step earlier, and staged in a wave-private LDS slot per tile at lane-fixed
-// positions: ring word w at slot[4 + w] (lanes past the tile's end leave copies of its last words behind it), the
-// last word w(8K - 1) again at slot[3] (written by lane 7, whose second load always ends the tile), so that a funnel
-// starting before the ring reads it. The step's 8 bitrates come from its lanes' kmap bytes (wave ballots): a step
+// each (lane i of a tile: words min(4i, 8K - 4) .. + 3, a 16-byte load inside the tile, and for K >= 5 words
+// min(32 + 4i, 8K - 4) .. + 3 at staging time) after their (kmap, woff) one step earlier, and staged in a wave-private
+// LDS slot per tile at lane-fixed positions: ring word w at slot[4 + w] (lanes past the tile's end leave copies of its
+// last words behind it), the last word w(8K - 1) again at slot[3] (written by lane 7, whose last load always ends the
+// tile), so that a funnel starting before the ring reads it. The step's 8 bitrates come from its lanes' kmap bytes (wave ballots): a step
 // whose tiles are all K <= 2 stages compactly (slot stride kMixTSF, the first load only) and decodes with per-lane funnel origins
 // and shifts precomputed for K = 1 and 2 (one select each per tile); other steps stage at stride kMixTS and decode
-// with the tile's K at run time. Rings of 4 (tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4
+// with the tile's K at run time. Rings of 4 (first tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4
 // steps ahead) make the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple
 // of 4. A as in MfmaPipe.
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
@@ -667,24 +667,32 @@ struct MfmaPipeMix {
         M[1] = ldg(wp + off);
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ void load_w(u32x4_t (&D)[2], const int (&M)[2]) const {
+    // the lane's first 16 bytes of its tile: words min(4i, 8K - 4) .. + 3 (all of the tile for K <= 4)
+    __device__ __forceinline__ void load_w(u32x4_t& D, const int (&M)[2]) const {
         const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 4u * (uint32_t)(lane & 7);
-        const uint32_t* t = wb + M[1];
-        D[0] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (i4 < e ? i4 : e)));
-        D[1] = ldg_nt(reinterpret_cast<const u32x4_t*>(t + (i4 + 32u < e ? i4 + 32u : e)));
+        D = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + M[1] + (i4 < e ? i4 : e)));
         __builtin_amdgcn_sched_barrier(0);
     }
-    __device__ __forceinline__ void stage_w(const u32x4_t (&D)[2], bool fast) const {
+    // Stage the step's tiles (M: this lane's (K, woff)). Lane 7's last loaded word ends its tile, so it writes the
+    // wrap word. Tiles of K >= 5 (words 32 .. 8K - 1) take a second load here, on the spot: such steps are rare, and
+    // keeping a second register ring for them would cost every step occupancy.
+    __device__ __forceinline__ void stage_w(const u32x4_t& D, const int (&M)[2], bool fast, bool big) const {
         const int sl = lane >> 3, i = lane & 7;
         if (fast) {
             uint32_t* t = wl + sl * kMixTSF;
-            if (i < 4) *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D[0];
-            if (i == 7) t[3] = D[1][3];
+            if (i < 4) *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D;
+            if (i == 7) t[3] = D[3];
         } else {
             uint32_t* t = wl + sl * kMixTS;
-            *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D[0];
-            *reinterpret_cast<u32x4_t*>(t + 36 + 4 * i) = D[1];
-            if (i == 7) t[3] = D[1][3];
+            *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D;
+            if (big) {
+                const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 32u + 4u * (uint32_t)i;
+                const u32x4_t D1 = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + M[1] + (i4 < e ? i4 : e)));
+                *reinterpret_cast<u32x4_t*>(t + 36 + 4 * i) = D1;
+                if (i == 7) t[3] = D1[3];
+            } else if (i == 7) {
+                t[3] = D[3];
+            }
         }
     }
     // A fragments of tile-row half sr in the k-permuted order: k 2g, 2g + 1 from chunk 2 sr, 2g + 8, 2g + 9 from
@@ -758,7 +766,7 @@ struct MfmaPipeMix {
     }
     // step s, R = s mod 4
     template <int R>
-    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4][2], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
+    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
                                          f4_t (&acc)[kMfT][RGA]) const {
         load_a(RA[R], s + 4);
         load_meta(M[(R + DW) % 4], s + DW);
@@ -766,13 +774,13 @@ struct MfmaPipeMix {
         const int m0 = M[R][0];
         const uint64_t two = __builtin_amdgcn_ballot_w64(m0 == 2);
         const bool fast = __builtin_amdgcn_ballot_w64(m0 > 2) == 0;
-        stage_w(W[R], fast);
+        stage_w(W[R], M[R], fast, !fast && __builtin_amdgcn_ballot_w64(m0 > 4) != 0);
         compute(R, acc, m0, two, fast);
         store_a(RA[(R + 2) % 4], (R + 2) % 4);
         if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
-        u32x4_t W[4][2];
+        u32x4_t W[4];
         int M[4][2];
         u32x4_t RA[4][CPT];
 #pragma unroll
