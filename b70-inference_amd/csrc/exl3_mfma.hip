@@ -799,6 +799,7 @@ struct MfmaPipeMix {
             step<2>(s + 2, W, M, RA, acc);
             step<3>(s + 3, W, M, RA, acc);
         }
+        __syncthreads();                                 // every wave's last LDS read done: callers may reuse it
     }
     // After words / kmap / woff / col / tn / wl / lane are set: the lane's tile entries and fast-path origins, and
     // the A staging of `cnt` rows (rowptr(plane, row) -> that row's first element)
@@ -887,9 +888,12 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * 2 * RGA * 64];
-    __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
-    __shared__ float C[2 * 16 * 128];
+    // the epilogue's C reuses the pipeline's A stages and weight slots (dead once the pipeline has drained)
+    constexpr int kStage = 4 * 2 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 2 * 16 * 128 * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];
+    u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
+    uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
+    float* C = reinterpret_cast<float*>(smem);
     __shared__ float rsum[2 * 64];
     const int nbI = a.I / 128;
     int idx, nb;
@@ -909,9 +913,11 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * RGA * 64];
-    __shared__ __attribute__((aligned(16))) uint32_t wlds[4 * 8 * kMixTS];
-    __shared__ float C[16 * 256];
+    constexpr int kStage = 4 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];   // C aliases, as above
+    u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
+    uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
+    float* C = reinterpret_cast<float*>(smem);
     __shared__ float rsum[64];
     __shared__ int s_comb[2 * 64];
     const int nbH2 = (a.H / 128 + 1) / 2;
