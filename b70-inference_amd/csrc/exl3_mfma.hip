@@ -97,25 +97,29 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Workgroup (row block, 128-column block kb of H): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128),
-// fp16 (the GEMM inputs xh) and their block sums (xsum). Wave w takes rows 16 w .. 16 w + 15: A fragments are
-// fp16(x * suh) (packed fp16 multiplies, one rounding: the reference's fp16(x * suh)), the Hadamard is 8 output tiles
-// x 4 k-steps of v_mfma_f32_16x16x32_f16 against the two base fragments (fp32 accumulation of exact +-x products),
-// and the sums of the fp16-rounded outputs reduce over the 16 lanes of a row.
+// Workgroup (row block, y < H / 128): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128), fp16 (the
+// GEMM inputs xh) and their block sums (xsum). Each wave takes one unit (128-column block kb, 16-row group): the
+// block's nrg = ceil(rows / 16) row groups of the workgroup's column blocks, so a block of up to 16 rows has its four
+// waves on four column blocks (and three quarters of its workgroups exit at once) instead of three idle waves. A
+// fragments are fp16(x * suh) (packed fp16 multiplies, one rounding: the reference's fp16(x * suh)), the Hadamard is
+// 8 output tiles x 4 k-steps of v_mfma_f32_16x16x32_f16 against the two base fragments (fp32 accumulation of exact
+// +-x products), and the sums of the fp16-rounded outputs reduce over the 16 lanes of a row.
 __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     __shared__ int s_tok[kMfmaRows];
     __shared__ __attribute__((aligned(16))) _Float16 s_out[4][16][136];    // per wave: 16 rows x 128 (+ pad)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int blk = blockIdx.x, kb = blockIdx.y;
+    const int blk = blockIdx.x;
     const ItemDesc* d = a.blocks + blk;
     const int cnt = d->cnt;
     if (cnt == 0) return;
     const int p0 = d->p0;
     const int nblk = a.H / 128;
+    const int nrg = (cnt + 15) >> 4, u = 4 * (int)blockIdx.y + wave;   // unit u: column block u / nrg, group u % nrg
+    if (4 * (int)blockIdx.y >= nrg * nblk) return;                      // uniform: the whole workgroup leaves
     if (threadIdx.x < cnt) s_tok[threadIdx.x] = a.pair_tok[p0 + threadIdx.x];
     __syncthreads();
-    const int r0 = 16 * wave;
-    if (r0 >= cnt) return;
+    if (u >= nrg * nblk) return;
+    const int kb = u / nrg, r0 = 16 * (u - kb * nrg);
     const int m = lane & 15, g = lane >> 4;
     const int row = r0 + m < cnt ? r0 + m : cnt - 1;          // rows past cnt repeat the last one (not stored)
     const uint16_t* xr = a.x + (int64_t)s_tok[row] * a.x_ld + kb * 128 + 8 * g;
