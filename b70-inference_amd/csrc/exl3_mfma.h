@@ -111,6 +111,43 @@ __device__ __forceinline__ h8_t frag_finish(uint32_t (&R)[FragCfg<K>::NW], uint3
     return __builtin_bit_cast(h8_t, v);
 }
 
+// k-permuted B fragments (K <= 5). Lane L = (n = L & 15, kg = L >> 4) takes tile-row kg >> 1 of the block and
+// decodes two runs of four consecutive positions of its tile, t0 + {0..3} and t0 + 8 + {0..3} with
+// t0 = 32 (n & 7) + 4 (n >> 3) + 16 (kg & 1): rows 4 (kg & 1) + {0, 1, 8, 9} and 4 (kg & 1) + {2, 3, 10, 11} of
+// column n. Packed as rows 4 (kg & 1) + {0..3}, then 4 (kg & 1) + 8 + {0..3}, the lane's eight k are the 4-k units
+// u = 4 (kg >> 1) + (kg & 1) and u + 2 of the 32-k block, so A must be staged with those two units side by side.
+// A run's bits [(t + 1) K - 16, (t + 4) K) fit one funnel-shifted word (window i at bit 16 - i K), read from a staged
+// slot laid out as [w(8K - 1), w(0) .. w(8K - 1), w(0), w(1), w(2)]: the funnel whose first bit is ring bit `a`
+// (>= -15) takes slot words (a + 31) >> 5 and the next one, shifted by 31 - ((a + 31) & 31).
+template <int K>
+__device__ __forceinline__ void fragp_origin(int lane, int (&off)[2], uint32_t (&sh)[2]) {
+    static_assert(K >= 1 && K <= 5, "k-permuted fragments need four windows in one funnel");
+    const int n = lane & 15, kg = lane >> 4;
+    const int t0 = 32 * (n & 7) + 4 * (n >> 3) + 16 * (kg & 1);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int b = (t0 + 8 * g + 1) * K + 15;            // first bit + 31
+        off[g] = b >> 5;
+        sh[g] = (uint32_t)(~b & 31);
+    }
+}
+
+// w[2g], w[2g + 1]: run g's two slot words
+template <int K>
+__device__ __forceinline__ h8_t fragp_finish(const uint32_t (&w)[4], const uint32_t (&sh)[2]) {
+    uint32_t p[4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const uint32_t F = __builtin_amdgcn_alignbit(w[2 * g], w[2 * g + 1], sh[g]);
+        p[g] = __builtin_bit_cast(uint32_t, mul1_pair_raw(F >> 16, __builtin_amdgcn_ubfe(F, 16 - K, 16)));
+        p[2 + g] = __builtin_bit_cast(
+            uint32_t, mul1_pair_raw(__builtin_amdgcn_ubfe(F, 16 - 2 * K, 16), __builtin_amdgcn_ubfe(F, 16 - 3 * K, 16)));
+    }
+    typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+    u4_t v = {p[0], p[1], p[2], p[3]};
+    return __builtin_bit_cast(h8_t, v);
+}
+
 // Per-tile K: dispatch on the tile's bitrate (all lanes of one tile take the same branch).
 __device__ __forceinline__ h8_t frag_decode_k(const uint32_t* __restrict__ tw, int Kt, int lane) {
     switch (Kt) {

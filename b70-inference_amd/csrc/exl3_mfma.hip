@@ -182,6 +182,11 @@ constexpr int kMfT = 4;                              // tile columns per wave
 // swizzled by row so that the 16 rows of a fragment read hit distinct banks.
 __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
 
+typedef __attribute__((address_space(3))) const uint32_t* lds_cu32_t;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 // One wave accumulates kMfT tile columns over all 32-k steps for RGA row groups. Tile column t of the wave belongs to
 // column pair t >> 1 (gate|up: the projection; down: columns c0, c0 + 1 or c0 + 2, c0 + 3), whose two adjacent tiles of
 // one tile-row are contiguous in memory.
@@ -189,13 +194,18 @@ __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ 
 //            per lane (16 lanes per 2-tile segment), loaded DW - 1 steps ahead into a register ring, and are staged in a
 //            wave-private LDS slot per tile laid out as [w(8K-1), w(0) .. w(8K-1), w(0), w(1), w(2)], so that every
 //            lane's fragment window (first word -1 .. 8K - 1, at most 8K + 2 past) is contiguous: no wrap logic, and
-//            per-lane scattered loads (64-bit addresses per lane into the texture unit) become LDS reads.
+//            per-lane scattered loads (64-bit addresses per lane into the texture unit) become LDS reads. For K <= 5
+//            the fragments are k-permuted (two funnels of four windows per lane, fragp_finish); K >= 6 keeps the
+//            natural k order (frag_finish).
 //   A:       staged per step by the whole workgroup: loaded into register slot s % 4 four steps ahead, stored to LDS
 //            stage s % 4 two steps ahead, with a barrier after the even steps only (a stage is rewritten two steps
 //            after its last read, with a barrier in between, and read at least one barrier after its write); memory-
-//            counter waits complete in issue order, so each step issues its A load before its weight load.
+//            counter waits complete in issue order, so each step issues its A load before its weight load. With
+//            k-permuted fragments a row's 4-k units are staged in the order 0 2 1 3 4 6 5 7 (two 8-byte stores per
+//            16-byte unit), so that a lane's 16-byte read holds the k of its B fragment.
 template <int K, int NP, int RGA, int NPS = NP>
 struct MfmaPipe {
+    static constexpr bool KP = K <= 5;                      // k-permuted fragments
     static constexpr int NW = FragCfg<K>::NW;
     static constexpr int DW = 4;
     static constexpr int TPP = kMfT / NP;
@@ -209,8 +219,11 @@ struct MfmaPipe {
     int wdst, wslot;                                         // this lane's staged words: slot wslot, word wdst
     int w0;                                                  // fragment window origin (ring word, -1 .. 8K - 1)
     uint32_t sh;
+    uint32_t fa[2], fsh[2];                                  // k-permuted: LDS byte address of each run's funnel
+                                                             // words in slot 0, and its shift
     const _Float16* asrc[CPT];                               // this thread's staged A units at step 0
-    int adst[CPT];
+    int adst[CPT];                                           // k-permuted: 8-byte units of the low and high halves
+    int adst2[CPT];
     u32x4_t* lds;                                            // [2][UNITS]
     int lane;
     int apl = 0;                                             // first staged plane this wave reads (NPS > NP)
@@ -240,14 +253,30 @@ struct MfmaPipe {
                 af[p][rg] = __builtin_bit_cast(
                     h8_t, lds[stage * UNITS + (p + apl) * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
         h8_t bf[kMfT];
+        if constexpr (KP) {
+            uint32_t fw[kMfT][4];
 #pragma unroll
-        for (int t = 0; t < kMfT; ++t) {
-            const int slot = 2 * (2 * (t >> 1) + (lane >> 5)) + (t & 1);
-            const uint32_t* r = wl + slot * TS + 1 + w0;
-            uint32_t R[NW];
+            for (int t = 0; t < kMfT; ++t) {
+                const int slot = 2 * (2 * (t >> 1) + (lane >> 5)) + (t & 1);
 #pragma unroll
-            for (int i = 0; i < NW; ++i) R[i] = r[i];
-            bf[t] = frag_finish<K>(R, sh);
+                for (int g = 0; g < 2; ++g) {
+                    const lds_cu32_t o = (lds_cu32_t)fa[g];
+                    fw[t][2 * g] = o[slot * TS];
+                    fw[t][2 * g + 1] = o[slot * TS + 1];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kMfT; ++t) bf[t] = fragp_finish<K>(fw[t], fsh);
+        } else {
+#pragma unroll
+            for (int t = 0; t < kMfT; ++t) {
+                const int slot = 2 * (2 * (t >> 1) + (lane >> 5)) + (t & 1);
+                const uint32_t* r = wl + slot * TS + 1 + w0;
+                uint32_t R[NW];
+#pragma unroll
+                for (int i = 0; i < NW; ++i) R[i] = r[i];
+                bf[t] = frag_finish<K>(R, sh);
+            }
         }
 #pragma unroll
         for (int t = 0; t < kMfT; ++t)
@@ -273,8 +302,19 @@ struct MfmaPipe {
         __builtin_amdgcn_sched_barrier(0);
     }
     __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
+        if constexpr (KP) {
+            typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+            u2_t* l2 = reinterpret_cast<u2_t*>(lds) + 2 * stage * UNITS;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
+            for (int j = 0; j < CPT; ++j) {
+                const u2_t lo = {Ra[j][0], Ra[j][1]}, hi = {Ra[j][2], Ra[j][3]};
+                l2[adst[j]] = lo;
+                l2[adst2[j]] = hi;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
+        }
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         uint32_t W[DW][K];
@@ -307,7 +347,14 @@ struct MfmaPipe {
         wl = wave_lds;
         wslot = 2 * g + ((lane & 15) >> 3);
         wdst = (lane & 7) * K;
-        frag_origin<K>(lane, w0, sh);
+        if constexpr (KP) {
+            int off[2];
+            fragp_origin<K>(lane, off, fsh);
+#pragma unroll
+            for (int g = 0; g < 2; ++g) fa[g] = lds_addr(wl) + 4u * (uint32_t)off[g];
+        } else {
+            frag_origin<K>(lane, w0, sh);
+        }
     }
     // staging set-up: unit u = (tid + 256 j) mod UNITS (UNITS < 256: several threads stage the same unit, writing
     // the same value, so that the loads and stores stay unconditional: a branch around them would make the compiler
@@ -320,7 +367,12 @@ struct MfmaPipe {
             const int u = (threadIdx.x + 256 * j) % UNITS;
             const int p = u / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
             asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
-            adst[j] = p * RGA * 64 + a_unit(row, ch);
+            if constexpr (KP) {                              // 4-k units 2 ch, 2 ch + 1 -> 16-byte units
+                adst[j] = 2 * (p * RGA * 64 + a_unit(row, ch & 2)) + (ch & 1);       // (ch & 2) and (ch & 2) + 1,
+                adst2[j] = 2 * (p * RGA * 64 + a_unit(row, (ch & 2) + 1)) + (ch & 1); // half ch & 1
+            } else {
+                adst[j] = p * RGA * 64 + a_unit(row, ch);
+            }
         }
     }
 };
@@ -644,10 +696,6 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 // of 4. A as in MfmaPipe.
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
 
-typedef __attribute__((address_space(3))) const uint32_t* lds_cu32_t;
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
-}
 
 template <int NP, int RGA>
 struct MfmaPipeMix {
