@@ -162,7 +162,9 @@ __device__ __forceinline__ void xcd_map(int nbc, int& blk, int& nb) {
 // ------------------------------------------------------------------------------------------------ pipelined K loop
 constexpr int kMfT = 4;                              // tile columns per wave
 
-// Workgroups per CU the uniform-K grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row groups)
+// Workgroups per CU (= waves per SIMD) the grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row
+// groups). The down passes take one more where their registers allow it without spills (the 4-row-group uniform
+// down kernel fits 168 VGPRs for K <= 4, the 1-row-group per-tile one 96); the gate|up kernels would spill.
 #ifndef EXL3_MFMA_OCC1
 #define EXL3_MFMA_OCC1 4
 #endif
@@ -173,10 +175,12 @@ constexpr int kMfT = 4;                              // tile columns per wave
 #define EXL3_MFMA_OCC4 2
 #endif
 #define EXL3_MFMA_OCC(RGA) ((RGA) == 1 ? EXL3_MFMA_OCC1 : (RGA) == 2 ? EXL3_MFMA_OCC2 : EXL3_MFMA_OCC4)
+#define EXL3_MFMA_DOWN_OCC(RGA, K) ((RGA) == 4 && (K) <= 4 ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
 #ifndef EXL3_MIX_OCC1
 #define EXL3_MIX_OCC1 4
 #endif
 #define EXL3_MIX_OCC(RGA) ((RGA) == 1 ? EXL3_MIX_OCC1 : (RGA) == 2 ? 3 : 2)
+#define EXL3_MIX_DOWN_OCC(RGA) ((RGA) == 1 ? EXL3_MIX_OCC1 + 1 : EXL3_MIX_OCC(RGA))
 
 // 16-byte unit of (row, chunk) in one staged A plane (16 * RGA rows x four 16-byte chunks = 32 k); the chunk is
 // swizzled by row so that the 16 rows of a fragment read hit distinct banks.
@@ -607,7 +611,7 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 }
 
 template <int K, int RGA>
-__global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void down_mfma_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_kernel(MoeArgs a) {
     mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[4 * RGA * 64];            // [4 stages][16 RGA rows x 4 units]
@@ -691,9 +695,10 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 // tile), so that a funnel starting before the ring reads it. The step's 8 bitrates come from its lanes' kmap bytes (wave ballots): a step
 // whose tiles are all K <= 2 stages compactly (slot stride kMixTSF, the first load only) and decodes with per-lane funnel origins
 // and shifts precomputed for K = 1 and 2 (one select each per tile); other steps stage at stride kMixTS and decode
-// with the tile's K at run time. Rings of 4 (first tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead, A 4
-// steps ahead) make the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple
-// of 4. A as in MfmaPipe.
+// with the tile's K at run time. Rings of 4 (first tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead) make
+// the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A is staged
+// as in MfmaPipe (four LDS stages written two steps ahead, a barrier every second step), but from a register ring of
+// two: loaded three steps ahead, stored one step later (the 1-row-group down kernel fits five waves per SIMD that way).
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
 
 
@@ -830,9 +835,9 @@ struct MfmaPipeMix {
     }
     // step s, R = s mod 4
     template <int R>
-    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4], int (&M)[4][2], u32x4_t (&RA)[4][CPT],
+    __device__ __forceinline__ void step(int s, u32x4_t (&W)[4], int (&M)[4][2], u32x4_t (&RA)[2][CPT],
                                          f4_t (&acc)[kMfT][RGA]) const {
-        load_a(RA[R], s + 4);
+        load_a(RA[R % 2], s + 3);
         load_meta(M[(R + DW) % 4], s + DW);
         load_w(W[(R + DW - 1) % 4], M[(R + DW - 1) % 4]);
         const int m0 = M[R][0];
@@ -840,22 +845,22 @@ struct MfmaPipeMix {
         const bool fast = __builtin_amdgcn_ballot_w64(m0 > 2) == 0;
         stage_w(W[R], M[R], fast, !fast && __builtin_amdgcn_ballot_w64(m0 > 4) != 0);
         compute(R, acc, m0, two, fast);
-        store_a(RA[(R + 2) % 4], (R + 2) % 4);
+        store_a(RA[(R + 1) % 2], (R + 2) % 4);
         if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         u32x4_t W[4];
         int M[4][2];
-        u32x4_t RA[4][CPT];
+        u32x4_t RA[2][CPT];
 #pragma unroll
         for (int i = 0; i < DW; ++i) load_meta(M[i], i);
+        load_a(RA[0], 0);
+        load_a(RA[1], 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            load_a(RA[i], i);
-            if (i < DW - 1) load_w(W[i], M[i]);
-        }
+        for (int i = 0; i < DW - 1; ++i) load_w(W[i], M[i]);
         store_a(RA[0], 0);
         store_a(RA[1], 1);
+        load_a(RA[1], 2);
         __syncthreads();
         for (int s = 0; s < nsteps; s += 4) {
             step<0>(s, W, M, RA, acc);
@@ -976,7 +981,7 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 }
 
 template <int RGA>
-__global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MIX_DOWN_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     constexpr int kStage = 4 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
