@@ -163,8 +163,8 @@ __device__ __forceinline__ void xcd_map(int nbc, int& blk, int& nb) {
 constexpr int kMfT = 4;                              // tile columns per wave
 
 // Workgroups per CU (= waves per SIMD) the grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row
-// groups). The down passes take one more where their registers allow it without spills (the 4-row-group uniform
-// down kernel fits 168 VGPRs for K <= 4, the 1-row-group per-tile one 96); the gate|up kernels would spill.
+// groups). The 4-row-group uniform kernels take one more where their registers allow it without spills (168 VGPRs:
+// gate|up at K = 1, 2 and 4, down at K <= 4), and so does the 1-row-group per-tile down kernel (96 VGPRs).
 #ifndef EXL3_MFMA_OCC1
 #define EXL3_MFMA_OCC1 4
 #endif
@@ -175,6 +175,8 @@ constexpr int kMfT = 4;                              // tile columns per wave
 #define EXL3_MFMA_OCC4 2
 #endif
 #define EXL3_MFMA_OCC(RGA) ((RGA) == 1 ? EXL3_MFMA_OCC1 : (RGA) == 2 ? EXL3_MFMA_OCC2 : EXL3_MFMA_OCC4)
+#define EXL3_MFMA_GU_OCC(RGA, K) \
+    ((RGA) == 4 && ((K) <= 2 || (K) == 4) ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
 #define EXL3_MFMA_DOWN_OCC(RGA, K) ((RGA) == 4 && (K) <= 4 ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
 #ifndef EXL3_MIX_OCC1
 #define EXL3_MIX_OCC1 4
@@ -201,8 +203,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //            per-lane scattered loads (64-bit addresses per lane into the texture unit) become LDS reads. For K <= 5
 //            the fragments are k-permuted (two funnels of four windows per lane, fragp_finish); K >= 6 keeps the
 //            natural k order (frag_finish).
-//   A:       staged per step by the whole workgroup: loaded into register slot s % 4 four steps ahead, stored to LDS
-//            stage s % 4 two steps ahead, with a barrier after the even steps only (a stage is rewritten two steps
+//   A:       staged per step by the whole workgroup: loaded into register slot s % 2 three steps ahead, stored to
+//            LDS stage s % 4 two steps ahead, with a barrier after the even steps only (a stage is rewritten two steps
 //            after its last read, with a barrier in between, and read at least one barrier after its write); memory-
 //            counter waits complete in issue order, so each step issues its A load before its weight load. With
 //            k-permuted fragments a row's 4-k units are staged in the order 0 2 1 3 4 6 5 7 (two 8-byte stores per
@@ -249,13 +251,6 @@ struct MfmaPipe {
             if (q == u / K) t[8 * K + 1 + u] = D[u % K];
     }
     __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA]) const {
-        h8_t af[NP][RGA];
-#pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-            for (int rg = 0; rg < RGA; ++rg)
-                af[p][rg] = __builtin_bit_cast(
-                    h8_t, lds[stage * UNITS + (p + apl) * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
         h8_t bf[kMfT];
         if constexpr (KP) {
             uint32_t fw[kMfT][4];
@@ -282,21 +277,30 @@ struct MfmaPipe {
                 bf[t] = frag_finish<K>(R, sh);
             }
         }
+        // A fragments per plane, after the B decode (fewer live registers: three waves per SIMD at four row groups)
 #pragma unroll
-        for (int t = 0; t < kMfT; ++t)
+        for (int p = 0; p < NP; ++p) {
+            h8_t af[RGA];
 #pragma unroll
             for (int rg = 0; rg < RGA; ++rg)
-                acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t / TPP][rg], bf[t], acc[t][rg], 0, 0, 0);
+                af[rg] = __builtin_bit_cast(
+                    h8_t, lds[stage * UNITS + (p + apl) * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
+#pragma unroll
+            for (int t = p * TPP; t < (p + 1) * TPP; ++t)
+#pragma unroll
+                for (int rg = 0; rg < RGA; ++rg)
+                    acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[rg], bf[t], acc[t][rg], 0, 0, 0);
+        }
     }
     // step s, with every ring slot known at compile time (R = s mod 4)
     template <int R>
-    __device__ __forceinline__ void step(int s, uint32_t (&W)[DW][K], u32x4_t (&RA)[4][CPT],
+    __device__ __forceinline__ void step(int s, uint32_t (&W)[DW][K], u32x4_t (&RA)[2][CPT],
                                          f4_t (&acc)[kMfT][RGA]) const {
-        load_a(RA[R], s + 4);                            // slot R held A(s), stored to LDS two steps ago
+        load_a(RA[R % 2], s + 3);
         load_w(W[(R + DW - 1) % DW], s + DW - 1);
         stage_w(W[R % DW]);
         compute(R, acc);
-        store_a(RA[(R + 2) % 4], (R + 2) % 4);
+        store_a(RA[(R + 1) % 2], (R + 2) % 4);
         if (R % 2 == 0) __syncthreads();
     }
     __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
@@ -322,14 +326,14 @@ struct MfmaPipe {
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         uint32_t W[DW][K];
-        u32x4_t RA[4][CPT];
+        u32x4_t RA[2][CPT];
+        load_a(RA[0], 0);
+        load_a(RA[1], 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            load_a(RA[i], i);
-            if (i < DW - 1) load_w(W[i], i);
-        }
+        for (int i = 0; i < DW - 1; ++i) load_w(W[i], i);
         store_a(RA[0], 0);
         store_a(RA[1], 1);
+        load_a(RA[1], 2);
         __syncthreads();
         int s = 0;
         for (; s + 4 <= nsteps; s += 4) {
@@ -492,7 +496,7 @@ __device__ __forceinline__ void mfma_class_priority() {
 // One instance per row class (RGA row groups of 16): workgroup (list index, column block); indices past the class's
 // block count exit at once.
 template <int K, int RGA>
-__global__ __launch_bounds__(256, EXL3_MFMA_OCC(RGA)) void gateup_mfma_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_kernel(MoeArgs a) {
     mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[4 * 2 * RGA * 64];        // [4 stages][2 planes][16 RGA rows x 4 units]
