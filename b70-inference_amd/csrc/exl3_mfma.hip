@@ -483,10 +483,10 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
     return v;
 }
 
-// Wave issue priority by row class: the classes run concurrently and the 64-row blocks of hot experts make the
-// longest chain (each block decodes its expert again), so their waves issue first when they share a SIMD with
-// smaller blocks (MoE prefill with a Zipf expert skew, 512 tokens: 822 -> 801 us; no change where small blocks
-// dominate).
+// Wave issue priority by row class for the per-tile-K kernels: the classes run concurrently, and the waves of the
+// larger blocks issue first when they share a SIMD with smaller ones. The uniform-K kernels run without it: once their
+// 64-row class ran three waves per SIMD, equal priorities balanced the class chains better (MoE prefill with a Zipf
+// expert skew, 512 tokens: 754 -> 730 us).
 template <int RGA>
 __device__ __forceinline__ void mfma_class_priority() {
     if constexpr (RGA == 4) __builtin_amdgcn_s_setprio(3);
@@ -497,7 +497,6 @@ __device__ __forceinline__ void mfma_class_priority() {
 // block count exit at once.
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_kernel(MoeArgs a) {
-    mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[4 * 2 * RGA * 64];        // [4 stages][2 planes][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
@@ -616,7 +615,6 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_kernel(MoeArgs a) {
-    mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     __shared__ u32x4_t stage[4 * RGA * 64];            // [4 stages][16 RGA rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
