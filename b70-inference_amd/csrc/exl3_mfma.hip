@@ -483,16 +483,6 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
     return v;
 }
 
-// Wave issue priority by row class for the per-tile-K kernels: the classes run concurrently, and the waves of the
-// larger blocks issue first when they share a SIMD with smaller ones. The uniform-K kernels run without it: once their
-// 64-row class ran three waves per SIMD, equal priorities balanced the class chains better (MoE prefill with a Zipf
-// expert skew, 512 tokens: 754 -> 730 us).
-template <int RGA>
-__device__ __forceinline__ void mfma_class_priority() {
-    if constexpr (RGA == 4) __builtin_amdgcn_s_setprio(3);
-    else if constexpr (RGA == 2) __builtin_amdgcn_s_setprio(2);
-}
-
 // One instance per row class (RGA row groups of 16): workgroup (list index, column block); indices past the class's
 // block count exit at once.
 template <int K, int RGA>
@@ -958,7 +948,6 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
 
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeArgs a) {
-    mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     // the epilogue's C reuses the pipeline's A stages and weight slots (dead once the pipeline has drained)
     constexpr int kStage = 4 * 2 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 2 * 16 * 128 * 4;
@@ -984,7 +973,6 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_DOWN_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
-    mfma_class_priority<RGA>();
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     constexpr int kStage = 4 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
     __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];   // C aliases, as above
