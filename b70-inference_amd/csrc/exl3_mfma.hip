@@ -189,6 +189,7 @@ constexpr int kMfT = 4;                              // tile columns per wave
 __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ ((row >> 1) & 3)); }
 
 typedef __attribute__((address_space(3))) const uint32_t* lds_cu32_t;
+constexpr int kBufferWord3 = 0x00020000;                     // buffer resource word 3 for raw 32-bit loads (gfx9)
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
@@ -227,7 +228,8 @@ struct MfmaPipe {
     uint32_t sh;
     uint32_t fa[2], fsh[2];                                  // k-permuted: LDS byte address of each run's funnel
                                                              // words in slot 0, and its shift
-    const _Float16* asrc[CPT];                               // this thread's staged A units at step 0
+    __amdgpu_buffer_rsrc_t abuf[CPT];                        // this thread's staged A units at step 0: a buffer
+    uint32_t aoff[CPT];                                      // the wave shares, and the lane's byte offset in it
     int adst[CPT];                                           // k-permuted: 8-byte units of the low and high halves
     int adst2[CPT];
     u32x4_t* lds;                                            // [2][UNITS]
@@ -306,7 +308,8 @@ struct MfmaPipe {
     __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
         const int ss = (s < nsteps ? s : nsteps - 1) * 32;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) Ra[j] = ldg(reinterpret_cast<const u32x4_t*>(asrc[j] + ss));
+        for (int j = 0; j < CPT; ++j)
+            Ra[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(abuf[j], aoff[j], 2 * ss, 0));
         __builtin_amdgcn_sched_barrier(0);
     }
     __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
@@ -367,14 +370,19 @@ struct MfmaPipe {
     // staging set-up: unit u = (tid + 256 j) mod UNITS (UNITS < 256: several threads stage the same unit, writing
     // the same value, so that the loads and stores stay unconditional: a branch around them would make the compiler
     // drain every outstanding load, the weight prefetch included) of plane p = u / (RGA * 64): row (u % (RGA * 64)) / 4
-    // (clamped to the block's last row), chunk u % 4, from row pointer rowptr(p, row) (k offset 0)
+    // (clamped to the block's last row), chunk u % 4, from row pointer rowptr(p, row) (k offset 0). A wave's 64 units
+    // lie in one plane (UNITS and RGA * 64 are multiples of 64), so the loads are buffer loads from the plane's row 0
+    // (a wave-uniform resource) at a 32-bit lane offset plus the step's scalar offset: no address arithmetic per step.
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            const int u = (threadIdx.x + 256 * j) % UNITS;
-            const int p = u / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
-            asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
+            const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
+            const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+            const _Float16* b = rowptr(p, 0);
+            abuf[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b), 0, 0x7fffffff, kBufferWord3);
+            aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
             if constexpr (KP) {                              // 4-k units 2 ch, 2 ch + 1 -> 16-byte units
                 adst[j] = 2 * (p * RGA * 64 + a_unit(row, ch & 2)) + (ch & 1);       // (ch & 2) and (ch & 2) + 1,
                 adst2[j] = 2 * (p * RGA * 64 + a_unit(row, (ch & 2) + 1)) + (ch & 1); // half ch & 1
@@ -713,7 +721,8 @@ struct MfmaPipeMix {
     uint32_t fa1, fa2;                                       // fast path: LDS byte address of the lane's funnel
     uint32_t sh1, sh2;                                       // word in compact slot 0 at K = 1 and 2, and the
                                                              // funnel shifts
-    const _Float16* asrc[CPT];
+    __amdgpu_buffer_rsrc_t abuf[CPT];                        // as in MfmaPipe
+    uint32_t aoff[CPT];
     int adst[CPT];
     u32x4_t* lds;
     int lane;
@@ -731,7 +740,7 @@ struct MfmaPipeMix {
     // the lane's first 16 bytes of its tile: words min(4i, 8K - 4) .. + 3 (all of the tile for K <= 4)
     __device__ __forceinline__ void load_w(u32x4_t& D, const int (&M)[2]) const {
         const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 4u * (uint32_t)(lane & 7);
-        D = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + M[1] + (i4 < e ? i4 : e)));
+        D = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + ((uint32_t)M[1] + (i4 < e ? i4 : e))));
         __builtin_amdgcn_sched_barrier(0);
     }
     // Stage the step's tiles (M: this lane's (K, woff)). Lane 7's last loaded word ends its tile, so it writes the
@@ -818,7 +827,8 @@ struct MfmaPipeMix {
     __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
         const int ss = (s < nsteps ? s : nsteps - 1) * 32;
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) Ra[j] = ldg(reinterpret_cast<const u32x4_t*>(asrc[j] + ss));
+        for (int j = 0; j < CPT; ++j)
+            Ra[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(abuf[j], aoff[j], 2 * ss, 0));
         __builtin_amdgcn_sched_barrier(0);
     }
     __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
@@ -866,11 +876,14 @@ struct MfmaPipeMix {
     // the A staging of `cnt` rows (rowptr(plane, row) -> that row's first element)
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
+        const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            const int u = (threadIdx.x + 256 * j) % UNITS;
-            const int p = u / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
-            asrc[j] = rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch;
+            const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
+            const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+            const _Float16* b = rowptr(p, 0);
+            abuf[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b), 0, 0x7fffffff, kBufferWord3);
+            aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
             adst[j] = p * RGA * 64 + a_unit(row, ch);
         }
         const int sl = lane >> 3, t = sl >> 1, hr = sl & 1, pr = t >> 1;
