@@ -190,6 +190,10 @@ __device__ __forceinline__ int a_unit(int row, int ch) { return row * 4 + (ch ^ 
 
 typedef __attribute__((address_space(3))) const uint32_t* lds_cu32_t;
 constexpr int kBufferWord3 = 0x00020000;                     // buffer resource word 3 for raw 32-bit loads (gfx9)
+// A wave-uniform buffer resource over `p` (loads at offsets below 2^31 bytes; beyond the range they return zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7fffffff, kBufferWord3);
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
@@ -381,7 +385,7 @@ struct MfmaPipe {
             const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
             const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
             const _Float16* b = rowptr(p, 0);
-            abuf[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b), 0, 0x7fffffff, kBufferWord3);
+            abuf[j] = buffer_rsrc(b);
             aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
             if constexpr (KP) {                              // 4-k units 2 ch, 2 ch + 1 -> 16-byte units
                 adst[j] = 2 * (p * RGA * 64 + a_unit(row, ch & 2)) + (ch & 1);       // (ch & 2) and (ch & 2) + 1,
@@ -407,14 +411,15 @@ __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDes
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
     const int tn = a.gu_tn;
-    const uint32_t* trp[2] = {reinterpret_cast<const uint32_t*>(d->tab[0]),
-                              reinterpret_cast<const uint32_t*>(d->tab[3])};
-    const int ct0 = nb * 8 + 2 * wave;
-    MfmaPipe<K, 2, RGA> L;
+    const int pw = wave >> 1;                              // this wave's projection (gate, up), its 4 tile columns
+    const uint32_t* trp = reinterpret_cast<const uint32_t*>(d->tab[3 * pw]);
+    const int ct0 = nb * 8 + 4 * (wave & 1);
+    MfmaPipe<K, 1, RGA, 2> L;
     L.nsteps = a.H / 32;
     L.lds = stage;
     L.lane = lane;
-    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) { return trp[pair] + (size_t)ct0 * (8 * K); });
+    L.apl = pw;
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) { return trp + (size_t)(ct0 + 2 * pair) * (8 * K); });
     L.setup_a(cnt, [&](int p, int row) { return a.xh + ((size_t)(p0 + row) * 2 + p) * a.H; });
     f4_t acc[kMfT][RGA];
 #pragma unroll
@@ -441,10 +446,11 @@ __device__ __forceinline__ void gateup_epilogue(const MoeArgs& a, const ItemDesc
     const int nbI = a.I / 128;
 #pragma unroll
     for (int rg = 0; rg < RGA; ++rg) {
-        // this row group's gate / up columns of the whole workgroup -> C[2][16][128]
+        // this row group's gate / up columns of the whole workgroup -> C[2][16][128]; wave w holds projection w >> 1,
+        // tile columns 4 (w & 1) .. + 3 of the block
 #pragma unroll
         for (int t = 0; t < kMfT; ++t) {
-            const int p = t >> 1, col = (2 * wave + (t & 1)) * 16 + (lane & 15);
+            const int p = wave >> 1, col = (4 * (wave & 1) + t) * 16 + (lane & 15);
 #pragma unroll
             for (int i = 0; i < 4; ++i) C[(p * 16 + 4 * (lane >> 4) + i) * 128 + col] = acc[t][rg][i];
         }
@@ -702,21 +708,18 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
 
 
-template <int NP, int RGA>
+template <int NPS, int RGA>
 struct MfmaPipeMix {
     static constexpr int DW = 3;
-    static constexpr int UNITS = NP * RGA * 64;
+    static constexpr int UNITS = NPS * RGA * 64;             // NPS staged A planes; a wave reads plane apl
     static constexpr int CPT = (UNITS + 255) / 256;
-    static constexpr int TPP = kMfT / NP;
-    const uint32_t* words[2];                                // per column pair: the projection's words
-    const uint8_t* kmap[2];
-    const int32_t* woff[2];
+    static constexpr int kNT = 2;                            // buffer-load cache policy: nontemporal
+    __amdgpu_buffer_rsrc_t wrs, krs, ors;                    // the wave's projection: words, kmap, woff
     int col[2];                                              // per column pair: its first tile column (even)
     int tn, nsteps;
+    int apl = 0;
     uint32_t* wl;                                            // the wave's LDS slots [8][kMixTS]
-    const uint8_t* kp;                                       // this lane's tile entries at step 0 (its slot's tile)
-    const int32_t* wp;
-    const uint32_t* wb;                                      // its column pair's words
+    uint32_t ktile;                                          // this lane's tile entry at step 0 (its slot's tile)
     uint32_t t0p1;                                           // t0 + 1 of the lane's k-permuted positions
     uint32_t fa1, fa2;                                       // fast path: LDS byte address of the lane's funnel
     uint32_t sh1, sh2;                                       // word in compact slot 0 at K = 1 and 2, and the
@@ -733,14 +736,18 @@ struct MfmaPipeMix {
     // LDS wait counter and may return out of order, so every LDS wait after one would wait for it too.
     __device__ __forceinline__ void load_meta(int (&M)[2], int s) const {
         const int off = (s < nsteps ? s : nsteps - 1) * 2 * tn;
-        M[0] = ldg(kp + off);
-        M[1] = ldg(wp + off);
+        M[0] = __builtin_amdgcn_raw_buffer_load_b8(krs, ktile, off, 0);
+        M[1] = (int)__builtin_amdgcn_raw_buffer_load_b32(ors, 4 * ktile, 4 * off, 0);
         __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ __forceinline__ u32x4_t load_words(const int (&M)[2], uint32_t first) const {
+        const uint32_t e = 8u * (uint32_t)M[0] - 4u;
+        return __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, 4u * ((uint32_t)M[1] + (first < e ? first : e)), 0, kNT));
     }
     // the lane's first 16 bytes of its tile: words min(4i, 8K - 4) .. + 3 (all of the tile for K <= 4)
     __device__ __forceinline__ void load_w(u32x4_t& D, const int (&M)[2]) const {
-        const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 4u * (uint32_t)(lane & 7);
-        D = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + ((uint32_t)M[1] + (i4 < e ? i4 : e))));
+        D = load_words(M, 4u * (uint32_t)(lane & 7));
         __builtin_amdgcn_sched_barrier(0);
     }
     // Stage the step's tiles (M: this lane's (K, woff)). Lane 7's last loaded word ends its tile, so it writes the
@@ -756,8 +763,7 @@ struct MfmaPipeMix {
             uint32_t* t = wl + sl * kMixTS;
             *reinterpret_cast<u32x4_t*>(t + 4 + 4 * i) = D;
             if (big) {
-                const uint32_t e = 8u * (uint32_t)M[0] - 4u, i4 = 32u + 4u * (uint32_t)i;
-                const u32x4_t D1 = ldg_nt(reinterpret_cast<const u32x4_t*>(wb + M[1] + (i4 < e ? i4 : e)));
+                const u32x4_t D1 = load_words(M, 32u + 4u * (uint32_t)i);
                 *reinterpret_cast<u32x4_t*>(t + 36 + 4 * i) = D1;
                 if (i == 7) t[3] = D1[3];
             } else if (i == 7) {
@@ -765,28 +771,26 @@ struct MfmaPipeMix {
             }
         }
     }
-    // A fragments of tile-row half sr in the k-permuted order: k 2g, 2g + 1 from chunk 2 sr, 2g + 8, 2g + 9 from
-    // chunk 2 sr + 1 (4 bytes at 4g in each unit)
-    __device__ __forceinline__ void load_af(int stage, int sr, h4_t (&af)[NP][RGA]) const {
+    // A fragments (plane apl) of tile-row half sr in the k-permuted order: k 2g, 2g + 1 from chunk 2 sr, 2g + 8, 2g + 9
+    // from chunk 2 sr + 1 (4 bytes at 4g in each unit)
+    __device__ __forceinline__ void load_af(int stage, int sr, h4_t (&af)[RGA]) const {
         const int g = lane >> 4;
 #pragma unroll
-        for (int p = 0; p < NP; ++p)
-#pragma unroll
-            for (int rg = 0; rg < RGA; ++rg) {
-                const u32x4_t* base = lds + stage * UNITS + p * RGA * 64;
-                const int row = 16 * rg + (lane & 15);
-                typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-                const u2_t v = {reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr))[g],
-                                reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr + 1))[g]};
-                af[p][rg] = __builtin_bit_cast(h4_t, v);
-            }
+        for (int rg = 0; rg < RGA; ++rg) {
+            const u32x4_t* base = lds + stage * UNITS + apl * RGA * 64;
+            const int row = 16 * rg + (lane & 15);
+            typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+            const u2_t v = {reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr))[g],
+                            reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr + 1))[g]};
+            af[rg] = __builtin_bit_cast(h4_t, v);
+        }
     }
     // slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1) of tile-row half sr; m0 = this lane's K
     __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], int m0, uint64_t two, bool fast) const {
         if (fast) {
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
-                h4_t af[NP][RGA];
+                h4_t af[RGA];
                 load_af(stage, sr, af);
                 uint32_t wlo[kMfT], whi[kMfT];                   // the tiles' funnel words, all reads issued first
 #pragma unroll
@@ -805,13 +809,13 @@ struct MfmaPipeMix {
                     const h4_t bf = decode4p12(F, k2);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
-                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
+                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[rg], bf, acc[t][rg], 0, 0, 0);
                 }
             }
         } else {
 #pragma unroll
             for (int sr = 0; sr < 2; ++sr) {
-                h4_t af[NP][RGA];
+                h4_t af[RGA];
                 load_af(stage, sr, af);
 #pragma unroll
                 for (int t = 0; t < kMfT; ++t) {
@@ -819,7 +823,7 @@ struct MfmaPipeMix {
                     const h4_t bf = decode4p_rt(wl + sl * kMixTS + 3, __builtin_amdgcn_readlane(m0, 8 * sl), t0p1);
 #pragma unroll
                     for (int rg = 0; rg < RGA; ++rg)
-                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t / TPP][rg], bf, acc[t][rg], 0, 0, 0);
+                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[rg], bf, acc[t][rg], 0, 0, 0);
                 }
             }
         }
@@ -872,8 +876,8 @@ struct MfmaPipeMix {
         }
         __syncthreads();                                 // every wave's last LDS read done: callers may reuse it
     }
-    // After words / kmap / woff / col / tn / wl / lane are set: the lane's tile entries and fast-path origins, and
-    // the A staging of `cnt` rows (rowptr(plane, row) -> that row's first element)
+    // After col / tn / wl / lane are set: the lane's tile entry and fast-path origins, and the A staging of `cnt` rows
+    // (rowptr(plane, row) -> that row's first element)
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
         const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -882,15 +886,12 @@ struct MfmaPipeMix {
             const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
             const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
             const _Float16* b = rowptr(p, 0);
-            abuf[j] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(b), 0, 0x7fffffff, kBufferWord3);
+            abuf[j] = buffer_rsrc(b);
             aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
             adst[j] = p * RGA * 64 + a_unit(row, ch);
         }
         const int sl = lane >> 3, t = sl >> 1, hr = sl & 1, pr = t >> 1;
-        const int tile = hr * tn + (pr ? col[1] : col[0]) + (t & 1);
-        kp = (pr ? kmap[1] : kmap[0]) + tile;
-        wp = (pr ? woff[1] : woff[0]) + tile;
-        wb = pr ? words[1] : words[0];
+        ktile = (uint32_t)(hr * tn + (pr ? col[1] : col[0]) + (t & 1));
         const int n = lane & 15, g = lane >> 4;
         t0p1 = (uint32_t)(32 * (n & 7) + 4 * (n >> 3) + 8 * g + 1);
         const uint32_t ta1 = t0p1 + 15u, ta2 = 2u * t0p1 + 15u;           // start + 31 at K = 1, 2
@@ -912,13 +913,13 @@ __device__ __forceinline__ void gateup_mix_body(const MoeArgs& a, const ItemDesc
     L.lds = stage;
     L.lane = lane;
     L.wl = wlds + wave * 8 * kMixTS;
+    const int pw = wave >> 1;                              // this wave's projection (gate, up), its 4 tile columns
+    L.apl = pw;
+    L.wrs = buffer_rsrc(reinterpret_cast<const void*>(d->tab[3 * pw]));
+    L.krs = buffer_rsrc(reinterpret_cast<const void*>(d->km[2 * pw]));
+    L.ors = buffer_rsrc(reinterpret_cast<const void*>(d->km[2 * pw + 1]));
 #pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-        L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[3 * pr]);
-        L.kmap[pr] = reinterpret_cast<const uint8_t*>(d->km[2 * pr]);
-        L.woff[pr] = reinterpret_cast<const int32_t*>(d->km[2 * pr + 1]);
-        L.col[pr] = nb * 8 + 2 * wave;
-    }
+    for (int pr = 0; pr < 2; ++pr) L.col[pr] = nb * 8 + 4 * (wave & 1) + 2 * pr;
     L.setup_a(cnt, [&](int p, int row) { return a.xh + ((size_t)(p0 + row) * 2 + p) * a.H; });
     f4_t acc[kMfT][RGA];
 #pragma unroll
@@ -941,11 +942,11 @@ __device__ __forceinline__ void down_mix_body(const MoeArgs& a, const ItemDesc* 
     L.lds = stage;
     L.lane = lane;
     L.wl = wlds + wave * 8 * kMixTS;
+    L.wrs = buffer_rsrc(reinterpret_cast<const void*>(d->tab[6]));
+    L.krs = buffer_rsrc(reinterpret_cast<const void*>(d->km[4]));
+    L.ors = buffer_rsrc(reinterpret_cast<const void*>(d->km[5]));
 #pragma unroll
     for (int pr = 0; pr < 2; ++pr) {
-        L.words[pr] = reinterpret_cast<const uint32_t*>(d->tab[6]);
-        L.kmap[pr] = reinterpret_cast<const uint8_t*>(d->km[4]);
-        L.woff[pr] = reinterpret_cast<const int32_t*>(d->km[5]);
         int ct = nb * 16 + 4 * wave + 2 * pr;
         L.col[pr] = ct < tn ? ct : tn - 2;             // a last half block: in-bounds loads, results unused
     }
@@ -1133,7 +1134,10 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_m
         ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
         return trk + (size_t)ct * (8 * K);
     });
-    L.setup_a(cnt, [&](int q, int row) { return a.xh + ((size_t)shard[q] * a.m + r0 + row) * a.k + kb0 * 128; });
+    L.setup_a(cnt, [&](int q, int row) {                 // a select, not an index: shard[] stays in registers
+        const int sq = (NPS > 1 && q != 0) ? shard[NPS - 1] : shard[0];
+        return a.xh + ((size_t)sq * a.m + r0 + row) * a.k + kb0 * 128;
+    });
     f4_t acc[kMfT][RGA];
 #pragma unroll
     for (int t = 0; t < kMfT; ++t)
