@@ -164,7 +164,7 @@ constexpr int kMfT = 4;                              // tile columns per wave
 
 // Workgroups per CU (= waves per SIMD) the grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row
 // groups). The 4-row-group uniform kernels take one more where their registers allow it without spills (168 VGPRs:
-// gate|up at K = 1, 2 and 4, down at K <= 4), and so does the 1-row-group per-tile down kernel (96 VGPRs).
+// gate|up at K = 1, 2 and 4, down at K <= 4); the 1-row-group per-tile kernels run five (96 VGPRs).
 #ifndef EXL3_MFMA_OCC1
 #define EXL3_MFMA_OCC1 4
 #endif
@@ -179,10 +179,9 @@ constexpr int kMfT = 4;                              // tile columns per wave
     ((RGA) == 4 && ((K) <= 2 || (K) == 4) ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
 #define EXL3_MFMA_DOWN_OCC(RGA, K) ((RGA) == 4 && (K) <= 4 ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
 #ifndef EXL3_MIX_OCC1
-#define EXL3_MIX_OCC1 4
+#define EXL3_MIX_OCC1 5
 #endif
 #define EXL3_MIX_OCC(RGA) ((RGA) == 1 ? EXL3_MIX_OCC1 : (RGA) == 2 ? 3 : 2)
-#define EXL3_MIX_DOWN_OCC(RGA) ((RGA) == 1 ? EXL3_MIX_OCC1 + 1 : EXL3_MIX_OCC(RGA))
 
 // 16-byte unit of (row, chunk) in one staged A plane (16 * RGA rows x four 16-byte chunks = 32 k); the chunk is
 // swizzled by row so that the 16 rows of a fragment read hit distinct banks.
@@ -704,7 +703,7 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 // with the tile's K at run time. Rings of 4 (first tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead) make
 // the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A is staged
 // as in MfmaPipe (four LDS stages written two steps ahead, a barrier every second step), but from a register ring of
-// two: loaded three steps ahead, stored one step later (the 1-row-group down kernel fits five waves per SIMD that way).
+// two: loaded three steps ahead, stored one step later (the 1-row-group kernels fit five waves per SIMD that way).
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
 
 
@@ -986,7 +985,7 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 }
 
 template <int RGA>
-__global__ __launch_bounds__(256, EXL3_MIX_DOWN_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     constexpr int kStage = 4 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
     __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];   // C aliases, as above
