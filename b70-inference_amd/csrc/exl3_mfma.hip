@@ -703,7 +703,8 @@ __device__ __forceinline__ h4_t decode4p_rt(const uint32_t* slot, int K, uint32_
 // with the tile's K at run time. Rings of 4 (first tile words DW - 1 = 2 steps ahead, (K, woff) DW = 3 steps ahead) make
 // the loop a 4-step unroll; the step count (H / 32 or I / 32, H and I multiples of 128) is a multiple of 4. A is staged
 // as in MfmaPipe (four LDS stages written two steps ahead, a barrier every second step), but from a register ring of
-// two: loaded three steps ahead, stored one step later (the 1-row-group kernels fit five waves per SIMD that way).
+// two: loaded three steps ahead, stored one step later (the 1-row-group kernels fit five waves per SIMD that way); with
+// one row group each wave stages its own plane in a private ring and the loop has no barrier.
 constexpr int kMixTSF = 20;                                 // compact slot: 3 pad, w(8K - 1), 16 words (K <= 2)
 
 
@@ -711,7 +712,11 @@ template <int NPS, int RGA>
 struct MfmaPipeMix {
     static constexpr int DW = 3;
     static constexpr int UNITS = NPS * RGA * 64;             // NPS staged A planes; a wave reads plane apl
-    static constexpr int CPT = (UNITS + 255) / 256;
+    // One row group: each wave stages its own plane (64 units, one per lane) in a private ring, so the loop needs no
+    // barrier; the loads and LDS writes are those of the shared ring, whose 256 threads stage its units twice or more.
+    static constexpr bool PRIV = RGA == 1;
+    static constexpr int SU = PRIV ? 64 : UNITS;             // 16-byte units per stage (of the wave's ring if PRIV)
+    static constexpr int CPT = PRIV ? 1 : (UNITS + 255) / 256;
     static constexpr int kNT = 2;                            // buffer-load cache policy: nontemporal
     __amdgpu_buffer_rsrc_t wrs, krs, ors;                    // the wave's projection: words, kmap, woff
     int col[2];                                              // per column pair: its first tile column (even)
@@ -776,7 +781,7 @@ struct MfmaPipeMix {
         const int g = lane >> 4;
 #pragma unroll
         for (int rg = 0; rg < RGA; ++rg) {
-            const u32x4_t* base = lds + stage * UNITS + apl * RGA * 64;
+            const u32x4_t* base = lds + stage * SU + (PRIV ? 0 : apl * RGA * 64);
             const int row = 16 * rg + (lane & 15);
             typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
             const u2_t v = {reinterpret_cast<const uint32_t*>(base + a_unit(row, 2 * sr))[g],
@@ -836,7 +841,7 @@ struct MfmaPipeMix {
     }
     __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
+        for (int j = 0; j < CPT; ++j) lds[stage * SU + adst[j]] = Ra[j];
     }
     // step s, R = s mod 4
     template <int R>
@@ -851,7 +856,9 @@ struct MfmaPipeMix {
         stage_w(W[R], M[R], fast, !fast && __builtin_amdgcn_ballot_w64(m0 > 4) != 0);
         compute(R, acc, m0, two, fast);
         store_a(RA[(R + 1) % 2], (R + 2) % 4);
-        if (R % 2 == 0) __syncthreads();
+        if constexpr (!PRIV) {
+            if (R % 2 == 0) __syncthreads();
+        }
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
         u32x4_t W[4];
@@ -880,14 +887,23 @@ struct MfmaPipeMix {
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
         const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if constexpr (PRIV) {                                // the wave's ring: lds + 4 stages * 64 units per wave
+            lds += wv * 4 * SU;
+            const int row = lane >> 2, ch = lane & 3;
+            const _Float16* b = rowptr(apl, 0);
+            abuf[0] = buffer_rsrc(b);
+            aoff[0] = (uint32_t)(2 * (rowptr(apl, row < cnt ? row : cnt - 1) + 8 * ch - b));
+            adst[0] = a_unit(row, ch);
+        } else {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
-            const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
-            const _Float16* b = rowptr(p, 0);
-            abuf[j] = buffer_rsrc(b);
-            aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
-            adst[j] = p * RGA * 64 + a_unit(row, ch);
+            for (int j = 0; j < CPT; ++j) {
+                const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
+                const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+                const _Float16* b = rowptr(p, 0);
+                abuf[j] = buffer_rsrc(b);
+                aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
+                adst[j] = p * RGA * 64 + a_unit(row, ch);
+            }
         }
         const int sl = lane >> 3, t = sl >> 1, hr = sl & 1, pr = t >> 1;
         ktile = (uint32_t)(hr * tn + (pr ? col[1] : col[0]) + (t & 1));
@@ -963,7 +979,7 @@ template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     // the epilogue's C reuses the pipeline's A stages and weight slots (dead once the pipeline has drained)
-    constexpr int kStage = 4 * 2 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 2 * 16 * 128 * 4;
+    constexpr int kStage = 4 * (RGA == 1 ? 4 : 2 * RGA) * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 2 * 16 * 128 * 4;
     __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];
     u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
     uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
@@ -987,7 +1003,7 @@ __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void gateup_mix_kernel(MoeA
 template <int RGA>
 __global__ __launch_bounds__(256, EXL3_MIX_OCC(RGA)) void down_mix_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    constexpr int kStage = 4 * RGA * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
+    constexpr int kStage = 4 * (RGA == 1 ? 4 : RGA) * 64 * 16, kW = 4 * 8 * kMixTS * 4, kC = 16 * 256 * 4;
     __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];   // C aliases, as above
     u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
     uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
