@@ -212,7 +212,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //            after its last read, with a barrier in between, and read at least one barrier after its write); memory-
 //            counter waits complete in issue order, so each step issues its A load before its weight load. With
 //            k-permuted fragments a row's 4-k units are staged in the order 0 2 1 3 4 6 5 7 (two 8-byte stores per
-//            16-byte unit), so that a lane's 16-byte read holds the k of its B fragment.
+//            16-byte unit), so that a lane's 16-byte read holds the k of its B fragment. With one row group and one
+//            plane read per wave, each wave stages its own plane in a private ring instead (one unit per lane, the
+//            loads and LDS writes of the shared ring, whose threads stage its units twice or more) and the loop has no
+//            barrier.
 template <int K, int NP, int RGA, int NPS = NP>
 struct MfmaPipe {
     static constexpr bool KP = K <= 5;                      // k-permuted fragments
@@ -221,7 +224,9 @@ struct MfmaPipe {
     static constexpr int TPP = kMfT / NP;
     static constexpr int TS = 8 * K + 4;                     // LDS words per staged tile
     static constexpr int UNITS = NPS * RGA * 64;             // 16-byte A units per stage (NPS staged planes)
-    static constexpr int CPT = (UNITS + 255) / 256;          // A units a thread stages per step
+    static constexpr bool PRIV = RGA == 1 && NP == 1;        // wave-private A ring
+    static constexpr int SU = PRIV ? 64 : UNITS;             // units per stage (of the wave's ring if PRIV)
+    static constexpr int CPT = PRIV ? 1 : (UNITS + 255) / 256;   // A units a thread stages per step
     const uint32_t* wsrc;                                    // this lane's K words at step 0
     uint32_t wstep;                                          // words between consecutive steps (two tile-rows)
     int nsteps;
@@ -235,7 +240,7 @@ struct MfmaPipe {
     uint32_t aoff[CPT];                                      // the wave shares, and the lane's byte offset in it
     int adst[CPT];                                           // k-permuted: 8-byte units of the low and high halves
     int adst2[CPT];
-    u32x4_t* lds;                                            // [2][UNITS]
+    u32x4_t* lds;                                            // [4][SU] (per wave if PRIV)
     int lane;
     int apl = 0;                                             // first staged plane this wave reads (NPS > NP)
 
@@ -289,7 +294,7 @@ struct MfmaPipe {
 #pragma unroll
             for (int rg = 0; rg < RGA; ++rg)
                 af[rg] = __builtin_bit_cast(
-                    h8_t, lds[stage * UNITS + (p + apl) * RGA * 64 + a_unit(16 * rg + (lane & 15), lane >> 4)]);
+                    h8_t, lds[stage * SU + (PRIV ? 0 : (p + apl) * RGA * 64) + a_unit(16 * rg + (lane & 15), lane >> 4)]);
 #pragma unroll
             for (int t = p * TPP; t < (p + 1) * TPP; ++t)
 #pragma unroll
@@ -306,7 +311,9 @@ struct MfmaPipe {
         stage_w(W[R % DW]);
         compute(R, acc);
         store_a(RA[(R + 1) % 2], (R + 2) % 4);
-        if (R % 2 == 0) __syncthreads();
+        if constexpr (!PRIV) {
+            if (R % 2 == 0) __syncthreads();
+        }
     }
     __device__ __forceinline__ void load_a(u32x4_t (&Ra)[CPT], int s) const {
         const int ss = (s < nsteps ? s : nsteps - 1) * 32;
@@ -318,7 +325,7 @@ struct MfmaPipe {
     __device__ __forceinline__ void store_a(const u32x4_t (&Ra)[CPT], int stage) const {
         if constexpr (KP) {
             typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
-            u2_t* l2 = reinterpret_cast<u2_t*>(lds) + 2 * stage * UNITS;
+            u2_t* l2 = reinterpret_cast<u2_t*>(lds) + 2 * stage * SU;
 #pragma unroll
             for (int j = 0; j < CPT; ++j) {
                 const u2_t lo = {Ra[j][0], Ra[j][1]}, hi = {Ra[j][2], Ra[j][3]};
@@ -327,7 +334,7 @@ struct MfmaPipe {
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < CPT; ++j) lds[stage * UNITS + adst[j]] = Ra[j];
+            for (int j = 0; j < CPT; ++j) lds[stage * SU + adst[j]] = Ra[j];
         }
     }
     __device__ __forceinline__ void run(f4_t (&acc)[kMfT][RGA]) const {
@@ -379,18 +386,20 @@ struct MfmaPipe {
     template <typename F>
     __device__ __forceinline__ void setup_a(int cnt, F rowptr) {
         const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        if constexpr (PRIV) lds += wv * 4 * SU;
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-            const int u0 = (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
+            const int u0 = PRIV ? apl * 64 : (64 * wv + 256 * j) % UNITS, u = u0 + (threadIdx.x & 63);
             const int p = u0 / (RGA * 64), rem = u - p * RGA * 64, row = rem >> 2, ch = rem & 3;
+            const int pd = PRIV ? 0 : p;                     // the unit's plane in the stage
             const _Float16* b = rowptr(p, 0);
             abuf[j] = buffer_rsrc(b);
             aoff[j] = (uint32_t)(2 * (rowptr(p, row < cnt ? row : cnt - 1) + 8 * ch - b));
             if constexpr (KP) {                              // 4-k units 2 ch, 2 ch + 1 -> 16-byte units
-                adst[j] = 2 * (p * RGA * 64 + a_unit(row, ch & 2)) + (ch & 1);       // (ch & 2) and (ch & 2) + 1,
-                adst2[j] = 2 * (p * RGA * 64 + a_unit(row, (ch & 2) + 1)) + (ch & 1); // half ch & 1
+                adst[j] = 2 * (pd * RGA * 64 + a_unit(row, ch & 2)) + (ch & 1);       // (ch & 2) and (ch & 2) + 1,
+                adst2[j] = 2 * (pd * RGA * 64 + a_unit(row, (ch & 2) + 1)) + (ch & 1); // half ch & 1
             } else {
-                adst[j] = p * RGA * 64 + a_unit(row, ch);
+                adst[j] = pd * RGA * 64 + a_unit(row, ch);
             }
         }
     }
@@ -501,7 +510,8 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * 2 * RGA * 64];        // [4 stages][2 planes][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * (RGA == 1 ? 4 : 2 * RGA) * 64];   // [4 stages][2 planes][16 RGA rows x 4 units],
+                                                                  // or per wave [4 stages][16 rows x 4 units]
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[2 * 16 * 128];
     __shared__ float rsum[2 * 64];
@@ -619,7 +629,8 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * RGA * 64];            // [4 stages][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * (RGA == 1 ? 4 : RGA) * 64];       // [4 stages][16 RGA rows x 4 units] (per wave
+                                                                  // at one row group)
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
     __shared__ float rsum[64];
@@ -1099,7 +1110,8 @@ __device__ __forceinline__ void linear_store(const LinArgs& a, int row, int col,
 // are staged and waves 0, 1 (first half) read plane 0, waves 2, 3 plane 1.
 template <int K, int RGA, int NPS>
 __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_mfma_kernel(LinArgs a) {
-    __shared__ u32x4_t stage[4 * NPS * RGA * 64];      // [4 stages][planes][16 RGA rows x 4 units]
+    __shared__ u32x4_t stage[4 * (RGA == 1 ? 4 : NPS * RGA) * 64];   // [4 stages][planes][16 RGA rows x 4 units]
+                                                                    // (per wave at one row group)
     __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
     __shared__ float C[16 * 256];
     __shared__ float rsum[NPS][16 * RGA];
