@@ -164,7 +164,8 @@ constexpr int kMfT = 4;                              // tile columns per wave
 
 // Workgroups per CU (= waves per SIMD) the grouped GEMM kernels are compiled for, by row class (1, 2 or 4 row
 // groups). The 4-row-group uniform kernels take one more where their registers allow it without spills (168 VGPRs:
-// gate|up at K = 1, 2 and 4, down at K <= 4); the 1-row-group per-tile kernels run five (96 VGPRs).
+// gate|up at K = 1, 2 and 4, down at K <= 4); the 1-row-group kernels run five (96 VGPRs; uniform K up to 4, above
+// which they would spill), their epilogue buffer aliasing the pipeline's LDS so that five fit.
 #ifndef EXL3_MFMA_OCC1
 #define EXL3_MFMA_OCC1 4
 #endif
@@ -174,10 +175,15 @@ constexpr int kMfT = 4;                              // tile columns per wave
 #ifndef EXL3_MFMA_OCC4
 #define EXL3_MFMA_OCC4 2
 #endif
+#ifndef EXL3_MFMA_OCC1_KMAX
+#define EXL3_MFMA_OCC1_KMAX 4
+#endif
 #define EXL3_MFMA_OCC(RGA) ((RGA) == 1 ? EXL3_MFMA_OCC1 : (RGA) == 2 ? EXL3_MFMA_OCC2 : EXL3_MFMA_OCC4)
 #define EXL3_MFMA_GU_OCC(RGA, K) \
-    ((RGA) == 4 && ((K) <= 2 || (K) == 4) ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
-#define EXL3_MFMA_DOWN_OCC(RGA, K) ((RGA) == 4 && (K) <= 4 ? EXL3_MFMA_OCC4 + 1 : EXL3_MFMA_OCC(RGA))
+    ((RGA) == 4 && ((K) <= 2 || (K) == 4) ? EXL3_MFMA_OCC4 + 1 : (RGA) == 1 && (K) <= EXL3_MFMA_OCC1_KMAX ? 5 \
+                                                                   : EXL3_MFMA_OCC(RGA))
+#define EXL3_MFMA_DOWN_OCC(RGA, K) \
+    ((RGA) == 4 && (K) <= 4 ? EXL3_MFMA_OCC4 + 1 : (RGA) == 1 && (K) <= EXL3_MFMA_OCC1_KMAX ? 5 : EXL3_MFMA_OCC(RGA))
 #ifndef EXL3_MIX_OCC1
 #define EXL3_MIX_OCC1 5
 #endif
@@ -358,6 +364,7 @@ struct MfmaPipe {
         if (s < nsteps) step<0>(s, W, RA, acc);
         if (s + 1 < nsteps) step<1>(s + 1, W, RA, acc);
         if (s + 2 < nsteps) step<2>(s + 2, W, RA, acc);
+        __syncthreads();                                 // every wave's last LDS read done: callers may reuse it
     }
     // weight set-up: pair_base(pair) = the pair's first tile (tile-row 0) in words; tile-rows are tn * 8K words apart
     template <typename F>
@@ -510,10 +517,13 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * (RGA == 1 ? 4 : 2 * RGA) * 64];   // [4 stages][2 planes][16 RGA rows x 4 units],
-                                                                  // or per wave [4 stages][16 rows x 4 units]
-    __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
-    __shared__ float C[2 * 16 * 128];
+    // A stages [4][2 planes][16 RGA rows x 4 units] (or per wave [4][16 rows x 4 units]) and per wave 8 staged tiles;
+    // the epilogue's C reuses them (dead once the pipeline has drained)
+    constexpr int kStage = 4 * (RGA == 1 ? 4 : 2 * RGA) * 64 * 16, kW = 4 * 8 * (8 * K + 4) * 4, kC = 2 * 16 * 128 * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];
+    u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
+    uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
+    float* C = reinterpret_cast<float*>(smem);
     __shared__ float rsum[2 * 64];
     const int nbI = a.I / 128;
     int idx, nb;
@@ -629,10 +639,12 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
 template <int K, int RGA>
 __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
-    __shared__ u32x4_t stage[4 * (RGA == 1 ? 4 : RGA) * 64];       // [4 stages][16 RGA rows x 4 units] (per wave
-                                                                  // at one row group)
-    __shared__ uint32_t wlds[4 * 8 * (8 * K + 4)];       // per wave: 8 staged tiles
-    __shared__ float C[16 * 256];
+    // A stages [4][16 RGA rows x 4 units] (per wave at one row group) and per wave 8 staged tiles; C aliases, as above
+    constexpr int kStage = 4 * (RGA == 1 ? 4 : RGA) * 64 * 16, kW = 4 * 8 * (8 * K + 4) * 4, kC = 16 * 256 * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kStage + kW > kC ? kStage + kW : kC];
+    u32x4_t* stage = reinterpret_cast<u32x4_t*>(smem);
+    uint32_t* wlds = reinterpret_cast<uint32_t*>(smem + kStage);
+    float* C = reinterpret_cast<float*>(smem);
     __shared__ float rsum[64];
     __shared__ int s_comb[2 * 64];
     const int nbH2 = (a.H / 128 + 1) / 2;
