@@ -97,7 +97,8 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Workgroup (row block, y < H / 128): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128), fp16 (the
+// Workgroup (y < H / 128, row block) (y the fast grid dimension, so a block's workgroups, which exit at once past
+// its units, are dispatched together rather than as one tail of exiting workgroups): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128), fp16 (the
 // GEMM inputs xh) and their block sums (xsum). Each wave takes one unit (128-column block kb, 16-row group): the
 // block's nrg = ceil(rows / 16) row groups of the workgroup's column blocks, so a block of up to 16 rows has its four
 // waves on four column blocks (and three quarters of its workgroups exit at once) instead of three idle waves. A
@@ -108,14 +109,14 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     __shared__ int s_tok[kMfmaRows];
     __shared__ __attribute__((aligned(16))) _Float16 s_out[4][16][136];    // per wave: 16 rows x 128 (+ pad)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int blk = blockIdx.x;
+    const int blk = blockIdx.y, y = blockIdx.x;
     const ItemDesc* d = a.blocks + blk;
     const int cnt = d->cnt;
     if (cnt == 0) return;
     const int p0 = d->p0;
     const int nblk = a.H / 128;
-    const int nrg = (cnt + 15) >> 4, u = 4 * (int)blockIdx.y + wave;   // unit u: column block u / nrg, group u % nrg
-    if (4 * (int)blockIdx.y >= nrg * nblk) return;                      // uniform: the whole workgroup leaves
+    const int nrg = (cnt + 15) >> 4, u = 4 * y + wave;                  // unit u: column block u / nrg, group u % nrg
+    if (4 * y >= nrg * nblk) return;                                    // uniform: the whole workgroup leaves
     if (threadIdx.x < cnt) s_tok[threadIdx.x] = a.pair_tok[p0 + threadIdx.x];
     __syncthreads();
     if (u >= nrg * nblk) return;
@@ -1278,7 +1279,7 @@ static int fork3(hipStream_t st, F launch) {
 // classes are combined by the last slot to finish), so one class's down pass overlaps the others' gate|up.
 int launch_moe_mfma(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
-    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.max_blocks, a.H / 128), dim3(256), 0, st, a);
+    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.H / 128, a.max_blocks), dim3(256), 0, st, a);
     const dim3 grid_gu(nxb * (a.I / 128)), grid_dn(nxb * ((a.H / 128 + 1) / 2));
     return fork3(st, [&](int rga, hipStream_t s) -> int {
         mfma_fn gu = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)

@@ -46,6 +46,8 @@ struct RouteArgs {
     void* out;
     int64_t out_ld;
     int out_f32, H;
+    int held;                          // align_kernel: each thread holds its (at most 8) pairs in registers and
+                                       // counts the tokens' valid slots in LDS (M more ints of dynamic LDS)
 };
 
 constexpr int kFusedRouteMaxE = 512;    // logits per row that the fused layer's in-layer routing handles (8 per lane)

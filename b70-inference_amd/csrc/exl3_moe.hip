@@ -105,6 +105,9 @@ __device__ __forceinline__ void load_pairs(const RouteArgs& r, int i0, int strid
     }
 }
 
+// The memory round trips are the kernel's cost, so with held pairs (np <= 8 * 1024) every load is issued at the start:
+// the thread's pairs (kept in registers for the scatter) and its first expert's table entries; the tokens' valid
+// slots are counted in LDS with the experts' rows instead of reloading each token's slots.
 __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     extern __shared__ int sm[];
     int* cnt = sm;                 // [E]
@@ -113,23 +116,47 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     int* nch = sm + 3 * r.E;       // [E] GEMV items of the expert, then their first index
     int* nbl = sm + 4 * r.E;       // [E] MFMA blocks of the expert, then their first index
     int* tmp = sm + 5 * r.E;       // [1024]
+    int* tokn = sm + 5 * r.E + 1024;   // [M] valid slots per token (held pairs)
     __shared__ int s_cls[3];
     const int t = threadIdx.x, T = blockDim.x;
     if (t < 3) s_cls[t] = 0;
     const int np = r.M * r.slots;
     const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
+    int hev[8];
+    float hwv[8];
+    if (r.held) load_pairs<8>(r, t, T, np, hev, hwv);
+    // this thread's first expert's table entries (index clamped: unconditional loads)
+    int64_t tb0[9], km0[6];
+    {
+        const int ec = t < r.E ? t : r.E - 1;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) tb0[i] = r.items ? ldg(r.tables + (int64_t)i * r.E + ec) : 0;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) km0[i] = r.items && r.kmaps ? ldg(r.kmaps + (int64_t)i * r.E + ec) : 0;
+    }
     for (int e = t; e < r.E; e += T) {
         cnt[e] = 0;
         fill[e] = 0;
     }
+    if (r.held)
+        for (int m = t; m < r.M; m += T) tokn[m] = 0;
     __syncthreads();
-    for (int i0 = t; i0 < np; i0 += 8 * T) {
-        int ev[8];
-        float wv[8];
-        load_pairs<8>(r, i0, T, np, ev, wv);
+    if (r.held) {
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-            if (ev[k] >= 0) atomicAdd(&cnt[ev[k]], 1);
+            if (hev[k] >= 0) {
+                atomicAdd(&cnt[hev[k]], 1);
+                atomicAdd(&tokn[(t + k * T) / r.slots], 1);
+            }
+    } else {
+        for (int i0 = t; i0 < np; i0 += 8 * T) {
+            int ev[8];
+            float wv[8];
+            load_pairs<8>(r, i0, T, np, ev, wv);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (ev[k] >= 0) atomicAdd(&cnt[ev[k]], 1);
+        }
     }
     __syncthreads();
     for (int e = t; e < r.E; e += T) {
@@ -148,13 +175,13 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         if (r.counts) r.counts[e] = c;
         if (!r.items || c == 0) continue;
         const bool big = r.use_mfma && c > r.MR;
-        // the expert's table entries, loaded once for all of its blocks / items
+        // the expert's table entries, loaded once for all of its blocks / items (the first expert's at the start)
         int64_t tb[9], km[6];
 #pragma unroll
-        for (int i = 0; i < 9; ++i) tb[i] = ldg(r.tables + (int64_t)i * r.E + e);
+        for (int i = 0; i < 9; ++i) tb[i] = e == t ? tb0[i] : ldg(r.tables + (int64_t)i * r.E + e);
         if (r.kmaps) {
 #pragma unroll
-            for (int i = 0; i < 6; ++i) km[i] = ldg(r.kmaps + (int64_t)i * r.E + e);
+            for (int i = 0; i < 6; ++i) km[i] = e == t ? km0[i] : ldg(r.kmaps + (int64_t)i * r.E + e);
         } else {
 #pragma unroll
             for (int i = 0; i < 6; ++i) km[i] = 0;
@@ -190,12 +217,16 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     if (r.tok_nvalid) {
         for (int tok = t; tok < r.M; tok += T) {
             int nv = 0;
-            for (int j0 = 0; j0 < r.slots; j0 += 8) {
-                int ev[8];
-                float wv[8];
-                load_pairs<8>(r, tok * r.slots + j0, 1, tok * r.slots + r.slots, ev, wv);
+            if (r.held) {
+                nv = tokn[tok];
+            } else {
+                for (int j0 = 0; j0 < r.slots; j0 += 8) {
+                    int ev[8];
+                    float wv[8];
+                    load_pairs<8>(r, tok * r.slots + j0, 1, tok * r.slots + r.slots, ev, wv);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) nv += ev[k] >= 0;
+                    for (int k = 0; k < 8; ++k) nv += ev[k] >= 0;
+                }
             }
             r.tok_nvalid[tok] = nv;
             if (nv == 0) {
@@ -210,7 +241,15 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     for (int i0 = t; i0 < np; i0 += 8 * T) {
         int ev[8];
         float wv[8];
-        load_pairs<8>(r, i0, T, np, ev, wv);
+        if (r.held) {                  // i0 == t: the pairs loaded at the start
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                ev[k] = hev[k];
+                wv[k] = hwv[k];
+            }
+        } else {
+            load_pairs<8>(r, i0, T, np, ev, wv);
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = i0 + k * T;
@@ -815,8 +854,11 @@ int launch_align(const RouteArgs& r, hipStream_t st) {
         EXL3_LAUNCH("moe_align", align_small_kernel, dim3(1), dim3(kAlignSmall), 0, st, r);
         return EXL3_OK;
     }
-    const size_t lds = align_lds_bytes(r.E);
-    EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), lds, st, r);
+    // held pairs when every pair fits the threads' registers and the token counts fit the 64 KB of dynamic LDS
+    RouteArgs h = r;
+    const size_t lds0 = align_lds_bytes(r.E), ldsh = lds0 + (size_t)r.M * sizeof(int);
+    h.held = (int64_t)r.M * r.slots <= 8 * 1024 && ldsh <= 65536;
+    EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), h.held ? ldsh : lds0, st, h);
     return EXL3_OK;
 }
 
@@ -1092,7 +1134,8 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
     if (mi > npairs) mi = npairs;
     a.max_items = (int)mi;
     a.max_blocks = mfma ? (int)(npairs / kMfmaRows + (E < npairs ? E : npairs) + 1) : 0;
-    EXL3_CHECK_ARG((int64_t)a.max_items * (a.H / 128) < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
+    EXL3_CHECK_ARG((int64_t)a.max_items * (a.H / 128) < 0x7FFFFFFF && a.max_blocks <= 65535,
+                   "exl3_moe_forward: grid too large");
     return moe_decode_path(a, npairs, st);
 }
 

@@ -391,8 +391,16 @@ def measure(name, wl, steps, cpu=True):
          "kernels": {k: {"launches_per_step": round(n / nprof, 2), "avg_us": round(t, 3)} for k, (n, t) in prof.items()}}
     if isinstance(wl, MoE):
         r["unique_experts"] = round(sum(wl.unique(j) for j in range(steps)) / steps, 2)
-    # dominant kernel: most time per step
-    dom = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])[0] if prof else None
+    # dominant kernel: most time per step; for an MFMA-bound workload the kernel with the most FLOP per step (the
+    # row-class kernels of a prefill layer run concurrently, and the longest-running one is the class of cold experts
+    # with the least matrix work)
+    def flop_per_step(name):
+        w = [wl.kernel_work(name, j) for j in range(nprof)]
+        return sum(x[1] for x in w) if all(x is not None for x in w) else -1.0
+    if prof and getattr(wl, "bound", "hbm") == "mfma":
+        dom = max(prof, key=flop_per_step)
+    else:
+        dom = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])[0] if prof else None
     work = [wl.kernel_work(dom, j) for j in range(nprof)] if dom else []
     if work and all(w is not None for w in work):
         k_n, k_us = prof[dom]

@@ -261,22 +261,25 @@ def test_moe_c3_full_size(exl3, oracle):
         assert max_rel(y2.cpu().numpy(), ref) <= MAX_REL, M
 
 
-def test_align_tables(exl3, oracle):
-    ids, w = _ids_w(9, 4, 16, 1000, dup=True, inactive=True)
-    counts, ptok, pw, pof = exl3.moe_align(ids.cuda(), w.cuda(), 16, shared=-1)
+@pytest.mark.parametrize("M,k,E", [(9, 4, 16), (300, 4, 37), (2600, 4, 37)])
+def test_align_tables(exl3, oracle, M, k, E):
+    """Up to 256 pairs take the one-thread-per-pair kernel, more the 1024-thread one: with the pairs held in
+    registers (300 x 4) and reloaded per phase (2600 x 4 = 10400 pairs, more than 8 per thread)."""
+    ids, w = _ids_w(M, k, E, 1000 + M, dup=True, inactive=True)
+    counts, ptok, pw, pof = exl3.moe_align(ids.cuda(), w.cuda(), E, shared=-1)
     counts, ptok, pw, pof = (t.cpu().numpy() for t in (counts, ptok, pw, pof))
-    ref = oracle.align(ids.numpy(), w.numpy(), 16)
+    ref = oracle.align(ids.numpy(), w.numpy(), E)
     assert np.array_equal(counts, ref["count"])
     flat = ids.numpy().reshape(-1)
+    wf = w.numpy().reshape(-1)
     starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
-    for i, e in enumerate(flat):
-        if e < 0:
-            assert pof[i] == -1
-            continue
-        assert starts[e] <= pof[i] < starts[e] + counts[e]      # grouped by expert
-        assert ptok[pof[i]] == i // 4 and pw[pof[i]] == w.numpy().reshape(-1)[i]
-    valid = pof[pof >= 0]
-    assert np.unique(valid).size == valid.size == counts.sum()
+    valid_i = np.nonzero(flat >= 0)[0]
+    assert (pof[flat < 0] == -1).all()
+    pv = pof[valid_i]
+    e = flat[valid_i]
+    assert ((starts[e] <= pv) & (pv < starts[e] + counts[e])).all()      # grouped by expert
+    assert (ptok[pv] == valid_i // k).all() and (pw[pv] == wf[valid_i]).all()
+    assert np.unique(pv).size == pv.size == counts.sum()
 
 
 def test_router_ties_bias_and_sizes(exl3, oracle):
