@@ -134,9 +134,12 @@ def graph_time(fns):
     return e0.elapsed_time(e1) * 1e3 / len(fns)
 
 
-def kernel_profile(fns):
+def kernel_profile(fns, warm=()):
     """Eager run of fns with the library's event profiler (a HIP event pair recorded with each dispatch on its own
-    stream): {kernel: (launches, avg us)}."""
+    stream): {kernel: (launches, avg us)}. The `warm` calls run first, unprofiled (eager launches of microsecond
+    kernels right after a graph replay otherwise read slow)."""
+    for f in warm:
+        f()
     torch.cuda.synchronize()
     exl3._lib.profile_enable(True)
     for f in fns:
@@ -378,7 +381,7 @@ def measure(name, wl, steps, cpu=True):
         f()
     us = graph_time(fns)
     nprof = min(steps, 16)
-    prof = kernel_profile([wl.step_fn(j) for j in range(nprof)])
+    prof = kernel_profile([wl.step_fn(j) for j in range(nprof)], [wl.step_fn(nprof + j) for j in range(nprof)])
     byts = sum(wl.bytes_per_step(j) for j in range(steps)) / steps
     flops = sum(wl.flops_per_step(j) for j in range(steps)) / steps
     wts = sum(wl.weights_per_step(j) for j in range(steps)) / steps
