@@ -197,20 +197,22 @@ __device__ __forceinline__ int popc_range(uint64_t lo, uint64_t hi, int b, int n
 // accesses in order).
 template <int MR>
 __device__ __forceinline__ void group_pairs(const FusedArgs& a, int lane, Groups& g, int* ge, const int* rid) {
-    const int np = a.np;
     const int l1 = lane + 64;
     g.e0 = pair_expert(a, lane, rid);
     g.e1 = pair_expert(a, l1, rid);
-    ge[lane] = g.e0;
-    ge[l1] = g.e1;
     int bf0 = 0, bf1 = 0;
-    for (int q4 = 0; q4 < np; q4 += 4) {          // entries past np are -1 and only match lanes without a pair
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ge + q4);
+    // one row per item: every valid pair starts an item, so no pair needs its index among its expert's pairs
+    if constexpr (MR > 1) {
+        ge[lane] = g.e0;
+        ge[l1] = g.e1;
+        for (int q4 = 0; q4 < a.np; q4 += 4) {        // entries past np are -1 and only match lanes without a pair
+            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ge + q4);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int eq = (int)v[k], q = q4 + k;
-            bf0 += (eq == g.e0) & (q < lane);
-            bf1 += (eq == g.e1) & (q < l1);
+            for (int k = 0; k < 4; ++k) {
+                const int eq = (int)v[k], q = q4 + k;
+                bf0 += (eq == g.e0) & (q < lane);
+                bf1 += (eq == g.e1) & (q < l1);
+            }
         }
     }
     g.bf0 = bf0;
@@ -235,8 +237,7 @@ __device__ __forceinline__ void item_info(const FusedArgs& a, const Groups& g, i
     const int p = s0 ? ctz64(s0) : 64 + ctz64(s1);
     const int e = p < 64 ? __builtin_amdgcn_readlane(g.e0, p) : __builtin_amdgcn_readlane(g.e1, p - 64);
     const int bfp = p < 64 ? __builtin_amdgcn_readlane(g.bf0, p) : __builtin_amdgcn_readlane(g.bf1, p - 64);
-    const int ce = popc64(__ballot(g.e0 == e)) + popc64(__ballot(g.e1 == e));
-    const int cnt = min(MR, ce - bfp);
+    const int cnt = MR == 1 ? 1 : min(MR, popc64(__ballot(g.e0 == e)) + popc64(__ballot(g.e1 == e)) - bfp);
     if (lane == 0) {
         s.it_e = e;
         s.it_cnt = cnt;
@@ -253,10 +254,14 @@ __device__ __forceinline__ void item_info(const FusedArgs& a, const Groups& g, i
         s.tab[lane] = a.uniform ? b + (int64_t)e * st : ldg(a.tables + (int64_t)lane * a.E + e);
     }
     if (K == 0 && lane < 6) s.km[lane] = ldg(a.kmaps + (int64_t)lane * a.E + e);
+    if constexpr (MR == 1) {
+        if (lane == 0) s.rows[0] = p;                    // the item is its first pair
+    } else {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        const uint64_t r0 = __ballot(g.e0 == e && g.bf0 == bfp + m), r1 = __ballot(g.e1 == e && g.bf1 == bfp + m);
-        if (lane == 0) s.rows[m] = m < cnt ? (r0 ? ctz64(r0) : 64 + ctz64(r1)) : 0;
+        for (int m = 0; m < MR; ++m) {
+            const uint64_t r0 = __ballot(g.e0 == e && g.bf0 == bfp + m), r1 = __ballot(g.e1 == e && g.bf1 == bfp + m);
+            if (lane == 0) s.rows[m] = m < cnt ? (r0 ? ctz64(r0) : 64 + ctz64(r1)) : 0;
+        }
     }
 }
 
