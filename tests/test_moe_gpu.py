@@ -430,6 +430,23 @@ def test_moe_prefill_per_tile_k_1_2_3(exl3, oracle):
     assert max_rel(y, ref) <= MAX_REL
 
 
+def test_moe_prefill_many_blocks(exl3, oracle):
+    """1100 experts (1200 pairs, more than a thousand row blocks, one expert with 40 rows): the prefill path's
+    tables and grids at that size; rows checked against the oracle."""
+    E, H, I = 1100, 128, 128
+    tables, orc = make_experts(exl3, oracle, E, H, I, 2, 2, 2100)
+    M = 600
+    g = torch.Generator().manual_seed(2101)
+    ids = torch.stack([torch.randperm(E, generator=g)[:2] for _ in range(M)]).to(torch.int32)
+    ids[:40, 0] = 7                                      # one expert with 40 rows (a 3-row-group block)
+    ids[:40, 1] = torch.where(ids[:40, 1] == 7, torch.full_like(ids[:40, 1], 8), ids[:40, 1])
+    w = torch.rand(M, 2, generator=g)
+    w = (w / w.sum(1, keepdim=True)).float()
+    x = torch.randn(M, H, generator=g).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
 def test_moe_prefill_deterministic_and_token_permutation(exl3, small):
     """Row results do not depend on which other rows share a block: permuting the tokens permutes the output rows
     bit for bit, and two calls agree exactly."""
