@@ -662,10 +662,11 @@ __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_ker
 }
 
 // ------------------------------------------------------------------------------------------------ per-tile K
-// Per-tile bitrate (K = 0: tile i of a projection holds 8 kmap[i] words at woff[i]). MFMA 16x16x16 per tile-row, so
-// the 64 lanes of a wave always share one tile and its K is wave-uniform. Fragment layout: B[k][n] lane L holds
-// n = L & 15, k = 4 (L >> 4) + j, j < 4; A[m][k] lane L holds m = L & 15, same k; D[m][n] n = L & 15,
-// m = 4 (L >> 4) + i (the tile rows behind the k slots are permuted, see decode4p).
+// Per-tile bitrate (K = 0: tile i of a projection holds 8 kmap[i] words at woff[i]). Each lane decodes 4 k of one
+// tile, so the 64 lanes of a wave always share one tile and its K is wave-uniform. Fragment layout (16x16x16): B[k][n]
+// lane L holds n = L & 15, k = 4 (L >> 4) + j, j < 4; A[m][k] lane L holds m = L & 15, same k; D[m][n] n = L & 15,
+// m = 4 (L >> 4) + i (the tile rows behind the k slots are permuted, see decode4p). Steps whose tiles are all K <= 2
+// join the two tile-rows of a column in one 16x16x32 MFMA (8 k per lane: 4 of each tile).
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 constexpr int kMixKMax = 8;
 constexpr int kMixTS = 8 * kMixKMax + 4;                    // LDS words per staged tile: 3 pad, w(8K - 1), 64 words
@@ -816,28 +817,33 @@ struct MfmaPipeMix {
     // slot sl = 2 t + sr holds tile column t (pair t >> 1, parity t & 1) of tile-row half sr; m0 = this lane's K
     __device__ __forceinline__ void compute(int stage, f4_t (&acc)[kMfT][RGA], int m0, uint64_t two, bool fast) const {
         if (fast) {
+            // both tile-row halves in one 16x16x32 MFMA per tile column: lane group g's eight k slots are its four of
+            // half 0 then its four of half 1, in A and B alike
+            h4_t af[2][RGA];
+            load_af(stage, 0, af[0]);
+            load_af(stage, 1, af[1]);
 #pragma unroll
-            for (int sr = 0; sr < 2; ++sr) {
-                h4_t af[RGA];
-                load_af(stage, sr, af);
-                uint32_t wlo[kMfT], whi[kMfT];                   // the tiles' funnel words, all reads issued first
+            for (int t = 0; t < kMfT; ++t) {
+                uint32_t whi[2], wlo[2];                         // the two tiles' funnel words, both reads issued first
 #pragma unroll
-                for (int t = 0; t < kMfT; ++t) {
+                for (int sr = 0; sr < 2; ++sr) {
                     const int sl = 2 * t + sr;
                     const bool k2 = (two >> (8 * sl)) & 1;       // wave-uniform select
                     const lds_cu32_t o = (lds_cu32_t)(k2 ? fa2 : fa1);
-                    whi[t] = o[sl * kMixTSF];
-                    wlo[t] = o[sl * kMixTSF + 1];
+                    whi[sr] = o[sl * kMixTSF];
+                    wlo[sr] = o[sl * kMixTSF + 1];
                 }
+                h4_t bf[2];
 #pragma unroll
-                for (int t = 0; t < kMfT; ++t) {
-                    const int sl = 2 * t + sr;
-                    const bool k2 = (two >> (8 * sl)) & 1;
-                    const uint32_t F = __builtin_amdgcn_alignbit(whi[t], wlo[t], k2 ? sh2 : sh1);
-                    const h4_t bf = decode4p12(F, k2);
+                for (int sr = 0; sr < 2; ++sr) {
+                    const bool k2 = (two >> (8 * (2 * t + sr))) & 1;
+                    bf[sr] = decode4p12(__builtin_amdgcn_alignbit(whi[sr], wlo[sr], k2 ? sh2 : sh1), k2);
+                }
+                const h8_t b8 = __builtin_shufflevector(bf[0], bf[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-                    for (int rg = 0; rg < RGA; ++rg)
-                        acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(af[rg], bf, acc[t][rg], 0, 0, 0);
+                for (int rg = 0; rg < RGA; ++rg) {
+                    const h8_t a8 = __builtin_shufflevector(af[0][rg], af[1][rg], 0, 1, 2, 3, 4, 5, 6, 7);
+                    acc[t][rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, b8, acc[t][rg], 0, 0, 0);
                 }
             }
         } else {
