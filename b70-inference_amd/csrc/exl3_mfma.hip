@@ -97,33 +97,36 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-// Workgroup (y < H / 128, row block) (y the fast grid dimension, so a block's workgroups, which exit at once past
-// its units, are dispatched together rather than as one tail of exiting workgroups): every row's x block times suh_gate and suh_up, Hadamard / sqrt(128), fp16 (the
-// GEMM inputs xh) and their block sums (xsum). Each wave takes one unit (128-column block kb, 16-row group): the
-// block's nrg = ceil(rows / 16) row groups of the workgroup's column blocks, so a block of up to 16 rows has its four
-// waves on four column blocks (and three quarters of its workgroups exit at once) instead of three idle waves. A
-// fragments are fp16(x * suh) (packed fp16 multiplies, one rounding: the reference's fp16(x * suh)), the Hadamard is
-// 8 output tiles x 4 k-steps of v_mfma_f32_16x16x32_f16 against the two base fragments (fp32 accumulation of exact
-// +-x products), and the sums of the fp16-rounded outputs reduce over the 16 lanes of a row.
+// One wave per job (16 consecutive pairs of the expert-sorted order, 128-column block kb; jobs row group major, four
+// per workgroup): every row's x block times its expert's suh_gate and suh_up, Hadamard / sqrt(128), fp16 (the GEMM
+// inputs xh) and their block sums (xsum). Rows are independent here, so a job's rows may belong to several experts
+// and no job is empty: the rows' tokens and experts come from the pair arrays in one round trip (no block
+// descriptor), then x and the signs in the next. A fragments are fp16(x * suh) (packed fp16 multiplies, one rounding:
+// the reference's fp16(x * suh)), the Hadamard is 8 output tiles x 4 k-steps of v_mfma_f32_16x16x32_f16 against the
+// two base fragments (fp32 accumulation of exact +-x products), and the sums of the fp16-rounded outputs reduce over
+// the 16 lanes of a row.
 __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
-    __shared__ int s_tok[kMfmaRows];
     __shared__ __attribute__((aligned(16))) _Float16 s_out[4][16][136];    // per wave: 16 rows x 128 (+ pad)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int blk = blockIdx.y, y = blockIdx.x;
-    const ItemDesc* d = a.blocks + blk;
-    const int cnt = d->cnt;
-    if (cnt == 0) return;
-    const int p0 = d->p0;
-    const int nblk = a.H / 128;
-    const int nrg = (cnt + 15) >> 4, u = 4 * y + wave;                  // unit u: column block u / nrg, group u % nrg
-    if (4 * y >= nrg * nblk) return;                                    // uniform: the whole workgroup leaves
-    if (threadIdx.x < cnt) s_tok[threadIdx.x] = a.pair_tok[p0 + threadIdx.x];
-    __syncthreads();
-    if (u >= nrg * nblk) return;
-    const int kb = u / nrg, r0 = 16 * (u - kb * nrg);
+    const int nblk = a.H / 128, np = a.M * a.slots;
+    const int job = 4 * blockIdx.x + wave, rg = job / nblk, kb = job - rg * nblk, r0 = 16 * rg;
+    if (r0 >= np) return;                                    // past the last row group (uniform)
     const int m = lane & 15, g = lane >> 4;
-    const int row = r0 + m < cnt ? r0 + m : cnt - 1;          // rows past cnt repeat the last one (not stored)
-    const uint16_t* xr = a.x + (int64_t)s_tok[row] * a.x_ld + kb * 128 + 8 * g;
+    const int p = r0 + m < np ? r0 + m : np - 1;
+    const int tok = a.pair_tok[p], e = a.pair_e[p];
+    const bool valid = r0 + m < np && e >= 0;
+    const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(valid) & 0xFFFFu;   // rows of this job to store
+    if (vmask == 0) return;
+    const int ec = valid ? e : 0;
+    const uint16_t* sgn[2];
+    if (a.uniform) {
+        sgn[0] = reinterpret_cast<const uint16_t*>(a.tb[1] + (int64_t)ec * a.ts[1]);
+        sgn[1] = reinterpret_cast<const uint16_t*>(a.tb[4] + (int64_t)ec * a.ts[4]);
+    } else {
+        sgn[0] = reinterpret_cast<const uint16_t*>(ldg(a.tables + (int64_t)1 * a.E + ec));
+        sgn[1] = reinterpret_cast<const uint16_t*>(ldg(a.tables + (int64_t)4 * a.E + ec));
+    }
+    const uint16_t* xr = a.x + (int64_t)(valid ? tok : 0) * a.x_ld + kb * 128 + 8 * g;
     const bool vx = ((uintptr_t)a.x & 15) == 0 && (a.x_ld & 7) == 0;
     h8_t xv[4];
 #pragma unroll
@@ -131,20 +134,21 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     const h8_t F[2] = {had_fragment(lane, 0), had_fragment(lane, 1)};
 #pragma unroll
     for (int proj = 0; proj < 2; ++proj) {
-        const uint16_t* sv = reinterpret_cast<const uint16_t*>(d->tab[proj ? 4 : 1]) + kb * 128 + 8 * g;
+        const uint16_t* sv = sgn[proj] + kb * 128 + 8 * g;
+        const bool vs = __builtin_amdgcn_ballot_w64(((uintptr_t)sv & 15) != 0) == 0;   // every row 16-byte aligned
         float part[4];
-        had16_rows(xv, sv, ((uintptr_t)sv & 15) == 0, F, lane, s_out[wave], part);
+        had16_rows(xv, sv, vs, F, lane, s_out[wave], part);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {                   // 16-byte row stores from the tile
             const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;
             const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_out[wave][rr][8 * ch]);
-            if (r0 + rr < cnt)
-                *reinterpret_cast<u32x4_t*>(a.xh + ((size_t)(p0 + r0 + rr) * 2 + proj) * a.H + kb * 128 + 8 * ch) = v;
+            if ((vmask >> rr) & 1)
+                *reinterpret_cast<u32x4_t*>(a.xh + ((size_t)(r0 + rr) * 2 + proj) * a.H + kb * 128 + 8 * ch) = v;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float v = row16_sum(part[i]);
-            if (m == 0 && r0 + 4 * g + i < cnt) a.xsum[((size_t)(p0 + r0 + 4 * g + i) * 2 + proj) * nblk + kb] = v;
+            if (m == 0 && ((vmask >> (4 * g + i)) & 1)) a.xsum[((size_t)(r0 + 4 * g + i) * 2 + proj) * nblk + kb] = v;
         }
         __builtin_amdgcn_wave_barrier();                // the tile is rewritten by the next projection
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1285,7 +1289,9 @@ static int fork3(hipStream_t st, F launch) {
 // classes are combined by the last slot to finish), so one class's down pass overlaps the others' gate|up.
 int launch_moe_mfma(const MoeArgs& a, hipStream_t st) {
     const int nxb = (a.max_blocks + 7) / 8 * 8;
-    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3(a.H / 128, a.max_blocks), dim3(256), 0, st, a);
+    const int64_t had_jobs = (int64_t)(a.M * a.slots + 15) / 16 * (a.H / 128);
+    EXL3_CHECK_ARG(had_jobs / 4 < 0x7FFFFFFF, "exl3_moe_forward: too many rows");
+    EXL3_LAUNCH("moe_pairs_had", pairs_had_kernel, dim3((unsigned)((had_jobs + 3) / 4)), dim3(256), 0, st, a);
     const dim3 grid_gu(nxb * (a.I / 128)), grid_dn(nxb * ((a.H / 128 + 1) / 2));
     return fork3(st, [&](int rga, hipStream_t s) -> int {
         mfma_fn gu = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)

@@ -42,6 +42,8 @@ struct RouteArgs {
     int* pair_tok;
     float* pair_w;
     int* pair_of;
+    int* pair_e;                       // optional [M * slots]: expert of each pair in sorted order, -1 past the valid
+                                       // pairs
     int* tok_nvalid;                   // optional [M]: valid slots per token; tokens with none get a zero output row
     void* out;
     int64_t out_ld;
@@ -92,6 +94,8 @@ struct MoeArgs {
     int* pair_tok;
     float* pair_w;
     int* pair_of;
+    int* pair_e;                       // [pairs] expert of each pair in sorted order, -1 past the valid pairs (MFMA
+                                       // path)
     int* tok_nvalid;                   // [M] valid slots per token
     int* cnt_tok;                      // [M][H/128] combine arrival counters
     // intermediates (workspace)

@@ -167,7 +167,9 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         nbl[e] = big ? (c + r.MB - 1) / r.MB : 0;
     }
     __syncthreads();
-    block_scan_exclusive(start, r.E, tmp);
+    const int nvalid = block_scan_exclusive(start, r.E, tmp);
+    if (r.pair_e)
+        for (int i = nvalid + t; i < np; i += T) r.pair_e[i] = -1;
     const int nitems = block_scan_exclusive(nch, r.E, tmp);
     const int nblocks = block_scan_exclusive(nbl, r.E, tmp);
     for (int e = t; e < r.E; e += T) {
@@ -262,6 +264,7 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
                 r.pair_tok[pos] = tok;
                 r.pair_w[pos] = wt;
                 r.pair_of[i] = pos;
+                if (r.pair_e) r.pair_e[pos] = e;
                 if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
                     ItemDesc& d = r.items[nch[e] + f / mr];
                     d.tok[f % mr] = tok;
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
     s_pos[t] = e >= 0 ? pos : 0x7FFFFFFF;
     s_lead[t] = lead;
     s_blead[t] = blead;
-    __syncthreads();
+    const int nvalid = __syncthreads_count(e >= 0);
     int nitems = 0, nblocks = 0, item = 0, block = 0;
     for (int q = 0; q < np; ++q) {
         const int pq = s_pos[q];
@@ -334,9 +337,11 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
             r.pair_tok[pos] = tok;
             r.pair_w[pos] = wt;
             r.pair_of[t] = pos;
+            if (r.pair_e) r.pair_e[pos] = e;
         } else {
             r.pair_of[t] = -1;
         }
+        if (r.pair_e && t >= nvalid) r.pair_e[t] = -1;
     }
     if (r.items) {
         if (lead) {
@@ -941,6 +946,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     size_t bytes = carve_size(1, 4) + carve_size(max_items, sizeof(ItemDesc)) +
                    carve_size(a.max_blocks, sizeof(ItemDesc)) +
                    (use_mfma ? carve_size(npairs * 2 * a.H, 2) + carve_size(npairs * 2 * (a.H / 128), 4) +
+                                   carve_size(npairs, 4) +
                                    carve_size(npairs * (a.I / 128), 4) + carve_size(3 * (size_t)a.max_blocks + 3, 4)
                              : 0) +
                    carve_size(npairs * 2, 4) + carve_size(npairs, 4) +
@@ -959,6 +965,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     a.xh = use_mfma ? c.take<_Float16>(npairs * 2 * a.H) : nullptr;
     a.xsum = use_mfma ? c.take<float>(npairs * 2 * (a.H / 128)) : nullptr;
     a.asum = use_mfma ? c.take<float>(npairs * (a.I / 128)) : nullptr;
+    a.pair_e = use_mfma ? c.take<int>(npairs) : nullptr;
     int* cls = use_mfma ? c.take<int>(3 * (size_t)a.max_blocks + 3) : nullptr;
     a.cls_list = cls;
     a.cls_cnt = cls ? cls + 3 * (size_t)a.max_blocks : nullptr;
@@ -999,6 +1006,7 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     r.pair_tok = a.pair_tok;
     r.pair_w = a.pair_w;
     r.pair_of = a.pair_of;
+    r.pair_e = a.pair_e;
     r.tok_nvalid = a.tok_nvalid;
     r.out = a.out;
     r.out_ld = a.out_ld;
