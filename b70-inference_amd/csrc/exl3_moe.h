@@ -50,6 +50,8 @@ struct RouteArgs {
     int out_f32, H;
     int held;                          // align_kernel: each thread holds its (at most 8) pairs in registers and
                                        // counts the tokens' valid slots in LDS (M more ints of dynamic LDS)
+    int staged;                        // align_kernel (held): the sorted pair arrays are built in LDS (3 * M * slots
+                                       // more ints) and written out with coalesced stores
 };
 
 constexpr int kFusedRouteMaxE = 512;    // logits per row that the fused layer's in-layer routing handles (8 per lane)

@@ -73,18 +73,80 @@ __device__ int block_scan_exclusive(int* a, int n, int* tmp /* [1024] */) {
     return total;
 }
 
-// Experts and weights of pairs i0 + k * stride, k < B (-1 / 0 past np or for an invalid id), every load issued
-// before any is used: indices are clamped instead of branched on, so a batch costs one memory round trip.
+// Workgroup barrier for LDS only: every LDS access before it has completed and is visible after it, while global
+// stores keep draining (a kernel whose global writes are read only by later kernels need not wait for them here).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Exclusive scans of three LDS arrays of n <= blockDim.x ints at once (shuffle scans within the waves; every wave
+// then adds up the wave totals below it itself, so two barriers in all); tot[] gets the totals.
+__device__ void block_scan3(int* a, int* b, int* c, int n, int* tmp /* [48] */, int (&tot)[3]) {
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, nw = blockDim.x >> 6;
+    int* arr[3] = {a, b, c};
+    int v[3], x[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) x[i] = v[i] = t < n ? arr[i][t] : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        int y[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) y[i] = __shfl_up(x[i], d);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) x[i] += lane >= d ? y[i] : 0;
+    }
+    if (lane == 63)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) tmp[16 * i + wv] = x[i];
+    lds_barrier();
+    int u[3][16];                      // every wave total read first (one LDS round trip), then summed
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int w = 0; w < 16; ++w) u[i][w] = w < nw ? tmp[16 * i + w] : 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        int below = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            below += w < wv ? u[i][w] : 0;
+            all += u[i][w];
+        }
+        if (t < n) arr[i][t] = below + x[i] - v[i];
+        tot[i] = all;
+    }
+    lds_barrier();
+}
+
+// Experts, weights and tokens of pairs i0 + k * stride, k < B (-1 / 0 past np or for an invalid id), every load
+// issued before any is used: indices are clamped instead of branched on, so a batch costs one memory round trip. The
+// (token, slot) of each pair is carried from the first by the stride's quotient and remainder (integer division is
+// a long VALU sequence here: three per call instead of two per pair).
 template <int B>
 __device__ __forceinline__ void load_pairs(const RouteArgs& r, int i0, int stride, int np, int (&e)[B],
-                                           float (&w)[B]) {
+                                           float (&w)[B], int (&tk)[B]) {
+    int jq[B];
+    {
+        int tok = i0 / r.slots, j = i0 - tok * r.slots;
+        const int dq = stride / r.slots, dr = stride - dq * r.slots;
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            tk[k] = tok;
+            jq[k] = j;
+            tok += dq;
+            j += dr;
+            if (j >= r.slots) {
+                j -= r.slots;
+                ++tok;
+            }
+        }
+    }
+    const int tlast = (np - 1) / r.slots, jlast = np - 1 - tlast * r.slots;   // the clamp target, pair np - 1
     int v[B];
     float wv[B];
     if (r.topk > 0) {
 #pragma unroll
         for (int k = 0; k < B; ++k) {
-            const int i = i0 + k * stride, ic = i < np ? i : np - 1;
-            const int tok = ic / r.slots, j = ic - tok * r.slots, jj = j < r.topk ? j : r.topk - 1;
+            const bool in = i0 + k * stride < np;
+            const int tok = in ? tk[k] : tlast, j = in ? jq[k] : jlast, jj = j < r.topk ? j : r.topk - 1;
             v[k] = ldg(r.ids + tok * r.topk + jj);
             wv[k] = ldg(r.tw + tok * r.topk + jj);
         }
@@ -97,17 +159,39 @@ __device__ __forceinline__ void load_pairs(const RouteArgs& r, int i0, int strid
     }
 #pragma unroll
     for (int k = 0; k < B; ++k) {
-        const int i = i0 + k * stride, ic = i < np ? i : np - 1;
-        const int tok = ic / r.slots, j = ic - tok * r.slots;
+        const bool in = i0 + k * stride < np;
+        const int j = jq[k];
         const int ek = j < r.topk ? v[k] : r.shared;
-        e[k] = i < np && ek >= 0 && ek < r.E ? ek : -1;
+        e[k] = in && ek >= 0 && ek < r.E ? ek : -1;
         w[k] = j < r.topk ? wv[k] : 1.0f;
     }
 }
 
+// An item or block descriptor's head and table entries in 16-byte stores (the tab and km fields are contiguous from a
+// 16-byte boundary), so that one thread writing many descriptors issues half as many scattered stores.
+__device__ __forceinline__ void write_desc(ItemDesc& d, int e, int p0, int cnt, const int64_t (&tb)[9],
+                                           const int64_t (&km)[6]) {
+    static_assert(offsetof(ItemDesc, tab) % 16 == 0 && offsetof(ItemDesc, km) == offsetof(ItemDesc, tab) + 72,
+                  "descriptor table layout");
+    typedef int64_t i64x2_t __attribute__((ext_vector_type(2)));
+    typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+    int64_t v[15];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) v[i] = tb[i];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) v[9 + i] = km[i];
+    *reinterpret_cast<i32x4_t*>(&d) = i32x4_t{e, p0, cnt, 0};
+    i64x2_t* q = reinterpret_cast<i64x2_t*>(d.tab);
+#pragma unroll
+    for (int j = 0; j < 7; ++j) q[j] = i64x2_t{v[2 * j], v[2 * j + 1]};
+    d.km[5] = v[14];
+}
+
 // The memory round trips are the kernel's cost, so with held pairs (np <= 8 * 1024) every load is issued at the start:
 // the thread's pairs (kept in registers for the scatter) and its first expert's table entries; the tokens' valid
-// slots are counted in LDS with the experts' rows instead of reloading each token's slots.
+// slots are counted in LDS with the experts' rows instead of reloading each token's slots, and the counting atomics'
+// values (a pair's rank within its expert) place the pairs, so the scatter needs no second atomic. The barriers order
+// LDS only: the tables written here are read by later kernels, so their stores drain behind the rest of the kernel.
 __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     extern __shared__ int sm[];
     int* cnt = sm;                 // [E]
@@ -117,14 +201,17 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     int* nbl = sm + 4 * r.E;       // [E] MFMA blocks of the expert, then their first index
     int* tmp = sm + 5 * r.E;       // [1024]
     int* tokn = sm + 5 * r.E + 1024;   // [M] valid slots per token (held pairs)
+    int* stok = tokn + r.M;            // [M * slots] x 3: pair_tok, pair_w, pair_e in sorted order (staged)
+    float* sw = reinterpret_cast<float*>(stok + r.M * r.slots);
+    int* se = stok + 2 * r.M * r.slots;
     __shared__ int s_cls[3];
     const int t = threadIdx.x, T = blockDim.x;
     if (t < 3) s_cls[t] = 0;
     const int np = r.M * r.slots;
     const int mr = r.MR > 0 ? r.MR : 1;   // MR == 0: every expert with rows is an MFMA expert (no GEMV items)
-    int hev[8];
+    int hev[8], htk[8];
     float hwv[8];
-    if (r.held) load_pairs<8>(r, t, T, np, hev, hwv);
+    if (r.held) load_pairs<8>(r, t, T, np, hev, hwv, htk);
     // this thread's first expert's table entries (index clamped: unconditional loads)
     int64_t tb0[9], km0[6];
     {
@@ -140,25 +227,26 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     }
     if (r.held)
         for (int m = t; m < r.M; m += T) tokn[m] = 0;
-    __syncthreads();
+    lds_barrier();
+    int hrk[8];                        // held pairs: each pair's rank within its expert (the counting atomic's value)
     if (r.held) {
 #pragma unroll
         for (int k = 0; k < 8; ++k)
             if (hev[k] >= 0) {
-                atomicAdd(&cnt[hev[k]], 1);
-                atomicAdd(&tokn[(t + k * T) / r.slots], 1);
+                hrk[k] = atomicAdd(&cnt[hev[k]], 1);
+                atomicAdd(&tokn[htk[k]], 1);
             }
     } else {
         for (int i0 = t; i0 < np; i0 += 8 * T) {
-            int ev[8];
+            int ev[8], tk[8];
             float wv[8];
-            load_pairs<8>(r, i0, T, np, ev, wv);
+            load_pairs<8>(r, i0, T, np, ev, wv, tk);
 #pragma unroll
             for (int k = 0; k < 8; ++k)
                 if (ev[k] >= 0) atomicAdd(&cnt[ev[k]], 1);
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int e = t; e < r.E; e += T) {
         const int c = cnt[e];
         const bool big = r.use_mfma && c > r.MR;
@@ -166,12 +254,21 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         nch[e] = big ? 0 : (c + mr - 1) / mr;
         nbl[e] = big ? (c + r.MB - 1) / r.MB : 0;
     }
-    __syncthreads();
-    const int nvalid = block_scan_exclusive(start, r.E, tmp);
+    lds_barrier();
+    int nvalid, nitems, nblocks;
+    if (r.E <= T) {
+        int tot[3];
+        block_scan3(start, nch, nbl, r.E, tmp, tot);
+        nvalid = tot[0];
+        nitems = tot[1];
+        nblocks = tot[2];
+    } else {
+        nvalid = block_scan_exclusive(start, r.E, tmp);
+        nitems = block_scan_exclusive(nch, r.E, tmp);
+        nblocks = block_scan_exclusive(nbl, r.E, tmp);
+    }
     if (r.pair_e)
         for (int i = nvalid + t; i < np; i += T) r.pair_e[i] = -1;
-    const int nitems = block_scan_exclusive(nch, r.E, tmp);
-    const int nblocks = block_scan_exclusive(nbl, r.E, tmp);
     for (int e = t; e < r.E; e += T) {
         const int c = cnt[e];
         if (r.counts) r.counts[e] = c;
@@ -190,23 +287,15 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
         }
         for (int q = 0, b = nbl[e]; big && q * r.MB < c; ++q, ++b) {
             ItemDesc& d = r.blocks[b];
-            d.e = e;
-            d.p0 = start[e] + q * r.MB;
-            d.cnt = min(r.MB, c - q * r.MB);
-            for (int i = 0; i < 9; ++i) d.tab[i] = tb[i];
-            for (int i = 0; i < 6; ++i) d.km[i] = km[i];
+            const int dc = min(r.MB, c - q * r.MB);
+            write_desc(d, e, start[e] + q * r.MB, dc, tb, km);
             if (r.cls_list) {
-                const int cl = mfma_row_class(d.cnt);
+                const int cl = mfma_row_class(dc);
                 r.cls_list[cl * r.max_blocks + atomicAdd(&s_cls[cl], 1)] = b;
             }
         }
         for (int q = 0, it = nch[e]; !big && q * mr < c; ++q, ++it) {
-            ItemDesc& d = r.items[it];
-            d.e = e;
-            d.p0 = start[e] + q * mr;
-            d.cnt = min(mr, c - q * mr);
-            for (int i = 0; i < 9; ++i) d.tab[i] = tb[i];
-            for (int i = 0; i < 6; ++i) d.km[i] = km[i];
+            write_desc(r.items[it], e, start[e] + q * mr, min(mr, c - q * mr), tb, km);
         }
     }
     if (r.items)
@@ -214,7 +303,7 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
     if (r.blocks)
         for (int b = nblocks + t; b < r.max_blocks; b += T) r.blocks[b].cnt = 0;
     if (t == 0 && r.n_items) r.n_items[0] = nitems;
-    __syncthreads();
+    lds_barrier();
     if (t < 3 && r.cls_cnt) r.cls_cnt[t] = s_cls[t];
     if (r.tok_nvalid) {
         for (int tok = t; tok < r.M; tok += T) {
@@ -223,9 +312,9 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
                 nv = tokn[tok];
             } else {
                 for (int j0 = 0; j0 < r.slots; j0 += 8) {
-                    int ev[8];
+                    int ev[8], tk[8];
                     float wv[8];
-                    load_pairs<8>(r, tok * r.slots + j0, 1, tok * r.slots + r.slots, ev, wv);
+                    load_pairs<8>(r, tok * r.slots + j0, 1, tok * r.slots + r.slots, ev, wv, tk);
 #pragma unroll
                     for (int k = 0; k < 8; ++k) nv += ev[k] >= 0;
                 }
@@ -239,32 +328,39 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
     for (int i0 = t; i0 < np; i0 += 8 * T) {
-        int ev[8];
+        int ev[8], tk[8];
         float wv[8];
         if (r.held) {                  // i0 == t: the pairs loaded at the start
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 ev[k] = hev[k];
                 wv[k] = hwv[k];
+                tk[k] = htk[k];
             }
         } else {
-            load_pairs<8>(r, i0, T, np, ev, wv);
+            load_pairs<8>(r, i0, T, np, ev, wv, tk);
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const int i = i0 + k * T;
             if (i >= np) break;
-            const int tok = i / r.slots, e = ev[k];
+            const int tok = tk[k], e = ev[k];
             if (e >= 0) {
-                const int f = atomicAdd(&fill[e], 1);
+                const int f = r.held ? hrk[k] : atomicAdd(&fill[e], 1);
                 const int pos = start[e] + f;
                 const float wt = wv[k];
-                r.pair_tok[pos] = tok;
-                r.pair_w[pos] = wt;
+                if (r.staged) {
+                    stok[pos] = tok;
+                    sw[pos] = wt;
+                    se[pos] = e;
+                } else {
+                    r.pair_tok[pos] = tok;
+                    r.pair_w[pos] = wt;
+                    if (r.pair_e) r.pair_e[pos] = e;
+                }
                 r.pair_of[i] = pos;
-                if (r.pair_e) r.pair_e[pos] = e;
                 if (r.items && !(r.use_mfma && cnt[e] > r.MR)) {
                     ItemDesc& d = r.items[nch[e] + f / mr];
                     d.tok[f % mr] = tok;
@@ -273,6 +369,14 @@ __global__ __launch_bounds__(1024) void align_kernel(RouteArgs r) {
             } else {
                 r.pair_of[i] = -1;
             }
+        }
+    }
+    if (r.staged) {                    // the sorted pairs out of LDS, coalesced
+        lds_barrier();
+        for (int q = t; q < nvalid; q += T) {
+            r.pair_tok[q] = stok[q];
+            r.pair_w[q] = sw[q];
+            if (r.pair_e) r.pair_e[q] = se[q];
         }
     }
 }
@@ -863,7 +967,9 @@ int launch_align(const RouteArgs& r, hipStream_t st) {
     RouteArgs h = r;
     const size_t lds0 = align_lds_bytes(r.E), ldsh = lds0 + (size_t)r.M * sizeof(int);
     h.held = (int64_t)r.M * r.slots <= 8 * 1024 && ldsh <= 65536;
-    EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), h.held ? ldsh : lds0, st, h);
+    const size_t ldss = ldsh + 3 * (size_t)r.M * r.slots * sizeof(int);
+    h.staged = h.held && ldss <= 65536;
+    EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), h.staged ? ldss : h.held ? ldsh : lds0, st, h);
     return EXL3_OK;
 }
 
