@@ -116,8 +116,9 @@ def weight_bytes(p):
 
 
 # ------------------------------------------------------------------------------------------------ timing
-def graph_time(fns):
-    """Capture fns (in order) into one HIP graph and replay it once (after an untimed replay): us per fn call."""
+def graph_time(fns, reps=1):
+    """Capture fns (in order) into one HIP graph and replay it `reps` times (after an untimed replay), each replay timed
+    on its own: us per fn call, the median over the replays."""
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -126,12 +127,15 @@ def graph_time(fns):
     torch.cuda.synchronize()
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / len(fns)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / len(fns))
+    return sorted(ts)[len(ts) // 2]
 
 
 def kernel_profile(fns, warm=()):
@@ -379,7 +383,7 @@ def measure(name, wl, steps, cpu=True):
     fns = [wl.step_fn(j) for j in range(steps)]
     for f in fns[: min(steps, 4)]:
         f()
-    us = graph_time(fns)
+    us = graph_time(fns, reps=5)
     nprof = min(steps, 16)
     prof = kernel_profile([wl.step_fn(j) for j in range(nprof)], [wl.step_fn(nprof + j) for j in range(nprof)])
     byts = sum(wl.bytes_per_step(j) for j in range(steps)) / steps
