@@ -55,13 +55,13 @@ __host__ __device__ constexpr bool had_sign_neg(int ks, int nb) {
 // L & 15, columns 32 ks + 8 (L >> 4) + j), sv points at s + 8 (L >> 4) (16-byte loads when vs). The results go to the
 // wave's LDS tile (16 x 128 fp16) and part[i] gets the sum of the fp16 results of row 4 (L >> 4) + i over this lane's
 // 8 columns (the caller reduces over the 16 lanes of a row).
-__device__ __forceinline__ void had16_rows(const h8_t (&xv)[4], const uint16_t* sv, bool vs, const h8_t (&F)[2],
-                                           int lane, _Float16 (*tile)[136], float (&part)[4]) {
+__device__ __forceinline__ void had16_rows(const h8_t (&xv)[4], const h8_t (&sg)[4], const h8_t (&F)[2], int lane,
+                                           _Float16 (*tile)[136], float (&part)[4]) {
     const int m = lane & 15, g = lane >> 4;
     h8_t A[4], An[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        A[ks] = xv[ks] * load_h8(sv + 32 * ks, vs);
+        A[ks] = xv[ks] * sg[ks];
         An[ks] = -A[ks];
     }
     f4_t acc[8];
@@ -86,6 +86,14 @@ __device__ __forceinline__ void had16_rows(const h8_t (&xv)[4], const uint16_t* 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// the signs from sv + 32 ks (16-byte loads when vs)
+__device__ __forceinline__ void had16_rows(const h8_t (&xv)[4], const uint16_t* sv, bool vs, const h8_t (&F)[2],
+                                           int lane, _Float16 (*tile)[136], float (&part)[4]) {
+    h8_t sg[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sg[ks] = load_h8(sv + 32 * ks, vs);
+    had16_rows(xv, sg, F, lane, tile, part);
 }
 
 // Sum of v over the 16 lanes of a row (lanes with equal L >> 4).
@@ -128,16 +136,22 @@ __global__ __launch_bounds__(256) void pairs_had_kernel(MoeArgs a) {
     }
     const uint16_t* xr = a.x + (int64_t)(valid ? tok : 0) * a.x_ld + kb * 128 + 8 * g;
     const bool vx = ((uintptr_t)a.x & 15) == 0 && (a.x_ld & 7) == 0;
-    h8_t xv[4];
+    // x and both projections' signs in one round trip
+    h8_t xv[4], sg[2][4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) xv[ks] = load_h8(xr + 32 * ks, vx);
-    const h8_t F[2] = {had_fragment(lane, 0), had_fragment(lane, 1)};
 #pragma unroll
     for (int proj = 0; proj < 2; ++proj) {
         const uint16_t* sv = sgn[proj] + kb * 128 + 8 * g;
         const bool vs = __builtin_amdgcn_ballot_w64(((uintptr_t)sv & 15) != 0) == 0;   // every row 16-byte aligned
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) sg[proj][ks] = load_h8(sv + 32 * ks, vs);
+    }
+    const h8_t F[2] = {had_fragment(lane, 0), had_fragment(lane, 1)};
+#pragma unroll
+    for (int proj = 0; proj < 2; ++proj) {
         float part[4];
-        had16_rows(xv, sv, vs, F, lane, s_out[wave], part);
+        had16_rows(xv, sg[proj], F, lane, s_out[wave], part);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {                   // 16-byte row stores from the tile
             const int u = lane + 64 * c, rr = u >> 4, ch = u & 15;
