@@ -968,7 +968,7 @@ int launch_align(const RouteArgs& r, hipStream_t st) {
     const size_t lds0 = align_lds_bytes(r.E), ldsh = lds0 + (size_t)r.M * sizeof(int);
     h.held = (int64_t)r.M * r.slots <= 8 * 1024 && ldsh <= 65536;
     const size_t ldss = ldsh + 3 * (size_t)r.M * r.slots * sizeof(int);
-    h.staged = h.held && ldss <= 65536;
+    h.staged = h.held && ldss + 256 <= 65536;        // (room for the kernel's static LDS)
     EXL3_LAUNCH("moe_align", align_kernel, dim3(1), dim3(1024), h.staged ? ldss : h.held ? ldsh : lds0, st, h);
     return EXL3_OK;
 }
