@@ -261,10 +261,11 @@ def test_moe_c3_full_size(exl3, oracle):
         assert max_rel(y2.cpu().numpy(), ref) <= MAX_REL, M
 
 
-@pytest.mark.parametrize("M,k,E", [(9, 4, 16), (300, 4, 37), (2600, 4, 37)])
+@pytest.mark.parametrize("M,k,E", [(9, 4, 16), (300, 4, 37), (1500, 4, 37), (2600, 4, 37)])
 def test_align_tables(exl3, oracle, M, k, E):
     """Up to 256 pairs take the one-thread-per-pair kernel, more the 1024-thread one: with the pairs held in
-    registers (300 x 4) and reloaded per phase (2600 x 4 = 10400 pairs, more than 8 per thread)."""
+    registers and the sorted arrays built in LDS (300 x 4), held but written directly (1500 x 4 = 6000 pairs: the
+    LDS copy would not fit 64 KB) and reloaded per phase (2600 x 4 = 10400 pairs, more than 8 per thread)."""
     ids, w = _ids_w(M, k, E, 1000 + M, dup=True, inactive=True)
     counts, ptok, pw, pof = exl3.moe_align(ids.cuda(), w.cuda(), E, shared=-1)
     counts, ptok, pw, pof = (t.cpu().numpy() for t in (counts, ptok, pw, pof))
