@@ -377,6 +377,19 @@ def _skewed_ids(M, k, E, seed, hot=(0, 1, 2)):
     return ids, (w / w.sum(1, keepdim=True)).float()
 
 
+def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small):
+    """Prefill (37 tokens: the MFMA grouped GEMM) with a shared expert and inactive slots in several tokens: the
+    expert-sorted pairs stop short of tokens x slots (145 of 148 here, not a multiple of 16), so the input transform's
+    last row group holds pairs past the valid ones, which it must skip."""
+    tables, orc = small
+    ids, w = _ids_w(37, 3, 11, 711, dup=True, inactive=True)     # experts 0..10 routed, 11 = shared
+    ids[5, 1] = -1
+    ids[20, 0] = -1
+    x = torch.randn(37, 256, generator=torch.Generator().manual_seed(712)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=11)
+    assert max_rel(y, ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("M", [24, 80])
 def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
     """More than 16 tokens: every expert's rows go through the MFMA grouped GEMM in blocks of up to 64 rows, hot and
