@@ -217,10 +217,11 @@ def test_moe_forward_logits_in_layer_fp16_and_router_kernel_switch(exl3, small, 
     assert torch.equal(a, b) and torch.equal(ia, ib) and torch.equal(wa, wb)
 
 
-@pytest.mark.parametrize("M", [1, 4, 12])
+@pytest.mark.parametrize("M", [1, 4, 12, 37])
 def test_moe_packed_tables_same_rows(exl3, small, M):
-    """ExpertTables.packed (uniform strides: the decode kernels compute expert addresses instead of loading them)
-    gives bit-identical rows to the same experts addressed through their pointer tables."""
+    """ExpertTables.packed (uniform strides: the decode kernels and the prefill input transform compute expert
+    addresses instead of loading them) gives bit-identical rows to the same experts addressed through their pointer
+    tables (37 tokens: the MFMA prefill path)."""
     tables, _ = small
     packed = exl3.ExpertTables.packed(*tables.projs)
     assert packed.layout is not None and list(packed.layout)[9] > 0
