@@ -378,6 +378,17 @@ def _skewed_ids(M, k, E, seed, hot=(0, 1, 2)):
     return ids, (w / w.sum(1, keepdim=True)).float()
 
 
+def test_moe_prefill_more_pairs_than_held(exl3, oracle, small):
+    """2100 tokens x 4 slots = 8400 pairs: more than the align kernel holds in registers (8 per thread), so it
+    reloads the pairs per phase and writes the sorted arrays, the pairs' experts included, from the scatter; every
+    row against the oracle."""
+    tables, orc = small
+    ids, w = _ids_w(2100, 4, 12, 713, dup=True, inactive=True)
+    x = torch.randn(2100, 256, generator=torch.Generator().manual_seed(714)).half()
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+
+
 def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small):
     """Prefill (37 tokens: the MFMA grouped GEMM) with a shared expert and inactive slots in several tokens: the
     expert-sorted pairs stop short of tokens x slots (145 of 148 here, not a multiple of 16), so the input transform's
