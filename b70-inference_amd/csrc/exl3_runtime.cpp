@@ -8,6 +8,7 @@
 #include <mutex>
 #include <string>
 #include <string.h>
+#include <utility>
 #include <vector>
 
 namespace exl3 {
@@ -79,6 +80,9 @@ int resident_blocks(const void* fn, int threads, int* out) {
 
 namespace {
 std::vector<void*> g_retired[kMaxDevices];   // outgrown workspace buffers, freed by exl3_release_workspace
+// Outgrown counter buffers (a subset of g_retired) with their sizes: graphs captured while one of them was current
+// still use it, so a timeout reset zeroes them too.
+std::vector<std::pair<int*, size_t>> g_retired_counters[kMaxDevices];
 
 __global__ void zero_ints_kernel(int* p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
@@ -117,12 +121,20 @@ int workspace(size_t bytes, size_t ncounters, hipStream_t st, Workspace* out) {
         w.status = d;
     }
     if (*reinterpret_cast<volatile int*>(g_status_host[dev]) != 0) {
-        const int rc = zero_ints(w.counters, w.ncounters, st);
-        *reinterpret_cast<volatile int*>(g_status_host[dev]) = 0;
+        // A reset recorded into a graph would not run now: under capture the word stays set and the next call
+        // outside capture resets.
+        if (capturing(st))
+            return fail(EXL3_ERR_HIP, "a fused MoE layer launch on device %d gave up waiting for its gate|up inputs; "
+                                      "the arrival counters are reset by the next library call outside stream "
+                                      "capture", dev);
+        int rc = zero_ints(w.counters, w.ncounters, st);
+        for (const auto& c : g_retired_counters[dev])
+            if (!rc) rc = zero_ints(c.first, c.second, st);
         if (rc) return rc;
+        *reinterpret_cast<volatile int*>(g_status_host[dev]) = 0;
         return fail(EXL3_ERR_HIP, "a fused MoE layer launch on device %d gave up waiting for its gate|up inputs (its "
-                                  "outputs are incomplete, and so may be those of calls queued behind it); the "
-                                  "counters have been reset, later calls run normally", dev);
+                                  "outputs are incomplete, and so may be those of calls queued behind it); every "
+                                  "counter buffer has been reset, later calls and graph replays run normally", dev);
     }
     if (bytes > w.scratch_bytes) {
         if (capturing(st))
@@ -148,7 +160,10 @@ int workspace(size_t bytes, size_t ncounters, hipStream_t st, Workspace* out) {
             (void)hipFree(c);
             return rc;
         }
-        if (w.counters) g_retired[dev].push_back(w.counters);
+        if (w.counters) {
+            g_retired[dev].push_back(w.counters);
+            g_retired_counters[dev].push_back({w.counters, w.ncounters});
+        }
         w.counters = c;
         w.ncounters = nc;
     }
@@ -200,6 +215,7 @@ int release_workspace() {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     for (void* p : g_retired[dev]) EXL3_CHECK_HIP(hipFree(p));
     g_retired[dev].clear();
+    g_retired_counters[dev].clear();
     return EXL3_OK;
 }
 

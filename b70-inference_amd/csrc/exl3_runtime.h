@@ -31,7 +31,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // at them) until exl3_release_workspace; it never synchronises, the new counters are zeroed by a fill kernel on
 // `stream`, and it is refused while `stream` is being captured (exl3_reserve_workspace beforehand).
 // Before anything else it checks the status word (a host read, no synchronisation): when a wait has timed out it
-// zeroes the counters on `stream`, clears the word and fails with EXL3_ERR_HIP.
+// zeroes every counters buffer of the device (current and outgrown) on `stream`, clears the word and fails with
+// EXL3_ERR_HIP; under stream capture it fails without the reset and leaves the word set.
 struct Workspace {
     char* scratch = nullptr;
     size_t scratch_bytes = 0;

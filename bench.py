@@ -3,8 +3,9 @@
 
 Headline: the largest layer, C5 below. One step = one layer call: 4 decode rows and a 256-row prefill chunk routed
 top-8 over 256 experts (+ 1 shared expert), per-tile 1/2-bit weights (1.62 bpw), in one library call
-(moe_forward). Timed as a HIP-graph replay of exactly --steps steps (--warmup steps run eagerly first); steps cycle
-through fresh routings. value = microseconds per token (lower is better). Prints one JSON line.
+(moe_forward). Timed as a HIP graph of exactly --steps steps (--warmup steps run eagerly first): one untimed replay,
+then the median of 5 timed replays; steps cycle through fresh routings. value = microseconds per token (lower is
+better). Prints one JSON line.
 
 Workloads (seeded synthetic EXL3 tensors generated on the device; parity is tested against the oracle separately):
   C1  dense linear 4096 -> 4096, K=4, 1 token (128 weight copies cycled: beyond the 256 MB Infinity Cache)
@@ -15,7 +16,8 @@ Workloads (seeded synthetic EXL3 tensors generated on the device; parity is test
   C5  MoE layer H=7168, 256 experts of I=2048 + 1 shared, per-tile K in {1, 2} (38/62), top-8, 4 decode + 256
       prefill rows in one call                                                                       (headline)
 
-Every config reports: time per layer and per token; algorithmic bytes and FLOP per layer and the HBM / fp16-MFMA
+Every config reports: time per layer and per token (graph replay) and the eager single-call latency; what the timed
+region holds; algorithmic bytes and FLOP per layer and the HBM / fp16-MFMA
 fractions they imply; the library's kernels per step with their event-timed durations; a roofline block for its
 dominant kernel (the kernel with the most time per step: its algorithmic bytes or FLOP per launch over its average
 launch duration, HIP events on the launch stream); and the CPU baseline (the oracle on this host, bounded sample).
@@ -116,6 +118,19 @@ def weight_bytes(p):
 
 
 # ------------------------------------------------------------------------------------------------ timing
+def eager_time(fns):
+    """Eager single-call latency: each fn called once between two device synchronisations, host wall clock (launch
+    overhead included); microseconds, the median over the calls."""
+    ts = []
+    for f in fns:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        f()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e6)
+    return statistics.median(ts)
+
+
 def graph_time(fns, reps=1):
     """Capture fns (in order) into one HIP graph and replay it `reps` times (after an untimed replay), each replay timed
     on its own: us per fn call, the median over the replays."""
@@ -155,16 +170,35 @@ def kernel_profile(fns, warm=()):
 
 
 def cpu_info():
+    """(cores this process may run on, the oracle's thread count, a description of the host CPU): lscpu's vendor,
+    model name, family / model / stepping, sockets and cores per socket, and /proc/cpuinfo's model name."""
     cores = len(os.sched_getaffinity(0))
-    model = None
+    fields = {}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
         for line in out.splitlines():
-            if line.startswith("Model name:"):
-                model = line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
     except (OSError, subprocess.SubprocessError):
         pass
-    return cores, model
+    proc = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    proc = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    keys = ("Vendor ID", "Model name", "CPU family", "Model", "Stepping", "Socket(s)", "Core(s) per socket",
+            "Thread(s) per core", "CPU(s)")
+    model = "; ".join(f"{k}: {fields[k]}" for k in keys if k in fields)
+    if proc:
+        model += f"; /proc/cpuinfo model name: {proc}"
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(cores, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else cores
+    return cores, threads, model or None
 
 
 def cpu_time(fn, runs=3):
@@ -181,6 +215,7 @@ def cpu_time(fn, runs=3):
 # ------------------------------------------------------------------------------------------------ workloads
 class Dense:
     """C1: one EXL3 linear k -> n over `copies` weight copies."""
+    timed_region = "exl3_gemm (input transform, decode GEMV, output transform)"
 
     def __init__(self, k, n, K, M, copies, seed):
         g = dev_gen(seed)
@@ -217,6 +252,7 @@ class Dense:
 
 class Mlp:
     """C2: dense gated MLP H <-> I (the fused decode layer with one always-on expert)."""
+    timed_region = "BC_GatedMLP.run_bszN (gate, up, activation, down in one launch)"
 
     def __init__(self, H, I, K, M, copies, seed):
         g = dev_gen(seed)
@@ -276,6 +312,9 @@ class MoE:
         self.E = t.E - (1 if shared else 0)
         self.shared = self.E if shared else -1
         self.act, self.bias, self.logits_api = act, bias, logits_api
+        self.timed_region = ("moe_forward_logits: routing from the router logits + the layer" if logits_api else
+                             "moe_forward on precomputed routing ids and weights (the reference op's boundary, "
+                             "moe_forward(x, topk_ids, topk_w, ...)): align, input transform, gate|up, down, combine")
         g = dev_gen(seed)
         self.x = [torch.randn(M, self.H, device="cuda", generator=g).half() for _ in range(nrout)]
         self.logits = [torch.randn(M, self.E, device="cuda", generator=g) for _ in range(nrout)]
@@ -384,6 +423,7 @@ def measure(name, wl, steps, cpu=True):
     for f in fns[: min(steps, 4)]:
         f()
     us = graph_time(fns, reps=5)
+    eager = eager_time([wl.step_fn(j) for j in range(min(steps, 9))])
     nprof = min(steps, 16)
     prof = kernel_profile([wl.step_fn(j) for j in range(nprof)], [wl.step_fn(nprof + j) for j in range(nprof)])
     byts = sum(wl.bytes_per_step(j) for j in range(steps)) / steps
@@ -391,6 +431,8 @@ def measure(name, wl, steps, cpu=True):
     wts = sum(wl.weights_per_step(j) for j in range(steps)) / steps
     gbs = byts / us / 1e3
     r = {"us_per_layer": round(us, 3), "us_per_token": round(us / wl.M, 3), "tokens": wl.M,
+         "timing": "median of 5 timed replays (after an untimed one) of a HIP graph of the steps, per step",
+         "timed_region": wl.timed_region, "eager_us_per_call": round(eager, 1),
          "bytes_per_layer": int(byts), "gbps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
          "flop_per_layer": int(flops), "tflops": round(flops / us / 1e6, 2),
          "mfma_frac": round(flops / us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4),
@@ -398,16 +440,9 @@ def measure(name, wl, steps, cpu=True):
          "kernels": {k: {"launches_per_step": round(n / nprof, 2), "avg_us": round(t, 3)} for k, (n, t) in prof.items()}}
     if isinstance(wl, MoE):
         r["unique_experts"] = round(sum(wl.unique(j) for j in range(steps)) / steps, 2)
-    # dominant kernel: most time per step; for an MFMA-bound workload the kernel with the most FLOP per step (the
-    # row-class kernels of a prefill layer run concurrently, and the longest-running one is the class of cold experts
-    # with the least matrix work)
-    def flop_per_step(name):
-        w = [wl.kernel_work(name, j) for j in range(nprof)]
-        return sum(x[1] for x in w) if all(x is not None for x in w) else -1.0
-    if prof and getattr(wl, "bound", "hbm") == "mfma":
-        dom = max(prof, key=flop_per_step)
-    else:
-        dom = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])[0] if prof else None
+    # dominant kernel: the most time per step (for a prefill layer whose row-class kernels run concurrently that is
+    # the class of cold experts, with the least matrix work; the layer's own MFMA fraction is reported beside it)
+    dom = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])[0] if prof else None
     work = [wl.kernel_work(dom, j) for j in range(nprof)] if dom else []
     if work and all(w is not None for w in work):
         k_n, k_us = prof[dom]
@@ -427,6 +462,8 @@ def measure(name, wl, steps, cpu=True):
                      "bytes_per_launch": int(kb), "flop_per_launch": int(kf),
                      "hbm_frac": round(kb / k_us / 1e3 / HBM_PEAK_GBS, 4),
                      "mfma_frac": round(kf / k_us / 1e6 / MFMA_F16_PEAK_TFLOPS, 4)})
+        roof["layer_mfma_frac"] = r["mfma_frac"]
+        roof["layer_hbm_frac"] = r["hbm_frac"]
         roof["traffic"] = recorded_traffic(dom, name)
         dw = [wl.kernel_weights(dom, j) for j in range(nprof)]
         vpw = recorded_valu(dom, name)
@@ -443,10 +480,11 @@ def measure(name, wl, steps, cpu=True):
         O = importlib.import_module("oracle.exl3_oracle")
         rows = getattr(wl, "cpu_rows", None)
         t, ntok, what = wl.cpu(O, np, rows) if rows is not None else wl.cpu(O, np)
-        cores, _ = cpu_info()
-        r["cpu_baseline"] = {"value": round(t * 1e6 / ntok, 1), "unit": "us/token", "cores": min(16, cores),
-                             "kind": "port", "sample": f"{what}, oracle (decode + float64 products in C, OpenMP), "
-                                                       f"1 warm-up + median of 3"}
+        cores, threads, _ = cpu_info()
+        r["cpu_baseline"] = {"value": round(t * 1e6 / ntok, 1), "unit": "us/token", "cores": threads,
+                             "affinity_cores": cores, "kind": "port",
+                             "sample": f"{what}, oracle (decode + float64 products in C, OpenMP over {threads} "
+                                       f"threads), 1 warm-up + median of 3"}
         log(name, "cpu", r["cpu_baseline"])
     return r
 
@@ -569,21 +607,29 @@ def main():
         for f in fns:
             f()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g.replay()
+    g.replay()                       # untimed replay: first-launch costs of the graph stay out of the timing
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    walls = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
     del g
+    wall = statistics.median(walls)
+    log("headline replays (s)", [round(w, 5) for w in walls])
     ms_step = wall * 1e3 / K
     us_tok = ms_step * 1e3 / wl.M
     byts = sum(wl.bytes_per_step(j) for j in range(K)) / K
+    wl_region = wl.timed_region
     c5 = measure("c5", wl, min(K, 16), cpu=not args.no_cpu_baseline)
     roofline = dict(c5.get("roofline", {}))
     if roofline:
         roofline["traffic"] = recorded_traffic(roofline["kernel"], "c5")
     roofline["layer_gbps"] = round(byts / (ms_step * 1e3) / 1e3, 1)
     cpu = c5.pop("cpu_baseline", None)
-    cores, model = cpu_info()
+    _, _, model = cpu_info()
     if cpu:
         cpu["model"] = model
     del wl, fns
@@ -609,7 +655,10 @@ def main():
                                "EXL3 weights (38/62, 1.62 bpw), softmax top-8, SiLU; 260 rows per step (4 decode + "
                                "256 prefill) in one call, fresh routing every step",
                    "hidden": 7168, "intermediate": 2048, "experts": 256, "shared_experts": 1, "topk": 8,
-                   "bits": 1.62, "rows_per_step": 260, "timing": "HIP graph replay of all steps, wall clock",
+                   "bits": 1.62, "rows_per_step": 260,
+                   "timing": "HIP graph of all steps: one untimed replay, then the median of 5 timed replays "
+                             "(each bracketed by device synchronisations, host wall clock)",
+                   "timed_region": wl_region, "eager_us_per_call": c5["eager_us_per_call"],
                    "layer_gbps": roofline["layer_gbps"],
                    "layer_hbm_frac": round(roofline["layer_gbps"] / HBM_PEAK_GBS, 4), "host_cpu": model},
         "roofline": roofline,

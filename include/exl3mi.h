@@ -53,8 +53,11 @@ int exl3_release_workspace(void);
 
 /* The current device's status word: 0, or 1 after a fused MoE layer launch gave up one of its bounded
  * cross-workgroup waits (its outputs, and possibly those of launches queued behind it, are then incomplete). Read on
- * the host without synchronising; the next library call on the device that uses the workspace zeroes the library's
- * arrival counters on its stream, clears the word and returns EXL3_ERR_HIP. No reference counterpart (the
+ * the host without synchronising. The next library call on the device that uses the workspace outside stream capture
+ * zeroes every arrival-counter buffer of the device on its stream (the current one and the outgrown ones that graphs
+ * captured earlier still use), clears the word and returns EXL3_ERR_HIP; a call under capture returns EXL3_ERR_HIP and
+ * leaves the word set. Graph replays do not check the word: code that replays graphs polls it and, when set, makes
+ * one eager call that takes the workspace (exl3_reserve_workspace(0, 0)) to reset. No reference counterpart (the
  * reference's kernels do not wait across work-groups). */
 int exl3_device_status(int* status);
 

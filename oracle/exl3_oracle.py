@@ -153,8 +153,14 @@ def _fast_lib():
 
 
 def _threads() -> int:
+    """Every core this process may run on, capped by OMP_NUM_THREADS when that is set (a host's CPU share)."""
     import os
-    return max(1, min(16, len(os.sched_getaffinity(0))))
+    n = len(os.sched_getaffinity(0))
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        cap = 0
+    return max(1, min(n, cap) if cap > 0 else n)
 
 
 def reconstruct_fast(trellis: np.ndarray, K: int, n0: int = 0, n_slice: int | None = None) -> np.ndarray:

@@ -371,6 +371,46 @@ def test_route_topk_residency_terms(score):
     assert np.array_equal(ids4, keep[idk]) and np.allclose(w4, wk, rtol=1e-6)
 
 
+def _logits_for_sqrt_softplus(s):
+    """Logits f with sqrt(softplus(f)) = s (f = log(expm1(s^2)))."""
+    return np.log(np.expm1(np.asarray(s, np.float64) ** 2)).astype(np.float32)
+
+
+def test_route_residency_terms_hand_computed():
+    """The residency form ranks by s * mul + b (+ res), hand-computed on three experts: s = (0.5, 0.75, 0.1),
+    mul = (3, 1, 1), b = (-0.2, 0.2, 0) give keys (1.3, 0.95, 0.1), so the picks are (0, 1) with weights
+    s / (0.5 + 0.75) = (0.4, 0.6). (s + b) * mul would give (0.9, 0.95, 0.1) and pick (1, 0); s * (mul + b) gives
+    (1.4, 0.95, 0.1) and agrees, so a second case separates it: res = (-0.4, 0, 0) makes the keys (0.9, 0.95, 0.1),
+    picks (1, 0) with weights (0.6, 0.4), where s * (mul + b) + res = (1.0, 0.95, 0.1) would keep (0, 1)."""
+    lg = _logits_for_sqrt_softplus([0.5, 0.75, 0.1])[None, :]
+    mul = np.array([3, 1, 1], np.float32)
+    b = np.array([-0.2, 0.2, 0.0], np.float32)
+    ids, w = O.route_topk(lg, 2, b, "sqrt_softplus", mul=mul)
+    assert ids.tolist() == [[0, 1]]
+    assert np.allclose(w, [[0.4, 0.6]], atol=1e-6)
+    ids, w = O.route_topk(lg, 2, b, "sqrt_softplus", mul=mul, res=np.array([-0.4, 0, 0], np.float32))
+    assert ids.tolist() == [[1, 0]]
+    assert np.allclose(w, [[0.6, 0.4]], atol=1e-6)
+
+
+def test_route_block_boost_hand_computed():
+    """Verify-block boost is multiplicative, s * mul * (1 + bb) + b, hand-computed on two experts in one block of two
+    rows: row 0 (s = 1.5, 0.3) picks expert 0; row 1 has s = (0.5, 1.2). With mul = 1 and bb = 1 expert 0's key is
+    0.5 * 2 = 1.0 < 1.2, so row 1 picks expert 1 (an additive boost s + bb = 1.5 would pick expert 0); with bb = 2 it
+    is 1.5 > 1.2 and row 1 picks expert 0. With mul = (2, 1) and bb = 0.25 it is 0.5 * 2 * 1.25 = 1.25 > 1.2: expert 0
+    (s * (mul + bb) = 1.125 would pick expert 1). The weights are the plain s renormalised over one pick: 1."""
+    lg = np.stack([_logits_for_sqrt_softplus([1.5, 0.3]), _logits_for_sqrt_softplus([0.5, 1.2])])
+    zero = np.zeros(2, np.float32)
+    for mul, bb, want in ((None, 1.0, 1), (None, 2.0, 0), (np.array([2, 1], np.float32), 0.25, 0),
+                          (np.array([2, 1], np.float32), 0.1, 1)):
+        ids, w = O.route_block(lg, 1, zero, mul, 2, bb)
+        assert ids[:, 0].tolist() == [0, want], (mul, bb)
+        assert np.allclose(w, 1.0)
+    # a bias adds after the boost: b = (0, 0.35) lifts expert 1 to 1.55 over 1.5 at bb = 2
+    ids, _ = O.route_block(lg, 1, np.array([0, 0.35], np.float32), None, 2, 2.0)
+    assert ids[:, 0].tolist() == [0, 1]
+
+
 def test_route_block_properties():
     """Verify-block routing pinned by properties: no boost (or blocks of one row) is the plain sqrt-softplus router row
     by row; a boost large enough makes every later row of a block take the first row's experts; the weights always

@@ -98,3 +98,61 @@ def test_graph_captured_before_growth_replays_on_live_buffers(exl3, oracle, laye
     torch.cuda.synchronize()
     lib.release_workspace()
     assert torch.equal(_call(exl3, layer), eager)
+
+
+def test_timeout_in_replay_resets_outgrown_counters_and_not_under_capture(exl3, oracle, layer):
+    """A lost wait inside a graph replay, on a counter buffer that the workspace has since outgrown: a library call made
+    under stream capture reports it and leaves the status word set (a reset recorded into a graph would not run now);
+    the next eager call zeroes every counter buffer, the outgrown one included, so a graph captured on it before the
+    growth replays the eager result afterwards. The lost wait is forced from the host (a spin limit of 1 captured
+    into one graph's launch), so every kernel exits normally."""
+    lib = exl3._lib
+    tables, x, ids, w, ref = layer
+    out_good = torch.empty(4, 1024, dtype=torch.float32, device="cuda")
+    out_bad = torch.empty_like(out_good)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        exl3.moe_forward(x, ids, w, tables, out=out_good)  # sizes the workspace before capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = out_good.clone()
+    assert max_rel(eager.cpu().numpy(), ref) <= MAX_REL
+    g_good, g_bad = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_good):
+        exl3.moe_forward(x, ids, w, tables, out=out_good)
+    os.environ["EXL3MI_SPIN_LIMIT"] = "1"
+    try:
+        with torch.cuda.graph(g_bad):
+            exl3.moe_forward(x, ids, w, tables, out=out_bad)
+    finally:
+        del os.environ["EXL3MI_SPIN_LIMIT"]
+    torch.cuda.synchronize()
+    lib.reserve_workspace(1 << 31, 1 << 22)                 # both graphs now run on outgrown buffers
+    print("timeout test: replaying a graph captured with a spin limit of 1", flush=True)
+    for _ in range(4):
+        g_bad.replay()
+        torch.cuda.synchronize()
+        if lib.device_status():
+            break
+    assert lib.device_status() == 1
+    g_cap = torch.cuda.CUDAGraph()
+    with pytest.raises(lib.Exl3Error, match="outside stream capture"):
+        with torch.cuda.graph(g_cap):
+            exl3.moe_forward(x, ids, w, tables, out=out_bad)
+    torch.cuda.synchronize()
+    assert lib.device_status() == 1
+    with pytest.raises(lib.Exl3Error, match="every counter buffer has been reset"):
+        lib.reserve_workspace(0, 0)
+    torch.cuda.synchronize()
+    assert lib.device_status() == 0
+    for _ in range(3):
+        out_good.zero_()
+        g_good.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_good, eager)
+        assert torch.equal(_call(exl3, layer), eager)
+    assert lib.device_status() == 0
+    del g_good, g_bad, g_cap
+    torch.cuda.synchronize()
+    lib.release_workspace()
