@@ -15,6 +15,7 @@ LIB_PATH = os.environ.get("EXL3MI_LIB") or os.path.join(HERE, "libexl3mi.so")
 
 EXL3_OK, EXL3_ERR_INVALID, EXL3_ERR_UNSUPPORTED, EXL3_ERR_HIP = 0, 1, 2, 3
 EXL3_F16, EXL3_F32 = 0, 1
+EXL3_WORDS_PLANAR4, EXL3_WORDS_TILE_ORDER = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 
 _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -42,7 +43,7 @@ SIGNATURES = {
     "exl3_moe_forward": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _f32,
                          _i64, _vp, _i64, _i32, _vp],
     "exl3_moe_forward_blobs": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _f32, _vp, _i64,
-                               _i32, _vp],
+                               _i32, _i32, _vp],
     "exl3_blob_unplanarize": [_vp, _i64, _i64, _i64, _i32, _vp],
     "exl3_moe_forward_logits": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i32, _i32,
                                 _i32, _i32, _f32, _i64, _vp, _vp, _vp, _vp, _i64, _i32, _vp],

@@ -83,13 +83,35 @@ __device__ __forceinline__ h2_t mul1_pair_raw(uint32_t s0, uint32_t s1) {
 __host__ __device__ constexpr int pos_row(int u) { return 8 * ((u >> 1) & 1) + 2 * ((u >> 3) & 3) + (u & 1); }
 __host__ __device__ constexpr int pos_half(int u) { return (u >> 2) & 1; }
 
+// Word order of a tile-row. Tile order (PL false): tile t's 8K words at 8K t. PLANAR4 (PL true; the reference's
+// expert blobs, glm/xpu/exl3xpu/moe_offload.py:68-78, glm/xpu/pack_store.py:35-54): a tile's words are G periods of
+// D = K / gcd(K, 32) words, and within every group of 4 consecutive tiles word (tile t, period g, plane i) sits at
+// 4G i + G t + g (G = 8K / D); D = 1 (K = 1, 2, 4, 8) is tile order. Word j of a lane's chunk q (tile word Kq + j) is
+// period q gcd + j / D, plane j % D. So both orders read a lane's K chunk words at
+//   group base + tile-in-group * G + q * gcd + word_off(j)
+// with G = 8K, gcd = K, word_off(j) = j in tile order: one K-dword load there, K dword loads at fixed offsets in
+// PLANAR4 (coalesced across the lanes of a plane).
+template <int K, bool PL>
+struct WordOrder {
+    static constexpr int GC = PL ? (K & -K) : K;         // gcd(K, 32) for K <= 8
+    static constexpr int D = K / GC;
+    static constexpr int G = 8 * K / D;
+    static_assert(K >= 1 && K <= 8, "K in 1..8");
+    __host__ __device__ static constexpr int word_off(int j) { return (j % D) * 4 * G + j / D; }
+    // first word of chunk q of tile `tile` of a tile-row (tile counted from the row's first tile)
+    __host__ __device__ static constexpr int chunk_base(int tile, int q) {
+        return (tile & ~3) * 8 * K + (tile & 3) * G + q * GC;
+    }
+};
+
 // Load the lane's K chunk words of one tile-row strip and the word before the chunk. `p` points at the strip's
 // first word; returns R[0..K].
-template <int K>
+template <int K, bool PL = false>
 __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ p, int lane, uint32_t* R) {
-    const uint32_t* q = p + lane * K;
+    typedef WordOrder<K, PL> O;
+    const uint32_t* q = p + O::chunk_base(lane >> 3, lane & 7);
 #pragma unroll
-    for (int i = 0; i < K; ++i) R[1 + i] = ldg_nt(q + i);
+    for (int i = 0; i < K; ++i) R[1 + i] = ldg_nt(q + O::word_off(i));
 }
 
 // R[0] = last word of the previous chunk of the lane's tile: lane l - 1, or l + 7 for chunk 0 (the ring wraps inside

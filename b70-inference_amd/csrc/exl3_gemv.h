@@ -133,13 +133,20 @@ __device__ __forceinline__ void strip_tile_row(const uint32_t (&D)[K], int lane,
 
 // Unconditional (the index is clamped to the last tile-row, nt > 0), so the waitcnt pass sees straight-line loads.
 // Offsets are 32-bit word counts (a projection's trellis holds fewer than 2^32 words; the host checks).
-template <int K>
+// `base` is the lane's first chunk word in tile-row 0 (strip_lane_base); PL: PLANAR4 word order (WordOrder).
+template <int K, bool PL = false>
 __device__ __forceinline__ void strip_load(uint32_t (&D)[K], const uint32_t* __restrict__ base, uint32_t rs, int lt,
                                            int nt) {
     const uint32_t off = (uint32_t)(lt < nt ? lt : nt - 1) * rs;
 #pragma unroll
-    for (int i = 0; i < K; ++i) D[i] = ldg_nt(base + off + i);
+    for (int i = 0; i < K; ++i) D[i] = ldg_nt(base + off + WordOrder<K, PL>::word_off(i));
     __builtin_amdgcn_sched_barrier(0);   // keep the prefetch where it is issued (the scheduler would sink it)
+}
+
+// The lane's first chunk word of a strip (8 consecutive tiles starting at a multiple of 4 tiles) at tile-row 0.
+template <int K, bool PL = false>
+__device__ __forceinline__ const uint32_t* strip_lane_base(const uint32_t* __restrict__ sp, int lane) {
+    return sp + WordOrder<K, PL>::chunk_base(lane >> 3, lane & 7);
 }
 
 // Ring of R register buffers: buffer r holds tile-row i + r of the wave's rows lt0 + i * step; loads run R - 1 rows
@@ -152,23 +159,23 @@ struct StripRing {
 
 // With CHECK false the caller guarantees lt0 < nt: the loads are then issued without a branch, so the wait counts of
 // loads issued before them stay exact (a branch around them makes the compiler drain every load at the join).
-template <int K, int R, bool CHECK = true>
+template <int K, int R, bool CHECK = true, bool PL = false>
 __device__ __forceinline__ void strip_prefetch(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
                                                int lane, StripRing<K, R>& ring) {
     if (CHECK && lt0 >= nt) return;
-    const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
+    const uint32_t* base = strip_lane_base<K, PL>(sp, lane) + (size_t)lt0 * rs;
     const int n = (nt - lt0 + step - 1) / step;
 #pragma unroll
-    for (int r = 0; r < R - 1; ++r) strip_load<K>(ring.D[r], base, (uint32_t)(rs * step), r, n);
+    for (int r = 0; r < R - 1; ++r) strip_load<K, PL>(ring.D[r], base, (uint32_t)(rs * step), r, n);
 }
 
-template <int K, int M, int R>
+template <int K, int M, int R, bool PL = false>
 __device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, size_t rs, int lt0, int nt, int step,
                                                int lane, const _Float16* xs, int xs_ld, float (&acc)[M][2],
                                                StripRing<K, R>& ring) {
     if (lt0 >= nt) return;
     const int n = (nt - lt0 + step - 1) / step;          // tile-rows of this wave: lt0 + i * step, i < n
-    const uint32_t* base = sp + lane * K + (size_t)lt0 * rs;
+    const uint32_t* base = strip_lane_base<K, PL>(sp, lane) + (size_t)lt0 * rs;
     const uint32_t rstep = (uint32_t)(rs * step);
     GemvAcc<M> ma;
     if constexpr (gemv_mfma<M>()) ma.zero();
@@ -186,7 +193,7 @@ __device__ __forceinline__ void strip_gemv_run(const uint32_t* __restrict__ sp, 
     for (; i + R <= n; i += R) {                         // branch-free body: loads stay R - 1 tile-rows ahead
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            strip_load<K>(ring.D[(r + R - 1) % R], base, rstep, i + r + R - 1, n);
+            strip_load<K, PL>(ring.D[(r + R - 1) % R], base, rstep, i + r + R - 1, n);
             tile_row(r, i + r);
         }
     }

@@ -241,7 +241,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 //            plane read per wave, each wave stages its own plane in a private ring instead (one unit per lane, the
 //            loads and LDS writes of the shared ring, whose threads stage its units twice or more) and the loop has no
 //            barrier.
-template <int K, int NP, int RGA, int NPS = NP>
+template <int K, int NP, int RGA, int NPS = NP, bool PL = false>
 struct MfmaPipe {
     static constexpr bool KP = K <= 5;                      // k-permuted fragments
     static constexpr int NW = FragCfg<K>::NW;
@@ -272,7 +272,7 @@ struct MfmaPipe {
     __device__ __forceinline__ void load_w(uint32_t (&D)[K], int s) const {
         const uint32_t* p = wsrc + (uint32_t)(s < nsteps ? s : nsteps - 1) * wstep;
 #pragma unroll
-        for (int i = 0; i < K; ++i) D[i] = ldg_nt(p + i);
+        for (int i = 0; i < K; ++i) D[i] = ldg_nt(p + WordOrder<K, PL>::word_off(i));
         __builtin_amdgcn_sched_barrier(0);
     }
     __device__ __forceinline__ void stage_w(const uint32_t (&D)[K]) const {
@@ -385,11 +385,14 @@ struct MfmaPipe {
         if (s + 2 < nsteps) step<2>(s + 2, W, RA, acc);
         __syncthreads();                                 // every wave's last LDS read done: callers may reuse it
     }
-    // weight set-up: pair_base(pair) = the pair's first tile (tile-row 0) in words; tile-rows are tn * 8K words apart
+    // weight set-up: tr = tile-row 0 of the projection, pair_col(pair) = the pair's first tile column (even); tile-rows
+    // are tn * 8K words apart. Lane (lane & 15) of a pair segment takes chunk lane & 7 of the pair's tile
+    // (lane & 15) >> 3, in the word order PL (WordOrder).
     template <typename F>
-    __device__ __forceinline__ void setup_w(int tn, uint32_t* wave_lds, F pair_base) {
+    __device__ __forceinline__ void setup_w(int tn, uint32_t* wave_lds, const uint32_t* tr, F pair_col) {
         const int g = lane >> 4, pair = g >> 1, hr = g & 1;
-        wsrc = pair_base(pair) + (size_t)hr * tn * (8 * K) + (lane & 15) * K;
+        wsrc = tr + (size_t)hr * tn * (8 * K) +
+               WordOrder<K, PL>::chunk_base(pair_col(pair) + ((lane & 15) >> 3), lane & 7);
         wstep = (uint32_t)(2 * tn * 8 * K);
         wl = wave_lds;
         wslot = 2 * g + ((lane & 15) >> 3);
@@ -439,7 +442,7 @@ template <int RGA>
 __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* d, int nb, int cnt,
                                               const f4_t (&acc)[kMfT][RGA], float* C, const float* rsum, int* s_comb);
 
-template <int K, int RGA>
+template <int K, int RGA, bool PL>
 __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
                                                  uint32_t* wlds, float* C, float* rsum) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -448,12 +451,12 @@ __device__ __forceinline__ void gateup_mfma_body(const MoeArgs& a, const ItemDes
     const int pw = wave >> 1;                              // this wave's projection (gate, up), its 4 tile columns
     const uint32_t* trp = reinterpret_cast<const uint32_t*>(d->tab[3 * pw]);
     const int ct0 = nb * 8 + 4 * (wave & 1);
-    MfmaPipe<K, 1, RGA, 2> L;
+    MfmaPipe<K, 1, RGA, 2, PL> L;
     L.nsteps = a.H / 32;
     L.lds = stage;
     L.lane = lane;
     L.apl = pw;
-    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) { return trp + (size_t)(ct0 + 2 * pair) * (8 * K); });
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), trp, [&](int pair) { return ct0 + 2 * pair; });
     L.setup_a(cnt, [&](int p, int row) { return a.xh + ((size_t)(p0 + row) * 2 + p) * a.H; });
     f4_t acc[kMfT][RGA];
 #pragma unroll
@@ -533,7 +536,7 @@ __device__ __forceinline__ float sum_ordered(const float* q, int n) {
 
 // One instance per row class (RGA row groups of 16): workgroup (list index, column block); indices past the class's
 // block count exit at once.
-template <int K, int RGA>
+template <int K, int RGA, bool PL = false>
 __global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     // A stages [4][2 planes][16 RGA rows x 4 units] (or per wave [4][16 rows x 4 units]) and per wave 8 staged tiles;
@@ -557,26 +560,25 @@ __global__ __launch_bounds__(256, EXL3_MFMA_GU_OCC(RGA, K)) void gateup_mfma_ker
         rsum[i] = m < cnt ? sum_ordered(a.xsum + ((size_t)(d->p0 + m) * 2 + p) * nblk, nblk) : 0.f;
     }
     __syncthreads();
-    gateup_mfma_body<K, RGA>(a, d, nb, cnt, stage, wlds, C, rsum);
+    gateup_mfma_body<K, RGA, PL>(a, d, nb, cnt, stage, wlds, C, rsum);
 }
 
 // ------------------------------------------------------------------------------------------------ down
 // 256 output columns per workgroup (two Hadamard blocks): wave w owns tile columns 4w .. 4w + 3.
-template <int K, int RGA>
+template <int K, int RGA, bool PL>
 __device__ __forceinline__ void down_mfma_body(const MoeArgs& a, const ItemDesc* d, int nb, int cnt, u32x4_t* stage,
                                                uint32_t* wlds, float* C, float* rsum, int* s_comb) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p0 = d->p0;
     const int tn = a.H / 16;
     const uint32_t* trd = reinterpret_cast<const uint32_t*>(d->tab[6]);
-    MfmaPipe<K, 1, RGA> L;
+    MfmaPipe<K, 1, RGA, 1, PL> L;
     L.nsteps = a.I / 32;
     L.lds = stage;
     L.lane = lane;
-    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) {
-        int ct = nb * 16 + 4 * wave + 2 * pair;
-        ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
-        return trd + (size_t)ct * (8 * K);
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), trd, [&](int pair) {
+        const int ct = nb * 16 + 4 * wave + 2 * pair;
+        return ct < tn ? ct : tn - 2;                  // a last half block: in-bounds loads, results unused
     });
     L.setup_a(cnt, [&](int, int row) { return reinterpret_cast<const _Float16*>(a.abuf) + (size_t)(p0 + row) * a.I; });
     f4_t acc[kMfT][RGA];
@@ -655,7 +657,7 @@ __device__ __forceinline__ void down_epilogue(const MoeArgs& a, const ItemDesc* 
         if (s_comb[i] >= 0) combine_token(a, s_comb[i], 2 * nb + (i & 1), lane);
 }
 
-template <int K, int RGA>
+template <int K, int RGA, bool PL = false>
 __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_kernel(MoeArgs a) {
     constexpr int CL = RGA == 1 ? 0 : RGA == 2 ? 1 : 2;
     // A stages [4][16 RGA rows x 4 units] (per wave at one row group) and per wave 8 staged tiles; C aliases, as above
@@ -676,7 +678,7 @@ __global__ __launch_bounds__(256, EXL3_MFMA_DOWN_OCC(RGA, K)) void down_mfma_ker
     for (int m = threadIdx.x; m < 64; m += 256)
         rsum[m] = m < cnt ? sum_ordered(a.asum + (size_t)(d->p0 + m) * nbI, nbI) : 0.f;
     __syncthreads();
-    down_mfma_body<K, RGA>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
+    down_mfma_body<K, RGA, PL>(a, d, nb, cnt, stage, wlds, C, rsum, s_comb);
 }
 
 // ------------------------------------------------------------------------------------------------ per-tile K
@@ -1193,10 +1195,9 @@ __global__ __launch_bounds__(256, RGA == 1 ? 4 : RGA == 2 ? 3 : 2) void linear_m
     L.lane = lane;
     L.apl = NPS > 1 ? (wave >> 1) : 0;
     const uint32_t* trk = a.tr + (size_t)kb0 * 8 * tn * (8 * K);
-    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), [&](int pair) {
-        int ct = nb * 16 + 4 * wave + 2 * pair;
-        ct = ct < tn ? ct : tn - 2;                    // a last half block: in-bounds loads, results unused
-        return trk + (size_t)ct * (8 * K);
+    L.setup_w(tn, wlds + wave * 8 * (8 * K + 4), trk, [&](int pair) {
+        const int ct = nb * 16 + 4 * wave + 2 * pair;
+        return ct < tn ? ct : tn - 2;                  // a last half block: in-bounds loads, results unused
     });
     L.setup_a(cnt, [&](int q, int row) {                 // a select, not an index: shard[] stays in registers
         const int sq = (NPS > 1 && q != 0) ? shard[NPS - 1] : shard[0];
@@ -1253,8 +1254,18 @@ static hipError_t set_max_lds(const void* fn, int bytes) {
     return e;
 }
 
+// PLANAR4 instantiations where that order differs from tile order (K = 3, 5, 6, 7)
 template <int RGA>
-static mfma_fn pick_gu(int K) {
+static mfma_fn pick_gu(int K, bool pl) {
+    if (pl) {
+        switch (K) {
+            case 3: return gateup_mfma_kernel<3, RGA, true>;
+            case 5: return gateup_mfma_kernel<5, RGA, true>;
+            case 6: return gateup_mfma_kernel<6, RGA, true>;
+            case 7: return gateup_mfma_kernel<7, RGA, true>;
+            default: break;
+        }
+    }
     switch (K) {
         case 1: return gateup_mfma_kernel<1, RGA>;
         case 2: return gateup_mfma_kernel<2, RGA>;
@@ -1268,7 +1279,16 @@ static mfma_fn pick_gu(int K) {
 }
 
 template <int RGA>
-static mfma_fn pick_dn(int K) {
+static mfma_fn pick_dn(int K, bool pl) {
+    if (pl) {
+        switch (K) {
+            case 3: return down_mfma_kernel<3, RGA, true>;
+            case 5: return down_mfma_kernel<5, RGA, true>;
+            case 6: return down_mfma_kernel<6, RGA, true>;
+            case 7: return down_mfma_kernel<7, RGA, true>;
+            default: break;
+        }
+    }
     switch (K) {
         case 1: return down_mfma_kernel<1, RGA>;
         case 2: return down_mfma_kernel<2, RGA>;
@@ -1309,9 +1329,11 @@ int launch_moe_mfma(const MoeArgs& a, hipStream_t st) {
     const dim3 grid_gu(nxb * (a.I / 128)), grid_dn(nxb * ((a.H / 128 + 1) / 2));
     return fork3(st, [&](int rga, hipStream_t s) -> int {
         mfma_fn gu = a.Kg == 0 ? (rga == 4 ? gateup_mix_kernel<4> : rga == 2 ? gateup_mix_kernel<2> : gateup_mix_kernel<1>)
-                               : (rga == 4 ? pick_gu<4>(a.Kg) : rga == 2 ? pick_gu<2>(a.Kg) : pick_gu<1>(a.Kg));
+                               : (rga == 4 ? pick_gu<4>(a.Kg, a.planar) : rga == 2 ? pick_gu<2>(a.Kg, a.planar)
+                                            : pick_gu<1>(a.Kg, a.planar));
         mfma_fn dn = a.Kd == 0 ? (rga == 4 ? down_mix_kernel<4> : rga == 2 ? down_mix_kernel<2> : down_mix_kernel<1>)
-                               : (rga == 4 ? pick_dn<4>(a.Kd) : rga == 2 ? pick_dn<2>(a.Kd) : pick_dn<1>(a.Kd));
+                               : (rga == 4 ? pick_dn<4>(a.Kd, a.planar) : rga == 2 ? pick_dn<2>(a.Kd, a.planar)
+                                            : pick_dn<1>(a.Kd, a.planar));
         EXL3_LAUNCH(rga == 4 ? "moe_gateup_mfma_r4" : rga == 2 ? "moe_gateup_mfma_r2" : "moe_gateup_mfma_r1", gu,
                     grid_gu, dim3(256), 0, s, a);
         EXL3_LAUNCH(rga == 4 ? "moe_down_mfma_r4" : rga == 2 ? "moe_down_mfma_r2" : "moe_down_mfma_r1", dn, grid_dn,

@@ -71,6 +71,8 @@ struct MoeArgs {
     int gu_tn;                         // tiles per tile-row of the gate and up trellises (uniform K): I / 16, or
                                        // 2 I / 16 for the reference's expert blob (gate and up tiles of a tile-row
                                        // side by side, up at gate + I / 16 tiles)
+    int planar;                        // weights in PLANAR4 word order (the reference's blobs at K = 3, 5, 6, 7):
+                                       // picks the kernels' PL instantiations (host side only)
     // routing from logits inside the fused layer (null: ids / tw hold the routing): softmax over logits (+ rbias)
     // -> top-k -> renormalised, picks written to ids_out / tw_out
     const float* logits;

@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kAlignSmall) void align_small_kernel(RouteArgs r) {
 }
 
 // ================================================================================================ gate | up
-template <int K, int MR>
+template <int K, int MR, bool PL = false>
 __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][MR][kGemvKBMax * 128];
     __shared__ float red[4][MR][2][64];
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     const size_t rs = (size_t)a.gu_tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
     StripRing<KL, 3> ring;
-    if (K > 0) strip_prefetch<KL, 3>(sp, rs, half, kb * 8, 2, lane, ring);
+    if (K > 0) strip_prefetch<KL, 3, true, PL>(sp, rs, half, kb * 8, 2, lane, ring);
 
     // phase 1: both projections' input transforms for the item's rows
     for (int i = wave; i < 2 * MR * kb; i += 4) {
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR, 3>(sp, rs, half, kb * 8, 2, lane, &xs[proj][0][0], kGemvKBMax * 128, acc, ring);
+        strip_gemv_run<KL, MR, 3, PL>(sp, rs, half, kb * 8, 2, lane, &xs[proj][0][0], kGemvKBMax * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[2 * proj]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[2 * proj + 1]);
@@ -609,7 +609,7 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
 // The last workgroup of an (item, column block) writes its rows' weighted outputs y, then counts them in per-(token,
 // column block) arrival counters; the workgroup that completes a token's slots sums them in slot order into `out`
 // (the reference's CombineKernel, fused: no separate launch).
-template <int K, int MR>
+template <int K, int MR, bool PL = false>
 __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[MR][kGemvKBMax * 128];
     __shared__ float red[4][MR][2][64];
@@ -631,7 +631,7 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
     StripRing<KL, 3> ring;
-    if (K > 0) strip_prefetch<KL, 3>(sp, rs, wave, kb * 8, 4, lane, ring);
+    if (K > 0) strip_prefetch<KL, 3, true, PL>(sp, rs, wave, kb * 8, 4, lane, ring);
 
     for (int i = wave; i < MR * kb; i += 4) {
         const int m = i / kb, b = i - m * kb;
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        strip_gemv_run<KL, MR, 3>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
+        strip_gemv_run<KL, MR, 3, PL>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(d->km[4]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(d->km[5]);
@@ -984,8 +984,18 @@ static int moe_splits(int units, int nblk) {
 
 typedef void (*moe_fn)(MoeArgs);
 
+// PLANAR4 instantiations exist where the order differs from tile order (D = K / gcd(K, 32) > 1: K = 3, 5, 6, 7)
 template <int MR>
-static moe_fn pick_gateup(int K) {
+static moe_fn pick_gateup(int K, bool pl) {
+    if (pl) {
+        switch (K) {
+            case 3: return gateup_kernel<3, MR, true>;
+            case 5: return gateup_kernel<5, MR, true>;
+            case 6: return gateup_kernel<6, MR, true>;
+            case 7: return gateup_kernel<7, MR, true>;
+            default: break;
+        }
+    }
     switch (K) {
         case 0: return gateup_kernel<0, MR>;
         case 1: return gateup_kernel<1, MR>;
@@ -1000,7 +1010,16 @@ static moe_fn pick_gateup(int K) {
 }
 
 template <int MR>
-static moe_fn pick_down(int K) {
+static moe_fn pick_down(int K, bool pl) {
+    if (pl) {
+        switch (K) {
+            case 3: return down_kernel<3, MR, true>;
+            case 5: return down_kernel<5, MR, true>;
+            case 6: return down_kernel<6, MR, true>;
+            case 7: return down_kernel<7, MR, true>;
+            default: break;
+        }
+    }
     switch (K) {
         case 0: return down_kernel<0, MR>;
         case 1: return down_kernel<1, MR>;
@@ -1014,21 +1033,21 @@ static moe_fn pick_down(int K) {
     }
 }
 
-static moe_fn gateup_select(int K, int MR) {
+static moe_fn gateup_select(int K, int MR, bool pl) {
     switch (MR) {
-        case 1: return pick_gateup<1>(K);
-        case 2: return pick_gateup<2>(K);
-        case 4: return pick_gateup<4>(K);
-        default: return pick_gateup<8>(K);
+        case 1: return pick_gateup<1>(K, pl);
+        case 2: return pick_gateup<2>(K, pl);
+        case 4: return pick_gateup<4>(K, pl);
+        default: return pick_gateup<8>(K, pl);
     }
 }
 
-static moe_fn down_select(int K, int MR) {
+static moe_fn down_select(int K, int MR, bool pl) {
     switch (MR) {
-        case 1: return pick_down<1>(K);
-        case 2: return pick_down<2>(K);
-        case 4: return pick_down<4>(K);
-        default: return pick_down<8>(K);
+        case 1: return pick_down<1>(K, pl);
+        case 2: return pick_down<2>(K, pl);
+        case 4: return pick_down<4>(K, pl);
+        default: return pick_down<8>(K, pl);
     }
 }
 
@@ -1122,9 +1141,10 @@ int moe_decode_path(MoeArgs a, int64_t npairs, hipStream_t st) {
     if (rc) return rc;
     if (use_mfma && (rc = launch_moe_mfma(a, st))) return rc;
     if (max_items > 0)
-        EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st, a);
+        EXL3_LAUNCH("moe_gateup", gateup_select(a.Kg, MR, a.planar), dim3(max_items * nbI, a.P_gu), dim3(256), 0, st,
+                    a);
     if (max_items > 0)
-        EXL3_LAUNCH("moe_down", down_select(a.Kd, MR), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
+        EXL3_LAUNCH("moe_down", down_select(a.Kd, MR, a.planar), dim3(max_items * nbH, a.P_d), dim3(256), 0, st, a);
     return EXL3_OK;
 }
 
@@ -1158,12 +1178,13 @@ __global__ void blob_tables_kernel(const int64_t* __restrict__ ptrs, int E, int6
     tab[8 * (int64_t)E + e] = sg + 4 * H + 6 * I;                  // svh_d
 }
 
-// In-place PLANAR4 -> tile order for odd K (D = K planes of G = 8 periods): within every group of 4 consecutive
-// tiles of a tile-row, word (tile t, period g, plane i) sits at 32 i + 8 t + g; in tile order it is word K g + i of
-// tile t, at 8K t + K g + i (glm/xpu/exl3xpu/moe_offload.py:68-78, glm/xpu/pack_store.py:41-54). Workgroup per
-// (expert, tile-row of gate|up then of down); the row's groups pass through LDS one at a time.
+// In-place PLANAR4 -> tile order where they differ (D = K / gcd(K, 32) > 1: K = 3, 5, 6, 7; G = 8K / D periods of D
+// words per tile): within every group of 4 consecutive tiles of a tile-row, word (tile t, period g, plane i) sits at
+// 4G i + G t + g; in tile order it is word D g + i of tile t, at 8K t + D g + i (glm/xpu/exl3xpu/moe_offload.py:68-78,
+// glm/xpu/pack_store.py:35-54). Workgroup per (expert, tile-row of gate|up then of down); the row's groups pass
+// through LDS one at a time.
 __global__ __launch_bounds__(256) void blob_unplanarize_kernel(const int64_t* __restrict__ ptrs, int64_t gu_bytes,
-                                                               int H, int I, int K) {
+                                                               int H, int I, int K, int D) {
     __shared__ uint32_t g[4 * 8 * 8];
     const int e = blockIdx.x, row = blockIdx.y;
     const int rows_gu = H / 16;
@@ -1176,14 +1197,14 @@ __global__ __launch_bounds__(256) void blob_unplanarize_kernel(const int64_t* __
         tiles = H / 16;
         base = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(base) + gu_bytes) + (size_t)(row - rows_gu) * tiles * 8 * K;
     }
-    const int W = 32 * K;                                         // words per group of 4 tiles
+    const int W = 32 * K, G = 8 * K / D;                          // words per group of 4 tiles, periods per tile
     for (int grp = 0; grp < tiles / 4; ++grp) {
         uint32_t* gp = base + (size_t)grp * W;
         for (int j = threadIdx.x; j < W; j += 256) g[j] = gp[j];
         __syncthreads();
-        for (int n = threadIdx.x; n < W; n += 256) {                // natural word n = 8K t + K gg + i
-            const int t = n / (8 * K), r = n - t * 8 * K, gg = r / K, i = r - gg * K;
-            gp[n] = g[32 * i + 8 * t + gg];
+        for (int n = threadIdx.x; n < W; n += 256) {                // natural word n = 8K t + D gg + i
+            const int t = n / (8 * K), r = n - t * 8 * K, gg = r / D, i = r - gg * D;
+            gp[n] = g[4 * G * i + G * t + gg];
         }
         __syncthreads();
     }
@@ -1270,10 +1291,15 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
     return moe_run(a, (hipStream_t)stream);
 }
 
+// D = K / gcd(K, 32): words per period of the PLANAR4 order (1: the order is tile order)
+static int planar_d(int K) { return K / (K & -K); }
+
 int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
                            const float* topk_w, int64_t topk, int64_t E, const int64_t* ptrs, int K, int act,
-                           float act_limit, void* out, int64_t out_ld, int out_dtype, void* stream) {
+                           float act_limit, void* out, int64_t out_ld, int out_dtype, int word_order, void* stream) {
     if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward_blobs: K=%d not in 1..8", K);
+    EXL3_CHECK_ARG(word_order == EXL3_WORDS_PLANAR4 || word_order == EXL3_WORDS_TILE_ORDER,
+                   "exl3_moe_forward_blobs: unknown word order %d", word_order);
     EXL3_CHECK_ARG(E > 0 && E <= kMoeMaxExperts && H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0,
                    "exl3_moe_forward_blobs: E=%lld, H=%lld, I=%lld out of range", (long long)E, (long long)H,
                    (long long)I);
@@ -1292,6 +1318,7 @@ int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H
     rc = moe_setup(x, x_ld, M, H, I, topk, E, tables, nullptr, K, K, K, act, act_limit, -1, out, out_ld, out_dtype, a);
     if (rc) return rc;
     a.gu_tn = (int)(2 * I / 16);
+    a.planar = word_order == EXL3_WORDS_PLANAR4 && planar_d(K) > 1;
     a.ids = topk_ids;
     a.tw = topk_w;
     return moe_run(a, st);
@@ -1299,16 +1326,14 @@ int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H
 
 int exl3_blob_unplanarize(const int64_t* ptrs, int64_t E, int64_t H, int64_t I, int K, void* stream) {
     if (K < 1 || K > 8) return fail(EXL3_ERR_UNSUPPORTED, "exl3_blob_unplanarize: K=%d not in 1..8", K);
-    if (K == 6)
-        return fail(EXL3_ERR_UNSUPPORTED, "exl3_blob_unplanarize: the reference defines PLANAR4 for K = 2, 3, 4, 5, 7, 8");
     EXL3_CHECK_ARG(E > 0 && E <= 65535 && H > 0 && I > 0 && H % 128 == 0 && I % 128 == 0 && H / 16 + I / 16 <= 65535,
                    "exl3_blob_unplanarize: E=%lld, H=%lld, I=%lld out of range", (long long)E, (long long)H,
                    (long long)I);
-    if (K % 2 == 0) return EXL3_OK;                                // D = K / gcd(K, 32) = 1: already in tile order
+    if (planar_d(K) == 1) return EXL3_OK;                          // K = 1, 2, 4, 8: already in tile order
     EXL3_CHECK_ARG(ptrs, "exl3_blob_unplanarize: null pointer");
     const int64_t gu_bytes = H / 16 * (2 * I / 16) * 8 * K * 4;
     EXL3_LAUNCH("blob_unplanarize", blob_unplanarize_kernel, dim3((unsigned)E, (unsigned)(H / 16 + I / 16)), dim3(256),
-                0, (hipStream_t)stream, ptrs, gu_bytes, (int)H, (int)I, K);
+                0, (hipStream_t)stream, ptrs, gu_bytes, (int)H, (int)I, K, planar_d(K));
     return EXL3_OK;
 }
 

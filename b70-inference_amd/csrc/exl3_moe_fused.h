@@ -301,30 +301,30 @@ __device__ __forceinline__ void sum_partials(const float* base, size_t stride, c
 
 // The strip GEMV sized to the item's row count (wave-uniform): most decode items hold one row, and at 4 rows the dot
 // products are a third of the GEMV's VALU work. Rows past the variant's size keep their zero accumulators.
-template <int KL, int MR>
+template <int KL, int MR, bool PL = false>
 __device__ __forceinline__ void item_gemv(int cnt, const uint32_t* sp, size_t rs, int lt0, int nt, int step, int lane,
                                           const _Float16* xs, int xs_ld, float (&acc)[MR][2],
                                           StripRing<KL, kFusedRing>& ring) {
     cnt = __builtin_amdgcn_readfirstlane(cnt);
     if constexpr (MR >= 2)
         if (cnt == 1) {
-            strip_gemv_run<KL, 1, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+            strip_gemv_run<KL, 1, kFusedRing, PL>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
                                               reinterpret_cast<float(&)[1][2]>(acc), ring);
             return;
         }
     if constexpr (MR >= 4)
         if (cnt == 2) {
-            strip_gemv_run<KL, 2, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+            strip_gemv_run<KL, 2, kFusedRing, PL>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
                                               reinterpret_cast<float(&)[2][2]>(acc), ring);
             return;
         }
     if constexpr (MR >= 8)
         if (cnt <= 4) {
-            strip_gemv_run<KL, 4, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
+            strip_gemv_run<KL, 4, kFusedRing, PL>(sp, rs, lt0, nt, step, lane, xs, xs_ld,
                                               reinterpret_cast<float(&)[4][2]>(acc), ring);
             return;
         }
-    strip_gemv_run<KL, MR, kFusedRing>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, ring);
+    strip_gemv_run<KL, MR, kFusedRing, PL>(sp, rs, lt0, nt, step, lane, xs, xs_ld, acc, ring);
 }
 
 template <int MR>
@@ -399,7 +399,7 @@ __device__ __forceinline__ void down_input(const FusedArgs& a, const int64_t* ta
     r1 = (float)(_Float16)(a1 * kRsqrt128);
 }
 
-template <int K, int MR>
+template <int K, int MR, bool PL = false>
 __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
                                              int nb, int p) {
     constexpr int KBF = FusedShared<MR>::KBF;
@@ -439,7 +439,7 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
             gv[j] = ldg(sg + c);
             uv[j] = ldg(su + c);
         }
-        if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, half, kr.nt, 2, lane, ring);   // nt >= 8 > half
+        if (K > 0) strip_prefetch<KL, kFusedRing, false, PL>(sp, rs, half, kr.nt, 2, lane, ring);   // nt >= 8 > half
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
             const int c = threadIdx.x + 256 * j;
@@ -484,7 +484,7 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        item_gemv<KL, MR>(cnt, sp, rs, half, kr.nt, 2, lane, &s.xs[proj][0][kr.xo], KBF * 128, acc, ring);
+        item_gemv<KL, MR, PL>(cnt, sp, rs, half, kr.nt, 2, lane, &s.xs[proj][0][kr.xo], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(proj ? it.km[2] : it.km[0]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(proj ? it.km[3] : it.km[1]);
@@ -540,7 +540,7 @@ __device__ __forceinline__ int split_of(int t, int P, int T) {
     return p < P - 1 ? p : P - 1;
 }
 
-template <int K, int MR>
+template <int K, int MR, bool PL = false>
 __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& s, uint64_t vm0, uint64_t vm1,
                                            const Item& it, int item, int nb, int p) {
     constexpr int KBF = FusedShared<MR>::KBF;
@@ -554,7 +554,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)kr.t0 * rs;
     StripRing<KL, kFusedRing> ring;
-    if (K > 0) strip_prefetch<KL, kFusedRing, false>(sp, rs, wave, kr.nt, 4, lane, ring);   // nt >= 8 > wave
+    if (K > 0) strip_prefetch<KL, kFusedRing, false, PL>(sp, rs, wave, kr.nt, 4, lane, ring);   // nt >= 8 > wave
     // the epilogue's output signs and row weights, loaded now so the epilogue waits for nothing
     constexpr int RW = (MR + 3) / 4;                     // rows m = wave + 4 j of this wave
     const uint16_t* svd = reinterpret_cast<const uint16_t*>(s.tab[8]) + nb * 128;
@@ -633,7 +633,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m][0] = acc[m][1] = 0.f;
     if (K > 0) {
-        item_gemv<KL, MR>(cnt, sp, rs, wave, kr.nt, 4, lane, &s.xs[0][0][kr.xo], KBF * 128, acc, ring);
+        item_gemv<KL, MR, PL>(cnt, sp, rs, wave, kr.nt, 4, lane, &s.xs[0][0][kr.xo], KBF * 128, acc, ring);
     } else {
         const uint8_t* km = reinterpret_cast<const uint8_t*>(it.km[4]);
         const int32_t* wo = reinterpret_cast<const int32_t*>(it.km[5]);
@@ -749,8 +749,8 @@ __device__ __forceinline__ void set_wave_priority(int p) {
     else __builtin_amdgcn_s_setprio(3);
 }
 
-// KG: bits of gate and up, KD: bits of down (equal, or both 0 for per-tile K).
-template <int KG, int KD, int MR>
+// KG: bits of gate and up, KD: bits of down (equal, or both 0 for per-tile K); PL: weights in PLANAR4 word order.
+template <int KG, int KD, int MR, bool PL = false>
 __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(16))) FusedShared<MR> s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -788,7 +788,7 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     // last items (the youngest workgroups) finish last and hold back their down jobs, the end of the layer. Gate|up
     // jobs run at 1..3 rising with the item number and down jobs at 0 (C3 at 4 tokens: 38.1 us against 39.9).
     set_wave_priority(1 + (3 * gi) / (nitems > 0 ? nitems : 1));
-    if (g < a.J_gu && gi < nitems) fused_gateup<KG, MR>(a, s, read_item<KG, MR>(s), gi, gr0 / a.P_gu, gr0 % a.P_gu);
+    if (g < a.J_gu && gi < nitems) fused_gateup<KG, MR, PL>(a, s, read_item<KG, MR>(s), gi, gr0 / a.P_gu, gr0 % a.P_gu);
     // the down jobs of the previous item (uniform branch)
     const int di = gi - 1;
     if (di < 0 || di >= nitems || gr0 >= a.DN) return;
@@ -799,7 +799,7 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const Item it = read_item<KG, MR>(s);
     for (int r = gr0; r < a.DN; r += a.GU) {
         // k-split major: the down jobs reading the first column blocks of I (published first) come first
-        fused_down<KD, MR>(a, s, v0, v1, it, di, r % (a.H / 128), r / (a.H / 128));
+        fused_down<KD, MR, PL>(a, s, v0, v1, it, di, r % (a.H / 128), r / (a.H / 128));
         __syncthreads();
     }
 }
@@ -808,5 +808,7 @@ typedef void (*fused_fn)(FusedArgs);
 
 // Mixed-bitrate instantiations (gate/up K != down K), exl3_moe_fused_mixed.hip; nullptr when not built.
 fused_fn pick_fused_mixed(int Kg, int Kd, int MR);
+// PLANAR4 instantiations (K = 3, 5, 6, 7), exl3_moe_fused_planar.hip; nullptr for other K.
+fused_fn pick_fused_planar(int K, int MR);
 
 }  // namespace exl3

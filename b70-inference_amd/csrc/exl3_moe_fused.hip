@@ -45,7 +45,8 @@ static int fused_splits(int want, int T, int kbf) {
 // Eligible: gate, up and down share one K (or all per-tile), or down has one or two bits more than gate/up; at most
 // kFusedMaxRows tokens and kFusedMaxPairs pairs; x rows 16-byte aligned.
 bool moe_fused_ok(const MoeArgs& a) {
-    return (a.Kg == a.Kd || pick_fused_mixed(a.Kg, a.Kd, 1) != nullptr) && a.M <= kFusedMaxRows &&
+    return (a.Kg == a.Kd || pick_fused_mixed(a.Kg, a.Kd, 1) != nullptr) && (!a.planar || a.Kg == a.Kd) &&
+           a.M <= kFusedMaxRows &&
            (int64_t)a.M * a.slots <= kFusedMaxPairs &&
            aligned(a.x, 16) && a.x_ld % 8 == 0 && env_int("EXL3MI_NO_FUSED", 0) == 0;
 }
@@ -95,7 +96,9 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) MR = mr_env;
     const int kbf = MR <= 4 ? 8 : 4;
     fused_fn fn;
-    if (m.Kg != m.Kd) {
+    if (m.planar) {
+        fn = pick_fused_planar(m.Kg, MR);
+    } else if (m.Kg != m.Kd) {
         fn = pick_fused_mixed(m.Kg, m.Kd, MR);
     } else {
         switch (MR) {

@@ -18,7 +18,8 @@ import ctypes
 
 import torch
 
-from ._lib import ACT_GELU_TANH, ACT_SILU, EXL3_F16, EXL3_F32, Exl3Error, check, lib, ptr, require_device, stream_of
+from ._lib import (ACT_GELU_TANH, ACT_SILU, EXL3_F16, EXL3_F32, EXL3_WORDS_PLANAR4, EXL3_WORDS_TILE_ORDER, Exl3Error,
+                   check, lib, ptr, require_device, stream_of)
 from .linear import BC_LinearEXL3
 
 ACTS = {"silu": ACT_SILU, "gelu_tanh": ACT_GELU_TANH, ACT_SILU: ACT_SILU, ACT_GELU_TANH: ACT_GELU_TANH}
@@ -169,17 +170,26 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, t
 
 def moe_forward_blobs(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, ptrs: torch.Tensor, I: int, K: int,
                       n_experts: int, act=ACT_SILU, act_limit: float = 0.0, out: torch.Tensor | None = None,
-                      out_dtype=None) -> torch.Tensor:
-    """exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) -> [M, H] (x's dtype unless out_dtype):
-    the routed layer over one expert blob per expert (ptrs: int64 device addresses, the reference's Geom layout in
-    tile order; odd-K blobs pass through blob_unplanarize once first)."""
+                      out_dtype=None, tile_order: bool = False) -> torch.Tensor:
+    """exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) -> [M, H] in x's dtype (unless out_dtype)
+    (glm/xpu/csrc/exl3_moe.n128.sycl:1380-1439): the routed layer over one expert blob per expert (ptrs: int64 device
+    addresses of blobs in the reference's Geom layout, trellis words in its PLANAR4 order as pack_expert writes them;
+    tile_order=True for blobs converted once by blob_unplanarize). x fp16 or bf16: bf16 rows are converted to fp16
+    first and the fp32 result rounded once to bf16, the reference kernel's own conversion points (its block loads
+    convert x to fp16, its combine stores the fp32 sum in x's dtype)."""
     require_device(x, topk_ids, topk_w, ptrs)
-    if x.dim() != 2 or x.dtype != torch.float16 or x.stride(1) != 1:
-        raise Exl3Error("moe_forward_blobs: x must be fp16 [M, H] with contiguous rows")
+    if x.dim() != 2 or x.dtype not in (torch.float16, torch.bfloat16) or x.stride(1) != 1:
+        raise Exl3Error("moe_forward_blobs: x must be fp16 or bf16 [M, H] with contiguous rows")
     if topk_ids.dtype != torch.int32 or topk_w.dtype != torch.float32 or topk_ids.shape != topk_w.shape:
         raise Exl3Error("moe_forward_blobs: topk_ids int32 and topk_w fp32 [M, k] expected")
     if ptrs.dtype != torch.int64 or ptrs.numel() < n_experts:
         raise Exl3Error("moe_forward_blobs: ptrs must be int64 [n_experts]")
+    if x.dtype == torch.bfloat16:
+        if out is not None:
+            raise Exl3Error("moe_forward_blobs: out= is for fp16 x")
+        y = moe_forward_blobs(x.half(), topk_ids, topk_w, ptrs, I, K, n_experts, act, act_limit,
+                              out_dtype=torch.float32, tile_order=tile_order)
+        return y if out_dtype == torch.float32 else y.to(out_dtype or torch.bfloat16)
     M, H = x.shape
     topk_ids, topk_w, ptrs = topk_ids.contiguous(), topk_w.contiguous(), ptrs.contiguous()
     if out is None:
@@ -192,14 +202,16 @@ def moe_forward_blobs(x: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Ten
     check(lib().exl3_moe_forward_blobs(ptr(x), x.stride(0), M, H, int(I), ptr(topk_ids), ptr(topk_w),
                                        topk_ids.shape[1] if topk_ids.dim() == 2 else 0, int(n_experts), ptr(ptrs),
                                        int(K), a, float(act_limit), ptr(out), out.stride(0),
-                                       EXL3_F32 if out.dtype == torch.float32 else EXL3_F16, stream_of(x)),
+                                       EXL3_F32 if out.dtype == torch.float32 else EXL3_F16,
+                                       EXL3_WORDS_TILE_ORDER if tile_order else EXL3_WORDS_PLANAR4, stream_of(x)),
           "moe_forward_blobs")
     return out
 
 
 def blob_unplanarize(ptrs: torch.Tensor, H: int, I: int, K: int) -> None:
-    """Put odd-K reference expert blobs (PLANAR4 word order) into tile order in place, once, before
-    moe_forward_blobs; even K needs nothing."""
+    """Optional: put the reference's expert blobs into tile order in place (K = 3, 5, 6, 7; other K need nothing),
+    exactly once; afterwards call moe_forward_blobs(..., tile_order=True). The converted blobs no longer serve the
+    reference's kernels."""
     require_device(ptrs)
     if ptrs.dtype != torch.int64:
         raise Exl3Error("blob_unplanarize: ptrs must be int64")

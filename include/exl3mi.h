@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 1
+#define EXL3_ABI_VERSION 2
 
 enum exl3_status {
     EXL3_OK = 0,
@@ -35,6 +35,7 @@ enum exl3_act { EXL3_ACT_SILU = 0, EXL3_ACT_GELU_TANH = 1 };
 enum exl3_score { EXL3_SCORE_SOFTMAX = 0, EXL3_SCORE_SIGMOID = 1, EXL3_SCORE_SQRT_SOFTPLUS = 2 };
 enum exl3_route_flags { EXL3_ROUTE_RENORM = 1, EXL3_ROUTE_BIAS_SELECT_ONLY = 2 };
 enum exl3_router_w { EXL3_ROUTER_W_HE = 0, EXL3_ROUTER_W_EH = 1 };
+enum exl3_word_order { EXL3_WORDS_PLANAR4 = 0, EXL3_WORDS_TILE_ORDER = 1 };
 
 /* Message for the last non-zero status returned on the calling thread. */
 const char* exl3_last_error(void);
@@ -186,23 +187,26 @@ int exl3_moe_forward(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
  * each blob laid out as the reference's Geom (glm/xpu/csrc/exl3_moe.n128.sycl:3-11, 56-68; packed by pack_expert,
  * glm/xpu/exl3xpu/moe_offload.py:81-94): gate|up trellis uint32 [H/16][2I/16][8K] (per tile-row the I/16 gate tiles,
  * then the I/16 up tiles), down trellis [I/16][H/16][8K], then fp16 suh_g[H] suh_u[H] svh_g[I] svh_u[I] suh_d[I]
- * svh_d[H]; blobs 16-byte aligned, every routed expert's pointer valid. The words must be in tile order: so they are
- * for even K (PLANAR4 is the identity there), odd-K blobs are converted once by exl3_blob_unplanarize. One K for all
- * projections; no shared expert (the reference adds it outside the op). Other arguments, paths and results as
- * exl3_moe_forward with the same weights.
+ * svh_d[H]; blobs 16-byte aligned, every routed expert's pointer valid. word_order EXL3_WORDS_PLANAR4: the trellis
+ * words as the reference packs them and its kernels read them, in place (PLANAR4: a tile's 8K words are G periods
+ * of D = K / gcd(K, 32) words, and within each group of 4 consecutive tiles of a tile-row word (tile t, period g,
+ * plane i) sits at 4G i + G t + g, G = 8K / D; for K = 1, 2, 4, 8 that is tile order; glm/xpu/exl3xpu/
+ * moe_offload.py:68-78, glm/xpu/pack_store.py:35-54). EXL3_WORDS_TILE_ORDER: blobs that exl3_blob_unplanarize has
+ * converted (every K; the same words at even K). One K for all projections, 1..8 (the reference op takes 2, 3 and 4);
+ * no shared expert (the reference adds it outside the op). Other arguments, paths and results as exl3_moe_forward
+ * with the same weights.
  * Replaces: exl3xpu_moe::moe_forward(x, topk_ids, topk_w, ptrs, I, K, n_experts) (glm/xpu/csrc/exl3_moe.n128.sycl:
  *           1380-1439, bound at :1681-1682). */
 int exl3_moe_forward_blobs(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int64_t I, const int32_t* topk_ids,
                            const float* topk_w, int64_t topk, int64_t E, const int64_t* ptrs, int K, int act,
-                           float act_limit, void* out, int64_t out_ld, int out_dtype, void* stream);
+                           float act_limit, void* out, int64_t out_ld, int out_dtype, int word_order, void* stream);
 
-/* One-time conversion of the reference's expert blobs to tile order, in place: for odd K (3, 5, 7) the trellis words
- * of every group of 4 tiles of a tile-row are stored plane by plane (PLANAR4, glm/xpu/exl3xpu/moe_offload.py:68-78,
- * glm/xpu/pack_store.py:41-54) and are put back into tile order; even K is already in tile order (no work). K = 6 is
- * not a PLANAR4 bitrate of the reference. Blobs and sizes as exl3_moe_forward_blobs. After it the blobs serve
- * exl3_moe_forward_blobs (and no longer the reference's kernels).
- * No reference counterpart: the reference's kernels read PLANAR4 directly (Xe register regions cannot stride by K);
- * the gfx950 kernels load K words per lane from tile order. */
+/* Optional one-time conversion of the reference's expert blobs to tile order, in place: where PLANAR4 differs from
+ * tile order (K = 3, 5, 6, 7) the words of every group of 4 tiles of a tile-row are put back into tile order; other K
+ * need no work. Blobs and sizes as exl3_moe_forward_blobs. Afterwards the blobs are read with EXL3_WORDS_TILE_ORDER
+ * (one K-dword load per lane instead of K dword loads) and no longer serve the reference's kernels; converting a blob
+ * twice scrambles it.
+ * No reference counterpart: the reference's kernels always read PLANAR4 (Xe register regions cannot stride by K). */
 int exl3_blob_unplanarize(const int64_t* ptrs, int64_t E, int64_t H, int64_t I, int K, void* stream);
 
 /* The routed MoE layer from router logits: exl3_route_softmax_topk followed by exl3_moe_forward, as one call, with

@@ -161,25 +161,34 @@ def test_arena_experts_same_outputs(exl3, M):
     assert err <= 2e-3, err
 
 
+# decode paths of the layer by batch shape: (tokens, top-k, experts) -> the one-launch fused layer (<= 16 tokens, <= 128
+# pairs), the multi-kernel decode GEMVs (<= 8 tokens, more than 128 pairs), the MFMA grouped GEMM (more than 8 tokens)
+BLOB_PATHS = {"fused": (3, 2, 6), "gemv": (8, 17, 20), "mfma": (40, 2, 6)}
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("K", [2, 3, 4])
-@pytest.mark.parametrize("M", [3, 40])
-def test_moe_forward_blobs_on_reference_blobs(exl3, K, M):
-    """The reference's blob-pointer op: experts packed as the reference packs them (pack_expert / planar4, restated in
-    the oracle), one device blob per expert, odd K put into tile order once; the layer equals exl3_moe_forward on
-    separately allocated tensors bit for bit (fused decode at 3 rows, MFMA at 40) and the oracle's layer."""
-    E, H, I = 6, 256, 256
-    experts = [_expert(H, I, K, K, 1200 + 10 * e) for e in range(E)]
-    blobs = [torch.from_numpy(O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in ex], K)).cuda()
-             for ex in experts]
+@pytest.mark.parametrize("K", [2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("HI", [(256, 384), (384, 256)])
+@pytest.mark.parametrize("path", list(BLOB_PATHS))
+def test_moe_forward_blobs_on_reference_blobs(exl3, K, HI, path):
+    """The reference's blob-pointer op on blobs exactly as the reference packs them (pack_expert / planar4, restated in
+    the oracle and pinned by the element-loop index map above; PLANAR4 differs from tile order at K = 3, 5, 6, 7), one
+    device blob per expert, read in place: the layer equals exl3_moe_forward on separately allocated tensors bit for
+    bit and the oracle's layer to 2e-3, on each decode path, with H != I both ways (so a swapped H / I in the blob
+    offsets fails). The blobs are not modified by the call."""
+    H, I = HI
+    M, topk, E = BLOB_PATHS[path]
+    experts = [_expert(H, I, K, K, 1200 + 10 * e + K) for e in range(E)]
+    host = [O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in ex], K) for ex in experts]
+    blobs = [torch.from_numpy(b).cuda() for b in host]
     ptrs = torch.tensor([b.data_ptr() for b in blobs], dtype=torch.int64, device="cuda")
-    exl3.blob_unplanarize(ptrs, H, I, K)
     g = torch.Generator().manual_seed(1300 + 10 * M + K)
     x = torch.randn(M, H, generator=g).half()
     logits = torch.randn(M, E, generator=g)
-    rid, rw = O.route_softmax_topk(logits.numpy(), 2)
+    rid, rw = O.route_softmax_topk(logits.numpy(), topk)
     ids = torch.from_numpy(rid.astype(np.int32)).cuda()
     w = torch.from_numpy(rw.astype(np.float32)).cuda()
+    print(f"blob op: K={K} H={H} I={I} {path} M={M} top-{topk} of {E}", flush=True)
     y = exl3.moe_forward_blobs(x.cuda(), ids, w, ptrs, I, K, E, out_dtype=torch.float32)
 
     def lin(p):
@@ -192,6 +201,60 @@ def test_moe_forward_blobs_on_reference_blobs(exl3, K, M):
            for ex in experts]
     ref = O.moe_layer(x.numpy(), orc, rid, rw, O.ACT_SILU)
     assert np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max() <= 2e-3
+    for b, h in zip(blobs, host):
+        assert np.array_equal(b.cpu().numpy(), h)
     # the reference op returns x's dtype
     y16 = exl3.moe_forward_blobs(x.cuda(), ids, w, ptrs, I, K, E)
     assert y16.dtype == torch.float16 and np.abs(y16.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= 2e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [3, 6])
+def test_blob_unplanarize_then_tile_order_reads_the_same_layer(exl3, K):
+    """The optional conversion: blob_unplanarize puts each blob's words into tile order (equal to the oracle's tile-
+    order words), and the tile-order read of the converted blobs gives the PLANAR4 read's layer bit for bit."""
+    H, I, E = 256, 384, 6
+    experts = [_expert(H, I, K, K, 1500 + 10 * e) for e in range(E)]
+    host = [O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in ex], K) for ex in experts]
+    blobs = [torch.from_numpy(b).cuda() for b in host]
+    ptrs = torch.tensor([b.data_ptr() for b in blobs], dtype=torch.int64, device="cuda")
+    g = torch.Generator().manual_seed(1600 + K)
+    x = torch.randn(5, H, generator=g).half().cuda()
+    rid, rw = O.route_softmax_topk(torch.randn(5, E, generator=g).numpy(), 2)
+    ids = torch.from_numpy(rid.astype(np.int32)).cuda()
+    w = torch.from_numpy(rw.astype(np.float32)).cuda()
+    y_pl = exl3.moe_forward_blobs(x, ids, w, ptrs, I, K, E, out_dtype=torch.float32)
+    exl3.blob_unplanarize(ptrs, H, I, K)
+    for ex, b in zip(experts, blobs):
+        gu = np.concatenate([ex[0]["trellis"].numpy(), ex[1]["trellis"].numpy()], axis=1)
+        nw = gu.size // 2
+        words = b.cpu().numpy().view(np.uint32)
+        assert np.array_equal(words[:nw], np.ascontiguousarray(gu).view(np.uint32).reshape(-1))
+        assert np.array_equal(words[nw:nw + ex[2]["trellis"].numel() // 2],
+                              np.ascontiguousarray(ex[2]["trellis"].numpy()).view(np.uint32).reshape(-1))
+    y_t = exl3.moe_forward_blobs(x, ids, w, ptrs, I, K, E, out_dtype=torch.float32, tile_order=True)
+    assert torch.equal(y_pl, y_t)
+
+
+@pytest.mark.gpu
+def test_moe_forward_blobs_bf16_x(exl3):
+    """bf16 x, as the reference op accepts it: rows converted to fp16 before the input transform and the fp32 layer
+    output rounded once to bf16 (the reference kernel's block-load conversion and its combine store), against the
+    oracle's layer on the fp16-converted rows."""
+    H, I, K, E = 256, 256, 3, 6
+    experts = [_expert(H, I, K, K, 1700 + 10 * e) for e in range(E)]
+    blobs = [torch.from_numpy(O.reference_blob(*[{k: v.numpy() for k, v in p.items()} for p in ex], K)).cuda()
+             for ex in experts]
+    ptrs = torch.tensor([b.data_ptr() for b in blobs], dtype=torch.int64, device="cuda")
+    g = torch.Generator().manual_seed(1800)
+    xb = torch.randn(4, H, generator=g).bfloat16()
+    rid, rw = O.route_softmax_topk(torch.randn(4, E, generator=g).numpy(), 2)
+    ids = torch.from_numpy(rid.astype(np.int32)).cuda()
+    w = torch.from_numpy(rw.astype(np.float32)).cuda()
+    y = exl3.moe_forward_blobs(xb.cuda(), ids, w, ptrs, I, K, E)
+    assert y.dtype == torch.bfloat16
+    orc = [tuple(O.Proj(p["suh"].numpy(), p["svh"].numpy(), trellis=p["trellis"].numpy(), K=K) for p in ex)
+           for ex in experts]
+    ref = O.moe_layer(xb.half().numpy(), orc, rid, rw, O.ACT_SILU)
+    # 2e-3 for the layer plus half a bf16 ulp (2^-9 relative) for the final rounding
+    assert np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= 2e-3 + 2 ** -9
