@@ -1304,6 +1304,11 @@ static mfma_fn pick_dn(int K, bool pl) {
 template <typename F>
 static int fork3(hipStream_t st, F launch) {
     // the three row classes run concurrently: 4 row groups on the caller's stream, 2 and 1 on the side streams
+    if (env_int("EXL3MI_SERIAL_CLASSES", 0)) {            // every class on the caller's stream, one after another
+        int rc = 0;
+        if ((rc = launch(4, st)) || (rc = launch(2, st)) || (rc = launch(1, st))) return rc;
+        return EXL3_OK;
+    }
     AuxStreams ax;
     int rc = aux_streams(&ax);
     if (rc) return rc;

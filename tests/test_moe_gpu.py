@@ -500,3 +500,34 @@ def test_moe_c4_shape_rows_vs_oracle(exl3, oracle):
     assert np.array_equal(ids.cpu().numpy(), rid)
     y, ref = _run(exl3, oracle, tables, orc, x, ids.cpu(), w.cpu())
     assert max_rel(y, ref) <= MAX_REL
+
+
+@pytest.mark.parametrize("Kgu,Kd", [(2, 3), (4, 4), (6, 6)])
+def test_moe_prefill_hot_experts_many_blocks(exl3, oracle, monkeypatch, Kgu, Kd):
+    """Hot experts cut into many 64-row blocks of every row class: experts of 520, 300, 257, 256, 130 and 65 rows
+    (8 blocks + 8 rows, 4 + 44, 4 + 1, 4, 2 + 2, 1 + 1) beside 40- and 10-row experts, at uniform K with k-permuted
+    (K <= 5) and natural-order (K = 6) fragments. Every row against the oracle; the row classes run concurrently on
+    three streams or one after another on the caller's stream (EXL3MI_SERIAL_CLASSES=1) with the same rows bit for
+    bit; a token permutation permutes the rows bit for bit."""
+    E, H, I = 8, 256, 384
+    tables, orc = make_experts(exl3, oracle, E, H, I, Kgu, Kd, 2300 + 10 * Kgu)
+    loads = [520, 300, 257, 256, 130, 65, 40, 10]
+    flat = torch.cat([torch.full((c,), e, dtype=torch.int32) for e, c in enumerate(loads)])
+    M = flat.numel() // 2
+    ids = torch.stack([flat[:M], flat[M:]], 1)              # sorted halves: a token's two experts differ
+    g = torch.Generator().manual_seed(2301)
+    ids = ids[torch.randperm(M, generator=g)].contiguous()
+    w = torch.rand(M, 2, generator=g)
+    w = (w / w.sum(1, keepdim=True)).float()
+    x = torch.randn(M, H, generator=g).half()
+    print(f"hot experts: K {Kgu}/{Kd}, {M} tokens, loads {loads}", flush=True)
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    a = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables)
+    monkeypatch.setenv("EXL3MI_SERIAL_CLASSES", "1")
+    b = exl3.moe_forward(x.cuda(), ids.cuda(), w.cuda(), tables)
+    monkeypatch.delenv("EXL3MI_SERIAL_CLASSES")
+    assert torch.equal(a, b)
+    perm = torch.randperm(M, generator=g)
+    c = exl3.moe_forward(x[perm].cuda(), ids[perm].cuda(), w[perm].cuda(), tables)
+    assert torch.equal(a[perm.cuda()], c)
