@@ -336,6 +336,27 @@ __device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, co
     return wave_sum_f32((float)ha + (float)hb);
 }
 
+// had_in_block split in two, so that a caller can issue the loads early: the block's x and sign elements lane and
+// lane + 64 (unconditional loads: x must point at readable memory), then the transform, with x taken as zeros unless
+// `valid`.
+struct HadIn {
+    uint16_t xa, xb, sa, sb;
+};
+__device__ __forceinline__ HadIn had_in_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ suh, int lane) {
+    return HadIn{ldg(x + lane), ldg(x + lane + 64), ldg(suh + lane), ldg(suh + lane + 64)};
+}
+__device__ __forceinline__ float had_in_finish(const HadIn& v, bool valid, _Float16* dst, int lane) {
+    float va = (float)(_Float16)(h2f(v.xa) * h2f(v.sa));
+    float vb = (float)(_Float16)(h2f(v.xb) * h2f(v.sb));
+    va = valid ? va : 0.f;
+    vb = valid ? vb : 0.f;
+    fwht128_wave(va, vb, lane);
+    _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
+    dst[lane] = ha;
+    dst[lane + 64] = hb;
+    return wave_sum_f32((float)ha + (float)hb);
+}
+
 // Same for an activation block that is already in the Hadamard domain (fp16): copy to LDS and sum.
 __device__ __forceinline__ float copy_block(const uint16_t* __restrict__ x, _Float16* dst, int lane) {
     _Float16 ha = (_Float16)0.f, hb = (_Float16)0.f;

@@ -180,10 +180,10 @@ __device__ __forceinline__ int64_t mgemm_matrix(const int64_t* idx, int z, int64
     return (q >= 0 && q < nmat) ? q : -1;
 }
 
-template <int K, int M, bool F32>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+template <int K, int M, bool F32, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[M][kGemvKBMax * 128];
-    __shared__ float red[4][M][2][64];
+    __shared__ float red[NW][M][2][64];
     __shared__ float bsum[M][kGemvKBMax];
     __shared__ int s_last;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -205,22 +205,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int kb = b1 - b0;
     const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
     const uint32_t* sp = tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
-    StripRing<K, kLinearRing> ring;
-    strip_prefetch<K, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, ring);   // weight loads in flight during phase 1
-
     // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums; the
-    // strip's shard selects the sign vector (clamped into [0, S))
+    // strip's shard selects the sign vector (clamped into [0, S)). The wave's first x block and its signs are loaded
+    // before the weight prefetch (loads complete in issue order: the transform then waits for nothing issued after
+    // them), with clamped addresses so that no load sits under a branch.
     int shard = 0;
     if (a.sonb) {
         shard = a.sonb[strip];
         shard = shard < 0 ? 0 : (shard >= a.S ? a.S - 1 : shard);
     }
     const uint16_t* suh = suh_all + (size_t)shard * (a.nblk * 128);
-    for (int i = wave; i < M * kb; i += 4) {
-        const int m = i / kb, b = i - m * kb;
-        const int k0 = (b0 + b) * 128;
-        float s = had_in_block(m < a.m ? x + (int64_t)m * a.x_ld + k0 : nullptr, suh + k0, &xs[m][b * 128], lane);
-        if (lane == 0) bsum[m][b] = s;
+    const int nbm = M * kb;                                         // (row, block) pairs of the split
+    auto block_ptrs = [&](int i, const uint16_t*& xp, const uint16_t*& sp_) {
+        const int m = i / kb, b = i - m * kb, k0 = (b0 + b) * 128;
+        xp = x + (int64_t)(m < a.m ? m : 0) * a.x_ld + k0;
+        sp_ = suh + k0;
+    };
+    constexpr int JB = (M * kGemvKBMax + NW - 1) / NW;              // blocks per wave, at most
+    HadIn hv[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int i = wave + j * NW;
+        const uint16_t *xp, *sq;
+        block_ptrs(i < nbm ? i : nbm - 1, xp, sq);
+        hv[j] = had_in_load(xp, sq, lane);
+    }
+    StripRing<K, kLinearRing> ring;
+    // weight loads in flight during phase 1, issued without a branch (wave < NW <= 8 <= kb * 8 tile-rows)
+    strip_prefetch<K, kLinearRing, false>(sp, rs, wave, kb * 8, NW, lane, ring);
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int i = wave + j * NW;
+        if (i < nbm) {
+            const int m = i / kb, b = i - m * kb;
+            const float s = had_in_finish(hv[j], m < a.m, &xs[m][b * 128], lane);
+            if (lane == 0) bsum[m][b] = s;
+        }
     }
     __syncthreads();
 
@@ -228,7 +248,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     float acc[M][2];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m][0] = acc[m][1] = 0.f;
-    strip_gemv_run<K, M, kLinearRing>(sp, rs, wave, kb * 8, 4, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
+    strip_gemv_run<K, M, kLinearRing>(sp, rs, wave, kb * 8, NW, lane, &xs[0][0], kGemvKBMax * 128, acc, ring);
 
     // phase 3: reduce waves, then splits
 #pragma unroll
@@ -246,13 +266,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
             for (int b = 0; b < kb; ++b) sx += bsum[m][b];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                float v = red[0][m][h][lane] + red[1][m][h][lane] + red[2][m][h][lane] + red[3][m][h][lane];
+                float v = red[0][m][h][lane];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) v += red[w][m][h][lane];
                 splitk_store(mypart + m * 128 + cbase + 8 * h, kMul1C1 * v + kMul1C2 * sx);
             }
         }
     }
     if (!splitk_arrive(&cnt[strip], a.P, &s_last)) return;
-    for (int m = wave; m < M && m < a.m; m += 4) {
+    for (int m = wave; m < M && m < a.m; m += NW) {
         float va = 0.f, vb = 0.f;
 #pragma unroll 8
         for (int pp = 0; pp < a.P; ++pp) {
@@ -280,35 +302,43 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 // ------------------------------------------------------------------------------------------------ dispatch
 typedef void (*gemv_fn)(GemvArgs);
 
+// Waves per workgroup: 4, or 8 for up to 2 rows when the grid is small enough for one round of workgroups (then two
+// waves per SIMD share a split's tile-rows: C1, 4096 x 4096 at one row, 7.66 -> 7.29 us; with more workgroups than
+// one round, eight-wave workgroups were slower: 5376 x 21504 at one row, 21.0 -> 21.3 us)
+constexpr int kGemvWideMaxWG = 512;
+
 template <int K, int M>
-static gemv_fn gemv_pick(bool f32) {
-    return f32 ? (gemv_fn)gemv_kernel<K, M, true> : (gemv_fn)gemv_kernel<K, M, false>;
+static gemv_fn gemv_pick(bool f32, bool wide) {
+    if constexpr (M <= 2) {
+        if (wide) return f32 ? (gemv_fn)gemv_kernel<K, M, true, 8> : (gemv_fn)gemv_kernel<K, M, false, 8>;
+    }
+    return f32 ? (gemv_fn)gemv_kernel<K, M, true, 4> : (gemv_fn)gemv_kernel<K, M, false, 4>;
 }
 
 template <int K>
-static gemv_fn gemv_pick_m(int M, bool f32) {
+static gemv_fn gemv_pick_m(int M, bool f32, bool wide) {
     switch (M) {
-        case 1: return gemv_pick<K, 1>(f32);
-        case 2: return gemv_pick<K, 2>(f32);
-        case 3: return gemv_pick<K, 3>(f32);
-        case 4: return gemv_pick<K, 4>(f32);
-        case 5: return gemv_pick<K, 5>(f32);
-        case 6: return gemv_pick<K, 6>(f32);
-        case 7: return gemv_pick<K, 7>(f32);
-        default: return gemv_pick<K, 8>(f32);
+        case 1: return gemv_pick<K, 1>(f32, wide);
+        case 2: return gemv_pick<K, 2>(f32, wide);
+        case 3: return gemv_pick<K, 3>(f32, wide);
+        case 4: return gemv_pick<K, 4>(f32, wide);
+        case 5: return gemv_pick<K, 5>(f32, wide);
+        case 6: return gemv_pick<K, 6>(f32, wide);
+        case 7: return gemv_pick<K, 7>(f32, wide);
+        default: return gemv_pick<K, 8>(f32, wide);
     }
 }
 
-static gemv_fn gemv_select(int K, int M, bool f32) {
+static gemv_fn gemv_select(int K, int M, bool f32, bool wide) {
     switch (K) {
-        case 1: return gemv_pick_m<1>(M, f32);
-        case 2: return gemv_pick_m<2>(M, f32);
-        case 3: return gemv_pick_m<3>(M, f32);
-        case 4: return gemv_pick_m<4>(M, f32);
-        case 5: return gemv_pick_m<5>(M, f32);
-        case 6: return gemv_pick_m<6>(M, f32);
-        case 7: return gemv_pick_m<7>(M, f32);
-        default: return gemv_pick_m<8>(M, f32);
+        case 1: return gemv_pick_m<1>(M, f32, wide);
+        case 2: return gemv_pick_m<2>(M, f32, wide);
+        case 3: return gemv_pick_m<3>(M, f32, wide);
+        case 4: return gemv_pick_m<4>(M, f32, wide);
+        case 5: return gemv_pick_m<5>(M, f32, wide);
+        case 6: return gemv_pick_m<6>(M, f32, wide);
+        case 7: return gemv_pick_m<7>(M, f32, wide);
+        default: return gemv_pick_m<8>(M, f32, wide);
     }
 }
 
@@ -346,11 +376,13 @@ static int gemv_chunks(GemvArgs ga, int64_t m, int K, bool f32, int strips, int 
         c.m = mm;
         c.out = f32 ? (void*)(reinterpret_cast<float*>(ga.out) + m0 * ga.out_ld)
                     : (void*)(reinterpret_cast<uint16_t*>(ga.out) + m0 * ga.out_ld);
-        gemv_fn fn = gemv_select(K, mm, f32);
+        const bool wide = mm <= 2 && (int64_t)strips * ga.P * slots <= kGemvWideMaxWG;
+        gemv_fn fn = gemv_select(K, mm, f32, wide);
+        const dim3 block(wide ? 512 : 256);
         if (profiled) {
-            EXL3_LAUNCH("gemv", fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+            EXL3_LAUNCH("gemv", fn, dim3(strips, ga.P, slots), block, 0, st, c);
         } else {
-            hipLaunchKernelGGL(fn, dim3(strips, ga.P, slots), dim3(256), 0, st, c);
+            hipLaunchKernelGGL(fn, dim3(strips, ga.P, slots), block, 0, st, c);
             EXL3_CHECK_HIP(hipGetLastError());
         }
     }
