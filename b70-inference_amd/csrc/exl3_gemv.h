@@ -319,26 +319,10 @@ __device__ __forceinline__ bool splitk_arrive(int* cnt, int nparts, int* s_flag)
     return last;
 }
 
-// Input transform of one 128-block for one row by one wave: returns fp16(H128(fp16(x * suh)) / sqrt(128)) at
-// elements lane and lane + 64 (as floats holding fp16 values) and writes them to dst[lane], dst[lane + 64].
-// x == nullptr gives zeros. Returns the block's element sum (every lane gets it).
-__device__ __forceinline__ float had_in_block(const uint16_t* __restrict__ x, const uint16_t* __restrict__ suh,
-                                              _Float16* dst, int lane) {
-    float va = 0.f, vb = 0.f;
-    if (x) {
-        va = (float)(_Float16)(h2f(ldg(x + lane)) * h2f(ldg(suh + lane)));
-        vb = (float)(_Float16)(h2f(ldg(x + lane + 64)) * h2f(ldg(suh + lane + 64)));
-    }
-    fwht128_wave(va, vb, lane);
-    _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
-    dst[lane] = ha;
-    dst[lane + 64] = hb;
-    return wave_sum_f32((float)ha + (float)hb);
-}
-
-// had_in_block split in two, so that a caller can issue the loads early: the block's x and sign elements lane and
-// lane + 64 (unconditional loads: x must point at readable memory), then the transform, with x taken as zeros unless
-// `valid`.
+// Input transform of one 128-block for one row by one wave, in two parts so that a caller can issue the loads early:
+// had_in_load loads the block's x and sign elements lane and lane + 64 (unconditional loads: x must point at readable
+// memory); had_in_finish writes fp16(H128(fp16(x * suh)) / sqrt(128)) at elements lane and lane + 64 to dst[lane],
+// dst[lane + 64], with x taken as zeros unless `valid`, and returns the block's element sum (every lane gets it).
 struct HadIn {
     uint16_t xa, xb, sa, sb;
 };
@@ -352,18 +336,6 @@ __device__ __forceinline__ float had_in_finish(const HadIn& v, bool valid, _Floa
     vb = valid ? vb : 0.f;
     fwht128_wave(va, vb, lane);
     _Float16 ha = (_Float16)(va * kRsqrt128), hb = (_Float16)(vb * kRsqrt128);
-    dst[lane] = ha;
-    dst[lane + 64] = hb;
-    return wave_sum_f32((float)ha + (float)hb);
-}
-
-// Same for an activation block that is already in the Hadamard domain (fp16): copy to LDS and sum.
-__device__ __forceinline__ float copy_block(const uint16_t* __restrict__ x, _Float16* dst, int lane) {
-    _Float16 ha = (_Float16)0.f, hb = (_Float16)0.f;
-    if (x) {
-        ha = __builtin_bit_cast(_Float16, ldg(x + lane));
-        hb = __builtin_bit_cast(_Float16, ldg(x + lane + 64));
-    }
     dst[lane] = ha;
     dst[lane + 64] = hb;
     return wave_sum_f32((float)ha + (float)hb);

@@ -522,17 +522,39 @@ __global__ __launch_bounds__(256) void gateup_kernel(MoeArgs a) {
     constexpr int KL = K > 0 ? K : 1;
     const size_t rs = (size_t)a.gu_tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
-    StripRing<KL, 3> ring;
-    if (K > 0) strip_prefetch<KL, 3, true, PL>(sp, rs, half, kb * 8, 2, lane, ring);
-
-    // phase 1: both projections' input transforms for the item's rows
-    for (int i = wave; i < 2 * MR * kb; i += 4) {
+    // phase 1: both projections' input transforms for the item's rows. The wave's first JB blocks of x and signs are
+    // loaded before the weight prefetch (unconditional loads at clamped addresses, prefetch without a branch:
+    // half < 8 <= kb * 8), so their transforms wait for nothing issued after them; later blocks load afterwards.
+    const int nbm = 2 * MR * kb;
+    auto block_ptrs = [&](int i, const uint16_t*& xp, const uint16_t*& sq) {
         const int proj = i / (MR * kb), rem = i - proj * MR * kb, m = rem / kb, b = rem - m * kb;
         const int k0 = (b0 + b) * 128;
-        const uint16_t* suh = reinterpret_cast<const uint16_t*>(d->tab[3 * proj + 1]);
-        const uint16_t* xr = m < cnt ? a.x + (int64_t)d->tok[m] * a.x_ld + k0 : nullptr;
-        float s = had_in_block(xr, suh + k0, &xs[proj][m][b * 128], lane);
+        sq = reinterpret_cast<const uint16_t*>(d->tab[3 * proj + 1]) + k0;
+        xp = a.x + (int64_t)d->tok[m < cnt ? m : 0] * a.x_ld + k0;
+    };
+    constexpr int JB = 2;
+    HadIn hv[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int i = wave + 4 * j;
+        const uint16_t *xp, *sq;
+        block_ptrs(i < nbm ? i : nbm - 1, xp, sq);
+        hv[j] = had_in_load(xp, sq, lane);
+    }
+    StripRing<KL, 3> ring;
+    if (K > 0) strip_prefetch<KL, 3, false, PL>(sp, rs, half, kb * 8, 2, lane, ring);
+    auto finish = [&](int i, const HadIn& h) {
+        const int proj = i / (MR * kb), rem = i - proj * MR * kb, m = rem / kb, b = rem - m * kb;
+        const float s = had_in_finish(h, m < cnt, &xs[proj][m][b * 128], lane);
         if (lane == 0) bsum[proj][m][b] = s;
+    };
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+        if (wave + 4 * j < nbm) finish(wave + 4 * j, hv[j]);
+    for (int i = wave + 4 * JB; i < nbm; i += 4) {
+        const uint16_t *xp, *sq;
+        block_ptrs(i, xp, sq);
+        finish(i, had_in_load(xp, sq, lane));
     }
     __syncthreads();
 
@@ -630,14 +652,38 @@ __global__ __launch_bounds__(256) void down_kernel(MoeArgs a) {
     constexpr int KL = K > 0 ? K : 1;
     const size_t rs = (size_t)tn * (8 * KL);
     const uint32_t* sp = tr + (size_t)nb * (64 * KL) + (size_t)b0 * 8 * rs;
-    StripRing<KL, 3> ring;
-    if (K > 0) strip_prefetch<KL, 3, true, PL>(sp, rs, wave, kb * 8, 4, lane, ring);
-
-    for (int i = wave; i < MR * kb; i += 4) {
+    // the wave's first JB input blocks loaded before the weight prefetch (as in gateup_kernel; wave < 8 <= kb * 8)
+    const int nbm = MR * kb;
+    auto src_of = [&](int i) {
         const int m = i / kb, b = i - m * kb;
-        const uint16_t* src = m < cnt ? a.abuf + (size_t)(p0 + m) * a.I + (b0 + b) * 128 : nullptr;
-        float s = copy_block(src, &xs[m][b * 128], lane);
+        return a.abuf + (size_t)(p0 + (m < cnt ? m : 0)) * a.I + (b0 + b) * 128;
+    };
+    constexpr int JB = 2;
+    uint16_t ca[JB], cb[JB];
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+        const int i = wave + 4 * j;
+        const uint16_t* src = src_of(i < nbm ? i : nbm - 1);
+        ca[j] = ldg(src + lane);
+        cb[j] = ldg(src + lane + 64);
+    }
+    StripRing<KL, 3> ring;
+    if (K > 0) strip_prefetch<KL, 3, false, PL>(sp, rs, wave, kb * 8, 4, lane, ring);
+    auto put = [&](int i, uint16_t va, uint16_t vb) {
+        const int m = i / kb, b = i - m * kb;
+        const _Float16 ha = m < cnt ? __builtin_bit_cast(_Float16, va) : (_Float16)0.f;
+        const _Float16 hb = m < cnt ? __builtin_bit_cast(_Float16, vb) : (_Float16)0.f;
+        xs[m][b * 128 + lane] = ha;
+        xs[m][b * 128 + lane + 64] = hb;
+        const float s = wave_sum_f32((float)ha + (float)hb);
         if (lane == 0) bsum[m][b] = s;
+    };
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+        if (wave + 4 * j < nbm) put(wave + 4 * j, ca[j], cb[j]);
+    for (int i = wave + 4 * JB; i < nbm; i += 4) {
+        const uint16_t* src = src_of(i);
+        put(i, ldg(src + lane), ldg(src + lane + 64));
     }
     __syncthreads();
 
