@@ -161,16 +161,21 @@ __device__ __forceinline__ void lane_top2(const uint32_t (&key)[V], const float 
     k1 = k2 = 0u;
     v1 = v2 = 0;
     g1 = g2 = 0.f;
+    // selects only (no branch per key: each would switch the exec mask on the routing's dependency chain)
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         const bool left = vl < 0 || key[v] < kl || (key[v] == kl && v > vl);
         const uint32_t kv = left ? key[v] : 0u;
-        if (kv > k1) {
-            k2 = k1; v2 = v1; g2 = g1;
-            k1 = kv; v1 = v; g1 = g[v];
-        } else if (kv > k2) {
-            k2 = kv; v2 = v; g2 = g[v];
-        }
+        const bool gt1 = kv > k1, gt2 = kv > k2;
+        const uint32_t nk2 = gt1 ? k1 : (gt2 ? kv : k2);
+        const int nv2 = gt1 ? v1 : (gt2 ? v : v2);
+        const float ng2 = gt1 ? g1 : (gt2 ? g[v] : g2);
+        k1 = gt1 ? kv : k1;
+        v1 = gt1 ? v : v1;
+        g1 = gt1 ? g[v] : g1;
+        k2 = nk2;
+        v2 = nv2;
+        g2 = ng2;
     }
 }
 
@@ -191,22 +196,22 @@ __device__ __forceinline__ void route_select(const uint32_t (&key)[V], const flo
         const uint32_t kmax = wave_max_u32(k1);
         if (kmax == 0u) break;            // fewer than k entries (k <= E is checked on the host)
         const uint64_t mask = __ballot(k1 == kmax);
-        int wl;
-        if (__popcll(mask) == 1) wl = __ffsll((unsigned long long)mask) - 1;
-        else wl = (int)(wave_min_u32(k1 == kmax ? (uint32_t)(lane + 64 * v1) : 0xFFFFFFFFu) & 63u);
-        const int widx = wl + 64 * __builtin_amdgcn_readlane(v1, wl);
+        int wl = __ffsll((unsigned long long)mask) - 1;
+        if (__popcll(mask) != 1) wl = (int)(wave_min_u32(k1 == kmax ? (uint32_t)(lane + 64 * v1) : 0xFFFFFFFFu) & 63u);
+        const int vw = __builtin_amdgcn_readlane(v1, wl);
         const float gw = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g1), wl));
         const bool empty = __builtin_amdgcn_readlane((int)k2, wl) == 0;
-        if (lane == wl) {
-            kl = k1;
-            vl = v1;
-            k1 = k2; v1 = v2; g1 = g2;
-            k2 = 0u;
-        }
-        if (lane == j) {
-            id = widx;
-            gv = gw;
-        }
+        // the winner's cache moves up one entry; selects rather than a branch on the lane, so that no exec-mask
+        // switch sits on the round's dependency chain
+        const bool win = lane == wl;
+        kl = win ? k1 : kl;
+        vl = win ? v1 : vl;
+        k1 = win ? k2 : k1;
+        v1 = win ? v2 : v1;
+        g1 = win ? g2 : g1;
+        k2 = win ? 0u : k2;
+        id = lane == j ? wl + 64 * vw : id;
+        gv = lane == j ? gw : gv;
         if (empty) lane_top2<V>(key, g, kl, vl, k1, v1, g1, k2, v2, g2);   // uniform: the winner's cache is empty
     }
     const float p = id >= 0 ? (SC == EXL3_SCORE_SOFTMAX ? expf(gv - mx) / sum : gv) : 0.f;
