@@ -399,7 +399,7 @@ __device__ __forceinline__ void down_input(const FusedArgs& a, const int64_t* ta
     r1 = (float)(_Float16)(a1 * kRsqrt128);
 }
 
-template <int K, int MR, bool PL = false>
+template <int K, int MR, bool PL, bool DIRECT>
 __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>& s, const Item& it, int item,
                                              int nb, int p) {
     constexpr int KBF = FusedShared<MR>::KBF;
@@ -511,7 +511,7 @@ __device__ __forceinline__ void fused_gateup(const FusedArgs& a, FusedShared<MR>
             }
         }
     }
-    if (a.direct) {
+    if constexpr (DIRECT) {
         // the down jobs build their inputs from the partials themselves: publish this split to the item counter
         __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
         __syncthreads();
@@ -540,7 +540,7 @@ __device__ __forceinline__ int split_of(int t, int P, int T) {
     return p < P - 1 ? p : P - 1;
 }
 
-template <int K, int MR, bool PL = false>
+template <int K, int MR, bool PL, bool DIRECT>
 __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& s, uint64_t vm0, uint64_t vm1,
                                            const Item& it, int item, int nb, int p) {
     constexpr int KBF = FusedShared<MR>::KBF;
@@ -563,15 +563,22 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
 #pragma unroll
     for (int j = 0; j < RW; ++j) wrow[j] = pair_weight(a, s.rows[wave + 4 * j < MR ? wave + 4 * j : 0], s.rw);
 
-    // wait for the down input this job reads, then count the job as a consumer (the last consumer clears the counter
-    // for the next call). Direct mode: every gate|up split of the item (nbI * P_gu arrivals on the item counter).
-    // Otherwise: just the column blocks of I in this job's k range, each published by its gate|up epilogue (counter
-    // P_gu + 1), so a down job starts as soon as its own blocks are in; lane b of wave 0 watches block b0 + b.
+    // wait for the down input this job reads and count the job as a consumer of its counter (the last consumer clears
+    // it for the next call; every consumer passed its wait before it counts itself, so the last count comes after
+    // every wait on the counter). Direct mode: every gate|up split of the item (nbI * P_gu arrivals on the item
+    // counter), counted right after the wait. Otherwise: just the column blocks of I in this job's k range, each
+    // published by its gate|up epilogue (counter P_gu + 1), so a down job starts as soon as its own blocks are in;
+    // lane b of wave 0 watches block b0 + b, and its count is issued once the GEMV's accumulators are stored and
+    // checked at the end of the job (consumer_done), off the job's path.
+    auto counter_of = [&](int lane0) {
+        return DIRECT ? &a.cnt_item[item * kCS]
+                      : &a.cnt_gu[((size_t)item * nbI + kr.b0 + (lane0 < kr.kbs ? lane0 : 0)) * kCS];
+    };
     if (threadIdx.x < 64) {
         const int lane0 = threadIdx.x;
-        const bool mine = a.direct ? lane0 == 0 : lane0 < kr.kbs;
-        int* c = a.direct ? &a.cnt_item[item * kCS] : &a.cnt_gu[((size_t)item * nbI + kr.b0 + (mine ? lane0 : 0)) * kCS];
-        const int need = a.direct ? nbI * a.P_gu : a.P_gu + 1;
+        const bool mine = DIRECT ? lane0 == 0 : lane0 < kr.kbs;
+        int* c = counter_of(lane0);
+        const int need = DIRECT ? nbI * a.P_gu : a.P_gu + 1;
         int n = 0, back = 1;
         while (__ballot(mine && atomic_load_agent(c) < need)) {
             if (++n > a.spin_max) {
@@ -581,22 +588,23 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
             for (int z = 0; z < back; ++z) __builtin_amdgcn_s_sleep(2);
             back = back < 4 ? 2 * back : 4;
         }
-        if (mine) {
-            const int old = atomic_add_agent(c, 1);
-            int last;
-            if (a.direct) {
-                last = need + a.DN - 1;
-            } else {
-                // consumers of block bi: every column block of H times the k splits whose range touches it
-                const int bi = kr.b0 + lane0, T = a.I / 16;
-                last = a.P_gu + nbH * (split_of(8 * bi + 7, a.P_d, T) - split_of(8 * bi, a.P_d, T) + 1);
-            }
-            if (old == last) atomic_store_agent(c, 0);
-        }
+        if (DIRECT && mine && atomic_add_agent(c, 1) == need + a.DN - 1) atomic_store_agent(c, 0);
     }
     __syncthreads();
+    int cons_old = 0;                                    // per-block mode: this lane's count, issued after the GEMV
+    auto consumer_done = [&]() {
+        if constexpr (!DIRECT) {
+            const int lane0 = threadIdx.x;
+            if (lane0 < kr.kbs) {                        // lanes of wave 0 (kbs <= 64)
+                // consumers of block bi: every column block of H times the k splits whose range touches it
+                const int bi = kr.b0 + lane0, T = a.I / 16;
+                const int last = a.P_gu + nbH * (split_of(8 * bi + 7, a.P_d, T) - split_of(8 * bi, a.P_d, T) + 1);
+                if (cons_old == last) atomic_store_agent(counter_of(lane0), 0);
+            }
+        }
+    };
 
-    if (a.direct) {
+    if constexpr (DIRECT) {
         // block (m, b) of the down input straight from the gate|up partials, one wave each
         for (int i = wave; i < cnt * kr.kbs; i += 4) {
             const int m = i / kr.kbs, b = i - m * kr.kbs, bi = kr.b0 + b;
@@ -647,6 +655,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         s.red[wave][m][1][lane] = acc[m][1];
     }
     __syncthreads();
+    if (!DIRECT && threadIdx.x < kr.kbs) cons_old = atomic_add_agent(counter_of(threadIdx.x), 1);
     const int cbase = 16 * (lane >> 3) + (lane & 7);
     const size_t slot = (size_t)item * nbH + nb;
     const bool split = a.P_d > 1;
@@ -664,7 +673,10 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         }
     }
     if (split) {
-        if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) return;
+        if (!splitk_arrive(&a.cnt_d[slot * kCS], a.P_d, &s.flag)) {
+            consumer_done();
+            return;
+        }
     } else {
         __syncthreads();
     }
@@ -739,6 +751,7 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
         }
         if (lane == 0) a.cnt_tok[((size_t)t * nbH + nb) * kCS] = 0;
     }
+    consumer_done();
 }
 
 // Wave issue priority 0..3 (s_setprio takes an immediate).
@@ -750,7 +763,9 @@ __device__ __forceinline__ void set_wave_priority(int p) {
 }
 
 // KG: bits of gate and up, KD: bits of down (equal, or both 0 for per-tile K); PL: weights in PLANAR4 word order.
-template <int KG, int KD, int MR, bool PL = false>
+// DIRECT: the down jobs build their inputs from the gate|up partials (FusedArgs::direct; one instantiation per mode,
+// so that neither carries the other's code and registers).
+template <int KG, int KD, int MR, bool PL, bool DIRECT>
 __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     __shared__ __attribute__((aligned(16))) FusedShared<MR> s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -788,7 +803,8 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     // last items (the youngest workgroups) finish last and hold back their down jobs, the end of the layer. Gate|up
     // jobs run at 1..3 rising with the item number and down jobs at 0 (C3 at 4 tokens: 38.1 us against 39.9).
     set_wave_priority(1 + (3 * gi) / (nitems > 0 ? nitems : 1));
-    if (g < a.J_gu && gi < nitems) fused_gateup<KG, MR, PL>(a, s, read_item<KG, MR>(s), gi, gr0 / a.P_gu, gr0 % a.P_gu);
+    if (g < a.J_gu && gi < nitems)
+        fused_gateup<KG, MR, PL, DIRECT>(a, s, read_item<KG, MR>(s), gi, gr0 / a.P_gu, gr0 % a.P_gu);
     // the down jobs of the previous item (uniform branch)
     const int di = gi - 1;
     if (di < 0 || di >= nitems || gr0 >= a.DN) return;
@@ -799,7 +815,7 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const Item it = read_item<KG, MR>(s);
     for (int r = gr0; r < a.DN; r += a.GU) {
         // k-split major: the down jobs reading the first column blocks of I (published first) come first
-        fused_down<KD, MR, PL>(a, s, v0, v1, it, di, r % (a.H / 128), r / (a.H / 128));
+        fused_down<KD, MR, PL, DIRECT>(a, s, v0, v1, it, di, r % (a.H / 128), r / (a.H / 128));
         __syncthreads();
     }
 }
@@ -807,8 +823,8 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
 typedef void (*fused_fn)(FusedArgs);
 
 // Mixed-bitrate instantiations (gate/up K != down K), exl3_moe_fused_mixed.hip; nullptr when not built.
-fused_fn pick_fused_mixed(int Kg, int Kd, int MR);
+fused_fn pick_fused_mixed(int Kg, int Kd, int MR, bool direct);
 // PLANAR4 instantiations (K = 3, 5, 6, 7), exl3_moe_fused_planar.hip; nullptr for other K.
-fused_fn pick_fused_planar(int K, int MR);
+fused_fn pick_fused_planar(int K, int MR, bool direct);
 
 }  // namespace exl3

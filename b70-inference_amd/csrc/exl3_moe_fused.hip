@@ -6,18 +6,30 @@
 namespace exl3 {
 
 
-template <int MR>
-static fused_fn pick_fused(int K) {
+template <int MR, bool D>
+static fused_fn pick_fused_d(int K) {
     switch (K) {
-        case 0: return moe_fused_kernel<0, 0, MR>;
-        case 1: return moe_fused_kernel<1, 1, MR>;
-        case 2: return moe_fused_kernel<2, 2, MR>;
-        case 3: return moe_fused_kernel<3, 3, MR>;
-        case 4: return moe_fused_kernel<4, 4, MR>;
-        case 5: return moe_fused_kernel<5, 5, MR>;
-        case 6: return moe_fused_kernel<6, 6, MR>;
-        case 7: return moe_fused_kernel<7, 7, MR>;
-        default: return moe_fused_kernel<8, 8, MR>;
+        case 0: return moe_fused_kernel<0, 0, MR, false, D>;
+        case 1: return moe_fused_kernel<1, 1, MR, false, D>;
+        case 2: return moe_fused_kernel<2, 2, MR, false, D>;
+        case 3: return moe_fused_kernel<3, 3, MR, false, D>;
+        case 4: return moe_fused_kernel<4, 4, MR, false, D>;
+        case 5: return moe_fused_kernel<5, 5, MR, false, D>;
+        case 6: return moe_fused_kernel<6, 6, MR, false, D>;
+        case 7: return moe_fused_kernel<7, 7, MR, false, D>;
+        default: return moe_fused_kernel<8, 8, MR, false, D>;
+    }
+}
+
+// The instantiation for (gate/up K, down K, rows per item, word order, down-input mode); nullptr when not built.
+static fused_fn pick_fused(const MoeArgs& m, int MR, bool direct) {
+    if (m.planar) return pick_fused_planar(m.Kg, MR, direct);
+    if (m.Kg != m.Kd) return pick_fused_mixed(m.Kg, m.Kd, MR, direct);
+    switch (MR) {
+        case 1: return direct ? pick_fused_d<1, true>(m.Kg) : pick_fused_d<1, false>(m.Kg);
+        case 2: return direct ? pick_fused_d<2, true>(m.Kg) : pick_fused_d<2, false>(m.Kg);
+        case 4: return direct ? pick_fused_d<4, true>(m.Kg) : pick_fused_d<4, false>(m.Kg);
+        default: return direct ? pick_fused_d<8, true>(m.Kg) : pick_fused_d<8, false>(m.Kg);
     }
 }
 
@@ -45,7 +57,7 @@ static int fused_splits(int want, int T, int kbf) {
 // Eligible: gate, up and down share one K (or all per-tile), or down has one or two bits more than gate/up; at most
 // kFusedMaxRows tokens and kFusedMaxPairs pairs; x rows 16-byte aligned.
 bool moe_fused_ok(const MoeArgs& a) {
-    return (a.Kg == a.Kd || pick_fused_mixed(a.Kg, a.Kd, 1) != nullptr) && (!a.planar || a.Kg == a.Kd) &&
+    return (a.Kg == a.Kd || pick_fused_mixed(a.Kg, a.Kd, 1, false) != nullptr) && (!a.planar || a.Kg == a.Kd) &&
            a.M <= kFusedMaxRows &&
            (int64_t)a.M * a.slots <= kFusedMaxPairs &&
            aligned(a.x, 16) && a.x_ld % 8 == 0 && env_int("EXL3MI_NO_FUSED", 0) == 0;
@@ -95,19 +107,7 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     const int mr_env = env_int("EXL3MI_FUSED_MR", 0);
     if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) MR = mr_env;
     const int kbf = MR <= 4 ? 8 : 4;
-    fused_fn fn;
-    if (m.planar) {
-        fn = pick_fused_planar(m.Kg, MR);
-    } else if (m.Kg != m.Kd) {
-        fn = pick_fused_mixed(m.Kg, m.Kd, MR);
-    } else {
-        switch (MR) {
-            case 1: fn = pick_fused<1>(m.Kg); break;
-            case 2: fn = pick_fused<2>(m.Kg); break;
-            case 4: fn = pick_fused<4>(m.Kg); break;
-            default: fn = pick_fused<8>(m.Kg); break;
-        }
-    }
+    fused_fn fn = pick_fused(m, MR, false);
     if (!fn) return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward: fused layer for K %d / %d not built", m.Kg, m.Kd);
     // items <= sum over active experts of ceil(rows / MR) <= (pairs + active * (MR - 1)) / MR
     const int active = a.np < a.E ? a.np : a.E;
@@ -137,6 +137,13 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     const int64_t jgu = (int64_t)a.max_items * a.GU, grid = jgu + a.GU;
     a.direct = a.P_d == 1 && a.P_gu <= 8 && nbH <= 64 && 2 * jgu <= resident &&
                env_int("EXL3MI_FUSED_EPILOGUE", 0) == 0;
+    if (a.direct) {                                      // the direct-mode instantiation (it must hold as many)
+        fused_fn fd = pick_fused(m, MR, true);
+        int resident_d = 0;
+        if (fd && (rc = resident_blocks(reinterpret_cast<const void*>(fd), 256, &resident_d))) return rc;
+        if (fd && 2 * jgu <= resident_d) fn = fd;
+        else a.direct = 0;
+    }
     EXL3_CHECK_ARG(grid < 0x7FFFFFFF, "exl3_moe_forward: grid too large");
     a.J_gu = (int)jgu;
 

@@ -5,18 +5,18 @@
 
 namespace exl3 {
 
-template <int K>
+template <int K, bool D>
 static fused_fn pick_planar_mr(int MR) {
-    return MR == 1 ? moe_fused_kernel<K, K, 1, true> : MR == 2 ? moe_fused_kernel<K, K, 2, true>
-         : MR == 4 ? moe_fused_kernel<K, K, 4, true> : moe_fused_kernel<K, K, 8, true>;
+    return MR == 1 ? moe_fused_kernel<K, K, 1, true, D> : MR == 2 ? moe_fused_kernel<K, K, 2, true, D>
+         : MR == 4 ? moe_fused_kernel<K, K, 4, true, D> : moe_fused_kernel<K, K, 8, true, D>;
 }
 
-fused_fn pick_fused_planar(int K, int MR) {
+fused_fn pick_fused_planar(int K, int MR, bool direct) {
     switch (K) {
-        case 3: return pick_planar_mr<3>(MR);
-        case 5: return pick_planar_mr<5>(MR);
-        case 6: return pick_planar_mr<6>(MR);
-        case 7: return pick_planar_mr<7>(MR);
+        case 3: return direct ? pick_planar_mr<3, true>(MR) : pick_planar_mr<3, false>(MR);
+        case 5: return direct ? pick_planar_mr<5, true>(MR) : pick_planar_mr<5, false>(MR);
+        case 6: return direct ? pick_planar_mr<6, true>(MR) : pick_planar_mr<6, false>(MR);
+        case 7: return direct ? pick_planar_mr<7, true>(MR) : pick_planar_mr<7, false>(MR);
         default: return nullptr;
     }
 }
