@@ -133,20 +133,30 @@ __device__ __forceinline__ void route_row(const float* __restrict__ z, const flo
         const int i = lane + 64 * v;
         key[v] = i < E ? (r != r ? 1u : float_key(r)) : 0u;
     }
+    // softmax denominators: renormalised weights need only the picks (w = exp(g - m) / sum over the picks of
+    // exp(g - m), m the largest picked g: the full softmax denominator cancels, route_select); a NaN anywhere in the
+    // row still makes every weight NaN, as the full softmax does. Unrenormalised weights need the full sum.
     float mx = 0.f, sum = 1.f;
     if (SC == EXL3_SCORE_SOFTMAX) {
-        uint32_t lmax = 0u;
+        if (renorm) {
+            bool ln = false;
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-            const int i = lane + 64 * v;
-            lmax = max(lmax, i < E ? (g[v] != g[v] ? 1u : float_key(g[v])) : 0u);
+            for (int v = 0; v < V; ++v) ln = ln || (lane + 64 * v < E && g[v] != g[v]);
+            sum = __ballot(ln) ? __builtin_nanf("") : 1.f;
+        } else {
+            uint32_t lmax = 0u;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                const int i = lane + 64 * v;
+                lmax = max(lmax, i < E ? (g[v] != g[v] ? 1u : float_key(g[v])) : 0u);
+            }
+            mx = key_float(wave_max_u32(lmax));
+            float se = 0.f;
+#pragma unroll
+            for (int v = 0; v < V; ++v)
+                if (lane + 64 * v < E) se += expf(g[v] - mx);
+            sum = wave_sum_f32(se);
         }
-        mx = key_float(wave_max_u32(lmax));
-        float se = 0.f;
-#pragma unroll
-        for (int v = 0; v < V; ++v)
-            if (lane + 64 * v < E) se += expf(g[v] - mx);
-        sum = wave_sum_f32(se);
     }
 
     route_select<V, SC>(key, g, mx, sum, k, lane, renorm, scaling, id, w);
@@ -214,7 +224,15 @@ __device__ __forceinline__ void route_select(const uint32_t (&key)[V], const flo
         gv = lane == j ? gw : gv;
         if (empty) lane_top2<V>(key, g, kl, vl, k1, v1, g1, k2, v2, g2);   // uniform: the winner's cache is empty
     }
-    const float p = id >= 0 ? (SC == EXL3_SCORE_SOFTMAX ? expf(gv - mx) / sum : gv) : 0.f;
+    float p;
+    if (SC == EXL3_SCORE_SOFTMAX && renorm) {
+        // exp relative to the largest picked g (sum is 1, or NaN when the row holds a NaN)
+        const uint32_t lk = id >= 0 ? (gv != gv ? 1u : float_key(gv)) : 0u;
+        const float mp = key_float(wave_max_u32(lk));
+        p = id >= 0 ? expf(gv - mp) * sum : 0.f;
+    } else {
+        p = id >= 0 ? (SC == EXL3_SCORE_SOFTMAX ? expf(gv - mx) / sum : gv) : 0.f;
+    }
     const float s = wave_sum_f32(p);
     w = renorm ? p * scaling / (s + 1e-20f) : p * scaling;
 }
