@@ -225,6 +225,38 @@ __device__ __forceinline__ void group_pairs(const FusedArgs& a, int lane, Groups
     g.nitems = g.n0 + popc64(g.L1);
 }
 
+// The (trellis, suh, svh) addresses of expert e for gate, up and down (and its kmaps when K is per tile) into LDS.
+template <int K, int MR>
+__device__ __forceinline__ void item_tables(const FusedArgs& a, int e, int lane, FusedShared<MR>& s) {
+    if (lane < 9) {
+        // uniform expert layout: entry i of expert e is at tb[i] + e * ts[i], no table load
+        int64_t b = 0, st = 0;
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            if (lane == i) {
+                b = a.tb[i];
+                st = a.ts[i];
+            }
+        s.tab[lane] = a.uniform ? b + (int64_t)e * st : ldg(a.tables + (int64_t)lane * a.E + e);
+    }
+    if (K == 0 && lane < 6) s.km[lane] = ldg(a.kmaps + (int64_t)lane * a.E + e);
+}
+
+// One row per item with the routing ranked inside the layer: every pair is valid (the picks are experts < E and the
+// shared slot, if any, names a valid expert) and starts an item, so item i is pair i and no grouping is needed. Every
+// wave writes the item's description itself (the same values), so no barrier is needed before it reads them back:
+// a wave's LDS accesses complete in order.
+template <int K>
+__device__ __forceinline__ void pair_item(const FusedArgs& a, int p, int lane, FusedShared<1>& s) {
+    const int e = pair_expert(a, p, s.rid);
+    if (lane == 0) {
+        s.it_e = e;
+        s.it_cnt = 1;
+        s.rows[0] = p;
+    }
+    item_tables<K, 1>(a, e, lane, s);
+}
+
 // Expert, row count, rows, tables (and kmaps) of item `item` (< nitems) into LDS, by the wave that grouped the pairs;
 // the other waves read them after a barrier (read_item).
 template <int K, int MR>
@@ -242,18 +274,7 @@ __device__ __forceinline__ void item_info(const FusedArgs& a, const Groups& g, i
         s.it_e = e;
         s.it_cnt = cnt;
     }
-    if (lane < 9) {
-        // uniform expert layout: entry i of expert e is at tb[i] + e * ts[i], no table load
-        int64_t b = 0, st = 0;
-#pragma unroll
-        for (int i = 0; i < 9; ++i)
-            if (lane == i) {
-                b = a.tb[i];
-                st = a.ts[i];
-            }
-        s.tab[lane] = a.uniform ? b + (int64_t)e * st : ldg(a.tables + (int64_t)lane * a.E + e);
-    }
-    if (K == 0 && lane < 6) s.km[lane] = ldg(a.kmaps + (int64_t)lane * a.E + e);
+    item_tables<K, MR>(a, e, lane, s);
     if constexpr (MR == 1) {
         if (lane == 0) s.rows[0] = p;                    // the item is its first pair
     } else {
@@ -775,20 +796,33 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
         route_in_layer(a, wave, lane, s.rid, s.rw);
         __syncthreads();
     }
-    // wave 0 groups the pairs and describes the gate|up job's item; the others wait at the barrier
+    // one row per item with in-layer routing: item i is pair i (pair_item), described by every wave; otherwise wave 0
+    // groups the pairs and describes the gate|up job's item while the others wait at the barrier
+    const bool by_pair = MR == 1 && a.logits && (a.slots == a.topk || (unsigned)a.shared < (unsigned)a.E);
     Groups gr;
-    if (wave == 0) {
-        group_pairs<MR>(a, lane, gr, s.ge, s.rid);
-        if (lane == 0) {
-            s.valid[0] = gr.v0;
-            s.valid[1] = gr.v1;
-            s.nitems = gr.nitems;
+    int nitems;
+    uint64_t v0, v1;
+    if (by_pair) {
+        nitems = a.np;
+        v0 = a.np >= 64 ? ~0ull : (1ull << a.np) - 1;
+        v1 = a.np <= 64 ? 0ull : a.np >= 128 ? ~0ull : (1ull << (a.np - 64)) - 1;
+        if constexpr (MR == 1)
+            if (g < a.J_gu && gi < nitems) pair_item<KG>(a, gi, lane, s);
+    } else {
+        if (wave == 0) {
+            group_pairs<MR>(a, lane, gr, s.ge, s.rid);
+            if (lane == 0) {
+                s.valid[0] = gr.v0;
+                s.valid[1] = gr.v1;
+                s.nitems = gr.nitems;
+            }
+            if (g < a.J_gu && gi < gr.nitems) item_info<KG, MR>(a, gr, gi, lane, s);
         }
-        if (g < a.J_gu && gi < gr.nitems) item_info<KG, MR>(a, gr, gi, lane, s);
+        __syncthreads();
+        nitems = s.nitems;
+        v0 = s.valid[0];
+        v1 = s.valid[1];
     }
-    __syncthreads();
-    const int nitems = s.nitems;
-    const uint64_t v0 = s.valid[0], v1 = s.valid[1];
     if (g == 0) {
         // tokens with no valid slot get a zero output row
         for (int tk = 0; tk < a.M; ++tk) {
@@ -809,8 +843,12 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const int di = gi - 1;
     if (di < 0 || di >= nitems || gr0 >= a.DN) return;
     __syncthreads();                    // the gate|up job's LDS (rows, tab, xs) is free again
-    if (wave == 0) item_info<KG, MR>(a, gr, di, lane, s);
-    __syncthreads();
+    if (by_pair) {
+        if constexpr (MR == 1) pair_item<KD>(a, di, lane, s);
+    } else {
+        if (wave == 0) item_info<KG, MR>(a, gr, di, lane, s);
+        __syncthreads();
+    }
     set_wave_priority(0);
     const Item it = read_item<KG, MR>(s);
     for (int r = gr0; r < a.DN; r += a.GU) {
