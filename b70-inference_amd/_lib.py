@@ -112,8 +112,8 @@ def profile_read() -> dict:
 
 
 def device_status() -> int:
-    """The current device's status word: non-zero after a fused MoE layer launch gave up waiting (read on the host,
-    no synchronisation; the next library call on the device reports and clears it)."""
+    """The current device's status word: non-zero after a fused MoE layer or split-K GEMV launch gave up waiting (read
+    on the host, no synchronisation; the next library call on the device reports and clears it)."""
     v = ctypes.c_int(0)
     check(lib().exl3_device_status(ctypes.byref(v)), "exl3_device_status")
     return v.value

@@ -142,8 +142,15 @@ __global__ __launch_bounds__(64) void had_kernel(const void* __restrict__ in, in
 // ================================================================================================ dense GEMV
 // Workgroup = 4 waves on one 128-column strip and one k-split (a run of Hadamard blocks). Phase 1 computes the
 // split's transformed activations into LDS; phase 2 streams the strip's tile-rows (wave w takes tile-rows w, w+4,..);
-// phase 3 reduces the waves in LDS and, across splits, through per-strip partials and an arrival counter: the last
-// workgroup of a strip sums the partials in split order (deterministic), applies the output Hadamard and svh.
+// phase 3 reduces the waves in LDS and, across splits, either through per-strip partials and an arrival counter (the
+// last workgroup of a strip sums the partials in split order, deterministic) or through tagged partials (`tag`): each
+// partial is stored as the word bits(v) ^ kPartEmpty, so that a zero word means "not written yet" (kPartEmpty is a
+// signalling NaN, which no arithmetic result is), and the strip's last split polls for the others' words, sums them
+// in split order, clears them to zero and finishes the strip. The tagged form has no arrival round trip (no store
+// drain, no atomic) on the path; its wait is bounded (spin_max polls, then the status word is set). Either way the
+// last step applies the output Hadamard and svh.
+constexpr uint32_t kPartEmpty = 0x7FBFDEADu;
+
 struct GemvArgs {
     const uint16_t* x;
     int64_t x_ld;
@@ -171,6 +178,11 @@ struct GemvArgs {
     int a_div;
     int64_t qmin, qmax;
     int64_t x_bs, out_bs;
+    // tagged partials [strips][P][128] (zero between calls), one row and one slot (gridDim.z == 1); null: arrival
+    // counters
+    uint32_t* tag;
+    int* status;                                     // set when the tagged wait gives up
+    int spin_max;
 };
 
 // Matrix of multi-matrix slot z (-1: skipped).
@@ -258,6 +270,82 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     const int cbase = 16 * (lane >> 3) + (lane & 7);
+    if constexpr (M == 1) {                                     // the tagged exchange serves one-row calls only
+        if (a.tag) {
+            __shared__ float own[128];                          // the last split's own partial
+            uint32_t* tg = a.tag + (size_t)strip * a.P * 128;
+            const bool fin = p == a.P - 1;
+            if (wave == 0) {
+                float sx = 0.f;
+                for (int b = 0; b < kb; ++b) sx += bsum[0][b];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float v = red[0][0][h][lane];
+#pragma unroll
+                    for (int w = 1; w < NW; ++w) v += red[w][0][h][lane];
+                    v = kMul1C1 * v + kMul1C2 * sx;
+                    const int c = cbase + 8 * h;
+                    if (fin) own[c] = v;
+                    else __hip_atomic_store(tg + (size_t)p * 128 + c, __builtin_bit_cast(uint32_t, v) ^ kPartEmpty,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            if (!fin) return;
+            // polled once the workgroup's own partial is in LDS (polling while wave 0 still reduced it found the
+            // other splits' words missing more often, and a miss costs a round trip)
+            __syncthreads();
+            if (wave != 0) return;
+            float sa = 0.f, sb = 0.f;
+            // splits 0 .. P - 2 in order, eight at a time: every word of a group loaded before any is checked
+            for (int q0 = 0; q0 < a.P - 1; q0 += 8) {
+                uint32_t wa[8], wb[8];
+                for (int n = 0;;) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = q0 + j < a.P - 1 ? q0 + j : q0;   // past the last split: re-read split q0
+                        wa[j] = __hip_atomic_load(tg + (size_t)q * 128 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        wb[j] = __hip_atomic_load(tg + (size_t)q * 128 + lane + 64, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    bool miss = false;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) miss = miss || wa[j] == 0u || wb[j] == 0u;
+                    if (!__ballot(miss)) break;
+                    if (++n > a.spin_max) {
+                        if (lane == 0) report_timeout(a.status);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (q0 + j < a.P - 1) {
+                        sa += __builtin_bit_cast(float, wa[j] ^ kPartEmpty);
+                        sb += __builtin_bit_cast(float, wb[j] ^ kPartEmpty);
+                    }
+            }
+            float va = sa + own[lane], vb = sb + own[lane + 64];
+            fwht128_wave(va, vb, lane);
+            const int c0 = strip * 128 + lane, c1 = c0 + 64;
+            va *= kRsqrt128 * h2f(ldg(svh + c0));
+            vb *= kRsqrt128 * h2f(ldg(svh + c1));
+            if (F32) {
+                float* o = reinterpret_cast<float*>(a.out);
+                o[c0] = va;
+                o[c1] = vb;
+            } else {
+                uint16_t* o = reinterpret_cast<uint16_t*>(a.out);
+                o[c0] = f2h(va);
+                o[c1] = f2h(vb);
+            }
+            // the words back to zero for the next call
+            for (int q = 0; q < a.P - 1; ++q) {
+                __hip_atomic_store(tg + (size_t)q * 128 + lane, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(tg + (size_t)q * 128 + lane + 64, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            return;
+        }
+    }
     float* mypart = part + ((size_t)strip * a.P + p) * M * 128;
     if (wave == 0) {
 #pragma unroll
@@ -414,12 +502,23 @@ int launch_gemv(const uint16_t* A, int64_t a_ld, int64_t m, int64_t k, const uin
                 hipStream_t st) {
     const int strips = (int)(n / 128), nblk = (int)(k / 128);
     const int P = gemv_splits(strips, nblk, m < kGemvMaxRows ? (int)m : kGemvMaxRows);
+    // One row: tagged partials, kept in the counter buffer (zero between calls; a timeout reset zeroes it): 4096 x
+    // 4096 7.21 -> 6.88 us, 5376 -> 21504 20.6 -> 19.2 us. With more rows the last split would poll and clear every
+    // row's words itself; those calls keep the arrival counters.
+    const bool tagged = m == 1;
     Workspace ws;
-    int rc = workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, st, &ws);
+    int rc = tagged ? workspace(0, (size_t)strips * P * 128, st, &ws)
+                    : workspace((size_t)strips * P * kGemvMaxRows * 128 * sizeof(float), (size_t)strips, st, &ws);
     if (rc) return rc;
     GemvArgs ga = gemv_args(A, a_ld, k, tr, n, C, c_ld, suh, S, sonb, svh, P);
-    ga.part = reinterpret_cast<float*>(ws.scratch);
-    ga.cnt = ws.counters;
+    if (tagged) {
+        ga.tag = reinterpret_cast<uint32_t*>(ws.counters);
+        ga.status = ws.status;
+        ga.spin_max = spin_limit();
+    } else {
+        ga.part = reinterpret_cast<float*>(ws.scratch);
+        ga.cnt = ws.counters;
+    }
     return gemv_chunks(ga, m, K, f32, strips, 1, st);
 }
 

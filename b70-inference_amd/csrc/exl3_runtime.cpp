@@ -124,17 +124,18 @@ int workspace(size_t bytes, size_t ncounters, hipStream_t st, Workspace* out) {
         // A reset recorded into a graph would not run now: under capture the word stays set and the next call
         // outside capture resets.
         if (capturing(st))
-            return fail(EXL3_ERR_HIP, "a fused MoE layer launch on device %d gave up waiting for its gate|up inputs; "
-                                      "the arrival counters are reset by the next library call outside stream "
-                                      "capture", dev);
+            return fail(EXL3_ERR_HIP, "a launch on device %d gave up waiting for its inputs (fused MoE layer: gate|up "
+                                      "partials; split-K GEMV: other splits' partials); the counter buffers are reset "
+                                      "by the next library call outside stream capture", dev);
         int rc = zero_ints(w.counters, w.ncounters, st);
         for (const auto& c : g_retired_counters[dev])
             if (!rc) rc = zero_ints(c.first, c.second, st);
         if (rc) return rc;
         *reinterpret_cast<volatile int*>(g_status_host[dev]) = 0;
-        return fail(EXL3_ERR_HIP, "a fused MoE layer launch on device %d gave up waiting for its gate|up inputs (its "
-                                  "outputs are incomplete, and so may be those of calls queued behind it); every "
-                                  "counter buffer has been reset, later calls and graph replays run normally", dev);
+        return fail(EXL3_ERR_HIP, "a launch on device %d gave up waiting for its inputs (fused MoE layer: gate|up "
+                                  "partials; split-K GEMV: other splits' partials; its outputs are incomplete, and so "
+                                  "may be those of calls queued behind it); every counter buffer has been reset, later "
+                                  "calls and graph replays run normally", dev);
     }
     if (bytes > w.scratch_bytes) {
         if (capturing(st))

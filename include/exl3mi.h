@@ -52,7 +52,8 @@ int exl3_reserve_workspace(int64_t bytes, int64_t ncounters);
  * buffers were current must not be replayed afterwards. No reference counterpart. */
 int exl3_release_workspace(void);
 
-/* The current device's status word: 0, or 1 after a fused MoE layer launch gave up one of its bounded
+/* The current device's status word: 0, or 1 after a fused MoE layer launch or a one-row decode GEMV launch of
+ * exl3_gemm / exl3_linear_sharded (whose last k-split waits for the other splits' partials) gave up one of its bounded
  * cross-workgroup waits (its outputs, and possibly those of launches queued behind it, are then incomplete). Read on
  * the host without synchronising. The next library call on the device that uses the workspace outside stream capture
  * zeroes every arrival-counter buffer of the device on its stream (the current one and the outgrown ones that graphs
@@ -98,7 +99,8 @@ int exl3_had_r_128(const void* in, int64_t in_ld, void* out, int64_t out_ld, int
 
 /* EXL3 linear: C[m, n] = Hn( Hk(A * suh) @ W_hat ) * svh for A fp16 [m, k] (row stride a_ld), C fp16 or fp32
  * [m, n] (row stride c_ld). A_had (fp16 scratch, >= m*k elements) is accepted for signature compatibility and not
- * used: the input transform is fused. cb must be 2 (mul1). Up to 8 rows: decode GEMV; 9 rows and more: the trellis
+ * used: the input transform is fused. cb must be 2 (mul1). Up to 8 rows: decode GEMV (at one row the last k-split
+ * waits, bounded, for the others' partials: exl3_device_status); 9 rows and more: the trellis
  * decoded into fp16 MFMA fragments once per row block of up to 64 rows (the reference's large-M linear,
  * exl3_ops.sycl:742-756, reconstructs fp16 slices and calls a GEMM instead; same results within the tolerance).
  * Replaces: exllamav3 ext exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1, force_num_sms)

@@ -1,5 +1,5 @@
-"""Library runtime on the GPU: the fused MoE layer's bounded wait reports a timeout through the device status word
-and the next call clears it (the wait is forced to give up from the host with a tiny spin limit, so every kernel
+"""Library runtime on the GPU: the fused MoE layer's and the one-row GEMV's bounded waits report a timeout through the
+device status word and the next call clears it (the wait is forced to give up from the host with a tiny spin limit, so every kernel
 still exits normally), and workspace growth keeps buffers alive that a HIP graph captured earlier still uses."""
 import os
 
@@ -63,6 +63,45 @@ def test_fused_wait_timeout_is_reported_then_cleared(exl3, oracle, layer):
     yl = lin.run_alloc(xs.cuda(), 1024, True).cpu().numpy()
     ref = oracle.exl3_linear(xs.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), 4, np.float32)
     assert max_rel(yl, ref) <= MAX_REL
+    # one row: the tagged split-K exchange, whose words live in the counter buffer that the reset zeroed
+    yl1 = lin.run_alloc(xs[:1].cuda(), 1024, True).cpu().numpy()
+    assert max_rel(yl1, ref[:1]) <= MAX_REL
+    assert lib.device_status() == 0
+
+
+def test_one_row_gemv_wait_timeout_is_reported_then_cleared(exl3, oracle):
+    """The one-row decode GEMV's last k-split waits (bounded) for the other splits' tagged partials. Under a spin
+    limit of 1 a wait gives up whenever its first poll misses a word: then the status word is set, the next call
+    reports it and zeroes the counter buffer, and later calls are exact again; when every first poll hits, the
+    outputs are exact. Either way no stale word survives into a later call."""
+    lib = exl3._lib
+    synth = __import__("importlib").import_module("b70-inference_amd.synth")
+    tr, suh, svh = synth.linear(4096, 5376, 4, 4104)
+    xs = synth.activations(1, 4096, 4105)
+    lin = exl3.BC_LinearEXL3(tr.cuda(), suh.cuda(), svh.cuda(), 4, None, False, True, None)
+    ref = oracle.exl3_linear(xs.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), 4, np.float32)
+    xg = xs.cuda()
+    print("timeout test: one-row GEMV under EXL3MI_SPIN_LIMIT=1", flush=True)
+    os.environ["EXL3MI_SPIN_LIMIT"] = "1"
+    try:
+        timed_out = False
+        for _ in range(8):
+            y = lin.run_alloc(xg, 5376, True)
+            torch.cuda.synchronize()
+            if lib.device_status():
+                timed_out = True
+                break
+            assert max_rel(y.cpu().numpy(), ref) <= MAX_REL
+    finally:
+        del os.environ["EXL3MI_SPIN_LIMIT"]
+    if timed_out:
+        with pytest.raises(lib.Exl3Error, match="gave up waiting"):
+            lin.run_alloc(xg, 5376, True)
+        torch.cuda.synchronize()
+        assert lib.device_status() == 0
+    for _ in range(3):
+        y = lin.run_alloc(xg, 5376, True)
+        assert max_rel(y.cpu().numpy(), ref) <= MAX_REL
     assert lib.device_status() == 0
 
 
