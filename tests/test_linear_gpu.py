@@ -148,6 +148,49 @@ def test_gemm_deterministic_and_bias(exl3):
     assert torch.allclose(y4.view(3, 1024).float(), y1, rtol=2e-3, atol=2e-3)
 
 
+def test_gemm_one_row_tagged_exchange_across_shapes_and_graph_replays(exl3, oracle):
+    """One-row calls exchange their split-K partials as tagged words that the last split clears: calls of different
+    shapes back to back (other strip and split layouts over the same words), a one-row call between multi-row calls
+    (which use the arrival counters), and replays of a captured one-row call each give the eager result bit for bit
+    and match the oracle."""
+    S = synth()
+    shapes = [(4096, 4096, 4, 5100), (1024, 3072, 3, 5101), (5376, 2048, 2, 5102), (512, 384, 5, 5103)]
+    cases = []
+    for k, n, K, seed in shapes:
+        tr, suh, svh = S.linear(k, n, K, seed)
+        x = S.activations(3, k, seed + 1)
+        lin = exl3.BC_LinearEXL3(tr.cuda(), suh.cuda(), svh.cuda(), K, None, False, True, None)
+        ref = oracle.exl3_linear(x[:1].numpy(), tr.numpy(), suh.numpy(), svh.numpy(), K, np.float32)
+        cases.append((lin, x.cuda(), n, ref))
+    first = []
+    for lin, x, n, ref in cases:
+        y = lin.run_alloc(x[:1], n, True)
+        assert max_rel(y.cpu().numpy(), ref) <= MAX_REL
+        first.append(y)
+    for _ in range(2):                                      # interleaved with three-row calls
+        for (lin, x, n, _), y0 in zip(cases, first):
+            lin.run_alloc(x, n, True)
+            assert torch.equal(lin.run_alloc(x[:1], n, True), y0)
+    lin, x, n, _ = cases[0]
+    out = torch.empty(1, n, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lin.run(x[:1], out)                                 # sizes the workspace before capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lin.run(x[:1], out)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first[0]), i
+        c_lin, c_x, c_n, _ = cases[1 + i % 3]               # eager one-row work between the replays
+        assert torch.equal(c_lin.run_alloc(c_x[:1], c_n, True), first[1 + i % 3])
+
+
 # Rows >= 9 run on the MFMA path (row blocks of 16 / 32 / 64, k-split with partials summed by the last workgroup).
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("M", [9, 24, 40, 64])
