@@ -38,8 +38,9 @@ constexpr int kLinearRing = EXL3_LINEAR_RING;   // register ring depth of the de
 #ifndef EXL3_GEMV_MFMA_MIN_ROWS
 #define EXL3_GEMV_MFMA_MIN_ROWS 2
 #endif
-// one-row GEMVs keep v_dot2 (16 per tile-row): there the MFMA form was 2-4 % slower (C1, one-token C2 and C3), from
-// two rows on it wins (two-row C2 -7 %, four-row -11 %)
+// one-row GEMVs keep v_dot2 (16 per tile-row): there the MFMA form is no clear win (4096 x 4096 linear -0.9 %, one-token
+// 5376 x 21504 dense MLP -1.5 %, one-token top-10 decode layer of 512 experts +1.3 %); from two rows on it wins (two-row
+// dense MLP -7 %, four-row -11 %)
 template <int M>
 constexpr bool gemv_mfma() { return EXL3_GEMV_MFMA && M >= EXL3_GEMV_MFMA_MIN_ROWS; }
 typedef _Float16 gh4_t __attribute__((ext_vector_type(4)));
