@@ -720,21 +720,41 @@ __device__ __forceinline__ void fused_down(const FusedArgs& a, FusedShared<MR>& 
             v1 = s.cv[m][lane + 64];
         }
         fwht128_wave(v0, v1, lane);
+        const float y0 = v0 * kRsqrt128 * sd0 * w, y1 = v1 * kRsqrt128 * sd1 * w;
+        if (!DIRECT && a.slots == 1) {
+            // one slot per token (a dense MLP, which runs in per-block mode): the token's output block is this row,
+            // as the combine would sum it (0 + y: the same bits), written here without the y round trip and the
+            // token count (the direct-mode instantiations leave this out: one-token decode layers measured it slower)
+            const int t = pr;
+            const int c0 = nb * 128 + lane, c1 = c0 + 64;
+            if (a.out_f32) {
+                float* o = reinterpret_cast<float*>(a.out) + (int64_t)t * a.out_ld;
+                o[c0] = 0.f + y0;
+                o[c1] = 0.f + y1;
+            } else {
+                uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + (int64_t)t * a.out_ld;
+                o[c0] = f2h(0.f + y0);
+                o[c1] = f2h(0.f + y1);
+            }
+            continue;
+        }
         float* dst = a.y + (size_t)pr * a.H + nb * 128;
-        splitk_store(dst + lane, v0 * kRsqrt128 * sd0 * w);
-        splitk_store(dst + lane + 64, v1 * kRsqrt128 * sd1 * w);
+        splitk_store(dst + lane, y0);
+        splitk_store(dst + lane + 64, y1);
     }
     if (split && threadIdx.x == 0) a.cnt_d[slot * kCS] = 0;
 
-    // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in
+    // combine: count this item's rows into their tokens; finish the tokens whose slots are now all in (with one slot
+    // per token the rows were written above)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x < cnt) {                 // lane m counts row m (rows of one item belong to different tokens)
         const int m = threadIdx.x;
         const int t = s.rows[m] / a.slots;
         const int nv = popc_range(vm0, vm1, t * a.slots, a.slots);
-        const int old = atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
-        s.comb[m] = (old == nv - 1) ? t : -1;
+        const bool written = !DIRECT && a.slots == 1;
+        const int old = written ? 0 : atomic_add_agent(&a.cnt_tok[((size_t)t * nbH + nb) * kCS], 1);
+        s.comb[m] = (!written && old == nv - 1) ? t : -1;
     }
     __syncthreads();
     for (int m = wave; m < cnt; m += 4) {
