@@ -55,7 +55,7 @@ struct RouteArgs {
 };
 
 constexpr int kFusedRouteMaxE = 512;    // logits per row that the fused layer's in-layer routing handles (8 per lane)
-constexpr int kFusedRouteMaxRows = 2;   // tokens up to which the routed entry point ranks inside the fused layer
+constexpr int kFusedRouteMaxRows = 4;   // tokens up to which the routed entry point ranks inside the fused layer
 
 struct MoeArgs {
     const uint16_t* x;

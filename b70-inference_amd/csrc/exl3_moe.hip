@@ -1407,9 +1407,10 @@ int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t 
         }
     }
     // Batches of up to kFusedRouteMaxRows tokens on the fused layer rank the logits inside it: every workgroup ranks
-    // every token itself, which costs less than the router launch (C3: 1 token 24.1 us against 25.0, 2 tokens 29.1
-    // against 29.9) until the rankings of more tokens in every workgroup outweigh it (4 tokens: 40.1 against 38.6).
-    // Otherwise the router kernel runs first.
+    // the tokens itself (with one row per item just those of its own two items), which costs less than the router
+    // launch (512 experts, top-10: 1 token 24.1 us against 25.0 with two-row items; with one-row items 3 tokens 28.4
+    // against 30.2, 4 tokens 32.0 against 33.7) until the rankings in every workgroup outweigh it (8 tokens: 47.4
+    // against 46.2). Otherwise the router kernel runs first.
     if (M <= kFusedRouteMaxRows && moe_fused_ok(a) && n_logits <= kFusedRouteMaxE &&
         env_int("EXL3MI_ROUTER_KERNEL", 0) == 0) {
         a.logits = logits;

@@ -164,23 +164,26 @@ __device__ __forceinline__ float pair_weight(const FusedArgs& a, int p, const fl
     return j < a.topk ? (a.logits ? rw[q] : ldg(a.tw + q)) : 1.0f;
 }
 
-// In-layer routing: wave w ranks the logits of tokens w, w + 4 (softmax over logits + bias, top-k, renormalised:
-// exl3_route_softmax_topk's route_row) into rid / rw; workgroup 0 also writes the picks out.
-__device__ __forceinline__ void route_in_layer(const FusedArgs& a, int wave, int lane, int* rid, float* rw) {
-    for (int t = wave; t < a.M; t += 4) {
-        int id;
-        float w;
-        route_row<kFusedRouteMaxE / 64, EXL3_SCORE_SOFTMAX>(a.logits + (int64_t)t * a.lg_ld, a.rbias, a.n_logits,
-                                                           a.topk, lane, true, true, 1.0f, id, w);
-        if (lane < a.topk) {
-            rid[t * a.topk + lane] = id;
-            rw[t * a.topk + lane] = w;
-            if (blockIdx.x == 0) {
-                a.ids_out[t * a.topk + lane] = id;
-                a.tw_out[t * a.topk + lane] = w;
-            }
+// In-layer routing of token t by one wave (softmax over logits + bias, top-k, renormalised: exl3_route_softmax_topk's
+// route_row) into rid / rw; `out`: also write the picks out.
+__device__ __forceinline__ void route_token(const FusedArgs& a, int t, int lane, int* rid, float* rw, bool out) {
+    int id;
+    float w;
+    route_row<kFusedRouteMaxE / 64, EXL3_SCORE_SOFTMAX>(a.logits + (int64_t)t * a.lg_ld, a.rbias, a.n_logits, a.topk,
+                                                       lane, true, true, 1.0f, id, w);
+    if (lane < a.topk) {
+        rid[t * a.topk + lane] = id;
+        rw[t * a.topk + lane] = w;
+        if (out) {
+            a.ids_out[t * a.topk + lane] = id;
+            a.tw_out[t * a.topk + lane] = w;
         }
     }
+}
+
+// Every token: wave w ranks tokens w, w + 4, ..; workgroup 0 writes the picks out.
+__device__ __forceinline__ void route_in_layer(const FusedArgs& a, int wave, int lane, int* rid, float* rw) {
+    for (int t = wave; t < a.M; t += 4) route_token(a, t, lane, rid, rw, blockIdx.x == 0);
 }
 
 __device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
@@ -812,13 +815,22 @@ __global__ __launch_bounds__(256) void moe_fused_kernel(FusedArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = blockIdx.x;
     const int gi = g / a.GU, gr0 = g - gi * a.GU;
-    if (a.logits) {
-        route_in_layer(a, wave, lane, s.rid, s.rw);
-        __syncthreads();
-    }
     // one row per item with in-layer routing: item i is pair i (pair_item), described by every wave; otherwise wave 0
     // groups the pairs and describes the gate|up job's item while the others wait at the barrier
     const bool by_pair = MR == 1 && a.logits && (a.slots == a.topk || (unsigned)a.shared < (unsigned)a.E);
+    if (a.logits) {
+        if (by_pair && a.M > 1) {
+            // just the tokens of this workgroup's items: its gate|up item's (wave 0) and its down item's (wave 1); the
+            // workgroup whose gate|up item is a token's first pair writes that token's picks out
+            const int tg = g < a.J_gu && gi < a.np ? gi / a.slots : -1;
+            const int td = gi >= 1 && gi - 1 < a.np && gr0 < a.DN ? (gi - 1) / a.slots : -1;
+            if (wave == 0 && tg >= 0) route_token(a, tg, lane, s.rid, s.rw, gr0 == 0 && gi == tg * a.slots);
+            if (wave == 1 && td >= 0 && td != tg) route_token(a, td, lane, s.rid, s.rw, false);
+        } else {
+            route_in_layer(a, wave, lane, s.rid, s.rw);
+        }
+        __syncthreads();
+    }
     Groups gr;
     int nitems;
     uint64_t v0, v1;

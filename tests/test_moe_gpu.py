@@ -184,11 +184,12 @@ def test_moe_forward_logits_matches_route_then_forward(exl3, small, M, n_logits,
 
 @pytest.mark.parametrize("E,k,H,I,biased", [(512, 10, 256, 256, False), (160, 8, 256, 256, True),
                                               (512, 32, 128, 128, True)])
-@pytest.mark.parametrize("M", [1, 2, 3])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5])
 def test_moe_forward_logits_in_layer_routing_exact(exl3, oracle, E, k, H, I, biased, M):
-    """Routing inside the fused layer (up to 2 tokens) returns the router kernel's picks and weights bit for bit and
-    the same rows as route_softmax_topk + moe_forward, at the C3 router shape (512 experts, top-10), a C4-like one
-    (160 experts, top-8, Zipf bias) and top-32; 3 tokens take the router kernel."""
+    """Routing inside the fused layer (up to 4 tokens; with one row per item each workgroup ranks just its own items'
+    tokens) returns the router kernel's picks and weights bit for bit and the same rows as route_softmax_topk +
+    moe_forward, at the C3 router shape (512 experts, top-10), a C4-like one (160 experts, top-8, Zipf bias) and
+    top-32; 5 tokens take the router kernel."""
     tables, _ = make_experts(exl3, oracle, E, H, I, 2, 2, 2100 + E + k, oracle=False)
     g = torch.Generator().manual_seed(2200 + E + M)
     x = torch.randn(M, H, generator=g).half().cuda()
