@@ -534,7 +534,9 @@ def build(name):
         layers = [dev_experts(160, 5120, 1536, 2, 3, 4000 + c) for c in range(2)]
         wl = MoE(layers, 512, 8, 4, 41, "silu", bias=zipf_bias(160, 1.1, 4100))
         wl.bound, wl.cpu_rows = "mfma", list(range(64))
-        return wl, 4
+        # 16 steps per graph, as for C5: per-step time at 4 / 8 / 16 / 32 steps per graph measured 620-676 / 609 / 602
+        # / 600 us (the replay's own start-up cost amortised over the steps)
+        return wl, 16
     if name == "c5":
         wl = c5_workload()
         return wl, 4
