@@ -1311,6 +1311,17 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
     const int64_t M = a.M, E = a.E, npairs = M * a.slots;
     const bool mfma = M > kMoeSmallRows;
     a.MR = mfma ? 0 : M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
+    // rows per GEMV item: one for sparse routing (pairs <= E / 2; experts of 2048 -> 512, 8 tokens, against eight rows
+    // per item: 512 experts top-17 170.6 -> 86.6 us), two up to 1.5 pairs per expert (128 experts top-17 78.7 against
+    // 83.2 with four, 86.0 with one), else four: eight never pays on this path, even with every expert taking all 8
+    // rows (8 experts top-8 34.5 us with four, 43.9 with eight; 32 experts top-32 83.0 with four, 102.4 with two;
+    // 64 experts top-17 69.9 with four, 72.8 with two, 105.7 with eight). EXL3MI_MOE_MR=1|2|4|8 overrides.
+    if (!mfma) {
+        const int cap = npairs * 2 <= E ? 1 : npairs * 2 <= 3 * E ? 2 : 4;
+        if (a.MR > cap) a.MR = cap;
+        const int mr_env = env_int("EXL3MI_MOE_MR", 0);
+        if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) a.MR = mr_env;
+    }
     int64_t mi = mfma ? 0 : E + npairs / a.MR;
     if (mi > npairs) mi = npairs;
     a.max_items = (int)mi;

@@ -80,6 +80,23 @@ def test_moe_fused_and_multi_kernel_paths(exl3, oracle, small, monkeypatch, M):
     assert max_rel(y2, ref) <= MAX_REL
 
 
+@pytest.mark.parametrize("mr", [1, 2, 4, 8])
+@pytest.mark.parametrize("M,k,E", [(8, 4, 4), (8, 3, 12), (5, 7, 9)])
+def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E):
+    """The multi-launch decode path with every rows-per-item width forced (EXL3MI_MOE_MR; by itself it takes one, two
+    or four): experts that take all 8 rows (4 experts top-4), a few rows, and a ragged 5-token batch, with repeated
+    experts and an inactive slot, meet the bar against the oracle; two calls in a row agree bit for bit."""
+    tables, orc = make_experts(exl3, oracle, E, 256, 256, 3, 3, 2500 + 10 * E + M)
+    ids, w = _ids_w(M, k, E, 2501 + M, dup=True, inactive=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2502 + M)).half()
+    monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    monkeypatch.setenv("EXL3MI_MOE_MR", str(mr))
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert np.array_equal(y, y1)
+
+
 @pytest.mark.parametrize("M,k,E,Kg,Kd", [(12, 10, 64, 3, 3), (16, 8, 40, 2, 2), (10, 12, 200, 2, 3), (16, 7, 16, 4, 4)])
 def test_moe_fused_up_to_16_tokens(exl3, oracle, monkeypatch, M, k, E, Kg, Kd):
     """9 to 16 tokens within 128 pairs take the one-launch layer (items of up to 8 rows, or 2 under sparse routing);
