@@ -63,6 +63,49 @@ bool moe_fused_ok(const MoeArgs& a) {
            aligned(a.x, 16) && a.x_ld % 8 == 0 && env_int("EXL3MI_NO_FUSED", 0) == 0;
 }
 
+// Expected items of a batch at `mr` rows per item, routing taken as uniform: the routed experts' row counts are
+// Binomial(M, p) with p = routed picks per token / routed experts, an item per started group of mr rows; a shared
+// expert takes every token.
+static double expected_items(const MoeArgs& m, int mr) {
+    const bool sh = (unsigned)m.shared < (unsigned)m.E;
+    const int routed_e = sh ? m.E - 1 : m.E, picks = sh ? m.slots - 1 : m.slots;
+    double items = sh ? (double)((m.M + mr - 1) / mr) : 0.0;
+    if (routed_e <= 0 || picks <= 0) return items;
+    const double p = picks >= routed_e ? 1.0 : (double)picks / routed_e;
+    double pmf = std::pow(1.0 - p, m.M), e_groups = 0.0;      // P(X = 0), then P(X = x) by the ratio recurrence
+    for (int x = 1; x <= m.M; ++x) {
+        pmf = p >= 1.0 ? (x == m.M ? 1.0 : 0.0) : pmf * (double)(m.M - x + 1) / x * p / (1.0 - p);
+        e_groups += pmf * ((x + mr - 1) / mr);
+    }
+    return items + routed_e * e_groups;
+}
+
+// The smallest rows per item (1, 2, 4, 8 up to `cap`) at which every gate|up job of the expected items, each item
+// split to its full k-split count, fits the device's resident grid for that instantiation (10 % slack), or 0 when
+// none does. Wider items hold more registers and LDS (5 / 4 / 4 / 3 workgroups per CU at 1 / 2 / 4 / 8 rows) and
+// run each tile-row longer; narrower items repeat an expert's decode for each group of rows. With the whole batch
+// resident the narrowest width that fits wins: dense routing over experts of 2048 -> 512 (24 jobs per item), 8 tokens:
+// 8 experts top-8 40.4 (eight rows) -> 28.8 us (two), 16 experts top-8 36.0 -> 32.1; 16 tokens: 8 experts top-2
+// 35.8 -> 23.8 (one), 16 experts top-8 42.4 -> 37.8 (four), 32 experts top-8 44.1 -> 38.2 (four).
+static int fused_fit_rows(const MoeArgs& m, int cap, int* out) {
+    *out = 0;
+    const int nbI = m.I / 128;
+    const int full = m.H / 16 / kFusedMinJobRows > 1 ? m.H / 16 / kFusedMinJobRows : 1;
+    for (int mr = 1; mr <= cap; mr *= 2) {
+        fused_fn fn = pick_fused(m, mr, false);
+        if (!fn) continue;
+        int resident = 0;
+        const int rc = resident_blocks(reinterpret_cast<const void*>(fn), 256, &resident);
+        if (rc) return rc;
+        const int P = fused_splits(full, m.H / 16, mr <= 4 ? 8 : 4);
+        if (expected_items(m, mr) * nbI * P <= 1.1 * resident) {
+            *out = mr;
+            return EXL3_OK;
+        }
+    }
+    return EXL3_OK;
+}
+
 int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     FusedArgs a{};
     if (m.uniform) {
@@ -103,16 +146,24 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     // rows per item: one when the routing is sparse (pairs <= E / 2: an expert rarely takes two rows, and the
     // one-row instantiation is the fastest; 512 experts of 2048 -> 512, top-10: 2 / 4 / 8 / 12 tokens 27.7 -> 25.8,
     // 36.2 -> 33.8, 54.5 -> 47.1, 68.3 -> 63.3 us against two rows per item; 64 experts, top-8, 4 tokens 28.8 -> 25.5);
-    // otherwise up to the batch size, capped by the rows an expert takes on average (at most one: two rows per item,
-    // 64 experts, top-8, 8 tokens 34.0 against 36.6 with eight; a dense MLP, one expert, takes every row)
+    // otherwise the narrowest width whose jobs all fit the resident grid (fused_fit_rows), else up to the batch size
+    // capped by the rows an expert takes on average (at most one: two rows per item, 64 experts, top-8, 8 tokens 34.0
+    // against 36.6 with eight; experts of 4096 -> 1536 or wider fill the device at any width and take the fewest
+    // items: 8 experts top-8, 8 tokens 52.6 us at eight rows, 63.0 at four; a dense MLP, one expert, takes every row)
     int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
     const int64_t pairs = (int64_t)m.M * m.slots;
     if (pairs * 2 <= m.E) {
         MR = 1;
     } else {
-        const int64_t rpe = (pairs + m.E - 1) / m.E;
-        const int cap = rpe <= 1 ? 2 : rpe <= 2 ? 4 : 8;
-        if (MR > cap) MR = cap;
+        int rc = 0, fit = 0;
+        if ((rc = fused_fit_rows(m, MR, &fit))) return rc;
+        if (fit) {
+            MR = fit;
+        } else {
+            const int64_t rpe = (pairs + m.E - 1) / m.E;
+            const int cap = rpe <= 1 ? 2 : rpe <= 2 ? 4 : 8;
+            if (MR > cap) MR = cap;
+        }
     }
     const int mr_env = env_int("EXL3MI_FUSED_MR", 0);
     if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) MR = mr_env;

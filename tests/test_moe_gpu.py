@@ -97,6 +97,23 @@ def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E):
     assert np.array_equal(y, y1)
 
 
+@pytest.mark.parametrize("mr", [1, 2, 4, 8])
+@pytest.mark.parametrize("M,k,E", [(8, 4, 4), (16, 7, 16), (5, 7, 9), (8, 1, 1)])
+def test_moe_fused_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E):
+    """The fused layer with every rows-per-item width forced (EXL3MI_FUSED_MR; by itself it takes the narrowest
+    width whose jobs fit the resident grid): experts that take all 8 rows, 16 tokens over 16 experts, a ragged batch
+    and a dense MLP (one expert), with repeated experts and an inactive slot, meet the bar against the oracle; two
+    calls in a row agree bit for bit."""
+    tables, orc = make_experts(exl3, oracle, E, 256, 256, 3, 3, 2600 + 10 * E + M)
+    ids, w = _ids_w(M, k, E, 2601 + M, dup=True, inactive=k > 1)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2602 + M)).half()
+    monkeypatch.setenv("EXL3MI_FUSED_MR", str(mr))
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert max_rel(y, ref) <= MAX_REL
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    assert np.array_equal(y, y1)
+
+
 @pytest.mark.parametrize("M,k,E,Kg,Kd", [(12, 10, 64, 3, 3), (16, 8, 40, 2, 2), (10, 12, 200, 2, 3), (16, 7, 16, 4, 4)])
 def test_moe_fused_up_to_16_tokens(exl3, oracle, monkeypatch, M, k, E, Kg, Kd):
     """9 to 16 tokens within 128 pairs take the one-launch layer (items of up to 8 rows, or 2 under sparse routing);
