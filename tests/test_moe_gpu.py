@@ -81,36 +81,40 @@ def test_moe_fused_and_multi_kernel_paths(exl3, oracle, small, monkeypatch, M):
 
 
 @pytest.mark.parametrize("mr", [1, 2, 4, 8])
-@pytest.mark.parametrize("M,k,E", [(8, 4, 4), (8, 3, 12), (5, 7, 9)])
-def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E):
+@pytest.mark.parametrize("M,k,E,shared", [(8, 4, 4, False), (8, 3, 12, False), (5, 7, 9, False), (7, 3, 10, True)])
+def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, shared):
     """The multi-launch decode path with every rows-per-item width forced (EXL3MI_MOE_MR; by itself it takes one, two
-    or four): experts that take all 8 rows (4 experts top-4), a few rows, and a ragged 5-token batch, with repeated
-    experts and an inactive slot, meet the bar against the oracle; two calls in a row agree bit for bit."""
-    tables, orc = make_experts(exl3, oracle, E, 256, 256, 3, 3, 2500 + 10 * E + M)
+    or four): experts that take all 8 rows (4 experts top-4), a few rows, a ragged 5-token batch, and a shared expert
+    (every token's extra slot: full items at each width beside sparse routed ones), with repeated experts and an
+    inactive slot, meet the bar against the oracle; two calls in a row agree bit for bit."""
+    tables, orc = make_experts(exl3, oracle, E + shared, 256, 256, 3, 3, 2500 + 10 * E + M)
     ids, w = _ids_w(M, k, E, 2501 + M, dup=True, inactive=True)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2502 + M)).half()
+    sh = E if shared else -1
     monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
     monkeypatch.setenv("EXL3MI_MOE_MR", str(mr))
-    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
     assert max_rel(y, ref) <= MAX_REL
-    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
     assert np.array_equal(y, y1)
 
 
 @pytest.mark.parametrize("mr", [1, 2, 4, 8])
-@pytest.mark.parametrize("M,k,E", [(8, 4, 4), (16, 7, 16), (5, 7, 9), (8, 1, 1)])
-def test_moe_fused_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E):
+@pytest.mark.parametrize("M,k,E,shared", [(8, 4, 4, False), (16, 7, 16, False), (5, 7, 9, False), (8, 1, 1, False),
+                                          (12, 6, 20, True)])
+def test_moe_fused_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, shared):
     """The fused layer with every rows-per-item width forced (EXL3MI_FUSED_MR; by itself it takes the narrowest
-    width whose jobs fit the resident grid): experts that take all 8 rows, 16 tokens over 16 experts, a ragged batch
-    and a dense MLP (one expert), with repeated experts and an inactive slot, meet the bar against the oracle; two
-    calls in a row agree bit for bit."""
-    tables, orc = make_experts(exl3, oracle, E, 256, 256, 3, 3, 2600 + 10 * E + M)
+    width whose jobs fit the resident grid): experts that take all 8 rows, 16 tokens over 16 experts, a ragged batch,
+    a dense MLP (one expert) and a shared expert beside routed ones, with repeated experts and an inactive slot, meet
+    the bar against the oracle; two calls in a row agree bit for bit."""
+    tables, orc = make_experts(exl3, oracle, E + shared, 256, 256, 3, 3, 2600 + 10 * E + M)
     ids, w = _ids_w(M, k, E, 2601 + M, dup=True, inactive=k > 1)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2602 + M)).half()
+    sh = E if shared else -1
     monkeypatch.setenv("EXL3MI_FUSED_MR", str(mr))
-    y, ref = _run(exl3, oracle, tables, orc, x, ids, w)
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
     assert max_rel(y, ref) <= MAX_REL
-    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w)
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
     assert np.array_equal(y, y1)
 
 
