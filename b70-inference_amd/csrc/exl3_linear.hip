@@ -218,9 +218,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     const size_t rs = (size_t)a.tn * (8 * K);                       // words per tile-row
     const uint32_t* sp = tr + (size_t)strip * (64 * K) + (size_t)b0 * 8 * rs;
     // phase 1: xh = fp16(H128(fp16(x * suh)) / sqrt(128)) for rows < m (zero otherwise), and its block sums; the
-    // strip's shard selects the sign vector (clamped into [0, S)). The wave's first x block and its signs are loaded
-    // before the weight prefetch (loads complete in issue order: the transform then waits for nothing issued after
-    // them), with clamped addresses so that no load sits under a branch.
+    // strip's shard selects the sign vector (clamped into [0, S)). The wave's first x blocks and their signs are
+    // loaded before the weight prefetch (loads complete in issue order: their transforms then wait for nothing issued
+    // after them), with clamped addresses so that no load sits under a branch.
     int shard = 0;
     if (a.sonb) {
         shard = a.sonb[strip];
@@ -233,10 +233,15 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
         xp = x + (int64_t)(m < a.m ? m : 0) * a.x_ld + k0;
         sp_ = suh + k0;
     };
+    // Only the wave's first blocks go ahead of the weight prefetch (two up to 4 rows, four above); the rest are
+    // loaded after it. Hoisting every block put up to 16 x loads per wave in front of the first weight rows: 4096 x
+    // 4096 at 8 rows 14.47 us against 12.84 with four hoisted (3 rows 9.71 against 9.33 with two, one row 6.89 / 6.75).
     constexpr int JB = (M * kGemvKBMax + NW - 1) / NW;              // blocks per wave, at most
-    HadIn hv[JB];
+    constexpr int JCAP = M <= 4 ? 2 : 4;
+    constexpr int JE = JB < JCAP ? JB : JCAP;
+    HadIn hv[JE];
 #pragma unroll
-    for (int j = 0; j < JB; ++j) {
+    for (int j = 0; j < JE; ++j) {
         const int i = wave + j * NW;
         const uint16_t *xp, *sq;
         block_ptrs(i < nbm ? i : nbm - 1, xp, sq);
@@ -246,13 +251,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_kernel(GemvArgs a) {
     // weight loads in flight during phase 1, issued without a branch (wave < NW <= 8 <= kb * 8 tile-rows)
     strip_prefetch<K, kLinearRing, false>(sp, rs, wave, kb * 8, NW, lane, ring);
 #pragma unroll
-    for (int j = 0; j < JB; ++j) {
+    for (int j = 0; j < JE; ++j) {
         const int i = wave + j * NW;
         if (i < nbm) {
             const int m = i / kb, b = i - m * kb;
             const float s = had_in_finish(hv[j], m < a.m, &xs[m][b * 128], lane);
             if (lane == 0) bsum[m][b] = s;
         }
+    }
+    for (int i = wave + JE * NW; i < nbm; i += NW) {
+        const uint16_t *xp, *sq;
+        block_ptrs(i, xp, sq);
+        const int m = i / kb, b = i - m * kb;
+        const float s = had_in_finish(had_in_load(xp, sq, lane), m < a.m, &xs[m][b * 128], lane);
+        if (lane == 0) bsum[m][b] = s;
     }
     __syncthreads();
 
