@@ -87,8 +87,10 @@ static double expected_items(const MoeArgs& m, int mr) {
 // resident the narrowest width that fits wins: dense routing over experts of 2048 -> 512 (24 jobs per item), 8 tokens:
 // 8 experts top-8 40.4 (eight rows) -> 28.8 us (two), 16 experts top-8 36.0 -> 32.1; 16 tokens: 8 experts top-2
 // 35.8 -> 23.8 (one), 16 experts top-8 42.4 -> 37.8 (four), 32 experts top-8 44.1 -> 38.2 (four).
-static int fused_fits(const MoeArgs& m, int mr, bool* fits) {
-    *fits = false;
+// Expected gate|up jobs of the batch at `mr` rows per item, each item split to its full k-split count, over the
+// workgroups the device holds at once for that instantiation (0 when it is not built).
+static int fused_load(const MoeArgs& m, int mr, double* load) {
+    *load = 0.0;
     fused_fn fn = pick_fused(m, mr, false);
     if (!fn) return EXL3_OK;
     int resident = 0;
@@ -96,8 +98,15 @@ static int fused_fits(const MoeArgs& m, int mr, bool* fits) {
     if (rc) return rc;
     const int full = m.H / 16 / kFusedMinJobRows > 1 ? m.H / 16 / kFusedMinJobRows : 1;
     const int P = fused_splits(full, m.H / 16, mr <= 4 ? 8 : 4);
-    *fits = expected_items(m, mr) * (m.I / 128) * P <= 1.1 * resident;
+    *load = expected_items(m, mr) * (m.I / 128) * P / (resident > 0 ? resident : 1);
     return EXL3_OK;
+}
+
+static int fused_fits(const MoeArgs& m, int mr, bool* fits) {
+    double load = 0.0;
+    const int rc = fused_load(m, mr, &load);
+    *fits = load > 0.0 && load <= 1.1;
+    return rc;
 }
 
 static int fused_fit_rows(const MoeArgs& m, int cap, int* out) {
@@ -178,7 +187,24 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
         } else {
             const int64_t rpe = (pairs + m.E - 1) / m.E;
             const int cap = rpe <= 1 ? 2 : rpe <= 2 ? 4 : 8;
+            const int mcap = MR;
             if (MR > cap) MR = cap;
+            // jobs of more than four resident grids: the layer runs at the device's throughput, so the width with
+            // the fewest items per unit of per-item cost wins (128 experts of 4096 -> 1536, top-8, 16 tokens: 270 us
+            // at two rows, 253 at four; per-item cost relative to two rows, from it: 0.81 / 1 / 1.02 / 1.27)
+            double load = 0.0;
+            if ((rc = fused_load(m, MR, &load))) return rc;
+            if (load > 4.0) {
+                static const double wt[4] = {0.81, 1.0, 1.02, 1.27};
+                double best = 0.0;
+                for (int mr = 1, q = 0; mr <= mcap; mr *= 2, ++q) {
+                    const double c = expected_items(m, mr) * wt[q];
+                    if (pick_fused(m, mr, false) && (best == 0.0 || c < best)) {
+                        best = c;
+                        MR = mr;
+                    }
+                }
+            }
         }
     }
     const int mr_env = env_int("EXL3MI_FUSED_MR", 0);
