@@ -170,15 +170,18 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     int MR = m.M <= 1 ? 1 : m.M <= 2 ? 2 : m.M <= 4 ? 4 : 8;
     const int64_t pairs = (int64_t)m.M * m.slots;
     if (pairs * 2 <= m.E) {
-        // sparse: one row per item, unless one-row jobs overfill the resident grid and two-row items save a tenth of
-        // the items (wide experts near E / 2 pairs: 8 experts of 4096 -> 14336, top-2, 2 tokens 95.5 -> 90.3 us;
-        // 16 experts, 4 tokens 173 -> 158; C3 at 8 or 12 tokens saves about 1 % of the items and keeps one row)
+        // sparse: one row per item, unless the one-row jobs fill more than three resident grids (the layer then runs
+        // at the device's throughput) and two-row items save a twentieth of the items: wide experts near E / 2
+        // pairs, 8 experts of 4096 -> 14336, top-2, 2 tokens 95.5 -> 90.3 us, 16 experts at 4 tokens 173 -> 158;
+        // 256 experts of 7168 -> 2048 and a shared expert, 4 tokens, whose shared rows pair up (9 % fewer items):
+        // 440 -> 407. Below that load the one-row instantiation wins even with fewer items at two rows: C3 at
+        // 8 tokens (1.5 grids, 7 % fewer items) 42 us at one row against 50 at two.
         const int cap = MR;
         MR = 1;
-        bool fits1 = true;
+        double load1 = 0.0;
         int rc = 0;
-        if (cap >= 2 && (rc = fused_fits(m, 1, &fits1))) return rc;
-        if (cap >= 2 && !fits1 && expected_items(m, 2) <= 0.9 * expected_items(m, 1)) MR = 2;
+        if (cap >= 2 && (rc = fused_load(m, 1, &load1))) return rc;
+        if (cap >= 2 && load1 > 3.0 && expected_items(m, 2) <= 0.95 * expected_items(m, 1)) MR = 2;
     } else {
         int rc = 0, fit = 0;
         if ((rc = fused_fit_rows(m, MR, &fit))) return rc;
