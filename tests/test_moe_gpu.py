@@ -99,6 +99,25 @@ def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, 
     assert np.array_equal(y, y1)
 
 
+@pytest.mark.parametrize("M,k,E,shared,no_fused", [(24, 4, 200, False, False), (12, 3, 150, True, True),
+                                                   (40, 3, 300, False, False)])
+def test_moe_sparse_batches_past_eight_tokens(exl3, oracle, monkeypatch, M, k, E, shared, no_fused):
+    """Sparse batches (pairs <= E / 2) of more than 8 tokens that the fused layer does not take (more than 16 tokens,
+    or forced off) run as one-row GEMV items on the multi-launch path: with repeated experts, an inactive slot and a
+    shared expert (every token's extra slot, a full item per row), they meet the bar against the oracle, and two calls
+    in a row agree bit for bit."""
+    tables, orc = make_experts(exl3, oracle, E + shared, 256, 256, 3, 3, 2800 + E + M)
+    ids, w = _ids_w(M, k, E, 2801 + M, dup=True, inactive=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2802 + M)).half()
+    if no_fused:
+        monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    sh = E if shared else -1
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
+    assert max_rel(y, ref) <= MAX_REL
+    y1, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
+    assert np.array_equal(y, y1)
+
+
 @pytest.mark.parametrize("mr", [1, 2, 4, 8])
 @pytest.mark.parametrize("M,k,E,shared", [(8, 4, 4, False), (16, 7, 16, False), (5, 7, 9, False), (8, 1, 1, False),
                                           (12, 6, 20, True)])
