@@ -66,7 +66,7 @@ bool moe_fused_ok(const MoeArgs& a) {
 // Expected items of a batch at `mr` rows per item, routing taken as uniform: the routed experts' row counts are
 // Binomial(M, p) with p = routed picks per token / routed experts, an item per started group of mr rows; a shared
 // expert takes every token.
-static double expected_items(const MoeArgs& m, int mr) {
+double moe_expected_items(const MoeArgs& m, int mr) {
     const bool sh = (unsigned)m.shared < (unsigned)m.E;
     const int routed_e = sh ? m.E - 1 : m.E, picks = sh ? m.slots - 1 : m.slots;
     double items = sh ? (double)((m.M + mr - 1) / mr) : 0.0;
@@ -98,7 +98,7 @@ static int fused_load(const MoeArgs& m, int mr, double* load) {
     if (rc) return rc;
     const int full = m.H / 16 / kFusedMinJobRows > 1 ? m.H / 16 / kFusedMinJobRows : 1;
     const int P = fused_splits(full, m.H / 16, mr <= 4 ? 8 : 4);
-    *load = expected_items(m, mr) * (m.I / 128) * P / (resident > 0 ? resident : 1);
+    *load = moe_expected_items(m, mr) * (m.I / 128) * P / (resident > 0 ? resident : 1);
     return EXL3_OK;
 }
 
@@ -181,7 +181,7 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
         double load1 = 0.0;
         int rc = 0;
         if (cap >= 2 && (rc = fused_load(m, 1, &load1))) return rc;
-        if (cap >= 2 && load1 > 3.0 && expected_items(m, 2) <= 0.95 * expected_items(m, 1)) MR = 2;
+        if (cap >= 2 && load1 > 3.0 && moe_expected_items(m, 2) <= 0.95 * moe_expected_items(m, 1)) MR = 2;
     } else {
         int rc = 0, fit = 0;
         if ((rc = fused_fit_rows(m, MR, &fit))) return rc;
@@ -201,7 +201,7 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
                 static const double wt[4] = {0.81, 1.0, 1.02, 1.27};
                 double best = 0.0;
                 for (int mr = 1, q = 0; mr <= mcap; mr *= 2, ++q) {
-                    const double c = expected_items(m, mr) * wt[q];
+                    const double c = moe_expected_items(m, mr) * wt[q];
                     if (pick_fused(m, mr, false) && (best == 0.0 || c < best)) {
                         best = c;
                         MR = mr;

@@ -99,6 +99,24 @@ def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, 
     assert np.array_equal(y, y1)
 
 
+@pytest.mark.parametrize("M,k,E,shared", [(24, 4, 12, False), (17, 3, 11, True), (32, 2, 6, True), (16, 9, 12, False)])
+def test_moe_items_up_to_32_tokens_and_forced_mfma(exl3, oracle, monkeypatch, M, k, E, shared):
+    """Batches of 9 to 32 tokens with uniform K and small experts (and routing dense enough that experts take many
+    rows: hot experts in most tokens) run as GEMV items of up to four rows; EXL3MI_MOE_MFMA=1 sends the same batch
+    through the MFMA grouped GEMM. Both meet the bar against the oracle, with a shared expert and inactive slots."""
+    tables, orc = make_experts(exl3, oracle, E + shared, 256, 256, 3, 3, 2900 + 10 * E + M)
+    ids, w = _skewed_ids(M, k, E, 2901 + M)
+    ids[0, -1] = -1
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2902 + M)).half()
+    sh = E if shared else -1
+    monkeypatch.setenv("EXL3MI_NO_FUSED", "1")
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
+    assert max_rel(y, ref) <= MAX_REL
+    monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")
+    y2, _ = _run(exl3, oracle, tables, orc, x, ids, w, shared=sh)
+    assert max_rel(y2, ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("M,k,E,shared,no_fused", [(24, 4, 200, False, False), (12, 3, 150, True, True),
                                                    (40, 3, 300, False, False)])
 def test_moe_sparse_batches_past_eight_tokens(exl3, oracle, monkeypatch, M, k, E, shared, no_fused):
@@ -460,9 +478,9 @@ def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small):
     assert max_rel(y, ref) <= MAX_REL
 
 
-@pytest.mark.parametrize("M", [24, 80])
+@pytest.mark.parametrize("M", [40, 80])
 def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
-    """More than 16 tokens: every expert's rows go through the MFMA grouped GEMM in blocks of up to 64 rows, hot and
+    """More than 32 tokens: every expert's rows go through the MFMA grouped GEMM in blocks of up to 64 rows, hot and
     cold experts in one call (80 tokens: the hot experts cross the 64-row block boundary)."""
     tables, orc = small
     ids, w = _skewed_ids(M, 4, 12, 1500 + M)
