@@ -158,7 +158,7 @@ def test_moe_fused_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, shared)
 @pytest.mark.parametrize("M,k,E,Kg,Kd", [(12, 10, 64, 3, 3), (16, 8, 40, 2, 2), (10, 12, 200, 2, 3), (16, 7, 16, 4, 4)])
 def test_moe_fused_up_to_16_tokens(exl3, oracle, monkeypatch, M, k, E, Kg, Kd):
     """9 to 16 tokens within 128 pairs take the one-launch layer (items of up to 8 rows, or 2 under sparse routing);
-    against the oracle and against the grouped multi-launch path (EXL3MI_NO_FUSED=1, MFMA above 8 rows)."""
+    against the oracle and against the grouped multi-launch path (EXL3MI_NO_FUSED=1: GEMV items up to 16 tokens)."""
     tables, orc = make_experts(exl3, oracle, E, 256, 256, Kg, Kd, 2400 + E + M)
     ids, w = _ids_w(M, k, E, 2401 + M, dup=True, inactive=True)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(2402 + M)).half()
