@@ -99,11 +99,13 @@ def test_moe_multi_kernel_rows_per_item(exl3, oracle, monkeypatch, mr, M, k, E, 
     assert np.array_equal(y, y1)
 
 
-@pytest.mark.parametrize("M,k,E,shared", [(24, 4, 12, False), (17, 3, 11, True), (32, 2, 6, True), (16, 9, 12, False)])
-def test_moe_items_up_to_32_tokens_and_forced_mfma(exl3, oracle, monkeypatch, M, k, E, shared):
-    """Batches of 9 to 32 tokens with uniform K and small experts (and routing dense enough that experts take many
-    rows: hot experts in most tokens) run as GEMV items of up to four rows; EXL3MI_MOE_MFMA=1 sends the same batch
-    through the MFMA grouped GEMM. Both meet the bar against the oracle, with a shared expert and inactive slots."""
+@pytest.mark.parametrize("M,k,E,shared", [(24, 4, 12, False), (17, 3, 11, True), (32, 2, 6, True), (16, 9, 12, False),
+                                          (48, 4, 12, True), (64, 2, 8, False)])
+def test_moe_items_up_to_64_tokens_and_forced_mfma(exl3, oracle, monkeypatch, M, k, E, shared):
+    """Batches of 9 to 64 tokens with uniform K and small experts (and routing dense enough that experts take many
+    rows: hot experts in most tokens; past 32 tokens a thin MFMA grid of a few experts) run as GEMV items of up to
+    four rows; EXL3MI_MOE_MFMA=1 sends the same batch through the MFMA grouped GEMM. Both meet the bar against the
+    oracle, with a shared expert and inactive slots."""
     tables, orc = make_experts(exl3, oracle, E + shared, 256, 256, 3, 3, 2900 + 10 * E + M)
     ids, w = _skewed_ids(M, k, E, 2901 + M)
     ids[0, -1] = -1
@@ -293,11 +295,11 @@ def test_moe_forward_logits_in_layer_fp16_and_router_kernel_switch(exl3, small, 
     assert torch.equal(a, b) and torch.equal(ia, ib) and torch.equal(wa, wb)
 
 
-@pytest.mark.parametrize("M", [1, 4, 12, 37])
+@pytest.mark.parametrize("M", [1, 4, 12, 37, 80])
 def test_moe_packed_tables_same_rows(exl3, small, M):
     """ExpertTables.packed (uniform strides: the decode kernels and the prefill input transform compute expert
     addresses instead of loading them) gives bit-identical rows to the same experts addressed through their pointer
-    tables (37 tokens: the MFMA prefill path)."""
+    tables (37 tokens: GEMV items; 80 tokens: the MFMA prefill path)."""
     tables, _ = small
     packed = exl3.ExpertTables.packed(*tables.projs)
     assert packed.layout is not None and list(packed.layout)[9] > 0
@@ -465,11 +467,12 @@ def test_moe_prefill_more_pairs_than_held(exl3, oracle, small):
     assert max_rel(y, ref) <= MAX_REL
 
 
-def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small):
-    """Prefill (37 tokens: the MFMA grouped GEMM) with a shared expert and inactive slots in several tokens: the
+def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small, monkeypatch):
+    """Prefill (37 tokens, the MFMA grouped GEMM forced) with a shared expert and inactive slots in several tokens: the
     expert-sorted pairs stop short of tokens x slots (145 of 148 here, not a multiple of 16), so the input transform's
     last row group holds pairs past the valid ones, which it must skip."""
     tables, orc = small
+    monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")
     ids, w = _ids_w(37, 3, 11, 711, dup=True, inactive=True)     # experts 0..10 routed, 11 = shared
     ids[5, 1] = -1
     ids[20, 0] = -1
@@ -479,9 +482,11 @@ def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small):
 
 
 @pytest.mark.parametrize("M", [40, 80])
-def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
-    """More than 32 tokens: every expert's rows go through the MFMA grouped GEMM in blocks of up to 64 rows, hot and
-    cold experts in one call (80 tokens: the hot experts cross the 64-row block boundary)."""
+def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, monkeypatch, M):
+    """The MFMA grouped GEMM (forced at 40 tokens, which by itself takes GEMV items over these 12 small experts; by
+    itself at 80): every expert's rows in blocks of up to 64 rows, hot and cold experts in one call (80 tokens: the
+    hot experts cross the 64-row block boundary)."""
+    monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")
     tables, orc = small
     ids, w = _skewed_ids(M, 4, 12, 1500 + M)
     x = torch.randn(M, 256, generator=torch.Generator().manual_seed(16)).half()
@@ -491,7 +496,8 @@ def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, M):
     assert counts.max() > 8 and (counts[counts > 0] <= 8).any()
 
 
-def test_moe_prefill_per_projection_k_and_gelu(exl3, oracle):
+def test_moe_prefill_per_projection_k_and_gelu(exl3, oracle, monkeypatch):
+    monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")                # the MFMA grouped GEMM at 40 tokens
     tables, orc = make_experts(exl3, oracle, 6, 512, 384, 2, 3, 1600)
     ids, w = _skewed_ids(40, 3, 6, 1601, hot=(1, 4))
     x = torch.randn(40, 512, generator=torch.Generator().manual_seed(17)).half()
