@@ -1099,6 +1099,7 @@ static moe_fn down_select(int K, int MR, bool pl) {
 
 int launch_moe_mfma(const MoeArgs& a, hipStream_t st);          // exl3_mfma.hip
 bool moe_fused_ok(const MoeArgs& a);                            // exl3_moe_fused.hip
+bool moe_fused_take(const MoeArgs& a);
 double moe_expected_items(const MoeArgs& m, int mr);
 int moe_fused_path(const MoeArgs& a, hipStream_t st);
 
@@ -1306,7 +1307,7 @@ static int moe_setup(const uint16_t* x, int64_t x_ld, int64_t M, int64_t H, int6
 }
 
 static int moe_run(MoeArgs& a, hipStream_t st) {
-    if (moe_fused_ok(a)) return moe_fused_path(a, st);
+    if (moe_fused_take(a)) return moe_fused_path(a, st);
     // GEMV items of up to MR rows per expert for decode batches (M <= 8), sparse batches of any size (pairs <= E / 2:
     // an expert takes one or two rows) and, with uniform K, batches of up to 16 tokens, up to 32 when the experts
     // are small (H * I <= 2^22), and up to 64 when the MFMA grid would be thin (active experts * I / 128 < 160 gate|up
@@ -1439,7 +1440,7 @@ int exl3_moe_forward_logits(const uint16_t* x, int64_t x_ld, int64_t M, int64_t 
     // launch (512 experts, top-10: 1 token 24.1 us against 25.0 with two-row items; with one-row items 3 tokens 28.4
     // against 30.2, 4 tokens 32.0 against 33.7) until the rankings in every workgroup outweigh it (8 tokens: 47.4
     // against 46.2). Otherwise the router kernel runs first.
-    if (M <= kFusedRouteMaxRows && moe_fused_ok(a) && n_logits <= kFusedRouteMaxE &&
+    if (M <= kFusedRouteMaxRows && moe_fused_take(a) && n_logits <= kFusedRouteMaxE &&
         env_int("EXL3MI_ROUTER_KERNEL", 0) == 0) {
         a.logits = logits;
         a.lg_ld = logits_ld;

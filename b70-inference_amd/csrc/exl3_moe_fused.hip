@@ -123,43 +123,8 @@ static int fused_fit_rows(const MoeArgs& m, int cap, int* out) {
     return EXL3_OK;
 }
 
-int moe_fused_path(const MoeArgs& m, hipStream_t st) {
-    FusedArgs a{};
-    if (m.uniform) {
-        a.uniform = 1;
-        for (int i = 0; i < 9; ++i) {
-            a.tb[i] = m.tb[i];
-            a.ts[i] = m.ts[i];
-        }
-    }
-    a.x = m.x;
-    a.x_ld = m.x_ld;
-    a.gu_tn = m.gu_tn;
-    a.M = m.M;
-    a.H = m.H;
-    a.I = m.I;
-    a.topk = m.topk;
-    a.slots = m.slots;
-    a.E = m.E;
-    a.shared = m.shared;
-    a.np = m.M * m.slots;
-    a.ids = m.ids;
-    a.tw = m.tw;
-    if (m.logits) {
-        a.logits = m.logits;
-        a.lg_ld = m.lg_ld;
-        a.n_logits = m.n_logits;
-        a.rbias = m.rbias;
-        a.ids_out = m.ids_out;
-        a.tw_out = m.tw_out;
-    }
-    a.tables = m.tables;
-    a.kmaps = m.kmaps;
-    a.act = m.act;
-    a.limit = m.limit;
-    a.out = m.out;
-    a.out_ld = m.out_ld;
-    a.out_f32 = m.out_f32;
+// Rows per item for the batch (1, 2, 4 or 8).
+static int fused_rows(const MoeArgs& m, int* out) {
     // rows per item: one when the routing is sparse (pairs <= E / 2: an expert rarely takes two rows, and the
     // one-row instantiation is the fastest; 512 experts of 2048 -> 512, top-10: 2 / 4 / 8 / 12 tokens 27.7 -> 25.8,
     // 36.2 -> 33.8, 54.5 -> 47.1, 68.3 -> 63.3 us against two rows per item; 64 experts, top-8, 4 tokens 28.8 -> 25.5);
@@ -212,6 +177,69 @@ int moe_fused_path(const MoeArgs& m, hipStream_t st) {
     }
     const int mr_env = env_int("EXL3MI_FUSED_MR", 0);
     if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) MR = mr_env;
+    *out = MR;
+    return EXL3_OK;
+}
+
+// Whether the fused layer takes the batch: eligible (moe_fused_ok), and its gate|up jobs at the chosen rows per item
+// fill at most four resident grids. Past that the layer runs at the device's throughput and the multi-launch GEMV
+// path is faster (fused against multi-launch: 129 experts of 4096 -> 1408 with a shared one, top-8, 4 / 8 / 14
+// tokens 104.5 / 162.6 / 236 against 93.7 / 139.2 / 204 us; 256 experts of 7168 -> 2048 at per-tile K with a shared
+// one, 2 / 4 / 8 tokens 251 / 406 / 746 against 217 / 375 / 683; 160 experts of 5120 -> 1536, 8 tokens 200.5 against
+// 182), while below it the fused layer's shorter chain wins (the same 129 experts at 1 / 2 tokens 38 / 50 against
+// 40.8 / 59.5; 128 experts of 2048 -> 768 at 4 / 8 tokens 35.2 / 49.5 against 43 / 62.3; C3). With 16 experts or
+// fewer the fused layer keeps batches up to twelve grids (8 experts of 4096 -> 14336, top-2, 4 / 8 tokens 134.3 /
+// 179 against 138.9 / 187; 16 tokens, 14 grids, 275.6 against 264). EXL3MI_FUSED_ALWAYS=1 takes every eligible
+// batch, EXL3MI_FUSED_DECLINE=1 none.
+bool moe_fused_take(const MoeArgs& m) {
+    if (!moe_fused_ok(m) || env_int("EXL3MI_FUSED_DECLINE", 0)) return false;
+    if (env_int("EXL3MI_FUSED_ALWAYS", 0)) return true;
+    int MR = 1;
+    double load = 0.0;
+    if (fused_rows(m, &MR) || fused_load(m, MR, &load)) return true;   // errors surface on the fused path itself
+    return !(load > 4.0 && (m.E > 16 || load > 12.0));
+}
+
+int moe_fused_path(const MoeArgs& m, hipStream_t st) {
+    FusedArgs a{};
+    if (m.uniform) {
+        a.uniform = 1;
+        for (int i = 0; i < 9; ++i) {
+            a.tb[i] = m.tb[i];
+            a.ts[i] = m.ts[i];
+        }
+    }
+    a.x = m.x;
+    a.x_ld = m.x_ld;
+    a.gu_tn = m.gu_tn;
+    a.M = m.M;
+    a.H = m.H;
+    a.I = m.I;
+    a.topk = m.topk;
+    a.slots = m.slots;
+    a.E = m.E;
+    a.shared = m.shared;
+    a.np = m.M * m.slots;
+    a.ids = m.ids;
+    a.tw = m.tw;
+    if (m.logits) {
+        a.logits = m.logits;
+        a.lg_ld = m.lg_ld;
+        a.n_logits = m.n_logits;
+        a.rbias = m.rbias;
+        a.ids_out = m.ids_out;
+        a.tw_out = m.tw_out;
+    }
+    a.tables = m.tables;
+    a.kmaps = m.kmaps;
+    a.act = m.act;
+    a.limit = m.limit;
+    a.out = m.out;
+    a.out_ld = m.out_ld;
+    a.out_f32 = m.out_f32;
+    int MR = 1;
+    int rc0 = fused_rows(m, &MR);
+    if (rc0) return rc0;
     const int kbf = MR <= 4 ? 8 : 4;
     fused_fn fn = pick_fused(m, MR, false);
     if (!fn) return fail(EXL3_ERR_UNSUPPORTED, "exl3_moe_forward: fused layer for K %d / %d not built", m.Kg, m.Kd);

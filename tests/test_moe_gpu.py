@@ -278,6 +278,27 @@ def test_moe_forward_logits_in_layer_routing_exact(exl3, oracle, E, k, H, I, bia
     assert torch.equal(out, exl3.moe_forward(x, rid, rw, tables))
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_moe_forward_logits_fused_declined(exl3, oracle, small, monkeypatch, M):
+    """A batch the fused layer declines (EXL3MI_FUSED_DECLINE=1; by itself it declines those whose gate|up jobs fill
+    more than four resident grids) takes the router kernel and the multi-launch path from the routed entry point, at
+    sizes that would otherwise rank inside the fused layer: the same picks and weights as the router kernel, the
+    same rows as moe_forward on them, and the oracle's rows to the bar, with a shared expert."""
+    tables, orc = small
+    g = torch.Generator().manual_seed(2350 + M)
+    x = torch.randn(M, 256, generator=g).half()
+    logits = torch.randn(M, 11, generator=g)
+    fused, _, _ = exl3.moe_forward_logits(x.cuda(), logits.cuda(), 3, tables, shared=11, return_routing=True)
+    monkeypatch.setenv("EXL3MI_FUSED_DECLINE", "1")
+    y, ids, w = exl3.moe_forward_logits(x.cuda(), logits.cuda(), 3, tables, shared=11, return_routing=True)
+    rid, rw = exl3.route_softmax_topk(logits.cuda(), 3)
+    assert torch.equal(ids, rid) and torch.equal(w, rw)
+    assert torch.equal(y, exl3.moe_forward(x.cuda(), rid, rw, tables, shared=11))
+    ref = oracle.moe_layer(x.numpy(), orc[:11], rid.cpu().numpy(), rw.cpu().numpy(), oracle.ACT_SILU, 0.0, orc[11])
+    assert max_rel(y.cpu().numpy(), ref) <= MAX_REL
+    assert max_rel(fused.cpu().numpy(), ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("M", [1, 2])
 def test_moe_forward_logits_in_layer_fp16_and_router_kernel_switch(exl3, small, M, monkeypatch):
     """fp16 outputs of the in-layer routing path, and the same call with the router kernel forced
