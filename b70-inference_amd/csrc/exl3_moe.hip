@@ -1336,12 +1336,13 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
     // 64 experts top-17 69.9 with four, 72.8 with two, 105.7 with eight). EXL3MI_MOE_MR=1|2|4|8 overrides.
     if (!mfma) {
         int cap = npairs * 2 <= E ? 1 : npairs * 2 <= 3 * E ? 2 : 4;
-        // wide experts (H * I > 2^22) under sparse routing: two rows per item when that saves a tenth of the expected
-        // items (a shared expert's rows pair up): 256 experts of 7168 -> 2048 (per-tile K) with a shared one, 8 tokens
-        // 686 -> 618 us; 160 experts of 5120 -> 1536, 8 tokens 182 -> 170.6; 129 experts of 4096 -> 1408 with a
-        // shared one, 4 tokens 94.2 -> 91.3 (2 tokens of the first, 7 % fewer items: 218 at one row, 221 at two)
+        // wide experts (H * I > 2^22) under sparse routing: two rows per item when that saves 8 % of the expected
+        // items (a shared expert's rows pair up): 256 experts of 7168 -> 2048 (per-tile K) with a shared one, 4 / 8
+        // tokens 377 -> 358.7, 686 -> 618 us; 160 experts of 5120 -> 1536, 8 tokens 182 -> 170.6; 129 experts of
+        // 4096 -> 1408 with a shared one, 4 tokens 94.2 -> 91.3 (2 tokens of the first, 7 % fewer items: 218 at one
+        // row, 221 at two)
         if (cap == 1 && M >= 2 && (int64_t)a.H * a.I > ((int64_t)1 << 22) &&
-            moe_expected_items(a, 2) <= 0.9 * moe_expected_items(a, 1))
+            moe_expected_items(a, 2) <= 0.92 * moe_expected_items(a, 1))
             cap = 2;
         if (a.MR > cap) a.MR = cap;
         const int mr_env = env_int("EXL3MI_MOE_MR", 0);
