@@ -1319,7 +1319,7 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
     // 103 -> 50. The MFMA path stays ahead for wide experts taking several rows each (16 experts of 4096 -> 4096,
     // top-4, 32 tokens 202 against 262 us on items), for grids of a few hundred workgroups or more past 32 tokens
     // (64 experts top-8, 64 tokens: 99 against 115), past 64 tokens, and for per-tile K (256 experts of 7168 -> 2048
-    // with a shared one, 16 tokens 729 against 1064). EXL3MI_MOE_MFMA=1 forces the MFMA path past 8 tokens.
+    // with a shared one, 16 tokens 729 against 1064). EXL3MI_MOE_MFMA=1 forces the MFMA path at any batch size.
     const int64_t M = a.M, E = a.E, npairs = M * a.slots;
     bool mfma = M > kMoeSmallRows && npairs * 2 > E;
     if (mfma && M <= 64 && a.Kg > 0 && a.Kd > 0) {
@@ -1327,7 +1327,14 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
         const bool thin = moe_expected_items(a, 64) * (a.I / 128) < 160.0;   // one MFMA block per active expert
         mfma = !(M <= 16 || (M <= 32 && small) || thin);
     }
-    if (M > kMoeSmallRows && env_int("EXL3MI_MOE_MFMA", 0)) mfma = true;
+    // Per-tile K over wide experts: the MFMA mix kernels' K 1 / 2 fast path outruns the GEMV items' per-tile decode
+    // once enough experts are active to amortise a block's unsplit k loop (256 experts of 7168 -> 2048 with a shared
+    // one: 8 / 10 tokens, about 62 / 75 active, 618 -> 491, 731 -> 557 us on MFMA; 2 / 4 tokens, 17 / 33 active, stay
+    // on items: 218 / 358 against 295 / 398).
+    if (!mfma && (a.Kg == 0 || a.Kd == 0) && (int64_t)a.H * a.I > ((int64_t)1 << 22) &&
+        moe_expected_items(a, 64) >= 48.0)
+        mfma = true;
+    if (env_int("EXL3MI_MOE_MFMA", 0)) mfma = true;
     a.MR = mfma ? 0 : M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : kMoeSmallRows;
     // rows per GEMV item: one for sparse routing (pairs <= E / 2; experts of 2048 -> 512, 8 tokens, against eight rows
     // per item: 512 experts top-17 170.6 -> 86.6 us), two up to 1.5 pairs per expert (128 experts top-17 78.7 against

@@ -278,6 +278,20 @@ def test_moe_forward_logits_in_layer_routing_exact(exl3, oracle, E, k, H, I, bia
     assert torch.equal(out, exl3.moe_forward(x, rid, rw, tables))
 
 
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_moe_mfma_path_at_decode_sizes(exl3, oracle, monkeypatch, M):
+    """The MFMA grouped GEMM at decode batch sizes (per-tile K over wide experts takes it from about 48 active experts
+    on; forced here with EXL3MI_MOE_MFMA=1 and the fused layer declined), per-tile K 1 / 2 and a shared expert:
+    every expert a single block of at most 16 rows, the oracle's rows to the bar."""
+    tables, orc = make_experts(exl3, oracle, 7, 256, 384, 0, 0, 3000 + M, per_tile=((1, 2), (0.38, 0.62)))
+    ids, w = _ids_w(M, 3, 6, 3001 + M, dup=True, inactive=True)
+    x = torch.randn(M, 256, generator=torch.Generator().manual_seed(3002 + M)).half()
+    monkeypatch.setenv("EXL3MI_FUSED_DECLINE", "1")
+    monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")
+    y, ref = _run(exl3, oracle, tables, orc, x, ids, w, shared=6)
+    assert max_rel(y, ref) <= MAX_REL
+
+
 @pytest.mark.parametrize("M", [1, 2, 4])
 def test_moe_forward_logits_fused_declined(exl3, oracle, small, monkeypatch, M):
     """A batch the fused layer declines (EXL3MI_FUSED_DECLINE=1; by itself it declines those whose gate|up jobs fill
