@@ -1310,19 +1310,19 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
     if (moe_fused_take(a)) return moe_fused_path(a, st);
     // GEMV items of up to MR rows per expert for decode batches (M <= 8), sparse batches of any size (pairs <= E / 2:
     // an expert takes one or two rows) and, with uniform K, batches of up to 16 tokens, up to 32 when the experts
-    // are small (H * I <= 2^22), and up to 64 when the MFMA grid would be thin (active experts * I / 128 < 160 gate|up
-    // workgroups). Other prefill batches: every expert with rows goes to the MFMA kernels in blocks of up to
+    // are small (H * I <= 2^22), and up to 128 when the MFMA grid would be thin (active experts * I / 128 < 160
+    // gate|up workgroups: 8 experts top-2, 128 tokens 116 -> 74 us; 32 experts top-4, 96 tokens 101 -> 87). Other prefill batches: every expert with rows goes to the MFMA kernels in blocks of up to
     // kMfmaRows rows (MR = 0: no GEMV items). Measured against the MFMA path: 512 experts of 2048 -> 512, top-10,
     // 16 / 20 / 25 tokens 141.5 -> 100.6, 153.5 -> 118.8, 165.6 -> 141.6 us; 16 experts top-9, 16 tokens 90.9 ->
     // 56.0; 8 experts top-8, 32 tokens 117.6 -> 72.5; 129 experts of 4096 -> 1408 with a shared one, 16 tokens
     // 254.6 -> 223.6; one expert of 4096 -> 4096, 32 / 64 tokens 176 -> 77, 210 -> 125; 8 experts top-2, 64 tokens
     // 103 -> 50. The MFMA path stays ahead for wide experts taking several rows each (16 experts of 4096 -> 4096,
     // top-4, 32 tokens 202 against 262 us on items), for grids of a few hundred workgroups or more past 32 tokens
-    // (64 experts top-8, 64 tokens: 99 against 115), past 64 tokens, and for per-tile K (256 experts of 7168 -> 2048
+    // (64 experts top-8, 64 tokens: 99 against 115), past 128 tokens, and for per-tile K (256 experts of 7168 -> 2048
     // with a shared one, 16 tokens 729 against 1064). EXL3MI_MOE_MFMA=1 forces the MFMA path at any batch size.
     const int64_t M = a.M, E = a.E, npairs = M * a.slots;
     bool mfma = M > kMoeSmallRows && npairs * 2 > E;
-    if (mfma && M <= 64 && a.Kg > 0 && a.Kd > 0) {
+    if (mfma && M <= 128 && a.Kg > 0 && a.Kd > 0) {
         const bool small = (int64_t)a.H * a.I <= ((int64_t)1 << 22);
         const bool thin = moe_expected_items(a, 64) * (a.I / 128) < 160.0;   // one MFMA block per active expert
         mfma = !(M <= 16 || (M <= 32 && small) || thin);

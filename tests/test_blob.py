@@ -162,8 +162,8 @@ def test_arena_experts_same_outputs(exl3, M):
 
 
 # decode paths of the layer by batch shape: (tokens, top-k, experts) -> the one-launch fused layer (<= 16 tokens, <= 128
-# pairs), the multi-kernel decode GEMVs (<= 8 tokens, more than 128 pairs), the MFMA grouped GEMM (80 tokens)
-BLOB_PATHS = {"fused": (3, 2, 6), "gemv": (8, 17, 20), "mfma": (80, 2, 6)}
+# pairs), the multi-kernel decode GEMVs (<= 8 tokens, more than 128 pairs), the MFMA grouped GEMM (160 tokens)
+BLOB_PATHS = {"fused": (3, 2, 6), "gemv": (8, 17, 20), "mfma": (160, 2, 6)}
 
 
 @pytest.mark.gpu

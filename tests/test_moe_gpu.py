@@ -330,11 +330,11 @@ def test_moe_forward_logits_in_layer_fp16_and_router_kernel_switch(exl3, small, 
     assert torch.equal(a, b) and torch.equal(ia, ib) and torch.equal(wa, wb)
 
 
-@pytest.mark.parametrize("M", [1, 4, 12, 37, 80])
+@pytest.mark.parametrize("M", [1, 4, 12, 37, 160])
 def test_moe_packed_tables_same_rows(exl3, small, M):
     """ExpertTables.packed (uniform strides: the decode kernels and the prefill input transform compute expert
     addresses instead of loading them) gives bit-identical rows to the same experts addressed through their pointer
-    tables (37 tokens: GEMV items; 80 tokens: the MFMA prefill path)."""
+    tables (37 tokens: GEMV items; 160 tokens: the MFMA prefill path)."""
     tables, _ = small
     packed = exl3.ExpertTables.packed(*tables.projs)
     assert packed.layout is not None and list(packed.layout)[9] > 0
@@ -518,9 +518,9 @@ def test_moe_prefill_inactive_slots_and_shared(exl3, oracle, small, monkeypatch)
 
 @pytest.mark.parametrize("M", [40, 80])
 def test_moe_prefill_gemv_and_mfma_paths(exl3, oracle, small, monkeypatch, M):
-    """The MFMA grouped GEMM (forced at 40 tokens, which by itself takes GEMV items over these 12 small experts; by
-    itself at 80): every expert's rows in blocks of up to 64 rows, hot and cold experts in one call (80 tokens: the
-    hot experts cross the 64-row block boundary)."""
+    """The MFMA grouped GEMM (forced: by itself a batch of up to 128 tokens over these 12 small experts takes GEMV
+    items): every expert's rows in blocks of up to 64 rows, hot and cold experts in one call (80 tokens: the hot
+    experts cross the 64-row block boundary)."""
     monkeypatch.setenv("EXL3MI_MOE_MFMA", "1")
     tables, orc = small
     ids, w = _skewed_ids(M, 4, 12, 1500 + M)
