@@ -1351,6 +1351,11 @@ static int moe_run(MoeArgs& a, hipStream_t st) {
         if (cap == 1 && M >= 2 && (int64_t)a.H * a.I > ((int64_t)1 << 22) &&
             moe_expected_items(a, 2) <= 0.92 * moe_expected_items(a, 1))
             cap = 2;
+        // wide experts taking many rows each, past 16 tokens: eight rows per item while at least 8 items remain (one
+        // expert of 4096 -> 4096, 64 / 128 tokens 124.5 -> 114, 220 -> 190 us; 4 experts top-2, 64 tokens 232 ->
+        // 210.5; with 4 items left four rows win: one expert at 32 tokens 76 against 86)
+        if (cap == 4 && M > 16 && (int64_t)a.H * a.I > ((int64_t)1 << 22) && moe_expected_items(a, 8) >= 8.0)
+            cap = 8;
         if (a.MR > cap) a.MR = cap;
         const int mr_env = env_int("EXL3MI_MOE_MR", 0);
         if (mr_env == 1 || mr_env == 2 || mr_env == 4 || mr_env == 8) a.MR = mr_env;
