@@ -380,7 +380,8 @@ def act_mul(g: np.ndarray, u: np.ndarray, act: int, limit: float = 0.0) -> np.nd
     g = g.astype(np.float64)
     u = u.astype(np.float64)
     if act == ACT_SILU:
-        s = g / (1.0 + np.exp(-g))
+        with np.errstate(over="ignore"):  # exp(-g) = inf for g < -709 gives the exact limit s = -0.0
+            s = g / (1.0 + np.exp(-g))
         if limit:
             s = np.minimum(s, limit)
             u = np.clip(u, -limit, limit)
