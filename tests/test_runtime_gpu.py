@@ -139,6 +139,8 @@ def test_graph_captured_before_growth_replays_on_live_buffers(exl3, oracle, laye
     assert torch.equal(_call(exl3, layer), eager)
 
 
+# the call refused under capture records nothing, so torch reports the third graph as empty
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
 def test_timeout_in_replay_resets_outgrown_counters_and_not_under_capture(exl3, oracle, layer):
     """A lost wait inside a graph replay, on a counter buffer that the workspace has since outgrown: a library call made
     under stream capture reports it and leaves the status word set (a reset recorded into a graph would not run now);
